@@ -1,0 +1,238 @@
+/*
+ * sandyrt_hip.h -- C ABI of the MI355X (gfx950) backend for SandyRT's
+ * data-parallel hot path.
+ *
+ * The reference dispatches every KernelIR op through one C++ launcher per
+ * kernel family, `launch_cuda_<family>(const CudaLaunchContext&, const
+ * Cuda<Family>Program&)` (src/device/cuda/CudaKernels.h:109-159), selected
+ * by `CudaDevice::run` (src/device/cuda/CudaDevice.cpp:520-578).  Each entry
+ * point below replaces one of those launchers.  Instead of the C++ context it
+ * takes plain tensor descriptors (device pointer, dtype, dims, strides,
+ * storage offset -- the fields of CudaDeviceBufferView/TensorViewDesc,
+ * src/device/cuda/CudaKernels.h:19-28, src/device/DeviceTypes.h:25-29), the
+ * op attributes that the Cuda<Family>Program carries, and a hipStream_t.
+ *
+ * Conventions
+ *   - Every call is stream-ordered on `stream` (a hipStream_t, NULL = the
+ *     default stream) and returns without synchronising the host.
+ *   - Return value 0 = success.  Non-zero = failure; a message worded like
+ *     the reference's Result<> error is written to err[0..err_cap).
+ *   - dtype codes follow sandy::core::DType (src/core/Tensor.h:13).
+ *   - Float tensors are F32 or BF16 (bf16 stores round to nearest even,
+ *     src/core/Tensor.h:43-49); index tensors are I32 or I64.
+ *   - Value checks that depend on device data (expert ids, token ids,
+ *     positions) cannot fail the call without a host round trip; kernels
+ *     record them in a sticky per-device error word instead, read with
+ *     sandy_hip_take_device_errors().
+ */
+#ifndef SANDYRT_HIP_H
+#define SANDYRT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SANDY_HIP_MAX_RANK 8
+#define SANDY_HIP_MAX_INPUTS 8
+#define SANDY_HIP_MAX_SCALARS 32
+
+enum SandyDType { SANDY_F32 = 0, SANDY_F16 = 1, SANDY_BF16 = 2, SANDY_I32 = 3, SANDY_I64 = 4, SANDY_U8 = 5 };
+
+enum SandyStatus {
+    SANDY_OK = 0,
+    SANDY_ERR_INVALID = 1,     /* shape / dtype / attribute rejected */
+    SANDY_ERR_UNSUPPORTED = 2, /* valid op this backend does not implement */
+    SANDY_ERR_HIP = 3,         /* HIP runtime failure */
+    SANDY_ERR_COMPILE = 4      /* hipRTC compilation failure */
+};
+
+/* Device-side value errors (bit flags of the sticky error word). */
+enum SandyDeviceError {
+    SANDY_DEVERR_EXPERT_ID = 1u << 0,   /* moe_gather topk expert id out of range */
+    SANDY_DEVERR_TOKEN_ID = 1u << 1,    /* moe_scatter_sum token id out of range */
+    SANDY_DEVERR_POSITION = 1u << 2,    /* rope position_ids must be non-negative */
+    SANDY_DEVERR_GATHER_ID = 1u << 3,   /* embedding id out of range */
+    SANDY_DEVERR_OFFSETS = 1u << 4,     /* moe_matmul invalid expert offsets */
+    SANDY_DEVERR_BLOCK = 1u << 5,       /* paged block id outside the pool */
+    SANDY_DEVERR_ATTN_POS = 1u << 6     /* attention position_offsets must be non-negative */
+};
+
+/* A strided view of device memory (TensorViewDesc, src/device/DeviceTypes.h:25-29). */
+typedef struct SandyTensor {
+    void* data;               /* device address of storage element 0 */
+    int32_t dtype;            /* enum SandyDType */
+    int32_t rank;             /* 0..8 */
+    int64_t dims[SANDY_HIP_MAX_RANK];
+    int64_t strides[SANDY_HIP_MAX_RANK]; /* in elements */
+    int64_t storage_offset;              /* in elements */
+} SandyTensor;
+
+/*
+ * A paged KV cache.  Every page holds `page_size` consecutive rows of the grow
+ * dimension for all `prefix` leading elements: page = [prefix, page_size,
+ * inner] (the reference's page layout, src/device/cuda/CudaPagedTensor.cpp:
+ * 187-226, addressing src/device/cuda/CudaKernelUtils.cuh:82-108).  Pages live
+ * in one pool allocation and are named by int32 block ids (pool + id *
+ * prefix * page_size * inner elements) instead of the reference's per-page
+ * void* table.
+ */
+typedef struct SandyPagedCache {
+    void* pool;               /* device base address of the page pool */
+    int32_t dtype;
+    int32_t reserved;
+    int64_t page_size;        /* rows of the grow dimension per page (power of two) */
+    int64_t prefix;           /* elements before the grow dim, e.g. kv heads */
+    int64_t inner;            /* elements after the grow dim, e.g. head dim */
+    int64_t num_pages;        /* pool capacity in pages */
+} SandyPagedCache;
+
+/* One node of a fused element-wise scalar DAG (ScalarNode, src/ir/KernelIR.h:346-355). */
+typedef struct SandyScalarNode {
+    uint32_t id;
+    int32_t op;               /* sandy::ir::kernel_ir::ScalarOp order, KernelIR.h:317-337 */
+    int32_t dtype;
+    uint32_t input_index;     /* Load: which input */
+    double constant;          /* Constant: the value */
+    int32_t operand_count;    /* 0..2 */
+    uint32_t operands[2];
+} SandyScalarNode;
+
+/* ---------------------------------------------------------------- library */
+
+/* Version string of the backend ("sandyrt-hip <semver> gfx950"). */
+const char* sandy_hip_version(void);
+
+/* Reads and clears the sticky device error word of the current device after
+ * synchronising `stream`.  *flags receives the SandyDeviceError bits; if any
+ * bit is set the call returns SANDY_ERR_INVALID with the reference's message
+ * for the lowest set bit.  Replaces the per-launch flag read-backs of
+ * CudaRoPEKernels.cu:310-333, CudaGatherKernels.cu:291-294 and
+ * CudaMoeScatterSumKernels.cu:218-239. */
+int sandy_hip_take_device_errors(void* stream, uint32_t* flags, char* err, size_t err_cap);
+
+/* ---------------------------------------------------------------- fused groups */
+
+/*
+ * One fused element-wise group (ElementwiseKernelOp, src/ir/KernelIR.h:357-387;
+ * replaces launch_cuda_elementwise, src/device/cuda/CudaElementwiseKernels.cu:
+ * 189-213).  The scalar DAG is turned into straight-line gfx950 HIP C++ and
+ * compiled with hipRTC on first use (cached by DAG hash).  broadcast[i] = 1
+ * marks a right-aligned broadcast input (element index = linear % numel).
+ */
+int sandy_hip_elementwise(const SandyScalarNode* nodes, int32_t node_count, uint32_t result,
+                          const SandyTensor* inputs, const int32_t* broadcast, int32_t input_count,
+                          const SandyTensor* out, void* stream, char* err, size_t err_cap);
+
+/*
+ * NormKernelOp (src/ir/KernelIR.h:544-573; replaces launch_cuda_norm,
+ * src/device/cuda/CudaNormKernels.cu:210-237).  kind 0 = RMSNorm
+ * (weight may be NULL, bias must be NULL), kind 1 = LayerNorm (weight and
+ * bias required).  Normalises the last dimension.
+ */
+int sandy_hip_norm(int32_t kind, const SandyTensor* x, const SandyTensor* weight,
+                   const SandyTensor* bias, double epsilon, const SandyTensor* out,
+                   void* stream, char* err, size_t err_cap);
+
+/*
+ * Residual add fused into the following RMSNorm -- the model pair
+ * `x = __add(x, h); y = __rms_norm(x, w)` (src/models/tinyllama/
+ * common.sandy.go:44-50) in one pass: sum_out = x + residual (rounded to the
+ * output dtype, exactly the reference add), out = rms_norm(sum_out, weight).
+ * sum_out may alias x.
+ */
+int sandy_hip_add_rms_norm(const SandyTensor* x, const SandyTensor* residual,
+                           const SandyTensor* weight, double epsilon,
+                           const SandyTensor* sum_out, const SandyTensor* out,
+                           void* stream, char* err, size_t err_cap);
+
+/*
+ * RoPEKernelOp (src/ir/KernelIR.h:575-610; replaces launch_cuda_rope,
+ * src/device/cuda/CudaRoPEKernels.cu:272-336).  position_ids may be NULL
+ * (position = index along dim -2) or hold 1 (offset), seq or vector-count
+ * entries.  rotary_dim < 0 means the full last dimension.  Negative position
+ * ids set SANDY_DEVERR_POSITION instead of synchronising.
+ */
+int sandy_hip_rope(const SandyTensor* x, const SandyTensor* position_ids, double theta,
+                   int64_t rotary_dim, int32_t split_half, const SandyTensor* out,
+                   void* stream, char* err, size_t err_cap);
+
+/* SoftmaxKernelOp (src/ir/KernelIR.h:494-515; replaces launch_cuda_softmax,
+ * src/device/cuda/CudaSoftmaxKernels.cu:145-169).  Any axis. */
+int sandy_hip_softmax(const SandyTensor* x, int64_t axis, const SandyTensor* out,
+                      void* stream, char* err, size_t err_cap);
+
+/* ReductionKernelOp with ReduceOp::Sum over one axis (replaces
+ * launch_cuda_reduction, src/device/cuda/CudaKernels.cu:88-151). */
+int sandy_hip_reduce_sum(const SandyTensor* x, int64_t axis, int32_t keep_dims,
+                         const SandyTensor* out, void* stream, char* err, size_t err_cap);
+
+/* GatherKernelOp / embedding (replaces launch_cuda_gather,
+ * src/device/cuda/CudaGatherKernels.cu:97-117,360-387). */
+int sandy_hip_gather(const SandyTensor* ids, const SandyTensor* table, const SandyTensor* out,
+                     void* stream, char* err, size_t err_cap);
+
+/* ---------------------------------------------------------------- attention */
+
+/*
+ * AttentionKernelOp on dense K/V (replaces launch_cuda_attention,
+ * src/device/cuda/CudaAttentionKernels.cu:680-766).  q [B,Hq,Tq,D] (or rank
+ * 3), k/v [B,Hkv,Tk,D]; position_offsets (NULL or [B]) shifts query
+ * positions; window > 0 is a sliding window; scale <= 0 means 1/sqrt(D).
+ */
+int sandy_hip_attention(const SandyTensor* q, const SandyTensor* k, const SandyTensor* v,
+                        const SandyTensor* position_offsets, int64_t window, double scale,
+                        const SandyTensor* out, void* stream, char* err, size_t err_cap);
+
+/*
+ * Decode attention (Tq = 1) over a paged KV cache -- the reference's
+ * AttentionKernelOp with paged K/V inputs (CudaAttentionKernels.cu:247-404,
+ * 469-563).  q [B,Hq,1,D] bf16 or f32; k_cache/v_cache pages are [Hkv,
+ * page_size, D]; block_table [B, max_blocks] int32 lists each sequence's pages
+ * in order; position_offsets [B] (i32/i64) is the position of each query, so
+ * keys 0..position (and >= position + 1 - window when window > 0) attend.
+ * GQA head groups share one pass over their KV head (bf16: MFMA tiles).
+ */
+int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedCache* k_cache,
+                              const SandyPagedCache* v_cache, const SandyTensor* block_table,
+                              const SandyTensor* position_offsets, int64_t window, double scale,
+                              const SandyTensor* out, void* stream, char* err, size_t err_cap);
+
+/* ---------------------------------------------------------------- MoE */
+
+/* TopKKernelOp (replaces launch_cuda_topk, src/device/cuda/CudaTopKKernels.cu:
+ * 616-646).  Order: value descending, index ascending on ties. */
+int sandy_hip_topk(const SandyTensor* x, int64_t k, int64_t axis, const SandyTensor* values,
+                   const SandyTensor* indices, void* stream, char* err, size_t err_cap);
+
+/* MoeGatherKernelOp (replaces launch_cuda_moe_gather, src/device/cuda/
+ * CudaGatherKernels.cu:389-649): stable permute, rows ordered expert, then
+ * token, then slot (src/core/TensorCalc.cpp:1634-1660), computed on the
+ * device with no host round trip. */
+int sandy_hip_moe_gather(const SandyTensor* x, const SandyTensor* topk_ids,
+                         const SandyTensor* topk_weights, int64_t num_experts, int64_t top_k,
+                         const SandyTensor* packed_x, const SandyTensor* packed_weights,
+                         const SandyTensor* token_ids, const SandyTensor* expert_offsets,
+                         void* stream, char* err, size_t err_cap);
+
+/* MoeMatMulKernelOp (replaces launch_cuda_moe_matmul, src/device/cuda/
+ * CudaMatMulKernels.cu:294-616): grouped expert GEMM over expert_offsets, on
+ * bf16 MFMA for bf16 operands. */
+int sandy_hip_moe_matmul(const SandyTensor* x, const SandyTensor* expert_offsets,
+                         const SandyTensor* weight, int32_t transpose_rhs, const SandyTensor* out,
+                         void* stream, char* err, size_t err_cap);
+
+/* MoeScatterSumKernelOp (replaces launch_cuda_moe_scatter_sum,
+ * src/device/cuda/CudaMoeScatterSumKernels.cu:243-405): deterministic
+ * per-token combine in packed-row order, no atomics. */
+int sandy_hip_moe_scatter_sum(const SandyTensor* packed_out, const SandyTensor* packed_weights,
+                              const SandyTensor* token_ids, const SandyTensor* out,
+                              void* stream, char* err, size_t err_cap);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,209 @@
+// common.h -- shared host/device helpers of the gfx950 backend.
+//
+// Host side: error reporting into the caller's buffer, SandyTensor checks,
+// the per-device sticky error word and the per-device workspace.
+// Device side: bf16 <-> f32 with the reference's rounding, 128-bit vector
+// loads/stores of 8 elements, wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/sandyrt_hip.h"
+
+namespace sandy_hip {
+
+// ---------------------------------------------------------------- host errors
+struct Err {
+    char* buf;
+    size_t cap;
+};
+
+inline int fail(Err e, int code, const char* fmt, ...) {
+    if (e.buf && e.cap) {
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(e.buf, e.cap, fmt, ap);
+        va_end(ap);
+    }
+    return code;
+}
+
+inline int ok(Err e) {
+    if (e.buf && e.cap) e.buf[0] = 0;
+    return SANDY_OK;
+}
+
+#define SANDY_HIP_TRY(expr, e, what)                                                   \
+    do {                                                                               \
+        hipError_t st_ = (expr);                                                       \
+        if (st_ != hipSuccess)                                                         \
+            return ::sandy_hip::fail(e, SANDY_ERR_HIP, "%s: %s", what, hipGetErrorString(st_)); \
+    } while (0)
+
+// ---------------------------------------------------------------- tensor helpers
+inline int64_t numel(const SandyTensor& t) {
+    int64_t n = 1;
+    for (int i = 0; i < t.rank; i++) n *= t.dims[i];
+    return n;
+}
+
+inline bool contiguous(const SandyTensor& t) {
+    int64_t s = 1;
+    for (int i = t.rank - 1; i >= 0; i--) {
+        if (t.dims[i] != 1 && t.strides[i] != s) return false;
+        s *= t.dims[i];
+    }
+    return true;
+}
+
+inline bool same_shape(const SandyTensor& a, const SandyTensor& b) {
+    if (a.rank != b.rank) return false;
+    for (int i = 0; i < a.rank; i++)
+        if (a.dims[i] != b.dims[i]) return false;
+    return true;
+}
+
+inline bool is_float(int32_t dt) { return dt == SANDY_F32 || dt == SANDY_BF16; }
+inline bool is_index(int32_t dt) { return dt == SANDY_I32 || dt == SANDY_I64; }
+inline size_t dtype_size(int32_t dt) {
+    switch (dt) {
+        case SANDY_F32: return 4;
+        case SANDY_F16: return 2;
+        case SANDY_BF16: return 2;
+        case SANDY_I32: return 4;
+        case SANDY_I64: return 8;
+        case SANDY_U8: return 1;
+    }
+    return 0;
+}
+
+// Element address of storage_offset (data + offset * element size).
+inline void* base_ptr(const SandyTensor& t) {
+    return static_cast<char*>(t.data) + t.storage_offset * static_cast<int64_t>(dtype_size(t.dtype));
+}
+
+inline bool valid_rank(const SandyTensor* t) { return t && t->rank >= 0 && t->rank <= SANDY_HIP_MAX_RANK; }
+
+// Per-device sticky error word (one uint32 in device memory, zeroed at
+// creation).  Kernels atomicOr SandyDeviceError bits into it.
+uint32_t* device_error_word(Err e, int* status);
+
+// Per-device, per-purpose grow-only scratch.  The returned memory stays valid
+// until the next call with the same slot and a larger size; callers that
+// need zeroed memory keep it zero themselves.
+void* device_workspace(int slot, size_t bytes, hipStream_t stream, Err e, int* status);
+
+// Zero-initialised companion area (counters); re-zeroed only when grown.
+void* device_counters(int slot, size_t bytes, hipStream_t stream, Err e, int* status);
+
+// ---------------------------------------------------------------- device helpers
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
+
+// round to nearest even, NaN not special-cased (src/core/Tensor.h:43-49)
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+struct BF16 {};
+struct F32 {};
+
+// Eight consecutive elements <-> eight floats (16 B for bf16, 32 B for f32).
+template <typename T>
+struct Vec8;
+
+template <>
+struct Vec8<BF16> {
+    using elem = uint16_t;
+    __device__ __forceinline__ static void load(const void* p, int64_t i, float (&v)[8]) {
+        uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i);
+        uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[2 * j] = __uint_as_float(w[j] << 16);
+            v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+        }
+    }
+    __device__ __forceinline__ static void store(void* p, int64_t i, const float (&v)[8]) {
+        uint4 r;
+        r.x = pack_bf16x2(v[0], v[1]);
+        r.y = pack_bf16x2(v[2], v[3]);
+        r.z = pack_bf16x2(v[4], v[5]);
+        r.w = pack_bf16x2(v[6], v[7]);
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p) + i) = r;
+    }
+    // value as it will read back after a store (rounded to bf16)
+    __device__ __forceinline__ static float round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+    __device__ __forceinline__ static float load1(const void* p, int64_t i) {
+        return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+    }
+    __device__ __forceinline__ static void store1(void* p, int64_t i, float f) {
+        static_cast<uint16_t*>(p)[i] = f32_to_bf16(f);
+    }
+};
+
+template <>
+struct Vec8<F32> {
+    using elem = float;
+    __device__ __forceinline__ static void load(const void* p, int64_t i, float (&v)[8]) {
+        const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+        float4 a = q[0], b = q[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+    __device__ __forceinline__ static void store(void* p, int64_t i, const float (&v)[8]) {
+        float4* q = reinterpret_cast<float4*>(static_cast<float*>(p) + i);
+        q[0] = make_float4(v[0], v[1], v[2], v[3]);
+        q[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    __device__ __forceinline__ static float round(float f) { return f; }
+    __device__ __forceinline__ static float load1(const void* p, int64_t i) { return static_cast<const float*>(p)[i]; }
+    __device__ __forceinline__ static void store1(void* p, int64_t i, float f) { static_cast<float*>(p)[i] = f; }
+};
+
+__device__ __forceinline__ float load_any(const void* p, int32_t dt, int64_t i) {
+    return dt == SANDY_BF16 ? Vec8<BF16>::load1(p, i) : Vec8<F32>::load1(p, i);
+}
+__device__ __forceinline__ void store_any(void* p, int32_t dt, int64_t i, float f) {
+    if (dt == SANDY_BF16)
+        Vec8<BF16>::store1(p, i, f);
+    else
+        Vec8<F32>::store1(p, i, f);
+}
+__device__ __forceinline__ int64_t load_index(const void* p, int32_t dt, int64_t i) {
+    return dt == SANDY_I32 ? static_cast<int64_t>(static_cast<const int32_t*>(p)[i]) : static_cast<const int64_t*>(p)[i];
+}
+__device__ __forceinline__ void store_index(void* p, int32_t dt, int64_t i, int64_t v) {
+    if (dt == SANDY_I32)
+        static_cast<int32_t*>(p)[i] = static_cast<int32_t>(v);
+    else
+        static_cast<int64_t*>(p)[i] = v;
+}
+
+// wave64 butterfly reductions (every lane ends with the full result)
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+
+constexpr int kWave = 64;
+
+} // namespace sandy_hip

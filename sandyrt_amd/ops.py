@@ -1,0 +1,271 @@
+"""Host-side operator API of the gfx950 backend.
+
+One function per KernelIR kernel family of the reference
+(src/ir/KernelIR.h:65-85), with the reference's argument meaning and error
+wording.  Tensors are torch tensors on the GPU (torch is the allocator and
+stream provider only); every call goes through the C ABI of
+include/sandyrt_hip.h into the hand-written HIP kernels.  There is no CPU
+path: without the built library every call raises BackendMissing.
+
+Outputs are allocated when `out` is not given.  Calls are stream-ordered on
+torch's current stream and do not synchronise, except `check_device_errors`.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import SandyError, call, desc
+
+# ScalarOp codes (src/ir/KernelIR.h:317-337)
+LOAD, CONST, ADD, SUB, MUL, DIV, MAX, MIN, NEG, SQRT, RSQRT, EXP, LOG, TANH, RELU, CAST = range(16)
+
+
+def _require_gpu(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise SandyError(1, "sandyrt_amd tensors must live on the GPU")
+
+
+def check_device_errors() -> None:
+    """Synchronise and raise the first recorded device-side value error
+    (bad expert/token/position ids), worded like the reference."""
+    _lib.take_device_errors()
+
+
+# ------------------------------------------------------------------ norms
+def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, epsilon: float, out=None):
+    """NormKernelOp RMSNorm (src/core/TensorCalc.cpp:1953-2000)."""
+    _require_gpu(x, weight)
+    out = torch.empty_like(x) if out is None else out
+    call("sandy_hip_norm", 0, desc(x), desc(weight), None, float(epsilon), desc(out))
+    return out
+
+
+def layer_norm(x, weight, bias, epsilon: float, out=None):
+    """NormKernelOp LayerNorm (src/core/TensorCalc.cpp:2010-2077)."""
+    _require_gpu(x, weight, bias)
+    out = torch.empty_like(x) if out is None else out
+    call("sandy_hip_norm", 1, desc(x), desc(weight), desc(bias), float(epsilon), desc(out))
+    return out
+
+
+def add_rms_norm(x, residual, weight, epsilon: float, sum_out=None, out=None):
+    """`s = x + residual; y = rms_norm(s, weight)` in one pass; returns (s, y)."""
+    _require_gpu(x, residual, weight)
+    sum_out = torch.empty_like(x) if sum_out is None else sum_out
+    out = torch.empty_like(x) if out is None else out
+    call("sandy_hip_add_rms_norm", desc(x), desc(residual), desc(weight), float(epsilon), desc(sum_out), desc(out))
+    return sum_out, out
+
+
+# ------------------------------------------------------------------ rope / softmax / reductions
+def rope(x, theta: float, rotary_dim: int = -1, split_half: bool = False, position_ids=None, out=None):
+    """RoPEKernelOp (src/core/TensorCalc.cpp:1823-1951)."""
+    _require_gpu(x, position_ids)
+    out = torch.empty_like(x) if out is None else out
+    call("sandy_hip_rope", desc(x), desc(position_ids), float(theta), int(rotary_dim), int(bool(split_half)),
+         desc(out))
+    return out
+
+
+def softmax(x, axis: int = -1, out=None):
+    """SoftmaxKernelOp (src/core/TensorCalc.cpp:1337-1399)."""
+    _require_gpu(x)
+    out = torch.empty_like(x) if out is None else out
+    call("sandy_hip_softmax", desc(x), int(axis), desc(out))
+    return out
+
+
+def sum(x, axis: int = -1, keep_dims: bool = True, out=None):  # noqa: A001 - reference op name
+    """ReductionKernelOp Sum over one axis (src/core/TensorCalc.cpp:1401-1445)."""
+    _require_gpu(x)
+    ax = axis % x.dim()
+    shape = list(x.shape)
+    if keep_dims:
+        shape[ax] = 1
+    else:
+        del shape[ax]
+    out = torch.empty(shape, dtype=x.dtype, device=x.device) if out is None else out
+    call("sandy_hip_reduce_sum", desc(x), int(axis), int(bool(keep_dims)), desc(out))
+    return out
+
+
+def embedding(ids, weight, out=None):
+    """GatherKernelOp / embedding (src/core/TensorCalc.cpp:1520-1563)."""
+    _require_gpu(ids, weight)
+    shape = list(ids.shape) + list(weight.shape[1:])
+    out = torch.empty(shape, dtype=weight.dtype, device=weight.device) if out is None else out
+    call("sandy_hip_gather", desc(ids), desc(weight), desc(out))
+    return out
+
+
+# ------------------------------------------------------------------ fused element-wise groups
+@dataclass
+class ScalarNode:
+    """One node of an ElementwiseKernelOp scalar DAG (src/ir/KernelIR.h:346-355)."""
+
+    id: int
+    op: int
+    input_index: int = 0
+    constant: float = 0.0
+    operands: tuple = ()
+
+
+def _nodes(nodes):
+    arr = (_lib.SandyScalarNode * len(nodes))()
+    for i, n in enumerate(nodes):
+        arr[i].id = n.id
+        arr[i].op = n.op
+        arr[i].dtype = _lib.F32
+        arr[i].input_index = n.input_index
+        arr[i].constant = float(n.constant)
+        arr[i].operand_count = len(n.operands)
+        for j, o in enumerate(n.operands):
+            arr[i].operands[j] = o
+    return arr
+
+
+def elementwise(nodes, result: int, inputs, broadcast=None, out_shape=None, out_dtype=None, out=None):
+    """Run one fused ElementwiseKernelOp.  `nodes` in dependency order;
+    broadcast[i] True marks a right-aligned broadcast input."""
+    _require_gpu(*inputs)
+    broadcast = broadcast or [False] * len(inputs)
+    if out is None:
+        shape = out_shape if out_shape is not None else inputs[0].shape
+        dtype = out_dtype if out_dtype is not None else inputs[0].dtype
+        out = torch.empty(shape, dtype=dtype, device=inputs[0].device)
+    n = len(inputs)
+    arr = (_lib.SandyTensor * max(1, n))()
+    for i, t in enumerate(inputs):
+        arr[i] = desc(t).contents
+    bc = (C.c_int32 * max(1, n))(*[int(bool(b)) for b in broadcast])
+    call("sandy_hip_elementwise", _nodes(nodes), len(nodes), int(result), arr, bc, n, desc(out))
+    return out
+
+
+# Scalar DAGs of the model-level builtins, as src/ir/BuiltinLowering.cpp
+# lowers them (gelu 116-140, silu 142-158, softcap 160-185).
+def silu_mul_nodes():
+    """silu(gate) * up with silu(x) = (0.5 x)(1 + tanh(0.5 x)); inputs (gate, up)."""
+    return [
+        ScalarNode(0, LOAD, 0), ScalarNode(1, CONST, constant=0.5), ScalarNode(2, MUL, operands=(1, 0)),
+        ScalarNode(3, TANH, operands=(2,)), ScalarNode(4, CONST, constant=1.0), ScalarNode(5, ADD, operands=(4, 3)),
+        ScalarNode(6, MUL, operands=(2, 5)), ScalarNode(7, LOAD, 1), ScalarNode(8, MUL, operands=(6, 7)),
+    ], 8
+
+
+def gelu_mul_nodes():
+    """gelu(gate) * up, gelu(x) = (0.5 x)(1 + tanh(0.7978845608028654 (x + 0.044715 x^3)))."""
+    return [
+        ScalarNode(0, LOAD, 0), ScalarNode(1, CONST, constant=0.5), ScalarNode(2, MUL, operands=(1, 0)),
+        ScalarNode(3, MUL, operands=(0, 0)), ScalarNode(4, MUL, operands=(3, 0)),
+        ScalarNode(5, CONST, constant=0.044715), ScalarNode(6, MUL, operands=(5, 4)),
+        ScalarNode(7, ADD, operands=(0, 6)), ScalarNode(8, CONST, constant=0.7978845608028654),
+        ScalarNode(9, MUL, operands=(8, 7)), ScalarNode(10, TANH, operands=(9,)),
+        ScalarNode(11, CONST, constant=1.0), ScalarNode(12, ADD, operands=(11, 10)),
+        ScalarNode(13, MUL, operands=(2, 12)), ScalarNode(14, LOAD, 1), ScalarNode(15, MUL, operands=(13, 14)),
+    ], 15
+
+
+def softcap_nodes(cap: float):
+    """softcap(x, c) = tanh(x * (1 / c)) * c; one input."""
+    return [
+        ScalarNode(0, LOAD, 0), ScalarNode(1, CONST, constant=1.0 / cap), ScalarNode(2, MUL, operands=(0, 1)),
+        ScalarNode(3, TANH, operands=(2,)), ScalarNode(4, CONST, constant=cap), ScalarNode(5, MUL, operands=(3, 4)),
+    ], 5
+
+
+def residual_add_nodes():
+    return [ScalarNode(0, LOAD, 0), ScalarNode(1, LOAD, 1), ScalarNode(2, ADD, operands=(0, 1))], 2
+
+
+# ------------------------------------------------------------------ attention
+def attention(q, k, v, position_offsets=None, window: int = 0, scale: float = -1.0, out=None):
+    """AttentionKernelOp over dense K/V (src/core/TensorCalc.cpp:1167-1314)."""
+    _require_gpu(q, k, v, position_offsets)
+    out = torch.empty_like(q) if out is None else out
+    call("sandy_hip_attention", desc(q), desc(k), desc(v), desc(position_offsets), int(window), float(scale),
+         desc(out))
+    return out
+
+
+@dataclass
+class PagedCache:
+    """A KV page pool: pool tensor [num_pages, prefix, page_size, inner]."""
+
+    pool: torch.Tensor
+
+    def struct(self):
+        p = self.pool
+        if p.dim() != 4 or not p.is_contiguous():
+            raise SandyError(1, "paged pool must be a contiguous [pages, prefix, page_size, inner] tensor")
+        s = _lib.SandyPagedCache()
+        s.pool = p.data_ptr()
+        s.dtype = _lib._TORCH_TO_CODE[p.dtype]
+        s.page_size = p.shape[2]
+        s.prefix = p.shape[1]
+        s.inner = p.shape[3]
+        s.num_pages = p.shape[0]
+        return C.pointer(s)
+
+
+def paged_attention(q, k_cache: PagedCache, v_cache: PagedCache, block_table, position_offsets,
+                    window: int = 0, scale: float = -1.0, out=None):
+    """Decode attention (Tq = 1) over paged K/V; block_table [B, max_blocks] int32."""
+    _require_gpu(q, block_table, position_offsets, k_cache.pool, v_cache.pool)
+    out = torch.empty_like(q) if out is None else out
+    call("sandy_hip_paged_attention", desc(q), k_cache.struct(), v_cache.struct(), desc(block_table),
+         desc(position_offsets), int(window), float(scale), desc(out))
+    return out
+
+
+# ------------------------------------------------------------------ MoE
+def topk(x, k: int, axis: int = -1, index_dtype=torch.int64, values=None, indices=None):
+    """TopKKernelOp: value descending, index ascending on ties (TensorCalc.cpp:1447-1518)."""
+    _require_gpu(x)
+    ax = axis % x.dim()
+    shape = list(x.shape)
+    shape[ax] = k
+    values = torch.empty(shape, dtype=x.dtype, device=x.device) if values is None else values
+    indices = torch.empty(shape, dtype=index_dtype, device=x.device) if indices is None else indices
+    call("sandy_hip_topk", desc(x), int(k), int(axis), desc(values), desc(indices))
+    return values, indices
+
+
+def moe_gather(x, topk_ids, topk_weights, num_experts: int, index_dtype=torch.int64):
+    """MoeGatherKernelOp (TensorCalc.cpp:1565-1667) -> packed_x, packed_weights, token_ids, expert_offsets."""
+    _require_gpu(x, topk_ids, topk_weights)
+    top_k = topk_ids.shape[-1]
+    lead = list(x.shape[:-2])
+    seq, hidden = x.shape[-2], x.shape[-1]
+    rows = seq * top_k
+    dev = x.device
+    packed_x = torch.empty(lead + [rows, hidden], dtype=x.dtype, device=dev)
+    packed_w = torch.empty(lead + [rows], dtype=topk_weights.dtype, device=dev)
+    token_ids = torch.empty(lead + [rows], dtype=index_dtype, device=dev)
+    offsets = torch.empty(lead + [num_experts + 1], dtype=index_dtype, device=dev)
+    call("sandy_hip_moe_gather", desc(x), desc(topk_ids), desc(topk_weights), int(num_experts), int(top_k),
+         desc(packed_x), desc(packed_w), desc(token_ids), desc(offsets))
+    return packed_x, packed_w, token_ids, offsets
+
+
+def moe_matmul(x, expert_offsets, weight, transpose_rhs: bool = True, out=None):
+    """MoeMatMulKernelOp (TensorCalc.cpp:1669-1743)."""
+    _require_gpu(x, expert_offsets, weight)
+    m = weight.shape[1] if transpose_rhs else weight.shape[2]
+    out = torch.empty(list(x.shape[:-1]) + [m], dtype=x.dtype, device=x.device) if out is None else out
+    call("sandy_hip_moe_matmul", desc(x), desc(expert_offsets), desc(weight), int(bool(transpose_rhs)), desc(out))
+    return out
+
+
+def moe_scatter_sum(packed_out, packed_weights, token_ids, seq: int, out=None):
+    """MoeScatterSumKernelOp (TensorCalc.cpp:1745-1811)."""
+    _require_gpu(packed_out, packed_weights, token_ids)
+    shape = list(packed_out.shape[:-2]) + [seq, packed_out.shape[-1]]
+    out = torch.empty(shape, dtype=packed_out.dtype, device=packed_out.device) if out is None else out
+    call("sandy_hip_moe_scatter_sum", desc(packed_out), desc(packed_weights), desc(token_ids), desc(out))
+    return out
