@@ -1,0 +1,292 @@
+// rope.hip -- rotary position embedding (RoPEKernelOp).
+//
+// Semantics: src/core/TensorCalc.cpp:1823-1937 (rope_impl).  Vector v of the
+// input ([..., seq, dim]) sits at position v % seq, or takes it from
+// position_ids (numel 1: ids[0] + v % seq; numel == vectors: ids[v];
+// numel == seq: ids[v % seq]).  Split-half rotates (x[i], x[i + dim/2]) by
+// pos / theta^(2i / dim); interleaved rotates (x[2i], x[2i+1]) by
+// pos / theta^(2i / rotary_dim); pairs past rotary_dim/2 are copied.
+//
+// The denominators theta^(2i/d) are evaluated on the host with the same
+// powf the CPU reference uses and passed as kernel arguments, so every angle
+// (a correctly rounded division on gfx950) equals the CPU's bit for bit; only
+// cos/sin differ, by the device libm's ulp error.  The reference CUDA kernel
+// evaluates powf per pair on the device and synchronises the host after every
+// launch to read an error flag (CudaRoPEKernels.cu:272-333); here a negative
+// position sets the sticky device error word instead.
+//
+// gfx950 design: when positions depend only on the sequence index, one thread
+// owns (sequence position, 8 pairs, a group of heads): it evaluates 8 sincos
+// once and reuses them for every head in its group, moving 2 x 16 B per head
+// with 128-bit loads/stores.  C2's q [1, 32, 4096, 64] therefore spends 1/4
+// of a sincos per element instead of one, and stays HBM-bound.
+#include "common.h"
+
+#include <cmath>
+
+namespace sandy_hip {
+namespace {
+
+constexpr int kMaxPairs = 256;  // rotary dims up to 512
+
+struct RopeArgs {
+    float denom[kMaxPairs];
+};
+
+// mode: 0 = position from sequence index, 1 = ids[0] + seq index,
+//       2 = ids[seq index], 3 = ids[vector]
+__device__ __forceinline__ int64_t rope_position(int mode, const void* ids, int32_t ids_dt, int64_t vec, int64_t s,
+                                                 uint32_t* errw) {
+    int64_t p = s;
+    if (mode == 1) p = load_index(ids, ids_dt, 0) + s;
+    else if (mode == 2) p = load_index(ids, ids_dt, s);
+    else if (mode == 3) p = load_index(ids, ids_dt, vec);
+    if (p < 0) {
+        atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_POSITION));
+        p = 0;
+    }
+    return p;
+}
+
+// Split-half, 8 pairs per thread.  grid: (seq * chunks * groups) threads.
+template <typename T>
+__global__ __launch_bounds__(256) void rope_split_kernel(
+        const void* __restrict__ x, void* __restrict__ out, const void* __restrict__ ids, int32_t ids_dt, int mode,
+        int64_t seq, int64_t outer, int dim, int rot_pairs, int groups, int per_group, RopeArgs args,
+        uint32_t* errw) {
+    const int half = dim >> 1;
+    const int chunks = half >> 3;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t total = seq * chunks * groups;
+    if (t >= total) return;
+    const int c = static_cast<int>(t % chunks);
+    const int64_t rest = t / chunks;
+    const int64_t s = rest % seq;
+    const int g = static_cast<int>(rest / seq);
+    const int64_t o_begin = static_cast<int64_t>(g) * per_group;
+    const int64_t o_end = min(outer, o_begin + per_group);
+    float cs[8], sn[8];
+    int64_t pos = -1;
+    for (int64_t o = o_begin; o < o_end; o++) {
+        const int64_t vec = o * seq + s;
+        if (mode == 3 || pos < 0) {
+            pos = rope_position(mode, ids, ids_dt, vec, s, errw);
+            const float fp = static_cast<float>(pos);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int p = c * 8 + i;
+                if (p < rot_pairs) {
+                    const float angle = fp / args.denom[p];
+                    sincosf(angle, &sn[i], &cs[i]);
+                }
+            }
+        }
+        const int64_t base = vec * dim;
+        float a[8], b[8];
+        Vec8<T>::load(x, base + c * 8, a);
+        Vec8<T>::load(x, base + half + c * 8, b);
+        float ra[8], rb[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int p = c * 8 + i;
+            if (p < rot_pairs) {
+                ra[i] = __fsub_rn(__fmul_rn(a[i], cs[i]), __fmul_rn(b[i], sn[i]));
+                rb[i] = __fadd_rn(__fmul_rn(a[i], sn[i]), __fmul_rn(b[i], cs[i]));
+            } else {
+                ra[i] = a[i];
+                rb[i] = b[i];
+            }
+        }
+        Vec8<T>::store(out, base + c * 8, ra);
+        Vec8<T>::store(out, base + half + c * 8, rb);
+    }
+}
+
+// Interleaved, 4 pairs (8 elements) per thread.
+template <typename T>
+__global__ __launch_bounds__(256) void rope_interleaved_kernel(
+        const void* __restrict__ x, void* __restrict__ out, const void* __restrict__ ids, int32_t ids_dt, int mode,
+        int64_t seq, int64_t outer, int dim, int rot_pairs, int groups, int per_group, RopeArgs args,
+        uint32_t* errw) {
+    const int chunks = dim >> 3;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t total = seq * chunks * groups;
+    if (t >= total) return;
+    const int c = static_cast<int>(t % chunks);
+    const int64_t rest = t / chunks;
+    const int64_t s = rest % seq;
+    const int g = static_cast<int>(rest / seq);
+    const int64_t o_begin = static_cast<int64_t>(g) * per_group;
+    const int64_t o_end = min(outer, o_begin + per_group);
+    float cs[4], sn[4];
+    int64_t pos = -1;
+    for (int64_t o = o_begin; o < o_end; o++) {
+        const int64_t vec = o * seq + s;
+        if (mode == 3 || pos < 0) {
+            pos = rope_position(mode, ids, ids_dt, vec, s, errw);
+            const float fp = static_cast<float>(pos);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int p = c * 4 + i;
+                if (p < rot_pairs) sincosf(fp / args.denom[p], &sn[i], &cs[i]);
+            }
+        }
+        const int64_t base = vec * dim;
+        float a[8], r[8];
+        Vec8<T>::load(x, base + c * 8, a);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int p = c * 4 + i;
+            if (p < rot_pairs) {
+                r[2 * i] = __fsub_rn(__fmul_rn(a[2 * i], cs[i]), __fmul_rn(a[2 * i + 1], sn[i]));
+                r[2 * i + 1] = __fadd_rn(__fmul_rn(a[2 * i], sn[i]), __fmul_rn(a[2 * i + 1], cs[i]));
+            } else {
+                r[2 * i] = a[2 * i];
+                r[2 * i + 1] = a[2 * i + 1];
+            }
+        }
+        Vec8<T>::store(out, base + c * 8, r);
+    }
+}
+
+// Generic: one thread per pair, strided tensors, any dims.
+struct Strided {
+    int64_t dims[SANDY_HIP_MAX_RANK];
+    int64_t xs[SANDY_HIP_MAX_RANK];
+    int64_t os[SANDY_HIP_MAX_RANK];
+    int rank;
+};
+
+__device__ __forceinline__ void offsets(const Strided& st, int64_t linear, int64_t& xo, int64_t& oo) {
+    xo = 0;
+    oo = 0;
+    for (int d = st.rank - 1; d >= 0; d--) {
+        const int64_t c = linear % st.dims[d];
+        linear /= st.dims[d];
+        xo += c * st.xs[d];
+        oo += c * st.os[d];
+    }
+}
+
+__global__ __launch_bounds__(256) void rope_generic_kernel(
+        const void* __restrict__ x, int32_t dt, void* __restrict__ out, const void* __restrict__ ids, int32_t ids_dt,
+        int mode, int64_t seq, int64_t vectors, int dim, int rot_pairs, int split, Strided st, RopeArgs args,
+        uint32_t* errw) {
+    const int pairs = dim >> 1;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= vectors * pairs) return;
+    const int p = static_cast<int>(t % pairs);
+    const int64_t vec = t / pairs;
+    const int64_t s = vec % seq;
+    const int64_t i0 = split ? p : 2 * p;
+    const int64_t i1 = split ? p + pairs : 2 * p + 1;
+    int64_t x0, o0, x1, o1;
+    offsets(st, vec * dim + i0, x0, o0);
+    offsets(st, vec * dim + i1, x1, o1);
+    const float a = load_any(x, dt, x0);
+    const float b = load_any(x, dt, x1);
+    if (p >= rot_pairs) {
+        store_any(out, dt, o0, a);
+        store_any(out, dt, o1, b);
+        return;
+    }
+    const int64_t pos = rope_position(mode, ids, ids_dt, vec, s, errw);
+    float sn, cs;
+    sincosf(static_cast<float>(pos) / args.denom[p], &sn, &cs);
+    store_any(out, dt, o0, __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn)));
+    store_any(out, dt, o1, __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, cs)));
+}
+
+} // namespace
+} // namespace sandy_hip
+
+using namespace sandy_hip;
+
+extern "C" int sandy_hip_rope(const SandyTensor* x, const SandyTensor* position_ids, double theta,
+                              int64_t rotary_dim, int32_t split_half, const SandyTensor* out,
+                              void* stream_, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    if (!valid_rank(x) || !valid_rank(out)) return fail(e, SANDY_ERR_INVALID, "rope tensor rank out of range");
+    if (!is_float(x->dtype)) return fail(e, SANDY_ERR_INVALID, "rope input unsupported dtype");
+    if (!same_shape(*x, *out)) return fail(e, SANDY_ERR_INVALID, "rope output shape mismatch");
+    if (out->dtype != x->dtype) return fail(e, SANDY_ERR_INVALID, "rope output dtype mismatch");
+    if (position_ids && !is_index(position_ids->dtype))
+        return fail(e, SANDY_ERR_INVALID, "rope position_ids must be i32 or i64");
+    if (x->rank < 2) return fail(e, SANDY_ERR_INVALID, "rope input must have rank >= 2");
+    const float th = static_cast<float>(theta);
+    if (th <= 0.0f) return fail(e, SANDY_ERR_INVALID, "rope theta must be > 0");
+    const int64_t seq = x->dims[x->rank - 2];
+    const int64_t dim = x->dims[x->rank - 1];
+    if (dim <= 0 || dim % 2 != 0) return fail(e, SANDY_ERR_INVALID, "rope last dimension must be positive and even");
+    if (rotary_dim < 0) rotary_dim = dim;
+    if (rotary_dim <= 0 || rotary_dim % 2 != 0) return fail(e, SANDY_ERR_INVALID, "rope rotary_dim must be positive and even");
+    if (rotary_dim > dim) return fail(e, SANDY_ERR_INVALID, "rope rotary_dim must be <= last dimension");
+    if (rotary_dim / 2 > kMaxPairs) return fail(e, SANDY_ERR_UNSUPPORTED, "rope rotary_dim above %d", 2 * kMaxPairs);
+    const int64_t total = numel(*x);
+    if (total == 0) return ok(e);
+    const int64_t vectors = total / dim;
+    const int64_t outer = seq ? vectors / seq : 0;
+    int mode = 0;
+    if (position_ids) {
+        const int64_t cnt = numel(*position_ids);
+        if (cnt != 1 && cnt != seq && cnt != vectors)
+            return fail(e, SANDY_ERR_INVALID, "rope position_ids numel must be 1, sequence length, or vector count");
+        if (!contiguous(*position_ids)) return fail(e, SANDY_ERR_UNSUPPORTED, "rope position_ids must be contiguous");
+        mode = cnt == 1 ? 1 : (cnt == vectors ? 3 : 2);
+        if (mode == 3 && outer == 1) mode = 2;  // ids[v] == ids[v % seq] when there is one sequence
+    }
+    RopeArgs args;
+    const int rot_pairs = static_cast<int>(rotary_dim / 2);
+    const float div = static_cast<float>(split_half ? dim : rotary_dim);
+    for (int p = 0; p < rot_pairs; p++) args.denom[p] = std::pow(th, static_cast<float>(2 * p) / div);
+    int status = 0;
+    uint32_t* errw = device_error_word(e, &status);
+    if (status) return status;
+    const void* ids = position_ids ? base_ptr(*position_ids) : nullptr;
+    const int32_t ids_dt = position_ids ? position_ids->dtype : SANDY_I64;
+    const void* px = base_ptr(*x);
+    void* po = base_ptr(*out);
+    const bool bf = x->dtype == SANDY_BF16;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(px) | reinterpret_cast<uintptr_t>(po)) & 15u) == 0;
+    const bool fast = contiguous(*x) && contiguous(*out) && aligned && dim <= 2 * kMaxPairs * 2 &&
+                      (split_half ? (dim / 2) % 8 == 0 : dim % 8 == 0);
+    if (fast) {
+        const int chunks = static_cast<int>(split_half ? dim / 16 : dim / 8);
+        const int64_t base_threads = seq * chunks;
+        int groups = 1, per = 1;
+        if (mode == 3) {
+            groups = static_cast<int>(outer);
+            per = 1;
+        } else {
+            // enough threads to fill 256 CUs (~128K), each reusing its sincos over per heads
+            const int64_t want = 131072;
+            groups = static_cast<int>(std::min<int64_t>(outer, std::max<int64_t>(1, want / std::max<int64_t>(1, base_threads))));
+            per = static_cast<int>((outer + groups - 1) / groups);
+            groups = static_cast<int>((outer + per - 1) / per);
+        }
+        const int64_t threads = base_threads * groups;
+        dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+        if (split_half) {
+            if (bf) hipLaunchKernelGGL(rope_split_kernel<BF16>, grid, dim3(256), 0, stream, px, po, ids, ids_dt, mode, seq, outer, static_cast<int>(dim), rot_pairs, groups, per, args, errw);
+            else hipLaunchKernelGGL(rope_split_kernel<F32>, grid, dim3(256), 0, stream, px, po, ids, ids_dt, mode, seq, outer, static_cast<int>(dim), rot_pairs, groups, per, args, errw);
+        } else {
+            if (bf) hipLaunchKernelGGL(rope_interleaved_kernel<BF16>, grid, dim3(256), 0, stream, px, po, ids, ids_dt, mode, seq, outer, static_cast<int>(dim), rot_pairs, groups, per, args, errw);
+            else hipLaunchKernelGGL(rope_interleaved_kernel<F32>, grid, dim3(256), 0, stream, px, po, ids, ids_dt, mode, seq, outer, static_cast<int>(dim), rot_pairs, groups, per, args, errw);
+        }
+    } else {
+        Strided st{};
+        st.rank = x->rank;
+        for (int i = 0; i < x->rank; i++) {
+            st.dims[i] = x->dims[i];
+            st.xs[i] = x->strides[i];
+            st.os[i] = out->strides[i];
+        }
+        const int64_t threads = vectors * (dim / 2);
+        dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+        hipLaunchKernelGGL(rope_generic_kernel, grid, dim3(256), 0, stream, px, x->dtype, po, ids, ids_dt, mode, seq,
+                           vectors, static_cast<int>(dim), rot_pairs, split_half ? 1 : 0, st, args, errw);
+    }
+    SANDY_HIP_TRY(hipGetLastError(), e, "rope launch");
+    return ok(e);
+}
