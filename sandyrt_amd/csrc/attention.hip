@@ -1,0 +1,625 @@
+// attention.hip -- AttentionKernelOp: paged decode on bf16 MFMA, plus a
+// general kernel for dense K/V, fp32 and uncommon shapes.
+//
+// Semantics: src/core/TensorCalc.cpp:1167-1314 (attention_impl).  Query qi of
+// batch b sits at position offsets[b] + qi; key ki attends when
+// ki <= position and (window == 0 or ki > position - window); scores are
+// (q . k) * scale with scale <= 0 meaning 1/sqrt(D); softmax over the keys;
+// an all-masked row gives zeros; GQA maps q head h to kv head h / (Hq/Hkv).
+//
+// Paged decode (the hot path).  The reference runs one
+// 32-lane warp per (split, q head, batch): every q head re-reads its KV head
+// (8x redundant for TinyLlama), with scalar fp32 FMAs, per-element paged
+// address math and a cudaMallocAsync of the split partials on every call
+// (CudaAttentionKernels.cu:247-404,469-563).  Here one 256-thread workgroup
+// owns (split of keys, kv head, sequence) and the whole GQA group of q heads:
+//   - K tiles of 16 keys are read from their page with 128-bit loads straight
+//     into MFMA A operands; S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (the head
+//     group padded to 16 columns);
+//   - online softmax in the exp2 domain, per q head (one MFMA column);
+//   - P^T leaves the S^T MFMA already in the B-operand layout of
+//     v_mfma_f32_16x16x16_bf16, and V tiles are transposed through LDS into A
+//     operands, so O^T += V^T P^T runs on MFMA with no register shuffles;
+//   - each wave prefetches its next tile while computing the current one;
+//   - the 4 waves merge in LDS; splits merge in the same launch: the last
+//     workgroup to finish a (sequence, kv head) combines the split partials
+//     (log-sum-exp) -- one launch per step, no host round trip, partials and
+//     counters in a persistent workspace.
+// The probabilities fed to the PV product are rounded to bf16 and the
+// normaliser sums those rounded values, so O / L stays a convex combination.
+#include "common.h"
+
+#include <algorithm>
+#include <cstdlib>
+
+namespace sandy_hip {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct PagedArgs {
+    const uint16_t* q;
+    int64_t q_sb, q_sh;  // element strides of q over batch and head (last dim contiguous)
+    uint16_t* out;
+    int64_t o_sb, o_sh;
+    const uint16_t* k_pool;
+    const uint16_t* v_pool;
+    int64_t page_elems;  // Hkv * P * D
+    int64_t num_pages;
+    const int32_t* table;
+    int64_t table_stride;
+    int64_t max_blocks;
+    const void* pos;
+    int32_t pos_dt;
+    int32_t page_size;
+    int32_t log2_page;
+    int32_t hq, hkv, group;
+    int64_t window;
+    float scale_log2;  // scale * log2(e)
+    int32_t split_keys;
+    int32_t max_splits;
+    float* ws_o;   // [B, Hq, max_splits, D]
+    float* ws_ml;  // [B, Hq, max_splits, 2]
+    uint32_t* counters;  // [B, Hkv]
+    uint32_t* errw;
+};
+
+__device__ __forceinline__ short4_t pack_p(const float (&p)[4]) {
+    short4_t r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) r[i] = static_cast<short>(f32_to_bf16(p[i]));
+    return r;
+}
+
+template <int D>
+struct TileRegs {
+    uint4 k[D / 32];
+    uint4 v[D / 32];
+};
+
+template <int D>
+__device__ __forceinline__ void load_tile(const PagedArgs& a, int64_t t0, int b, int kh, int lane, TileRegs<D>& r,
+                                          bool& ok) {
+    const int64_t page = t0 >> a.log2_page;
+    const int32_t blk = a.table[b * a.table_stride + page];
+    ok = blk >= 0 && blk < a.num_pages;
+    if (!ok) {
+        if (lane == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
+#pragma unroll
+        for (int kk = 0; kk < D / 32; kk++) r.k[kk] = r.v[kk] = make_uint4(0, 0, 0, 0);
+        return;
+    }
+    const int64_t in_page = t0 & (a.page_size - 1);
+    const int64_t row = static_cast<int64_t>(blk) * a.page_elems + static_cast<int64_t>(kh) * a.page_size * D +
+                        (in_page + (lane & 15)) * D + 8 * (lane >> 4);
+    const uint4* kp = reinterpret_cast<const uint4*>(a.k_pool + row);
+    const uint4* vp = reinterpret_cast<const uint4*>(a.v_pool + row);
+#pragma unroll
+    for (int kk = 0; kk < D / 32; kk++) {
+        r.k[kk] = kp[kk * 4];  // + 32 elements per step
+        r.v[kk] = vp[kk * 4];
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    constexpr int kRow = 2 * D + 8;  // bytes per V row in LDS (8-byte pad: conflict-free transposed reads)
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
+    const int G = a.group;
+
+    const int64_t pos = load_index(a.pos, a.pos_dt, b);
+    if (pos < 0) {
+        if (threadIdx.x == 0 && split == 0 && kh == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
+        return;
+    }
+    const int64_t n_keys = min(pos + 1, a.max_blocks * static_cast<int64_t>(a.page_size));
+    const int64_t min_key = a.window > 0 ? max<int64_t>(0, pos + 1 - a.window) : 0;
+    const int64_t key_begin = (min_key >> 4) << 4;
+    const int64_t span = max<int64_t>(0, n_keys - key_begin);
+    const int n_splits = max(1, static_cast<int>((span + a.split_keys - 1) / a.split_keys));
+    if (split >= n_splits) return;
+    const int64_t s_begin = key_begin + static_cast<int64_t>(split) * a.split_keys;
+    const int64_t s_end = min(n_keys, s_begin + a.split_keys);
+
+    const int g = lane & 15;
+    const int j = lane >> 4;
+    // Q^T as B operands: column g, d = 32 kk + 8 j .. + 7
+    uint4 qv[D / 32];
+    if (g < G) {
+        const uint4* qp = reinterpret_cast<const uint4*>(a.q + b * a.q_sb + (kh * G + g) * a.q_sh + 8 * j);
+#pragma unroll
+        for (int kk = 0; kk < D / 32; kk++) qv[kk] = qp[kk * 4];
+    } else {
+#pragma unroll
+        for (int kk = 0; kk < D / 32; kk++) qv[kk] = make_uint4(0, 0, 0, 0);
+    }
+
+    float m = -INFINITY, l = 0.0f;
+    f32x4_t acc[D / 16];
+#pragma unroll
+    for (int t = 0; t < D / 16; t++) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    unsigned char* vl = smem + wave * 16 * kRow;  // this wave's V tile
+
+    // One 16-key tile: S^T on MFMA, online softmax, V^T through LDS, PV on MFMA.
+    auto compute = [&](const TileRegs<D>& cur, int64_t t0) {
+        f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < D / 32; kk++)
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, cur.k[kk]),
+                                                         __builtin_bit_cast(bf16x8_t, qv[kk]), sc, 0, 0, 0);
+        float sv[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int64_t key = t0 + 4 * j + i;
+            const bool valid = key < s_end && key >= min_key;
+            sv[i] = valid ? sc[i] * a.scale_log2 : -INFINITY;
+            mx = fmaxf(mx, sv[i]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m, mx);
+        float p[4];
+        float rs = 0.0f;
+        if (m_new == -INFINITY) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) p[i] = 0.0f;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                p[i] = sv[i] == -INFINITY ? 0.0f : bf16_to_f32(f32_to_bf16(exp2f(sv[i] - m_new)));
+                rs += p[i];
+            }
+        }
+        rs += __shfl_xor(rs, 16, 64);
+        rs += __shfl_xor(rs, 32, 64);
+        const float alpha = m == -INFINITY ? 0.0f : exp2f(m - m_new);
+        l = l * alpha + rs;
+        m = m_new;
+#pragma unroll
+        for (int t = 0; t < D / 16; t++) acc[t] *= alpha;
+
+        // V tile -> LDS (row = key, masked keys zeroed so they cannot inject NaN)
+        {
+            const int64_t vkey = t0 + (lane & 15);
+            const bool vvalid = vkey < s_end && vkey >= min_key;
+            unsigned char* row = vl + (lane & 15) * kRow + 16 * j;
+#pragma unroll
+            for (int kk = 0; kk < D / 32; kk++) {
+                uint4 v = vvalid ? cur.v[kk] : make_uint4(0, 0, 0, 0);
+                uint2* dst = reinterpret_cast<uint2*>(row + 64 * kk);
+                dst[0] = make_uint2(v.x, v.y);
+                dst[1] = make_uint2(v.z, v.w);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        const short4_t pb = pack_p(p);
+#pragma unroll
+        for (int t = 0; t < D / 16; t++) {
+            short4_t va;
+            const unsigned char* col = vl + 2 * (16 * t + (lane & 15));
+#pragma unroll
+            for (int i = 0; i < 4; i++) va[i] = *reinterpret_cast<const short*>(col + (4 * j + i) * kRow);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, acc[t], 0, 0, 0);
+        }
+        __builtin_amdgcn_wave_barrier();
+    };
+
+    // Ping-pong register buffers: the next tile's loads are in flight while
+    // the current one is computed.
+    TileRegs<D> buf0, buf1;
+    bool ok0 = false, ok1 = false;
+    int64_t t0 = s_begin + 16 * wave;
+    if (t0 < s_end) load_tile<D>(a, t0, b, kh, lane, buf0, ok0);
+    for (; t0 < s_end; t0 += 128) {
+        if (t0 + 64 < s_end) load_tile<D>(a, t0 + 64, b, kh, lane, buf1, ok1);
+        if (ok0) compute(buf0, t0);
+        if (t0 + 64 >= s_end) break;
+        if (t0 + 128 < s_end) load_tile<D>(a, t0 + 128, b, kh, lane, buf0, ok0);
+        if (ok1) compute(buf1, t0 + 64);
+    }
+
+    // ---- merge the 4 waves through LDS (reuses the V staging area)
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(smem);   // [4][G][D]
+    float* ml = red + 4 * G * D;                    // [4][G][2]
+    if (g < G) {
+#pragma unroll
+        for (int t = 0; t < D / 16; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) red[(wave * G + g) * D + 16 * t + 4 * j + i] = acc[t][i];
+        if (j == 0) {
+            ml[(wave * G + g) * 2] = m;
+            ml[(wave * G + g) * 2 + 1] = l;
+        }
+    }
+    __syncthreads();
+    const int hq = a.hq;
+    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
+        const int gg = idx / D, d = idx % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, ml[(w * G + gg) * 2]);
+        float O = 0.0f, L = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float mw = ml[(w * G + gg) * 2];
+                if (mw == -INFINITY) continue;
+                const float f = exp2f(mw - M);
+                O += red[(w * G + gg) * D + d] * f;
+                L += ml[(w * G + gg) * 2 + 1] * f;
+            }
+        }
+        const int h = kh * G + gg;
+        if (n_splits == 1) {
+            a.out[b * a.o_sb + h * a.o_sh + d] = f32_to_bf16(L > 0.0f ? O / L : 0.0f);
+        } else {
+            const int64_t slot = (static_cast<int64_t>(b) * hq + h) * a.max_splits + split;
+            a.ws_o[slot * D + d] = O;
+            if (d == 0) {
+                a.ws_ml[slot * 2] = M;
+                a.ws_ml[slot * 2 + 1] = L;
+            }
+        }
+    }
+    if (n_splits == 1) return;
+
+    // ---- the last workgroup of this (sequence, kv head) merges the splits
+    __shared__ int is_last;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = atomicAdd(&a.counters[b * a.hkv + kh], 1u);
+        is_last = prev == static_cast<uint32_t>(n_splits - 1);
+    }
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
+        const int gg = idx / D, d = idx % D;
+        const int h = kh * G + gg;
+        const int64_t base = (static_cast<int64_t>(b) * hq + h) * a.max_splits;
+        float M = -INFINITY;
+        for (int s = 0; s < n_splits; s++) M = fmaxf(M, __builtin_nontemporal_load(&a.ws_ml[(base + s) * 2]));
+        float O = 0.0f, L = 0.0f;
+        if (M != -INFINITY) {
+            for (int s = 0; s < n_splits; s++) {
+                const float ms = __builtin_nontemporal_load(&a.ws_ml[(base + s) * 2]);
+                if (ms == -INFINITY) continue;
+                const float f = exp2f(ms - M);
+                O += __builtin_nontemporal_load(&a.ws_o[(base + s) * D + d]) * f;
+                L += __builtin_nontemporal_load(&a.ws_ml[(base + s) * 2 + 1]) * f;
+            }
+        }
+        a.out[b * a.o_sb + h * a.o_sh + d] = f32_to_bf16(L > 0.0f ? O / L : 0.0f);
+    }
+    if (threadIdx.x == 0) a.counters[b * a.hkv + kh] = 0u;  // ready for the next launch
+}
+
+// ---------------------------------------------------------------- general kernel
+struct GenArgs {
+    const void* q;
+    int64_t qs[4];  // strides over (b, h, qi, d)
+    void* out;
+    int64_t os[4];
+    const void* k;
+    const void* v;
+    int64_t ks[4];  // dense strides over (b, kh, key, d)
+    int64_t vs[4];
+    int32_t dt;
+    int32_t paged;
+    // paged cache (decode only)
+    int64_t page_elems;
+    int64_t page_size;
+    int64_t num_pages;
+    const int32_t* table;
+    int64_t table_stride;
+    int64_t max_blocks;
+    const void* pos;
+    int32_t pos_dt;
+    int32_t hq, hkv, tq;
+    int64_t tk;  // dense key count (paged: max_blocks * page_size)
+    int64_t d;
+    int64_t window;
+    float scale;
+    float* scores;  // [B, Hq, Tq, tk]
+    uint32_t* errw;
+};
+
+template <typename T>
+__device__ __forceinline__ float kv_load(const GenArgs& a, const void* base, const int64_t* st, int b, int kh,
+                                         int64_t key, int64_t d, bool& ok) {
+    if (!a.paged) return Vec8<T>::load1(base, b * st[0] + kh * st[1] + key * st[2] + d * st[3]);
+    const int64_t page = key / a.page_size;
+    const int32_t blk = a.table[b * a.table_stride + page];
+    if (blk < 0 || blk >= a.num_pages) {
+        ok = false;
+        return 0.0f;
+    }
+    return Vec8<T>::load1(base, static_cast<int64_t>(blk) * a.page_elems + (kh * a.page_size + key % a.page_size) * a.d + d);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void attention_general_kernel(GenArgs a) {
+    __shared__ float fred[4];
+    __shared__ double dred[4];
+    const int qi = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int kh = h / (a.hq / a.hkv);
+    int64_t base_pos = 0;
+    if (a.pos) {
+        base_pos = load_index(a.pos, a.pos_dt, b);
+        if (base_pos < 0) {
+            if (tid == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
+            return;
+        }
+    }
+    const int64_t qpos = base_pos + qi;
+    const int64_t min_key = a.window > 0 ? max<int64_t>(0, qpos + 1 - a.window) : 0;
+    const int64_t tk = a.tk;
+    float* sc = a.scores + ((static_cast<int64_t>(b) * a.hq + h) * a.tq + qi) * tk;
+    const int64_t qoff = b * a.qs[0] + h * a.qs[1] + qi * a.qs[2];
+    float lmax = -INFINITY;
+    bool ok = true;
+    for (int64_t key = tid; key < tk; key += 256) {
+        float s = -INFINITY;
+        if (key <= qpos && key >= min_key) {
+            float acc = 0.0f;
+            for (int64_t d = 0; d < a.d; d++)
+                acc = __fadd_rn(acc, __fmul_rn(Vec8<T>::load1(a.q, qoff + d * a.qs[3]),
+                                               kv_load<T>(a, a.k, a.ks, b, kh, key, d, ok)));
+            s = __fmul_rn(acc, a.scale);
+        }
+        sc[key] = s;
+        lmax = fmaxf(lmax, s);
+    }
+    if (!ok) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
+    lmax = wave_max(lmax);
+    if ((tid & 63) == 0) fred[tid >> 6] = lmax;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(fred[0], fred[1]), fmaxf(fred[2], fred[3]));
+    const int64_t ooff = b * a.os[0] + h * a.os[1] + qi * a.os[2];
+    if (mx == -INFINITY) {
+        for (int64_t d = tid; d < a.d; d += 256) Vec8<T>::store1(a.out, ooff + d * a.os[3], 0.0f);
+        return;
+    }
+    double sum = 0.0;
+    for (int64_t key = tid; key < tk; key += 256) sum += exp(static_cast<double>(__fsub_rn(sc[key], mx)));
+    sum = wave_sum(sum);
+    if ((tid & 63) == 0) dred[tid >> 6] = sum;
+    __syncthreads();
+    const double total = dred[0] + dred[1] + dred[2] + dred[3];
+    for (int64_t d = tid; d < a.d; d += 256) {
+        float acc = 0.0f;
+        if (total != 0.0) {
+            const float inv = 1.0f / static_cast<float>(total);
+            for (int64_t key = 0; key < tk; key++) {
+                const float s = sc[key];
+                if (s == -INFINITY) continue;
+                const float prob = __fmul_rn(expf(__fsub_rn(s, mx)), inv);
+                acc = __fadd_rn(acc, __fmul_rn(prob, kv_load<T>(a, a.v, a.vs, b, kh, key, d, ok)));
+            }
+        }
+        Vec8<T>::store1(a.out, ooff + d * a.os[3], acc);
+    }
+}
+
+int env_int(const char* name, int dflt) {
+    const char* v = std::getenv(name);
+    return v ? std::atoi(v) : dflt;
+}
+
+} // namespace
+} // namespace sandy_hip
+
+using namespace sandy_hip;
+
+extern "C" int sandy_hip_attention(const SandyTensor* q, const SandyTensor* k, const SandyTensor* v,
+                                   const SandyTensor* position_offsets, int64_t window, double scale,
+                                   const SandyTensor* out, void* stream_, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    if (!valid_rank(q) || !valid_rank(k) || !valid_rank(v) || !valid_rank(out))
+        return fail(e, SANDY_ERR_INVALID, "attention tensor rank out of range");
+    if (!is_float(q->dtype) || !is_float(k->dtype) || !is_float(v->dtype))
+        return fail(e, SANDY_ERR_INVALID, "attention q unsupported dtype");
+    if (q->dtype != k->dtype || q->dtype != v->dtype) return fail(e, SANDY_ERR_INVALID, "attention operands must have same dtype");
+    const int rank = q->rank;
+    if ((rank != 3 && rank != 4) || k->rank != rank || v->rank != rank)
+        return fail(e, SANDY_ERR_INVALID, "attention q, k, and v must all have rank 3 or rank 4");
+    if (window < 0) return fail(e, SANDY_ERR_INVALID, "attention window must be >= 0");
+    const int o = rank == 4 ? 1 : 0;
+    const int64_t B = rank == 4 ? q->dims[0] : 1;
+    if (rank == 4 && (k->dims[0] != B || v->dims[0] != B)) return fail(e, SANDY_ERR_INVALID, "attention batch dimension mismatch");
+    const int64_t hq = q->dims[o], hkv = k->dims[o], tq = q->dims[o + 1], tk = k->dims[o + 1], D = q->dims[o + 2];
+    if (v->dims[o] != hkv) return fail(e, SANDY_ERR_INVALID, "attention k and v head count mismatch");
+    if (v->dims[o + 1] != tk) return fail(e, SANDY_ERR_INVALID, "attention k and v sequence dimension mismatch");
+    if (k->dims[o + 2] != D || v->dims[o + 2] != D) return fail(e, SANDY_ERR_INVALID, "attention head dimension mismatch");
+    if (hq <= 0 || hkv <= 0 || hq % hkv != 0) return fail(e, SANDY_ERR_INVALID, "attention heads must be divisible by kv_heads");
+    if (!same_shape(*q, *out) || out->dtype != q->dtype) return fail(e, SANDY_ERR_INVALID, "attention output shape mismatch");
+    if (position_offsets) {
+        if (!is_index(position_offsets->dtype)) return fail(e, SANDY_ERR_INVALID, "attention position_offsets must be i32 or i64");
+        const int64_t n = numel(*position_offsets);
+        if (rank == 4 && n != B) return fail(e, SANDY_ERR_INVALID, "attention position_offsets length must match batch");
+        if (rank == 3 && n != 1) return fail(e, SANDY_ERR_INVALID, "attention unbatched position_offsets must have one element");
+        if (!contiguous(*position_offsets)) return fail(e, SANDY_ERR_UNSUPPORTED, "attention position_offsets must be contiguous");
+    }
+    if (numel(*q) == 0) return ok(e);
+    int status = 0;
+    uint32_t* errw = device_error_word(e, &status);
+    if (status) return status;
+    GenArgs a{};
+    auto fill4 = [&](const SandyTensor* t, int64_t* s) {
+        if (rank == 4) for (int i = 0; i < 4; i++) s[i] = t->strides[i];
+        else { s[0] = 0; for (int i = 0; i < 3; i++) s[i + 1] = t->strides[i]; }
+    };
+    a.q = base_ptr(*q);
+    fill4(q, a.qs);
+    a.out = base_ptr(*out);
+    fill4(out, a.os);
+    a.k = base_ptr(*k);
+    a.v = base_ptr(*v);
+    fill4(k, a.ks);
+    fill4(v, a.vs);
+    a.dt = q->dtype;
+    a.paged = 0;
+    a.pos = position_offsets ? base_ptr(*position_offsets) : nullptr;
+    a.pos_dt = position_offsets ? position_offsets->dtype : SANDY_I64;
+    a.hq = static_cast<int32_t>(hq);
+    a.hkv = static_cast<int32_t>(hkv);
+    a.tq = static_cast<int32_t>(tq);
+    a.tk = tk;
+    a.d = D;
+    a.window = window;
+    a.scale = scale <= 0.0 ? 1.0f / sqrtf(static_cast<float>(D)) : static_cast<float>(scale);
+    const size_t sbytes = static_cast<size_t>(B * hq * tq * std::max<int64_t>(tk, 1)) * sizeof(float);
+    a.scores = static_cast<float*>(device_workspace(1, sbytes, stream, e, &status));
+    if (status) return status;
+    a.errw = errw;
+    dim3 grid(static_cast<unsigned>(tq), static_cast<unsigned>(hq), static_cast<unsigned>(B));
+    if (q->dtype == SANDY_BF16) hipLaunchKernelGGL(attention_general_kernel<BF16>, grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL(attention_general_kernel<F32>, grid, dim3(256), 0, stream, a);
+    SANDY_HIP_TRY(hipGetLastError(), e, "attention launch");
+    return ok(e);
+}
+
+extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedCache* kc, const SandyPagedCache* vc,
+                                         const SandyTensor* table, const SandyTensor* position_offsets,
+                                         int64_t window, double scale, const SandyTensor* out, void* stream_,
+                                         char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    if (!valid_rank(q) || !valid_rank(out) || !valid_rank(table) || !valid_rank(position_offsets) || !kc || !vc)
+        return fail(e, SANDY_ERR_INVALID, "paged attention requires q, caches, block table, positions and output");
+    if (!is_float(q->dtype)) return fail(e, SANDY_ERR_INVALID, "attention q unsupported dtype");
+    if (kc->dtype != q->dtype || vc->dtype != q->dtype) return fail(e, SANDY_ERR_INVALID, "attention operands must have same dtype");
+    if (q->rank != 4 || q->dims[2] != 1) return fail(e, SANDY_ERR_INVALID, "paged attention expects q [B, Hq, 1, D]");
+    const int64_t B = q->dims[0], hq = q->dims[1], D = q->dims[3];
+    const int64_t hkv = kc->prefix, P = kc->page_size;
+    if (vc->prefix != hkv || vc->page_size != P || vc->inner != kc->inner || vc->num_pages != kc->num_pages)
+        return fail(e, SANDY_ERR_INVALID, "attention k and v head count mismatch");
+    if (kc->inner != D) return fail(e, SANDY_ERR_INVALID, "attention head dimension mismatch");
+    if (P <= 0 || (P & (P - 1)) != 0) return fail(e, SANDY_ERR_INVALID, "paged tensor pool page_size must be a power of two");
+    if (hq <= 0 || hkv <= 0 || hq % hkv != 0) return fail(e, SANDY_ERR_INVALID, "attention heads must be divisible by kv_heads");
+    if (window < 0) return fail(e, SANDY_ERR_INVALID, "attention window must be >= 0");
+    if (!same_shape(*q, *out) || out->dtype != q->dtype) return fail(e, SANDY_ERR_INVALID, "attention output shape mismatch");
+    if (table->dtype != SANDY_I32 || table->rank != 2 || table->dims[0] != B || table->strides[1] != 1)
+        return fail(e, SANDY_ERR_INVALID, "paged attention block table must be [B, max_blocks] int32 with unit inner stride");
+    if (!is_index(position_offsets->dtype) || numel(*position_offsets) != B || !contiguous(*position_offsets))
+        return fail(e, SANDY_ERR_INVALID, "attention position_offsets length must match batch");
+    if (q->strides[3] != 1 || out->strides[3] != 1) return fail(e, SANDY_ERR_UNSUPPORTED, "paged attention needs unit head-dim stride");
+    if (B == 0) return ok(e);
+    int status = 0;
+    uint32_t* errw = device_error_word(e, &status);
+    if (status) return status;
+    const int64_t G = hq / hkv;
+    const int64_t max_blocks = table->dims[1];
+    const float sc = scale <= 0.0 ? 1.0f / sqrtf(static_cast<float>(D)) : static_cast<float>(scale);
+
+    const bool aligned = ((reinterpret_cast<uintptr_t>(base_ptr(*q)) | reinterpret_cast<uintptr_t>(kc->pool) |
+                           reinterpret_cast<uintptr_t>(vc->pool)) & 15u) == 0 &&
+                         q->strides[0] % 8 == 0 && q->strides[1] % 8 == 0;
+    const bool mfma = q->dtype == SANDY_BF16 && (D == 64 || D == 128 || D == 256) && G <= 16 && P % 16 == 0 &&
+                      aligned && env_int("SANDY_PAGED_GENERIC", 0) == 0;
+    if (mfma) {
+        PagedArgs a{};
+        a.q = static_cast<const uint16_t*>(base_ptr(*q));
+        a.q_sb = q->strides[0];
+        a.q_sh = q->strides[1];
+        a.out = static_cast<uint16_t*>(base_ptr(*out));
+        a.o_sb = out->strides[0];
+        a.o_sh = out->strides[1];
+        a.k_pool = static_cast<const uint16_t*>(kc->pool);
+        a.v_pool = static_cast<const uint16_t*>(vc->pool);
+        a.page_elems = hkv * P * D;
+        a.num_pages = kc->num_pages;
+        a.table = static_cast<const int32_t*>(base_ptr(*table));
+        a.table_stride = table->strides[0];
+        a.max_blocks = max_blocks;
+        a.pos = base_ptr(*position_offsets);
+        a.pos_dt = position_offsets->dtype;
+        a.page_size = static_cast<int32_t>(P);
+        int lg = 0;
+        while ((1LL << lg) < P) lg++;
+        a.log2_page = lg;
+        a.hq = static_cast<int32_t>(hq);
+        a.hkv = static_cast<int32_t>(hkv);
+        a.group = static_cast<int32_t>(G);
+        a.window = window;
+        a.scale_log2 = sc * kLog2e;
+        // split size: enough workgroups to cover ~2 per CU at the average context
+        const int64_t max_keys = max_blocks * P;
+        int64_t split = env_int("SANDY_PAGED_SPLIT", 0);
+        if (split <= 0) {
+            split = (max_keys * B * hkv) / 1024;
+            split = std::min<int64_t>(2048, std::max<int64_t>(256, split));
+        }
+        split = (split + 63) / 64 * 64;
+        a.split_keys = static_cast<int32_t>(split);
+        a.max_splits = static_cast<int32_t>((max_keys + split - 1) / split + 1);
+        const size_t ws_o = static_cast<size_t>(B * hq * a.max_splits * D) * sizeof(float);
+        const size_t ws_ml = static_cast<size_t>(B * hq * a.max_splits * 2) * sizeof(float);
+        char* ws = static_cast<char*>(device_workspace(0, ws_o + ws_ml, stream, e, &status));
+        if (status) return status;
+        a.ws_o = reinterpret_cast<float*>(ws);
+        a.ws_ml = reinterpret_cast<float*>(ws + ws_o);
+        a.counters = static_cast<uint32_t*>(device_counters(0, static_cast<size_t>(B * hkv) * sizeof(uint32_t), stream, e, &status));
+        if (status) return status;
+        a.errw = errw;
+        dim3 grid(static_cast<unsigned>(a.max_splits), static_cast<unsigned>(hkv), static_cast<unsigned>(B));
+        const size_t lds_v = 4 * 16 * (2 * D + 8);
+        const size_t lds_r = (4 * G * D + 4 * G * 2) * sizeof(float);
+        const size_t lds = std::max(lds_v, lds_r);
+        switch (D) {
+            case 64: hipLaunchKernelGGL(paged_decode_mfma_kernel<64>, grid, dim3(256), lds, stream, a); break;
+            case 128: hipLaunchKernelGGL(paged_decode_mfma_kernel<128>, grid, dim3(256), lds, stream, a); break;
+            default: hipLaunchKernelGGL(paged_decode_mfma_kernel<256>, grid, dim3(256), lds, stream, a); break;
+        }
+        SANDY_HIP_TRY(hipGetLastError(), e, "paged attention launch");
+        return ok(e);
+    }
+    GenArgs a{};
+    a.q = base_ptr(*q);
+    for (int i = 0; i < 4; i++) {
+        a.qs[i] = q->strides[i];
+        a.os[i] = out->strides[i];
+    }
+    a.out = base_ptr(*out);
+    a.k = kc->pool;
+    a.v = vc->pool;
+    a.dt = q->dtype;
+    a.paged = 1;
+    a.page_elems = hkv * P * D;
+    a.page_size = P;
+    a.num_pages = kc->num_pages;
+    a.table = static_cast<const int32_t*>(base_ptr(*table));
+    a.table_stride = table->strides[0];
+    a.max_blocks = max_blocks;
+    a.pos = base_ptr(*position_offsets);
+    a.pos_dt = position_offsets->dtype;
+    a.hq = static_cast<int32_t>(hq);
+    a.hkv = static_cast<int32_t>(hkv);
+    a.tq = 1;
+    a.tk = max_blocks * P;
+    a.d = D;
+    a.window = window;
+    a.scale = sc;
+    const size_t sbytes = static_cast<size_t>(B * hq * std::max<int64_t>(a.tk, 1)) * sizeof(float);
+    a.scores = static_cast<float*>(device_workspace(1, sbytes, stream, e, &status));
+    if (status) return status;
+    a.errw = errw;
+    dim3 grid(1, static_cast<unsigned>(hq), static_cast<unsigned>(B));
+    if (q->dtype == SANDY_BF16) hipLaunchKernelGGL(attention_general_kernel<BF16>, grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL(attention_general_kernel<F32>, grid, dim3(256), 0, stream, a);
+    SANDY_HIP_TRY(hipGetLastError(), e, "paged attention launch");
+    return ok(e);
+}
