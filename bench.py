@@ -1,0 +1,293 @@
+#!/usr/bin/env python3
+"""Benchmark of the SandyRT hot path on one MI355X.
+
+One step = one pass of the hot path over one batch of synthetic input:
+
+  BASELINE config 2 (TinyLlama-1.1B shape, 4096 tokens x 2048 hidden, bf16,
+  inputs N(0,1), seed 1):
+    1. residual add + RMSNorm        x, h [4096, 2048] -> x + h, rmsnorm(x + h) * w
+    2. RoPE (theta 1e4, split-half)  q [1, 32, 4096, 64]
+    3. RoPE                          k [1, 4, 4096, 64]
+    4. SiLU-gate group               silu(gate) * up, [4096, 2048] (hipRTC-generated)
+  BASELINE config 3 (paged decode, bf16 KV, block 16, seed 2):
+    5. decode attention, 32 sequences, ctx U[512, 4096], 32 q / 4 kv heads,
+       D 64, block table = random permutation of a 32768-block pool.
+
+Inputs are resident in HBM before timing.  Each kernel rotates over several
+independent replicas of its inputs (> 256 MB MALL per rotation) so repeated
+launches cannot hit in the Infinity Cache.  `value` is the whole step's
+algorithmic bytes / measured step time.  Per-kernel durations come from HIP
+events on the launch stream around back-to-back launches; the dominant kernel
+gives the `roofline` object.  `cpu_baseline` times the reference's own CPU
+math (oracle/_ref, built from the reference sources) or, where that build is
+absent, the oracle restatement -- on one host core, on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+T, HID, HQ, HKV, HD = 4096, 2048, 32, 4, 64
+DEC_B, DEC_POOL, DEC_PAGE = 32, 32768, 16
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--replicas", type=int, default=4)
+    p.add_argument("--kernel-iters", type=int, default=64)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--cpu-tokens", type=int, default=4096, help="C2 rows timed on the CPU")
+    p.add_argument("--cpu-seqs", type=int, default=8, help="decode sequences timed on the CPU")
+    p.add_argument("--only", default="", help="comma list of kernels to run (profiling)")
+    return p.parse_args()
+
+
+class Prepared:
+    """A C-ABI call with its ctypes arguments built once (no per-call Python
+    tensor inspection), so back-to-back launches keep the GPU queue full."""
+
+    def __init__(self, name, *args):
+        from sandyrt_amd import _lib
+        self.fn = getattr(_lib.lib(), name)
+        self.args = args
+        self.buf = C.create_string_buffer(256)
+
+    def __call__(self, stream):
+        rc = self.fn(*self.args, C.c_void_p(stream), self.buf, C.c_size_t(256))
+        if rc:
+            raise RuntimeError(self.buf.value.decode())
+
+
+def build_workload(replicas):
+    import numpy as np
+    import torch
+    from sandyrt_amd import _lib, ops
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    desc = _lib.desc
+    kernels = {k: [] for k in ("add_rms_norm", "rope_q", "rope_k", "silu_gate", "paged_decode")}
+    keep = []
+    nodes, result = ops.silu_mul_nodes()
+    cnodes = ops._nodes(nodes)
+    r = np.random.default_rng(2)
+    ctx = r.integers(512, 4097, DEC_B).astype(np.int64)
+    nblk = (ctx + DEC_PAGE - 1) // DEC_PAGE
+    max_blocks = int(nblk.max())
+    host = {}
+    for rep in range(replicas):
+        g.manual_seed(1 + 1000 * rep)
+        bf = torch.bfloat16
+        x = torch.randn(T, HID, generator=g, device=dev).to(bf)
+        h = torch.randn(T, HID, generator=g, device=dev).to(bf)
+        w = torch.randn(HID, generator=g, device=dev).to(bf)
+        s_out = torch.empty_like(x)
+        y = torch.empty_like(x)
+        q = torch.randn(1, HQ, T, HD, generator=g, device=dev).to(bf)
+        k = torch.randn(1, HKV, T, HD, generator=g, device=dev).to(bf)
+        q_out, k_out = torch.empty_like(q), torch.empty_like(k)
+        gate = torch.randn(T, HID, generator=g, device=dev).to(bf)
+        up = torch.randn(T, HID, generator=g, device=dev).to(bf)
+        act = torch.empty_like(gate)
+        g.manual_seed(2 + 1000 * rep)
+        kpool = torch.randn(DEC_POOL, HKV, DEC_PAGE, HD, generator=g, device=dev).to(bf)
+        vpool = torch.randn(DEC_POOL, HKV, DEC_PAGE, HD, generator=g, device=dev).to(bf)
+        qd = torch.randn(DEC_B, HQ, 1, HD, generator=g, device=dev).to(bf)
+        od = torch.empty_like(qd)
+        perm = np.random.default_rng(2 + rep).permutation(DEC_POOL).astype(np.int32)
+        table = np.zeros((DEC_B, max_blocks), np.int32)
+        off = 0
+        for b in range(DEC_B):
+            table[b, :nblk[b]] = perm[off:off + nblk[b]]
+            off += nblk[b]
+        table_t = torch.from_numpy(table).to(dev)
+        pos_t = torch.from_numpy(ctx - 1).to(dev)
+        kc, vc = ops.PagedCache(kpool).struct(), ops.PagedCache(vpool).struct()
+        keep += [x, h, w, s_out, y, q, k, q_out, k_out, gate, up, act, kpool, vpool, qd, od, table_t, pos_t, kc, vc]
+        d = {n: desc(t) for n, t in dict(x=x, h=h, w=w, s=s_out, y=y, q=q, k=k, qo=q_out, ko=k_out,
+                                         gate=gate, up=up, act=act, qd=qd, od=od, table=table_t, pos=pos_t).items()}
+        keep.append(d)
+        kernels["add_rms_norm"].append(Prepared("sandy_hip_add_rms_norm", d["x"], d["h"], d["w"], C.c_double(1e-5),
+                                                d["s"], d["y"]))
+        kernels["rope_q"].append(Prepared("sandy_hip_rope", d["q"], None, C.c_double(1e4), C.c_int64(-1), C.c_int32(1),
+                                          d["qo"]))
+        kernels["rope_k"].append(Prepared("sandy_hip_rope", d["k"], None, C.c_double(1e4), C.c_int64(-1), C.c_int32(1),
+                                          d["ko"]))
+        arr = (_lib.SandyTensor * 2)(d["gate"].contents, d["up"].contents)
+        bc = (C.c_int32 * 2)(0, 0)
+        keep += [arr, bc]
+        kernels["silu_gate"].append(Prepared("sandy_hip_elementwise", cnodes, C.c_int32(len(nodes)),
+                                             C.c_uint32(result), arr, bc, C.c_int32(2), d["act"]))
+        kernels["paged_decode"].append(Prepared("sandy_hip_paged_attention", d["qd"], kc, vc, d["table"], d["pos"],
+                                                C.c_int64(0), C.c_double(0.125), d["od"]))
+        if rep == 0:
+            host = dict(x=x, h=h, w=w, q=q, k=k, gate=gate, up=up, kpool=kpool, vpool=vpool, qd=qd,
+                        table=table, ctx=ctx)
+    bytes_per = {
+        "add_rms_norm": 4 * T * HID * 2 + HID * 2,
+        "rope_q": 2 * HQ * T * HD * 2,
+        "rope_k": 2 * HKV * T * HD * 2,
+        "silu_gate": 3 * T * HID * 2,
+        "paged_decode": int(ctx.sum()) * HKV * HD * 2 * 2 + 2 * DEC_B * HQ * HD * 2 + int(nblk.sum()) * 4,
+    }
+    return kernels, bytes_per, keep, host
+
+
+def time_kernels(kernels, iters, stream, torch):
+    """Average launch duration of each kernel from HIP events on its stream
+    around `iters` back-to-back launches rotating over the replicas."""
+    out = {}
+    for name, calls in kernels.items():
+        for c in calls:  # warm (compiles hipRTC groups, sizes workspaces)
+            c(stream)
+        torch.cuda.synchronize()
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for i in range(iters):
+            calls[i % len(calls)](stream)
+        ev1.record()
+        ev1.synchronize()
+        out[name] = ev0.elapsed_time(ev1) / iters * 1e3  # us
+    return out
+
+
+def cpu_baseline(host, bytes_per, n_tokens, n_seqs):
+    """Time the reference CPU math (or the oracle restatement) on one core."""
+    import numpy as np
+    from oracle import oracle as O
+    from tests.helpers import to_oracle
+
+    kind = "reference" if os.path.exists(O.REF_PATH) else "port"
+    if not os.path.exists(O.LIB_PATH):
+        O.build()
+    cpu = O.Oracle(reference=(kind == "reference"))
+    x = to_oracle(host["x"])[:n_tokens]
+    h = to_oracle(host["h"])[:n_tokens]
+    w = to_oracle(host["w"])
+    q = to_oracle(host["q"])[:, :, :n_tokens]
+    k = to_oracle(host["k"])[:, :, :n_tokens]
+    gate = to_oracle(host["gate"])[:n_tokens]
+    up = to_oracle(host["up"])[:n_tokens]
+    half = O.f32_to_bf16(np.array(0.5, np.float32))
+    one = O.f32_to_bf16(np.array(1.0, np.float32))
+    t0 = time.perf_counter()
+    s = cpu.binary("add", x, h)                      # reference: __add then __rms_norm
+    cpu.rms_norm(s, w, 1e-5)
+    cpu.rope(q, 1e4, split_half=True)
+    cpu.rope(k, 1e4, split_half=True)
+    hx = cpu.binary("mul", half, gate)               # silu lowered to mul/tanh/add/mul, then * up
+    t = cpu.unary("tanh", hx)
+    a = cpu.binary("add", one, t)
+    sg = cpu.binary("mul", hx, a)
+    cpu.binary("mul", sg, up)
+    t_c2 = (time.perf_counter() - t0) * (T / n_tokens)
+    kpool, vpool, table, ctx = to_oracle(host["kpool"]), to_oracle(host["vpool"]), host["table"], host["ctx"]
+    qd = to_oracle(host["qd"])
+    t_dec = 0.0
+    sample_ctx = 0
+    for b in range(n_seqs):
+        c = int(ctx[b])
+        kd = O.Oracle().paged_to_dense(kpool, table[b], HKV, c, DEC_PAGE, HD)[None]
+        vd = O.Oracle().paged_to_dense(vpool, table[b], HKV, c, DEC_PAGE, HD)[None]
+        t0 = time.perf_counter()
+        cpu.attention(qd[b:b + 1], kd, vd, np.array([c - 1], np.int64), 0, 0.125)
+        t_dec += time.perf_counter() - t0
+        sample_ctx += c
+    t_dec *= float(ctx.sum()) / sample_ctx
+    total_bytes = sum(bytes_per.values())
+    return {
+        "value": round(total_bytes / (t_c2 + t_dec) / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": (f"config-2 groups on {n_tokens} of {T} tokens and decode attention for {n_seqs} of {DEC_B} "
+                   f"sequences, single thread, scaled linearly to one full step; paged->dense K/V copy not timed"),
+        "step_seconds": round(t_c2 + t_dec, 3),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the workload shards by rows and by "
+              "sequence with no exchange); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from sandyrt_amd import _lib
+
+    _lib.lib()  # fail loudly if the backend is not built
+    torch.cuda.set_device(0)
+    kernels, bytes_per, keep, host = build_workload(args.replicas)
+    if args.only:
+        kernels = {k: v for k, v in kernels.items() if k in args.only.split(",")}
+        bytes_per = {k: v for k, v in bytes_per.items() if k in kernels}
+    stream = torch.cuda.current_stream().cuda_stream
+    per_kernel_us = time_kernels(kernels, args.kernel_iters, stream, torch)
+
+    order = list(kernels)
+    reps = args.replicas
+    for i in range(args.warmup):
+        for n in order:
+            kernels[n][i % reps](stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        for n in order:
+            kernels[n][i % reps](stream)
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t0) / args.steps
+    _lib.take_device_errors()
+
+    step_bytes = sum(bytes_per.values())
+    value = step_bytes / step_s / 1e9
+    dominant = max(per_kernel_us, key=per_kernel_us.get)
+    achieved = bytes_per[dominant] / (per_kernel_us[dominant] * 1e-6) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    if os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get(dominant)
+    kern = {n: {"us": round(per_kernel_us[n], 2), "bytes": bytes_per[n],
+                "gbs": round(bytes_per[n] / (per_kernel_us[n] * 1e-6) / 1e9, 1),
+                "frac": round(bytes_per[n] / (per_kernel_us[n] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)} for n in per_kernel_us}
+    line = {
+        "metric": "fused-group + paged-decode HBM GB/s (% of 8 TB/s) and decode tok/s, 1 GPU",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) (seeds 1 and 2), inputs resident in HBM, rotated over replicas",
+        "config": {"workload": "config2 TinyLlama fused groups (4096x2048 bf16) + config3 paged decode "
+                               "(B32, ctx U[512,4096], 32q/4kv, D64, block 16, pool 32768)",
+                   "tokens": T, "hidden": HID, "decode_batch": DEC_B, "replicas": args.replicas},
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "decode_tok_s": round(DEC_B / (per_kernel_us["paged_decode"] * 1e-6), 1) if "paged_decode" in per_kernel_us else None,
+        "kernels": kern,
+        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu and not args.only:
+        line["cpu_baseline"] = cpu_baseline(host, bytes_per, args.cpu_tokens, args.cpu_seqs)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -64,7 +64,7 @@ struct PagedArgs {
     int32_t max_splits;
     float* ws_o;   // [B, Hq, max_splits, D]
     float* ws_ml;  // [B, Hq, max_splits, 2]
-    uint32_t* counters;  // [B, Hkv]
+    uint32_t* counters;  // unused
     uint32_t* errw;
 };
 
@@ -81,20 +81,14 @@ struct TileRegs {
     uint4 v[D / 32];
 };
 
+// Loads one 16-key tile of K and V (this lane: key lane%16, 8 dims per MFMA
+// k-step) from block `blk` (already validated; -1 = skip).
 template <int D>
-__device__ __forceinline__ void load_tile(const PagedArgs& a, int64_t t0, int b, int kh, int lane, TileRegs<D>& r,
-                                          bool& ok) {
-    const int64_t page = t0 >> a.log2_page;
-    const int32_t blk = a.table[b * a.table_stride + page];
-    ok = blk >= 0 && blk < a.num_pages;
-    if (!ok) {
-        if (lane == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
-#pragma unroll
-        for (int kk = 0; kk < D / 32; kk++) r.k[kk] = r.v[kk] = make_uint4(0, 0, 0, 0);
-        return;
-    }
+__device__ __forceinline__ void load_tile(const PagedArgs& a, int64_t t0, int32_t blk, int kh, int lane,
+                                          TileRegs<D>& r) {
+    const int64_t safe = blk < 0 ? 0 : blk;
     const int64_t in_page = t0 & (a.page_size - 1);
-    const int64_t row = static_cast<int64_t>(blk) * a.page_elems + static_cast<int64_t>(kh) * a.page_size * D +
+    const int64_t row = safe * a.page_elems + static_cast<int64_t>(kh) * a.page_size * D +
                         (in_page + (lane & 15)) * D + 8 * (lane >> 4);
     const uint4* kp = reinterpret_cast<const uint4*>(a.k_pool + row);
     const uint4* vp = reinterpret_cast<const uint4*>(a.v_pool + row);
@@ -105,7 +99,26 @@ __device__ __forceinline__ void load_tile(const PagedArgs& a, int64_t t0, int b,
     }
 }
 
-template <int D>
+// Key range of one split of sequence b; shared by the attention and merge kernels.
+struct SplitRange {
+    int64_t n_keys, min_key, key_begin;
+    int n_splits;
+};
+
+__device__ __forceinline__ SplitRange split_range(const PagedArgs& a, int64_t pos) {
+    SplitRange r;
+    r.n_keys = min(pos + 1, a.max_blocks * static_cast<int64_t>(a.page_size));
+    r.min_key = a.window > 0 ? max<int64_t>(0, pos + 1 - a.window) : 0;
+    r.key_begin = (r.min_key >> 4) << 4;
+    const int64_t span = max<int64_t>(0, r.n_keys - r.key_begin);
+    r.n_splits = max(1, static_cast<int>((span + a.split_keys - 1) / a.split_keys));
+    return r;
+}
+
+constexpr int kMaxSplitKeys = 2048;
+constexpr int kMaxSplitPages = kMaxSplitKeys / 16 + 2;
+
+template <int D, int NB>
 __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     constexpr int kRow = 2 * D + 8;  // bytes per V row in LDS (8-byte pad: conflict-free transposed reads)
@@ -119,14 +132,25 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
         if (threadIdx.x == 0 && split == 0 && kh == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
         return;
     }
-    const int64_t n_keys = min(pos + 1, a.max_blocks * static_cast<int64_t>(a.page_size));
-    const int64_t min_key = a.window > 0 ? max<int64_t>(0, pos + 1 - a.window) : 0;
-    const int64_t key_begin = (min_key >> 4) << 4;
-    const int64_t span = max<int64_t>(0, n_keys - key_begin);
-    const int n_splits = max(1, static_cast<int>((span + a.split_keys - 1) / a.split_keys));
+    const SplitRange sr = split_range(a, pos);
+    const int n_splits = sr.n_splits;
+    const int64_t min_key = sr.min_key;
     if (split >= n_splits) return;
-    const int64_t s_begin = key_begin + static_cast<int64_t>(split) * a.split_keys;
-    const int64_t s_end = min(n_keys, s_begin + a.split_keys);
+    const int64_t s_begin = sr.key_begin + static_cast<int64_t>(split) * a.split_keys;
+    const int64_t s_end = min(sr.n_keys, s_begin + a.split_keys);
+
+    // Stage this split's block ids in LDS: the K/V loads of a tile then
+    // depend on one LDS read, not on a global load per tile.
+    __shared__ int32_t blk_lds[kMaxSplitPages];
+    const int64_t page0 = s_begin >> a.log2_page;
+    const int n_pages = s_end > s_begin ? static_cast<int>(((s_end - 1) >> a.log2_page) - page0 + 1) : 0;
+    for (int i = threadIdx.x; i < n_pages; i += 256) {
+        const int32_t blk = a.table[b * a.table_stride + page0 + i];
+        const bool ok = blk >= 0 && blk < a.num_pages;
+        if (!ok) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
+        blk_lds[i] = ok ? blk : -1;
+    }
+    __syncthreads();
 
     const int g = lane & 15;
     const int j = lane >> 4;
@@ -213,18 +237,31 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
         __builtin_amdgcn_wave_barrier();
     };
 
-    // Ping-pong register buffers: the next tile's loads are in flight while
-    // the current one is computed.
-    TileRegs<D> buf0, buf1;
-    bool ok0 = false, ok1 = false;
-    int64_t t0 = s_begin + 16 * wave;
-    if (t0 < s_end) load_tile<D>(a, t0, b, kh, lane, buf0, ok0);
-    for (; t0 < s_end; t0 += 128) {
-        if (t0 + 64 < s_end) load_tile<D>(a, t0 + 64, b, kh, lane, buf1, ok1);
-        if (ok0) compute(buf0, t0);
-        if (t0 + 64 >= s_end) break;
-        if (t0 + 128 < s_end) load_tile<D>(a, t0 + 128, b, kh, lane, buf0, ok0);
-        if (ok1) compute(buf1, t0 + 64);
+    // Ping-pong batches of NB tiles: the next batch's loads are in flight
+    // while the current batch is computed.  Wave w owns tiles w, w+4, ...
+    TileRegs<D> bufA[NB], bufB[NB];
+    auto load_batch = [&](TileRegs<D> (&buf)[NB], int64_t tb) {
+#pragma unroll
+        for (int n = 0; n < NB; n++) {
+            const int64_t t = tb + 64 * n;
+            if (t < s_end) load_tile<D>(a, t, blk_lds[(t >> a.log2_page) - page0], kh, lane, buf[n]);
+        }
+    };
+    auto compute_batch = [&](const TileRegs<D> (&buf)[NB], int64_t tb) {
+#pragma unroll
+        for (int n = 0; n < NB; n++) {
+            const int64_t t = tb + 64 * n;
+            if (t < s_end && blk_lds[(t >> a.log2_page) - page0] >= 0) compute(buf[n], t);
+        }
+    };
+    int64_t tb = s_begin + 16 * wave;
+    load_batch(bufA, tb);
+    for (; tb < s_end; tb += 128 * NB) {
+        load_batch(bufB, tb + 64 * NB);
+        compute_batch(bufA, tb);
+        if (tb + 64 * NB >= s_end) break;
+        load_batch(bufA, tb + 128 * NB);
+        compute_batch(bufB, tb + 64 * NB);
     }
 
     // ---- merge the 4 waves through LDS (reuses the V staging area)
@@ -271,38 +308,35 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
             }
         }
     }
-    if (n_splits == 1) return;
+}
 
-    // ---- the last workgroup of this (sequence, kv head) merges the splits
-    __shared__ int is_last;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(&a.counters[b * a.hkv + kh], 1u);
-        is_last = prev == static_cast<uint32_t>(n_splits - 1);
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
-        const int gg = idx / D, d = idx % D;
-        const int h = kh * G + gg;
-        const int64_t base = (static_cast<int64_t>(b) * hq + h) * a.max_splits;
-        float M = -INFINITY;
-        for (int s = 0; s < n_splits; s++) M = fmaxf(M, __builtin_nontemporal_load(&a.ws_ml[(base + s) * 2]));
-        float O = 0.0f, L = 0.0f;
-        if (M != -INFINITY) {
-            for (int s = 0; s < n_splits; s++) {
-                const float ms = __builtin_nontemporal_load(&a.ws_ml[(base + s) * 2]);
-                if (ms == -INFINITY) continue;
-                const float f = exp2f(ms - M);
-                O += __builtin_nontemporal_load(&a.ws_o[(base + s) * D + d]) * f;
-                L += __builtin_nontemporal_load(&a.ws_ml[(base + s) * 2 + 1]) * f;
-            }
+// Combines the split partials of one (sequence, q head): log-sum-exp merge of
+// (max, sum, O[D]).  Sequences that fit one split were written directly.
+template <int D>
+__global__ __launch_bounds__(64) void paged_decode_merge_kernel(PagedArgs a) {
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int64_t pos = load_index(a.pos, a.pos_dt, b);
+    if (pos < 0) return;
+    const int n_splits = split_range(a, pos).n_splits;
+    if (n_splits == 1) return;
+    const int64_t base = (static_cast<int64_t>(b) * a.hq + h) * a.max_splits;
+    float M = -INFINITY;
+    for (int s = 0; s < n_splits; s++) M = fmaxf(M, a.ws_ml[(base + s) * 2]);
+    float L = 0.0f;
+    if (M != -INFINITY)
+        for (int s = 0; s < n_splits; s++) {
+            const float ms = a.ws_ml[(base + s) * 2];
+            if (ms != -INFINITY) L += a.ws_ml[(base + s) * 2 + 1] * exp2f(ms - M);
         }
+    for (int d = threadIdx.x; d < D; d += 64) {
+        float O = 0.0f;
+        if (M != -INFINITY)
+            for (int s = 0; s < n_splits; s++) {
+                const float ms = a.ws_ml[(base + s) * 2];
+                if (ms != -INFINITY) O += a.ws_o[(base + s) * D + d] * exp2f(ms - M);
+            }
         a.out[b * a.o_sb + h * a.o_sh + d] = f32_to_bf16(L > 0.0f ? O / L : 0.0f);
     }
-    if (threadIdx.x == 0) a.counters[b * a.hkv + kh] = 0u;  // ready for the next launch
 }
 
 // ---------------------------------------------------------------- general kernel
@@ -556,14 +590,14 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         a.group = static_cast<int32_t>(G);
         a.window = window;
         a.scale_log2 = sc * kLog2e;
-        // split size: enough workgroups to cover ~2 per CU at the average context
+        // split size: ~4 workgroups per CU at the average context
+        const int nb = D == 64 ? 2 : 1;
         const int64_t max_keys = max_blocks * P;
         int64_t split = env_int("SANDY_PAGED_SPLIT", 0);
-        if (split <= 0) {
-            split = (max_keys * B * hkv) / 1024;
-            split = std::min<int64_t>(2048, std::max<int64_t>(256, split));
-        }
-        split = (split + 63) / 64 * 64;
+        if (split <= 0) split = (max_keys * B * hkv) / 1024;
+        split = std::min<int64_t>(kMaxSplitKeys, std::max<int64_t>(128, split));
+        split = (split + 64 * nb - 1) / (64 * nb) * (64 * nb);
+        if (split > kMaxSplitKeys) split = kMaxSplitKeys;
         a.split_keys = static_cast<int32_t>(split);
         a.max_splits = static_cast<int32_t>((max_keys + split - 1) / split + 1);
         const size_t ws_o = static_cast<size_t>(B * hq * a.max_splits * D) * sizeof(float);
@@ -572,17 +606,26 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         if (status) return status;
         a.ws_o = reinterpret_cast<float*>(ws);
         a.ws_ml = reinterpret_cast<float*>(ws + ws_o);
-        a.counters = static_cast<uint32_t*>(device_counters(0, static_cast<size_t>(B * hkv) * sizeof(uint32_t), stream, e, &status));
-        if (status) return status;
+        a.counters = nullptr;
         a.errw = errw;
         dim3 grid(static_cast<unsigned>(a.max_splits), static_cast<unsigned>(hkv), static_cast<unsigned>(B));
         const size_t lds_v = 4 * 16 * (2 * D + 8);
         const size_t lds_r = (4 * G * D + 4 * G * 2) * sizeof(float);
         const size_t lds = std::max(lds_v, lds_r);
+        dim3 mgrid(static_cast<unsigned>(hq), static_cast<unsigned>(B));
         switch (D) {
-            case 64: hipLaunchKernelGGL(paged_decode_mfma_kernel<64>, grid, dim3(256), lds, stream, a); break;
-            case 128: hipLaunchKernelGGL(paged_decode_mfma_kernel<128>, grid, dim3(256), lds, stream, a); break;
-            default: hipLaunchKernelGGL(paged_decode_mfma_kernel<256>, grid, dim3(256), lds, stream, a); break;
+            case 64:
+                hipLaunchKernelGGL((paged_decode_mfma_kernel<64, 2>), grid, dim3(256), lds, stream, a);
+                if (a.max_splits > 1) hipLaunchKernelGGL(paged_decode_merge_kernel<64>, mgrid, dim3(64), 0, stream, a);
+                break;
+            case 128:
+                hipLaunchKernelGGL((paged_decode_mfma_kernel<128, 1>), grid, dim3(256), lds, stream, a);
+                if (a.max_splits > 1) hipLaunchKernelGGL(paged_decode_merge_kernel<128>, mgrid, dim3(64), 0, stream, a);
+                break;
+            default:
+                hipLaunchKernelGGL((paged_decode_mfma_kernel<256, 1>), grid, dim3(256), lds, stream, a);
+                if (a.max_splits > 1) hipLaunchKernelGGL(paged_decode_merge_kernel<256>, mgrid, dim3(64), 0, stream, a);
+                break;
         }
         SANDY_HIP_TRY(hipGetLastError(), e, "paged attention launch");
         return ok(e);
