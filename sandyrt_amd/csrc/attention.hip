@@ -20,11 +20,12 @@
 //   - P^T leaves the S^T MFMA already in the B-operand layout of
 //     v_mfma_f32_16x16x16_bf16, and V tiles are transposed through LDS into A
 //     operands, so O^T += V^T P^T runs on MFMA with no register shuffles;
-//   - each wave prefetches its next tile while computing the current one;
-//   - the 4 waves merge in LDS; splits merge in the same launch: the last
-//     workgroup to finish a (sequence, kv head) combines the split partials
-//     (log-sum-exp) -- one launch per step, no host round trip, partials and
-//     counters in a persistent workspace.
+//   - block ids, Q and the position are fetched together; each wave keeps
+//     two batches of tiles in flight (ping-pong) while computing;
+//   - the 4 waves merge in LDS and every split slot writes a (max, sum,
+//     O[D]) partial to a persistent workspace (empty slots write max = -inf);
+//     a small second kernel merges the slots (log-sum-exp) with one round of
+//     loads.  No host round trip and no allocation per call.
 // The probabilities fed to the PV product are rounded to bf16 and the
 // normaliser sums those rounded values, so O / L stays a convex combination.
 #include "common.h"
@@ -64,7 +65,6 @@ struct PagedArgs {
     int32_t max_splits;
     float* ws_o;   // [B, Hq, max_splits, D]
     float* ws_ml;  // [B, Hq, max_splits, 2]
-    uint32_t* counters;  // unused
     uint32_t* errw;
 };
 
@@ -127,33 +127,21 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
     const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
     const int G = a.group;
 
-    const int64_t pos = load_index(a.pos, a.pos_dt, b);
-    if (pos < 0) {
-        if (threadIdx.x == 0 && split == 0 && kh == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
-        return;
-    }
-    const SplitRange sr = split_range(a, pos);
-    const int n_splits = sr.n_splits;
-    const int64_t min_key = sr.min_key;
-    if (split >= n_splits) return;
-    const int64_t s_begin = sr.key_begin + static_cast<int64_t>(split) * a.split_keys;
-    const int64_t s_end = min(sr.n_keys, s_begin + a.split_keys);
-
-    // Stage this split's block ids in LDS: the K/V loads of a tile then
-    // depend on one LDS read, not on a global load per tile.
-    __shared__ int32_t blk_lds[kMaxSplitPages];
-    const int64_t page0 = s_begin >> a.log2_page;
-    const int n_pages = s_end > s_begin ? static_cast<int>(((s_end - 1) >> a.log2_page) - page0 + 1) : 0;
-    for (int i = threadIdx.x; i < n_pages; i += 256) {
-        const int32_t blk = a.table[b * a.table_stride + page0 + i];
-        const bool ok = blk >= 0 && blk < a.num_pages;
-        if (!ok) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
-        blk_lds[i] = ok ? blk : -1;
-    }
-    __syncthreads();
-
     const int g = lane & 15;
     const int j = lane >> 4;
+    const int tiles_pw = a.split_keys >> 6;  // tiles per wave (<= 32)
+
+    // Issue the position, this wave's block ids and Q together.  With no
+    // sliding window the split starts at split * split_keys whatever the
+    // position, so the block-id loads need not wait for it.
+    const int64_t pos = load_index(a.pos, a.pos_dt, b);
+    int32_t blkv = -1;  // lane i: block id of this wave's tile i
+    auto load_ids = [&](int64_t sb) {
+        const int64_t t = sb + 16 * wave + 64 * lane;
+        const int64_t page = t >> a.log2_page;
+        blkv = (lane < tiles_pw && page < a.max_blocks) ? a.table[b * a.table_stride + page] : -1;
+    };
+    if (a.window == 0) load_ids(static_cast<int64_t>(split) * a.split_keys);
     // Q^T as B operands: column g, d = 32 kk + 8 j .. + 7
     uint4 qv[D / 32];
     if (g < G) {
@@ -164,45 +152,78 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
 #pragma unroll
         for (int kk = 0; kk < D / 32; kk++) qv[kk] = make_uint4(0, 0, 0, 0);
     }
+    if (pos < 0 && threadIdx.x == 0 && split == 0 && kh == 0)
+        atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
+    const SplitRange sr = split_range(a, pos);
+    const int n_splits = sr.n_splits;
+    const int64_t min_key = sr.min_key;
+    if (pos < 0 || split >= n_splits) {
+        // empty split slot: mark it so the merge needs no position
+        for (int gg = threadIdx.x; gg < G; gg += 256) {
+            const int64_t slot = (static_cast<int64_t>(b) * a.hq + kh * G + gg) * a.max_splits + split;
+            a.ws_ml[slot * 2] = -INFINITY;
+            a.ws_ml[slot * 2 + 1] = 0.0f;
+        }
+        return;
+    }
+    const int64_t s_begin = sr.key_begin + static_cast<int64_t>(split) * a.split_keys;
+    const int64_t s_end = min(sr.n_keys, s_begin + a.split_keys);
+    if (a.window != 0) load_ids(s_begin);
+    {
+        const int64_t t = s_begin + 16 * wave + 64 * lane;
+        const bool used = lane < tiles_pw && t < s_end;
+        const bool ok = blkv >= 0 && blkv < a.num_pages;
+        if (used && !ok) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
+        if (!ok) blkv = -1;
+    }
+    auto blk_of = [&](int it) -> int32_t { return __builtin_amdgcn_readlane(blkv, it); };
 
     float m = -INFINITY, l = 0.0f;
     f32x4_t acc[D / 16];
 #pragma unroll
     for (int t = 0; t < D / 16; t++) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    unsigned char* vl = smem + wave * 16 * kRow;  // this wave's V tile
+    unsigned char* vl = smem + wave * NB * 16 * kRow;  // this wave's V tiles
 
-    // One 16-key tile: S^T on MFMA, online softmax, V^T through LDS, PV on MFMA.
-    auto compute = [&](const TileRegs<D>& cur, int64_t t0) {
-        f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+    // A batch of NB 16-key tiles: S^T on MFMA, one online-softmax update for
+    // the whole batch (one cross-lane max and sum), V^T through LDS, PV on MFMA.
+    auto compute_batch = [&](const TileRegs<D> (&buf)[NB], int it0) {
+        const int64_t tb = s_begin + 16 * wave + 64 * it0;
+        bool live_n[NB];
 #pragma unroll
-        for (int kk = 0; kk < D / 32; kk++)
-            sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, cur.k[kk]),
-                                                         __builtin_bit_cast(bf16x8_t, qv[kk]), sc, 0, 0, 0);
-        float sv[4];
+        for (int n = 0; n < NB; n++) live_n[n] = tb + 64 * n < s_end && blk_of(it0 + n) >= 0;
+        float sv[NB][4];
         float mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int64_t key = t0 + 4 * j + i;
-            const bool valid = key < s_end && key >= min_key;
-            sv[i] = valid ? sc[i] * a.scale_log2 : -INFINITY;
-            mx = fmaxf(mx, sv[i]);
+        for (int n = 0; n < NB; n++) {
+            const int64_t t0 = tb + 64 * n;
+            const bool live = live_n[n];
+            f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < D / 32; kk++)
+                sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, buf[n].k[kk]),
+                                                             __builtin_bit_cast(bf16x8_t, qv[kk]), sc, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int64_t key = t0 + 4 * j + i;
+                const bool valid = live && key < s_end && key >= min_key;
+                sv[n][i] = valid ? sc[i] * a.scale_log2 : -INFINITY;
+                mx = fmaxf(mx, sv[n][i]);
+            }
         }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float m_new = fmaxf(m, mx);
-        float p[4];
+        if (m_new == -INFINITY) return;  // nothing visible yet: state unchanged
+        float p[NB][4];
         float rs = 0.0f;
-        if (m_new == -INFINITY) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) p[i] = 0.0f;
-        } else {
+        for (int n = 0; n < NB; n++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                p[i] = sv[i] == -INFINITY ? 0.0f : bf16_to_f32(f32_to_bf16(exp2f(sv[i] - m_new)));
-                rs += p[i];
+                p[n][i] = sv[n][i] == -INFINITY ? 0.0f : bf16_to_f32(f32_to_bf16(exp2f(sv[n][i] - m_new)));
+                rs += p[n][i];
             }
-        }
         rs += __shfl_xor(rs, 16, 64);
         rs += __shfl_xor(rs, 32, 64);
         const float alpha = m == -INFINITY ? 0.0f : exp2f(m - m_new);
@@ -211,28 +232,34 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
 #pragma unroll
         for (int t = 0; t < D / 16; t++) acc[t] *= alpha;
 
-        // V tile -> LDS (row = key, masked keys zeroed so they cannot inject NaN)
-        {
+        // V tiles -> LDS (row = key; masked keys zeroed so they cannot inject NaN)
+#pragma unroll
+        for (int n = 0; n < NB; n++) {
+            const int64_t t0 = tb + 64 * n;
+            const bool live = live_n[n];
             const int64_t vkey = t0 + (lane & 15);
-            const bool vvalid = vkey < s_end && vkey >= min_key;
-            unsigned char* row = vl + (lane & 15) * kRow + 16 * j;
+            const bool vvalid = live && vkey < s_end && vkey >= min_key;
+            unsigned char* row = vl + (n * 16 + (lane & 15)) * kRow + 16 * j;
 #pragma unroll
             for (int kk = 0; kk < D / 32; kk++) {
-                uint4 v = vvalid ? cur.v[kk] : make_uint4(0, 0, 0, 0);
+                uint4 v = vvalid ? buf[n].v[kk] : make_uint4(0, 0, 0, 0);
                 uint2* dst = reinterpret_cast<uint2*>(row + 64 * kk);
                 dst[0] = make_uint2(v.x, v.y);
                 dst[1] = make_uint2(v.z, v.w);
             }
         }
         __builtin_amdgcn_wave_barrier();
-        const short4_t pb = pack_p(p);
 #pragma unroll
-        for (int t = 0; t < D / 16; t++) {
-            short4_t va;
-            const unsigned char* col = vl + 2 * (16 * t + (lane & 15));
+        for (int n = 0; n < NB; n++) {
+            const short4_t pb = pack_p(p[n]);
 #pragma unroll
-            for (int i = 0; i < 4; i++) va[i] = *reinterpret_cast<const short*>(col + (4 * j + i) * kRow);
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, acc[t], 0, 0, 0);
+            for (int t = 0; t < D / 16; t++) {
+                short4_t va;
+                const unsigned char* col = vl + n * 16 * kRow + 2 * (16 * t + (lane & 15));
+#pragma unroll
+                for (int i = 0; i < 4; i++) va[i] = *reinterpret_cast<const short*>(col + (4 * j + i) * kRow);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, acc[t], 0, 0, 0);
+            }
         }
         __builtin_amdgcn_wave_barrier();
     };
@@ -240,28 +267,21 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
     // Ping-pong batches of NB tiles: the next batch's loads are in flight
     // while the current batch is computed.  Wave w owns tiles w, w+4, ...
     TileRegs<D> bufA[NB], bufB[NB];
-    auto load_batch = [&](TileRegs<D> (&buf)[NB], int64_t tb) {
+    auto load_batch = [&](TileRegs<D> (&buf)[NB], int it0) {
 #pragma unroll
         for (int n = 0; n < NB; n++) {
-            const int64_t t = tb + 64 * n;
-            if (t < s_end) load_tile<D>(a, t, blk_lds[(t >> a.log2_page) - page0], kh, lane, buf[n]);
+            const int64_t t = s_begin + 16 * wave + 64 * (it0 + n);
+            if (t < s_end) load_tile<D>(a, t, blk_of(it0 + n), kh, lane, buf[n]);
         }
     };
-    auto compute_batch = [&](const TileRegs<D> (&buf)[NB], int64_t tb) {
-#pragma unroll
-        for (int n = 0; n < NB; n++) {
-            const int64_t t = tb + 64 * n;
-            if (t < s_end && blk_lds[(t >> a.log2_page) - page0] >= 0) compute(buf[n], t);
-        }
-    };
-    int64_t tb = s_begin + 16 * wave;
-    load_batch(bufA, tb);
-    for (; tb < s_end; tb += 128 * NB) {
-        load_batch(bufB, tb + 64 * NB);
-        compute_batch(bufA, tb);
-        if (tb + 64 * NB >= s_end) break;
-        load_batch(bufA, tb + 128 * NB);
-        compute_batch(bufB, tb + 64 * NB);
+    const int my_tiles = static_cast<int>(max<int64_t>(0, (s_end - s_begin - 16 * wave + 63) / 64));
+    load_batch(bufA, 0);
+    for (int it = 0; it < my_tiles; it += 2 * NB) {
+        load_batch(bufB, it + NB);
+        compute_batch(bufA, it);
+        if (it + NB >= my_tiles) break;
+        load_batch(bufA, it + 2 * NB);
+        compute_batch(bufB, it + NB);
     }
 
     // ---- merge the 4 waves through LDS (reuses the V staging area)
@@ -297,46 +317,53 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
             }
         }
         const int h = kh * G + gg;
-        if (n_splits == 1) {
-            a.out[b * a.o_sb + h * a.o_sh + d] = f32_to_bf16(L > 0.0f ? O / L : 0.0f);
-        } else {
-            const int64_t slot = (static_cast<int64_t>(b) * hq + h) * a.max_splits + split;
-            a.ws_o[slot * D + d] = O;
-            if (d == 0) {
-                a.ws_ml[slot * 2] = M;
-                a.ws_ml[slot * 2 + 1] = L;
-            }
+        const int64_t slot = (static_cast<int64_t>(b) * hq + h) * a.max_splits + split;
+        a.ws_o[slot * D + d] = O;
+        if (d == 0) {
+            a.ws_ml[slot * 2] = M;
+            a.ws_ml[slot * 2 + 1] = L;
         }
     }
 }
 
 // Combines the split partials of one (sequence, q head): log-sum-exp merge of
-// (max, sum, O[D]).  Sequences that fit one split were written directly.
+// (max, sum, O[D]) over all max_splits slots (empty slots carry max = -inf),
+// every load issued at once -- one memory round trip, no position read.
 template <int D>
 __global__ __launch_bounds__(64) void paged_decode_merge_kernel(PagedArgs a) {
     const int h = blockIdx.x, b = blockIdx.y;
-    const int64_t pos = load_index(a.pos, a.pos_dt, b);
-    if (pos < 0) return;
-    const int n_splits = split_range(a, pos).n_splits;
-    if (n_splits == 1) return;
+    constexpr int PER = D / 64;  // head dims per thread
     const int64_t base = (static_cast<int64_t>(b) * a.hq + h) * a.max_splits;
-    float M = -INFINITY;
-    for (int s = 0; s < n_splits; s++) M = fmaxf(M, a.ws_ml[(base + s) * 2]);
-    float L = 0.0f;
-    if (M != -INFINITY)
-        for (int s = 0; s < n_splits; s++) {
-            const float ms = a.ws_ml[(base + s) * 2];
-            if (ms != -INFINITY) L += a.ws_ml[(base + s) * 2 + 1] * exp2f(ms - M);
+    float M = -INFINITY, L = 0.0f, O[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) O[i] = 0.0f;
+    for (int s0 = 0; s0 < a.max_splits; s0 += 8) {
+        float ms[8], ls[8], os[8][PER];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const bool in = s0 + u < a.max_splits;
+            const int64_t slot = base + (in ? s0 + u : 0);
+            const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + slot * 2);
+            ms[u] = in ? ml.x : -INFINITY;
+            ls[u] = ml.y;
+#pragma unroll
+            for (int i = 0; i < PER; i++) os[u][i] = a.ws_o[slot * D + threadIdx.x + 64 * i];
         }
-    for (int d = threadIdx.x; d < D; d += 64) {
-        float O = 0.0f;
-        if (M != -INFINITY)
-            for (int s = 0; s < n_splits; s++) {
-                const float ms = a.ws_ml[(base + s) * 2];
-                if (ms != -INFINITY) O += a.ws_o[(base + s) * D + d] * exp2f(ms - M);
-            }
-        a.out[b * a.o_sb + h * a.o_sh + d] = f32_to_bf16(L > 0.0f ? O / L : 0.0f);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (ms[u] == -INFINITY) continue;  // empty slot: its O was never written
+            const float mn = fmaxf(M, ms[u]);
+            const float fo = M == -INFINITY ? 0.0f : exp2f(M - mn);
+            const float fs = exp2f(ms[u] - mn);
+            L = L * fo + ls[u] * fs;
+#pragma unroll
+            for (int i = 0; i < PER; i++) O[i] = O[i] * fo + os[u][i] * fs;
+            M = mn;
+        }
     }
+#pragma unroll
+    for (int i = 0; i < PER; i++)
+        a.out[b * a.o_sb + h * a.o_sh + threadIdx.x + 64 * i] = f32_to_bf16(L > 0.0f ? O[i] / L : 0.0f);
 }
 
 // ---------------------------------------------------------------- general kernel
@@ -591,40 +618,40 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         a.window = window;
         a.scale_log2 = sc * kLog2e;
         // split size: ~4 workgroups per CU at the average context
-        const int nb = D == 64 ? 2 : 1;
+        const int nb = D == 64 ? (env_int("SANDY_PAGED_NB", 2) == 4 ? 4 : 2) : 1;
         const int64_t max_keys = max_blocks * P;
         int64_t split = env_int("SANDY_PAGED_SPLIT", 0);
-        if (split <= 0) split = (max_keys * B * hkv) / 1024;
+        if (split <= 0) split = (max_keys * B * hkv) / 512;
         split = std::min<int64_t>(kMaxSplitKeys, std::max<int64_t>(128, split));
         split = (split + 64 * nb - 1) / (64 * nb) * (64 * nb);
         if (split > kMaxSplitKeys) split = kMaxSplitKeys;
         a.split_keys = static_cast<int32_t>(split);
-        a.max_splits = static_cast<int32_t>((max_keys + split - 1) / split + 1);
+        a.max_splits = static_cast<int32_t>((max_keys + split - 1) / split);
         const size_t ws_o = static_cast<size_t>(B * hq * a.max_splits * D) * sizeof(float);
         const size_t ws_ml = static_cast<size_t>(B * hq * a.max_splits * 2) * sizeof(float);
         char* ws = static_cast<char*>(device_workspace(0, ws_o + ws_ml, stream, e, &status));
         if (status) return status;
         a.ws_o = reinterpret_cast<float*>(ws);
         a.ws_ml = reinterpret_cast<float*>(ws + ws_o);
-        a.counters = nullptr;
         a.errw = errw;
         dim3 grid(static_cast<unsigned>(a.max_splits), static_cast<unsigned>(hkv), static_cast<unsigned>(B));
-        const size_t lds_v = 4 * 16 * (2 * D + 8);
+        const size_t lds_v = 4 * nb * 16 * (2 * D + 8);
         const size_t lds_r = (4 * G * D + 4 * G * 2) * sizeof(float);
         const size_t lds = std::max(lds_v, lds_r);
         dim3 mgrid(static_cast<unsigned>(hq), static_cast<unsigned>(B));
         switch (D) {
             case 64:
-                hipLaunchKernelGGL((paged_decode_mfma_kernel<64, 2>), grid, dim3(256), lds, stream, a);
-                if (a.max_splits > 1) hipLaunchKernelGGL(paged_decode_merge_kernel<64>, mgrid, dim3(64), 0, stream, a);
+                if (nb == 4) hipLaunchKernelGGL((paged_decode_mfma_kernel<64, 4>), grid, dim3(256), lds, stream, a);
+                else hipLaunchKernelGGL((paged_decode_mfma_kernel<64, 2>), grid, dim3(256), lds, stream, a);
+                hipLaunchKernelGGL(paged_decode_merge_kernel<64>, mgrid, dim3(64), 0, stream, a);
                 break;
             case 128:
                 hipLaunchKernelGGL((paged_decode_mfma_kernel<128, 1>), grid, dim3(256), lds, stream, a);
-                if (a.max_splits > 1) hipLaunchKernelGGL(paged_decode_merge_kernel<128>, mgrid, dim3(64), 0, stream, a);
+                hipLaunchKernelGGL(paged_decode_merge_kernel<128>, mgrid, dim3(64), 0, stream, a);
                 break;
             default:
                 hipLaunchKernelGGL((paged_decode_mfma_kernel<256, 1>), grid, dim3(256), lds, stream, a);
-                if (a.max_splits > 1) hipLaunchKernelGGL(paged_decode_merge_kernel<256>, mgrid, dim3(64), 0, stream, a);
+                hipLaunchKernelGGL(paged_decode_merge_kernel<256>, mgrid, dim3(64), 0, stream, a);
                 break;
         }
         SANDY_HIP_TRY(hipGetLastError(), e, "paged attention launch");

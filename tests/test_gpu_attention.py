@@ -182,3 +182,12 @@ def test_dense_attention_seeded_fuzz(ops, oracle):
                             torch.from_numpy(pos).cuda(), window, scale)
         want = oracle.attention(qf, kf, vf, pos, window, scale)
         np.testing.assert_allclose(got.cpu().numpy(), want, atol=5e-4, err_msg=f"iteration {it}")
+
+
+@pytest.mark.parametrize("split", ["128", "512", "2048"])
+def test_paged_decode_split_sizes(ops, oracle, monkeypatch, split):
+    """Split partials merged by the merge kernel; repeated launches agree."""
+    monkeypatch.setenv("SANDY_PAGED_SPLIT", split)
+    out1 = run_case(ops, oracle, 40, 5, 32, 4, 64, 16, [1, 300, 1500, 2049, 700], torch.bfloat16)
+    out2 = run_case(ops, oracle, 40, 5, 32, 4, 64, 16, [1, 300, 1500, 2049, 700], torch.bfloat16)
+    assert torch.equal(out1, out2)
