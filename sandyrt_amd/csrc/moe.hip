@@ -1,0 +1,618 @@
+// moe.hip -- MoE routing and expert execution: top-k, stable permute
+// (moe_gather), grouped expert GEMM on MFMA (moe_matmul) and the weighted
+// combine (moe_scatter_sum).
+//
+// Semantics (src/core/TensorCalc.cpp):
+//   topk 1447-1518          k largest by (value desc, index asc)
+//   moe_gather 1565-1667    packed rows ordered expert, then token, then slot;
+//                           expert_offsets[e] = first row of expert e
+//   moe_matmul 1669-1743    rows [off[e], off[e+1]) times W[e]^T (or W[e])
+//   moe_scatter_sum 1745-1811  out[token] accumulated in packed-row order, the
+//                           accumulator rounded to the output dtype after
+//                           every add
+//
+// The reference CUDA path (CudaGatherKernels.cu:283-649,
+// CudaMoeScatterSumKernels.cu:152-405, CudaMatMulKernels.cu:294-616) assigns
+// rows with atomics (nondeterministic order within an expert), round-trips
+// counts and offsets through the host with stream syncs, combines with fp32
+// atomics and hands the grouped GEMM to cuBLAS.  Here:
+//   - the permute is a device-side stable counting sort in one workgroup per
+//     batch (wave ballots rank equal experts inside each wave; per-wave
+//     counts are prefix-summed in LDS), so rows come out in exactly the CPU
+//     order and no host round trip is needed;
+//   - the combine is a gather-reduce: one wave per (token, 512 columns)
+//     finds its rows with ballots in row order and accumulates with the
+//     reference's per-add rounding -- bit-identical to the CPU, no atomics;
+//   - the grouped GEMM streams each expert's weights once through
+//     v_mfma_f32_16x16x32_bf16 tiles (rows of the expert as the M dimension),
+//     HBM-bound like the reference's cuBLAS grouped GEMM.
+#include "common.h"
+
+#include <algorithm>
+
+namespace sandy_hip {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- top-k
+__device__ __forceinline__ bool better(float v, int64_t i, float bv, int64_t bi) {
+    return v != bv ? v > bv : i < bi;
+}
+
+// One wave per row (last axis, <= 64 * NV elements); k rounds of a wave
+// argmax under (value desc, index asc).
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void topk_rows_kernel(const void* __restrict__ x, void* __restrict__ values,
+                                                        void* __restrict__ indices, int32_t idx_dt, int64_t rows,
+                                                        int axis, int k) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    float v[NV];
+    bool taken[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int c = lane + 64 * j;
+        v[j] = c < axis ? Vec8<T>::load1(x, row * axis + c) : 0.0f;
+        taken[j] = c >= axis;
+    }
+    for (int r = 0; r < k; r++) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        bool have = false;
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int c = lane + 64 * j;
+            if (!taken[j] && (!have || better(v[j], c, bv, bi))) {
+                bv = v[j];
+                bi = c;
+                have = true;
+            }
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+            const float ov = __shfl_xor(bv, m, 64);
+            const int oi = __shfl_xor(bi, m, 64);
+            const bool oh = __shfl_xor(static_cast<int>(have), m, 64) != 0;
+            if (oh && (!have || better(ov, oi, bv, bi))) {
+                bv = ov;
+                bi = oi;
+                have = true;
+            }
+        }
+        // bi is now the same in every lane: its owner marks it taken
+#pragma unroll
+        for (int j = 0; j < NV; j++)
+            if (lane + 64 * j == bi) taken[j] = true;
+        if (lane == 0) {
+            Vec8<T>::store1(values, row * k + r, bv);
+            store_index(indices, idx_dt, row * k + r, bi);
+        }
+    }
+}
+
+// Any axis: one thread per (outer, inner) column, selection over the axis.
+template <typename T>
+__global__ __launch_bounds__(256) void topk_columns_kernel(const void* __restrict__ x, void* __restrict__ values,
+                                                           void* __restrict__ indices, int32_t idx_dt, int64_t outer,
+                                                           int64_t axis, int64_t inner, int64_t k) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= outer * inner) return;
+    const int64_t o = t / inner, in = t % inner;
+    const int64_t base = o * axis * inner + in;
+    float pv = INFINITY;
+    int64_t pi = -1;  // previous pick: next pick must come strictly after it in the order
+    for (int64_t r = 0; r < k; r++) {
+        float bv = 0.0f;
+        int64_t bi = -1;
+        for (int64_t a = 0; a < axis; a++) {
+            const float v = Vec8<T>::load1(x, base + a * inner);
+            const bool after_prev = pi < 0 || better(pv, pi, v, a);
+            if (after_prev && (bi < 0 || better(v, a, bv, bi))) {
+                bv = v;
+                bi = a;
+            }
+        }
+        const int64_t oi = o * k * inner + r * inner + in;
+        Vec8<T>::store1(values, oi, bv);
+        store_index(indices, idx_dt, oi, bi);
+        pv = bv;
+        pi = bi;
+    }
+}
+
+// ---------------------------------------------------------------- moe_gather
+constexpr int kRouteThreads = 1024;
+constexpr int kRouteWaves = kRouteThreads / 64;
+
+// One workgroup per batch.  Pass 1 counts routes per expert; pass 2 walks the
+// routes in order, 1024 at a time: inside a wave, lanes routed to the same
+// expert are ranked by ballot; waves are ordered through LDS prefix sums; a
+// per-expert cursor carries across chunks.  dest[r] receives the packed row
+// of route r (token-major route order r = token * top_k + slot).
+__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
+        const void* __restrict__ ids, int32_t ids_dt, const void* __restrict__ w, int32_t w_dt, int64_t seq,
+        int64_t top_k, int64_t experts, void* __restrict__ packed_w, void* __restrict__ token_ids, int32_t tok_dt,
+        void* __restrict__ offsets, int32_t off_dt, int32_t* __restrict__ dest, uint32_t* errw) {
+    extern __shared__ int32_t lds[];
+    int32_t* cursor = lds;                      // [E]
+    int32_t* wcount = lds + experts;            // [kRouteWaves][E]
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t routes = seq * top_k;
+    const int64_t rb = static_cast<int64_t>(b) * routes;
+    for (int64_t e = tid; e < experts; e += kRouteThreads) cursor[e] = 0;
+    __syncthreads();
+    for (int64_t r = tid; r < routes; r += kRouteThreads) {
+        const int64_t e = load_index(ids, ids_dt, rb + r);
+        if (e < 0 || e >= experts) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_EXPERT_ID));
+        else atomicAdd(&cursor[e], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {  // exclusive scan -> offsets and starting cursors
+        int32_t run = 0;
+        for (int64_t e = 0; e < experts; e++) {
+            const int32_t c = cursor[e];
+            cursor[e] = run;
+            store_index(offsets, off_dt, static_cast<int64_t>(b) * (experts + 1) + e, run);
+            run += c;
+        }
+        store_index(offsets, off_dt, static_cast<int64_t>(b) * (experts + 1) + experts, run);
+    }
+    __syncthreads();
+    for (int64_t c0 = 0; c0 < routes; c0 += kRouteThreads) {
+        const int64_t r = c0 + tid;
+        int64_t e = r < routes ? load_index(ids, ids_dt, rb + r) : -1;
+        if (e >= experts) e = -1;
+        for (int64_t i = lane; i < experts; i += 64) wcount[wave * experts + i] = 0;
+        __syncthreads();
+        // rank among equal experts inside the wave
+        int rank = 0;
+        uint64_t pending = __ballot(e >= 0);
+        while (pending) {
+            const int leader = __ffsll(static_cast<long long>(pending)) - 1;
+            const int64_t le = __shfl(e, leader, 64);
+            const uint64_t same = __ballot(e == le);
+            if (e == le) rank = __popcll(same & ((1ull << lane) - 1ull));
+            if (lane == leader) wcount[wave * experts + le] = __popcll(same);
+            pending &= ~same;
+        }
+        __syncthreads();
+        // per expert: prefix over the waves, then advance the cursor
+        for (int64_t x = tid; x < experts; x += kRouteThreads) {
+            int32_t run = cursor[x];
+            for (int wv = 0; wv < kRouteWaves; wv++) {
+                const int32_t c = wcount[wv * experts + x];
+                wcount[wv * experts + x] = run;
+                run += c;
+            }
+            cursor[x] = run;
+        }
+        __syncthreads();
+        if (e >= 0) {
+            const int32_t row = wcount[wave * experts + e] + rank;
+            dest[rb + r] = row;
+            const int64_t mb = static_cast<int64_t>(b) * routes;
+            store_any(packed_w, w_dt, mb + row, load_any(w, w_dt, rb + r));
+            store_index(token_ids, tok_dt, mb + row, r / top_k);
+        } else if (r < routes) {
+            dest[rb + r] = -1;
+        }
+        __syncthreads();
+    }
+}
+
+// packed_x[dest[r]] = x[token(r)]: one wave per route, 16-byte copies.
+__global__ __launch_bounds__(256) void moe_copy_rows_kernel(const char* __restrict__ x, char* __restrict__ packed,
+                                                            const int32_t* __restrict__ dest, int64_t batch,
+                                                            int64_t seq, int64_t top_k, int64_t row_bytes,
+                                                            int aligned) {
+    const int lane = threadIdx.x & 63;
+    const int64_t gr = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // global route
+    const int64_t routes = seq * top_k;
+    if (gr >= batch * routes) return;
+    const int64_t b = gr / routes, r = gr % routes;
+    const int32_t row = dest[gr];
+    if (row < 0) return;
+    const char* src = x + (b * seq + r / top_k) * row_bytes;
+    char* dst = packed + (b * routes + row) * row_bytes;
+    if (aligned) {
+        for (int64_t o = lane * 16; o < row_bytes; o += 64 * 16)
+            *reinterpret_cast<uint4*>(dst + o) = *reinterpret_cast<const uint4*>(src + o);
+    } else {
+        for (int64_t o = lane; o < row_bytes; o += 64) dst[o] = src[o];
+    }
+}
+
+// ---------------------------------------------------------------- moe_scatter_sum
+// One wave per (batch, token, 512-column chunk): finds the rows of its token
+// in row order with ballots and accumulates w * packed[row] with the
+// reference's two roundings (product, then sum rounded to the output dtype).
+template <typename T>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict__ packed,
+                                                          const void* __restrict__ pw,
+                                                          const void* __restrict__ tok, int32_t tok_dt,
+                                                          void* __restrict__ out, int64_t batch, int64_t rows,
+                                                          int64_t hidden, int64_t seq, uint32_t* errw) {
+    const int lane = threadIdx.x & 63;
+    const int64_t chunks = (hidden + 511) / 512;
+    const int64_t wid = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (wid >= batch * seq * chunks) return;
+    const int64_t ch = wid % chunks;
+    const int64_t t = (wid / chunks) % seq;
+    const int64_t b = wid / (chunks * seq);
+    const int64_t c0 = ch * 512 + lane * 8;
+    const bool vec = (hidden & 7) == 0;
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[i] = 0.0f;
+    const int64_t mb = b * rows;
+    for (int64_t r0 = 0; r0 < rows; r0 += 64) {
+        const int64_t r = r0 + lane;
+        const int64_t tr = r < rows ? load_index(tok, tok_dt, mb + r) : -1;
+        if (r < rows && (tr < 0 || tr >= seq) && t == 0 && ch == 0)
+            atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_TOKEN_ID));
+        uint64_t hits = __ballot(tr == t);
+        while (hits) {
+            const int hl = __ffsll(static_cast<long long>(hits)) - 1;
+            hits &= hits - 1;
+            const int64_t row = r0 + hl;
+            const float wv = load_any(pw, sizeof(typename Vec8<T>::elem) == 2 ? SANDY_BF16 : SANDY_F32, mb + row);
+            const int64_t src = (mb + row) * hidden + c0;
+            if (c0 < hidden) {
+                float pv[8];
+                if (vec) {
+                    Vec8<T>::load(packed, src, pv);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) pv[i] = c0 + i < hidden ? Vec8<T>::load1(packed, src + i) : 0.0f;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc[i] = Vec8<T>::round(__fadd_rn(acc[i], __fmul_rn(wv, pv[i])));
+            }
+        }
+    }
+    if (c0 < hidden) {
+        const int64_t dst = (b * seq + t) * hidden + c0;
+        if (vec) {
+            Vec8<T>::store(out, dst, acc);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (c0 + i < hidden) Vec8<T>::store1(out, dst + i, acc[i]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- moe_matmul
+// Grouped GEMM, bf16, transpose_rhs: out[row, n] = sum_k x[row, k] W[e, n, k].
+// Workgroup = (expert, 64 output columns); wave w owns 16 columns and up to
+// 16 * RT rows of the expert per pass.  A = x rows (lane: row lane%16, k chunk
+// 8 (lane/16)), B = W rows (lane: column lane%16, same k chunk): both are
+// 16-byte loads along k.  The weight slice is streamed once per pass, KU
+// k-steps of loads in flight ahead of the MFMAs.
+template <int RT>
+__global__ __launch_bounds__(256) void moe_gemm_mfma_kernel(const uint16_t* __restrict__ x,
+                                                            const void* __restrict__ offs, int32_t off_dt,
+                                                            const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
+                                                            int64_t rows, int64_t K, int64_t M, int64_t experts,
+                                                            int64_t batch, uint32_t* errw) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t e = blockIdx.x % experts;
+    const int64_t b = blockIdx.x / experts;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.y) * 64 + wave * 16;
+    const int64_t ob = b * (experts + 1);
+    const int64_t begin = load_index(offs, off_dt, ob + e);
+    const int64_t end = load_index(offs, off_dt, ob + e + 1);
+    if (begin < 0 || end < begin || end > rows) {
+        if (threadIdx.x == 0 && blockIdx.y == 0) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_OFFSETS));
+        return;
+    }
+    if (end == begin) return;
+    const int64_t xb = b * rows * K, yb = b * rows * M;
+    const int64_t ncol = n0 + (lane & 15);
+    const bool col_ok = ncol < M;
+    const uint4* wrow = reinterpret_cast<const uint4*>(w + (e * M + (col_ok ? ncol : 0)) * K + 8 * (lane >> 4));
+    constexpr int KU = 4;
+    for (int64_t r0 = begin; r0 < end; r0 += 16 * RT) {
+        const uint4* xrow[RT];
+        bool row_ok[RT];
+#pragma unroll
+        for (int t = 0; t < RT; t++) {
+            const int64_t rr = r0 + 16 * t + (lane & 15);
+            row_ok[t] = rr < end;
+            xrow[t] = reinterpret_cast<const uint4*>(x + xb + (row_ok[t] ? rr : begin) * K + 8 * (lane >> 4));
+        }
+        f32x4_t acc[RT];
+#pragma unroll
+        for (int t = 0; t < RT; t++) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        const int64_t ksteps = K / 32;
+        for (int64_t ks = 0; ks < ksteps; ks += KU) {
+            uint4 bw[KU], ax[KU][RT];
+#pragma unroll
+            for (int u = 0; u < KU; u++) {
+                const bool in = ks + u < ksteps;
+                bw[u] = in && col_ok ? wrow[(ks + u) * 4] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+                for (int t = 0; t < RT; t++)
+                    ax[u][t] = in && row_ok[t] ? xrow[t][(ks + u) * 4] : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < KU; u++)
+#pragma unroll
+                for (int t = 0; t < RT; t++)
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ax[u][t]),
+                                                                     __builtin_bit_cast(bf16x8_t, bw[u]), acc[t], 0, 0, 0);
+        }
+        // acc[t][i]: row r0 + 16 t + 4 (lane/16) + i, column ncol
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int64_t rr = r0 + 16 * t + 4 * (lane >> 4) + i;
+                if (rr < end && col_ok) out[yb + rr * M + ncol] = f32_to_bf16(acc[t][i]);
+            }
+    }
+}
+
+// Any dtype / layout: one thread per (row, column), float accumulation in k
+// order like the reference.
+template <typename T>
+__global__ __launch_bounds__(256) void moe_gemm_generic_kernel(const void* __restrict__ x,
+                                                               const void* __restrict__ offs, int32_t off_dt,
+                                                               const void* __restrict__ w, void* __restrict__ out,
+                                                               int64_t rows, int64_t K, int64_t M, int64_t experts,
+                                                               int64_t batch, int32_t transpose_rhs, uint32_t* errw) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= batch * rows * M) return;
+    const int64_t o = t % M, r = (t / M) % rows, b = t / (M * rows);
+    const int64_t ob = b * (experts + 1);
+    // expert of row r: last e with off[e] <= r < off[e + 1]
+    int64_t e = -1;
+    int64_t lo = 0, hi = experts;  // binary search on the monotone offsets
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) / 2;
+        if (load_index(offs, off_dt, ob + mid + 1) <= r) lo = mid + 1;
+        else hi = mid;
+    }
+    if (lo < experts && load_index(offs, off_dt, ob + lo) <= r && r < load_index(offs, off_dt, ob + lo + 1)) e = lo;
+    if (e < 0) return;  // row outside every expert range: the reference leaves it untouched
+    float acc = 0.0f;
+    for (int64_t k = 0; k < K; k++) {
+        const float xv = Vec8<T>::load1(x, (b * rows + r) * K + k);
+        const int64_t wi = transpose_rhs ? (e * M + o) * K + k : (e * K + k) * M + o;
+        acc = __fadd_rn(acc, __fmul_rn(xv, Vec8<T>::load1(w, wi)));
+    }
+    Vec8<T>::store1(out, (b * rows + r) * M + o, acc);
+}
+
+__global__ void validate_offsets_kernel(const void* __restrict__ offs, int32_t off_dt, int64_t experts, int64_t rows,
+                                        int64_t batch, uint32_t* errw) {
+    const int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (b >= batch) return;
+    for (int64_t e = 0; e < experts; e++) {
+        const int64_t lo = load_index(offs, off_dt, b * (experts + 1) + e);
+        const int64_t hi = load_index(offs, off_dt, b * (experts + 1) + e + 1);
+        if (lo < 0 || hi < lo || hi > rows) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_OFFSETS));
+    }
+}
+
+} // namespace
+} // namespace sandy_hip
+
+using namespace sandy_hip;
+
+extern "C" int sandy_hip_topk(const SandyTensor* x, int64_t k, int64_t axis, const SandyTensor* values,
+                              const SandyTensor* indices, void* stream_, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    if (!valid_rank(x) || !valid_rank(values) || !valid_rank(indices)) return fail(e, SANDY_ERR_INVALID, "topk tensor rank out of range");
+    if (!is_float(x->dtype)) return fail(e, SANDY_ERR_INVALID, "topk input unsupported dtype");
+    const int rank = x->rank;
+    if (rank < 1) return fail(e, SANDY_ERR_INVALID, "topk input must have rank >= 1");
+    if (axis < -rank || axis >= rank) return fail(e, SANDY_ERR_INVALID, "topk dim out of range");
+    if (axis < 0) axis += rank;
+    if (k <= 0) return fail(e, SANDY_ERR_INVALID, "topk k must be > 0");
+    const int64_t n = x->dims[axis];
+    if (n <= 0 || k > n) return fail(e, SANDY_ERR_INVALID, "topk invalid k or axis dimension");
+    bool shape_ok = values->rank == rank && indices->rank == rank && values->dtype == x->dtype;
+    for (int i = 0; shape_ok && i < rank; i++) {
+        const int64_t want = i == axis ? k : x->dims[i];
+        shape_ok = values->dims[i] == want && indices->dims[i] == want;
+    }
+    if (!shape_ok || values->dtype != x->dtype) return fail(e, SANDY_ERR_INVALID, "topk values output shape mismatch");
+    if (!is_index(indices->dtype)) return fail(e, SANDY_ERR_INVALID, "topk indices output shape or dtype mismatch");
+    if (!contiguous(*x) || !contiguous(*values) || !contiguous(*indices))
+        return fail(e, SANDY_ERR_UNSUPPORTED, "topk requires contiguous tensors");
+    int64_t outer = 1, inner = 1;
+    for (int i = 0; i < axis; i++) outer *= x->dims[i];
+    for (int i = static_cast<int>(axis) + 1; i < rank; i++) inner *= x->dims[i];
+    if (outer * inner == 0) return ok(e);
+    const bool bf = x->dtype == SANDY_BF16;
+    const void* px = base_ptr(*x);
+    void* pv = base_ptr(*values);
+    void* pi = base_ptr(*indices);
+    if (inner == 1 && n <= 1024) {
+        dim3 grid(static_cast<unsigned>((outer + 3) / 4));
+        const int ax = static_cast<int>(n), kk = static_cast<int>(k);
+#define TOPK_LAUNCH(NV)                                                                                                 \
+    if (bf) hipLaunchKernelGGL((topk_rows_kernel<BF16, NV>), grid, dim3(256), 0, stream, px, pv, pi, indices->dtype, outer, ax, kk); \
+    else hipLaunchKernelGGL((topk_rows_kernel<F32, NV>), grid, dim3(256), 0, stream, px, pv, pi, indices->dtype, outer, ax, kk)
+        if (n <= 64) { TOPK_LAUNCH(1); }
+        else if (n <= 128) { TOPK_LAUNCH(2); }
+        else if (n <= 256) { TOPK_LAUNCH(4); }
+        else if (n <= 512) { TOPK_LAUNCH(8); }
+        else { TOPK_LAUNCH(16); }
+#undef TOPK_LAUNCH
+    } else {
+        const int64_t threads = outer * inner;
+        dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+        if (bf) hipLaunchKernelGGL(topk_columns_kernel<BF16>, grid, dim3(256), 0, stream, px, pv, pi, indices->dtype, outer, n, inner, k);
+        else hipLaunchKernelGGL(topk_columns_kernel<F32>, grid, dim3(256), 0, stream, px, pv, pi, indices->dtype, outer, n, inner, k);
+    }
+    SANDY_HIP_TRY(hipGetLastError(), e, "topk launch");
+    return ok(e);
+}
+
+extern "C" int sandy_hip_moe_gather(const SandyTensor* x, const SandyTensor* topk_ids, const SandyTensor* topk_weights,
+                                    int64_t num_experts, int64_t top_k, const SandyTensor* packed_x,
+                                    const SandyTensor* packed_weights, const SandyTensor* token_ids,
+                                    const SandyTensor* expert_offsets, void* stream_, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    const SandyTensor* all[] = {x, topk_ids, topk_weights, packed_x, packed_weights, token_ids, expert_offsets};
+    for (const SandyTensor* t : all)
+        if (!valid_rank(t)) return fail(e, SANDY_ERR_INVALID, "moe_gather requires every tensor");
+    if (!is_float(x->dtype)) return fail(e, SANDY_ERR_INVALID, "moe_gather x unsupported dtype");
+    if (!is_float(topk_weights->dtype)) return fail(e, SANDY_ERR_INVALID, "moe_gather topk_weights unsupported dtype");
+    if (!is_index(topk_ids->dtype)) return fail(e, SANDY_ERR_INVALID, "moe_gather topk_ids must be i32 or i64");
+    if (!is_index(token_ids->dtype)) return fail(e, SANDY_ERR_INVALID, "moe_gather token_ids must be i32 or i64");
+    if (!is_index(expert_offsets->dtype)) return fail(e, SANDY_ERR_INVALID, "moe_gather expert_offsets must be i32 or i64");
+    const int xr = x->rank;
+    if ((xr != 2 && xr != 3) || topk_ids->rank != xr || topk_weights->rank != xr)
+        return fail(e, SANDY_ERR_INVALID, "moe_gather inputs must have rank 2 or rank 3");
+    if (num_experts <= 0 || top_k <= 0) return fail(e, SANDY_ERR_INVALID, "moe_gather num_experts and top_k must be positive");
+    const int64_t batch = xr == 3 ? x->dims[0] : 1;
+    const int64_t seq = x->dims[xr - 2], hidden = x->dims[xr - 1];
+    for (int i = 0; i < xr - 1; i++)
+        if (x->dims[i] != topk_ids->dims[i] || x->dims[i] != topk_weights->dims[i])
+            return fail(e, SANDY_ERR_INVALID, "moe_gather leading dimension mismatch");
+    if (topk_ids->dims[xr - 1] != top_k || topk_weights->dims[xr - 1] != top_k)
+        return fail(e, SANDY_ERR_INVALID, "moe_gather top_k dimension mismatch");
+    const int64_t routes = seq * top_k;
+    if (numel(*packed_x) != batch * routes * hidden || packed_x->dtype != x->dtype ||
+        packed_x->dims[packed_x->rank - 1] != hidden)
+        return fail(e, SANDY_ERR_INVALID, "moe_gather packed_x output shape mismatch");
+    if (numel(*packed_weights) != batch * routes || packed_weights->dtype != topk_weights->dtype)
+        return fail(e, SANDY_ERR_INVALID, "moe_gather packed_weights output shape mismatch");
+    if (numel(*token_ids) != batch * routes || numel(*expert_offsets) != batch * (num_experts + 1))
+        return fail(e, SANDY_ERR_INVALID, "moe_gather metadata output shape mismatch");
+    for (const SandyTensor* t : all)
+        if (!contiguous(*t)) return fail(e, SANDY_ERR_UNSUPPORTED, "moe_gather requires contiguous tensors");
+    const size_t lds = static_cast<size_t>(num_experts) * (1 + kRouteWaves) * sizeof(int32_t);
+    if (lds > 64 * 1024) return fail(e, SANDY_ERR_UNSUPPORTED, "moe_gather supports up to %d experts", (64 * 1024 / 4) / (1 + kRouteWaves));
+    if (batch == 0) return ok(e);
+    int status = 0;
+    uint32_t* errw = device_error_word(e, &status);
+    if (status) return status;
+    int32_t* dest = static_cast<int32_t*>(device_workspace(2, static_cast<size_t>(batch * routes) * sizeof(int32_t), stream, e, &status));
+    if (status) return status;
+    hipLaunchKernelGGL(moe_route_kernel, dim3(static_cast<unsigned>(batch)), dim3(kRouteThreads), lds, stream,
+                       base_ptr(*topk_ids), topk_ids->dtype, base_ptr(*topk_weights), topk_weights->dtype, seq, top_k,
+                       num_experts, base_ptr(*packed_weights), base_ptr(*token_ids), token_ids->dtype,
+                       base_ptr(*expert_offsets), expert_offsets->dtype, dest, errw);
+    if (routes > 0 && hidden > 0) {
+        const int64_t waves = batch * routes;
+        const int64_t row_bytes = hidden * static_cast<int64_t>(dtype_size(x->dtype));
+        const int aligned = (row_bytes % 16 == 0) &&
+                            ((reinterpret_cast<uintptr_t>(base_ptr(*x)) | reinterpret_cast<uintptr_t>(base_ptr(*packed_x))) & 15) == 0;
+        hipLaunchKernelGGL(moe_copy_rows_kernel, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, stream,
+                           static_cast<const char*>(base_ptr(*x)), static_cast<char*>(base_ptr(*packed_x)), dest, batch,
+                           seq, top_k, row_bytes, aligned);
+    }
+    SANDY_HIP_TRY(hipGetLastError(), e, "moe_gather launch");
+    return ok(e);
+}
+
+extern "C" int sandy_hip_moe_matmul(const SandyTensor* x, const SandyTensor* expert_offsets, const SandyTensor* weight,
+                                    int32_t transpose_rhs, const SandyTensor* out, void* stream_, char* err,
+                                    size_t err_cap) {
+    Err e{err, err_cap};
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    if (!valid_rank(x) || !valid_rank(expert_offsets) || !valid_rank(weight) || !valid_rank(out))
+        return fail(e, SANDY_ERR_INVALID, "moe_matmul requires every tensor");
+    if (!is_float(x->dtype) || !is_float(weight->dtype)) return fail(e, SANDY_ERR_INVALID, "moe_matmul x unsupported dtype");
+    if (x->dtype != weight->dtype) return fail(e, SANDY_ERR_INVALID, "moe_matmul x and weight must have same dtype");
+    if (!is_index(expert_offsets->dtype)) return fail(e, SANDY_ERR_INVALID, "moe_matmul expert_offsets must be i32 or i64");
+    const int xr = x->rank;
+    if ((xr != 2 && xr != 3) || expert_offsets->rank != xr - 1 || weight->rank != 3)
+        return fail(e, SANDY_ERR_INVALID, "moe_matmul expects ranks [N,K], [E+1], [E,M,K] or [B,N,K], [B,E+1], [E,M,K]");
+    const int64_t batch = xr == 3 ? x->dims[0] : 1;
+    const int64_t rows = x->dims[xr - 2], K = x->dims[xr - 1], experts = weight->dims[0];
+    const int64_t M = transpose_rhs ? weight->dims[1] : weight->dims[2];
+    const int64_t rk = transpose_rhs ? weight->dims[2] : weight->dims[1];
+    if (batch <= 0 || rows < 0 || K <= 0 || experts <= 0 || M <= 0)
+        return fail(e, SANDY_ERR_INVALID, "moe_matmul expects static positive dimensions");
+    if (rk != K) return fail(e, SANDY_ERR_INVALID, "moe_matmul contracting dimension mismatch");
+    if (expert_offsets->dims[xr - 2] != experts + 1) return fail(e, SANDY_ERR_INVALID, "moe_matmul expert_offsets shape mismatch");
+    if (xr == 3 && expert_offsets->dims[0] != batch) return fail(e, SANDY_ERR_INVALID, "moe_matmul batch dimension mismatch");
+    if (out->rank != xr || out->dtype != x->dtype || out->dims[xr - 1] != M || out->dims[xr - 2] != rows)
+        return fail(e, SANDY_ERR_INVALID, "moe_matmul output shape mismatch");
+    if (!contiguous(*x) || !contiguous(*expert_offsets) || !contiguous(*weight) || !contiguous(*out))
+        return fail(e, SANDY_ERR_UNSUPPORTED, "moe_matmul requires contiguous tensors");
+    if (rows == 0) return ok(e);
+    int status = 0;
+    uint32_t* errw = device_error_word(e, &status);
+    if (status) return status;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(base_ptr(*x)) | reinterpret_cast<uintptr_t>(base_ptr(*weight))) & 15) == 0;
+    if (x->dtype == SANDY_BF16 && transpose_rhs && K % 32 == 0 && aligned) {
+        hipLaunchKernelGGL(validate_offsets_kernel, dim3(static_cast<unsigned>((batch + 63) / 64)), dim3(64), 0, stream,
+                           base_ptr(*expert_offsets), expert_offsets->dtype, experts, rows, batch, errw);
+        dim3 grid(static_cast<unsigned>(batch * experts), static_cast<unsigned>((M + 63) / 64));
+        // rows per expert: 16 rows per pass for decode-sized batches, 64 otherwise
+        const int64_t avg = rows / experts;
+        const auto* px = static_cast<const uint16_t*>(base_ptr(*x));
+        const auto* pw = static_cast<const uint16_t*>(base_ptr(*weight));
+        auto* po = static_cast<uint16_t*>(base_ptr(*out));
+        const void* po_ = base_ptr(*expert_offsets);
+        if (avg <= 16)
+            hipLaunchKernelGGL(moe_gemm_mfma_kernel<1>, grid, dim3(256), 0, stream, px, po_, expert_offsets->dtype, pw, po, rows, K, M, experts, batch, errw);
+        else
+            hipLaunchKernelGGL(moe_gemm_mfma_kernel<4>, grid, dim3(256), 0, stream, px, po_, expert_offsets->dtype, pw, po, rows, K, M, experts, batch, errw);
+    } else {
+        hipLaunchKernelGGL(validate_offsets_kernel, dim3(static_cast<unsigned>((batch + 63) / 64)), dim3(64), 0, stream,
+                           base_ptr(*expert_offsets), expert_offsets->dtype, experts, rows, batch, errw);
+        const int64_t threads = batch * rows * M;
+        dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+        if (x->dtype == SANDY_BF16)
+            hipLaunchKernelGGL(moe_gemm_generic_kernel<BF16>, grid, dim3(256), 0, stream, base_ptr(*x), base_ptr(*expert_offsets),
+                               expert_offsets->dtype, base_ptr(*weight), base_ptr(*out), rows, K, M, experts, batch, transpose_rhs, errw);
+        else
+            hipLaunchKernelGGL(moe_gemm_generic_kernel<F32>, grid, dim3(256), 0, stream, base_ptr(*x), base_ptr(*expert_offsets),
+                               expert_offsets->dtype, base_ptr(*weight), base_ptr(*out), rows, K, M, experts, batch, transpose_rhs, errw);
+    }
+    SANDY_HIP_TRY(hipGetLastError(), e, "moe_matmul launch");
+    return ok(e);
+}
+
+extern "C" int sandy_hip_moe_scatter_sum(const SandyTensor* packed_out, const SandyTensor* packed_weights,
+                                         const SandyTensor* token_ids, const SandyTensor* out, void* stream_, char* err,
+                                         size_t err_cap) {
+    Err e{err, err_cap};
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    if (!valid_rank(packed_out) || !valid_rank(packed_weights) || !valid_rank(token_ids) || !valid_rank(out))
+        return fail(e, SANDY_ERR_INVALID, "moe_scatter_sum requires every tensor");
+    if (!is_float(packed_out->dtype)) return fail(e, SANDY_ERR_INVALID, "moe_scatter_sum packed_out unsupported dtype");
+    if (!is_index(token_ids->dtype)) return fail(e, SANDY_ERR_INVALID, "moe_scatter_sum token_ids must be i32 or i64");
+    const int pr = packed_out->rank, orr = out->rank;
+    if ((pr != 2 && pr != 3) || packed_weights->rank != pr - 1 || token_ids->rank != pr - 1 || (orr != 2 && orr != 3) || pr != orr)
+        return fail(e, SANDY_ERR_INVALID, "moe_scatter_sum expects ranks [N,H], [N], [N], [T,H] or [B,N,H], [B,N], [B,N], [B,T,H]");
+    if (packed_out->dtype != packed_weights->dtype || packed_out->dtype != out->dtype)
+        return fail(e, SANDY_ERR_INVALID, "moe_scatter_sum dtype mismatch");
+    const int64_t rows = packed_out->dims[pr - 2], hidden = packed_out->dims[pr - 1];
+    const int64_t batch = orr == 3 ? out->dims[0] : 1;
+    const int64_t seq = out->dims[orr - 2];
+    if ((pr == 3 && (packed_out->dims[0] != batch || packed_weights->dims[0] != batch || token_ids->dims[0] != batch)) ||
+        packed_weights->dims[pr - 2] != rows || token_ids->dims[pr - 2] != rows || out->dims[orr - 1] != hidden)
+        return fail(e, SANDY_ERR_INVALID, "moe_scatter_sum shape mismatch");
+    if (!contiguous(*packed_out) || !contiguous(*packed_weights) || !contiguous(*token_ids) || !contiguous(*out))
+        return fail(e, SANDY_ERR_UNSUPPORTED, "moe_scatter_sum requires contiguous tensors");
+    if (batch * seq * hidden == 0) return ok(e);
+    int status = 0;
+    uint32_t* errw = device_error_word(e, &status);
+    if (status) return status;
+    const int64_t waves = batch * seq * ((hidden + 511) / 512);
+    dim3 grid(static_cast<unsigned>((waves + 3) / 4));
+    const bool aligned = ((reinterpret_cast<uintptr_t>(base_ptr(*packed_out)) | reinterpret_cast<uintptr_t>(base_ptr(*out))) & 15) == 0;
+    if (!aligned && hidden % 8 == 0) return fail(e, SANDY_ERR_UNSUPPORTED, "moe_scatter_sum needs 16-byte aligned rows");
+    if (packed_out->dtype == SANDY_BF16)
+        hipLaunchKernelGGL(moe_combine_kernel<BF16>, grid, dim3(256), 0, stream, base_ptr(*packed_out), base_ptr(*packed_weights),
+                           base_ptr(*token_ids), token_ids->dtype, base_ptr(*out), batch, rows, hidden, seq, errw);
+    else
+        hipLaunchKernelGGL(moe_combine_kernel<F32>, grid, dim3(256), 0, stream, base_ptr(*packed_out), base_ptr(*packed_weights),
+                           base_ptr(*token_ids), token_ids->dtype, base_ptr(*out), batch, rows, hidden, seq, errw);
+    SANDY_HIP_TRY(hipGetLastError(), e, "moe_scatter_sum launch");
+    return ok(e);
+}

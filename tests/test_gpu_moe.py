@@ -1,0 +1,216 @@
+"""GPU parity of the MoE path against the oracle (src/core/TensorCalc.cpp
+topk 1447-1518, moe_gather 1565-1667, moe_matmul 1669-1743, moe_scatter_sum
+1745-1811) and of the router chain of src/models/gemma4a4b26b/common.sandy.go:
+11-28.  Index outputs are compared exactly; the combine is bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import assert_close, assert_equal, from_f32, from_oracle, normal, rng, to_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from sandyrt_amd import ops
+    return ops
+
+
+# ------------------------------------------------------------------ top-k
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape,k", [((512, 128), 8), ((7, 64), 64), ((3, 1000), 17), ((4, 3000), 5), ((1, 1), 1)])
+def test_topk_bit_exact(ops, oracle, dtype, shape, k):
+    r = rng(shape[-1] + k)
+    xf = np.round(normal(r, shape) * 3) / 3  # frequent ties: index order decides
+    x = from_f32(xf, dtype)
+    v, i = ops.topk(x, k)
+    wv, wi = oracle.topk(to_oracle(x), k)
+    assert_equal(i, wi, "topk indices")
+    assert_equal(v, wv, "topk values")
+
+
+def test_topk_middle_axis_and_i32(ops, oracle):
+    r = rng(3)
+    x = from_f32(np.round(normal(r, (3, 40, 5)) * 2) / 2, torch.float32)
+    v, i = ops.topk(x, 6, axis=1, index_dtype=torch.int32)
+    wv, wi = oracle.topk(to_oracle(x), 6, axis=1, index_dtype=np.int32)
+    assert_equal(i, wi, "topk axis 1 indices")
+    assert_equal(v, wv, "topk axis 1 values")
+
+
+# ------------------------------------------------------------------ router chain (config 5)
+def test_router_chain_config5(ops, oracle):
+    """softmax -> top-8 -> sum -> div -> per-expert scale, logits [512, 128]
+    N(0,1) seed 4 (fp32, as the router matmul produces)."""
+    r = rng(4)
+    logits = from_f32(normal(r, (512, 128)), torch.float32)
+    scale_t = from_f32(np.abs(normal(r, (128,))) + 0.5, torch.float32)
+    probs = ops.softmax(logits, -1)
+    tw, tid = ops.topk(probs, 8)
+    denom = ops.sum(tw, -1, True)
+    div_nodes = [ops.ScalarNode(0, ops.LOAD, 0), ops.ScalarNode(1, ops.LOAD, 1), ops.ScalarNode(2, ops.DIV, operands=(0, 1))]
+    tw = ops.elementwise(div_nodes, 2, [tw, denom.expand(512, 8).contiguous()])
+    es = ops.embedding(tid, scale_t)
+    mul_nodes = [ops.ScalarNode(0, ops.LOAD, 0), ops.ScalarNode(1, ops.LOAD, 1), ops.ScalarNode(2, ops.MUL, operands=(0, 1))]
+    tw = ops.elementwise(mul_nodes, 2, [tw, es])
+
+    p_ = oracle.softmax(to_oracle(logits), -1)
+    wv, wi = oracle.topk(p_, 8)
+    d_ = oracle.sum(wv, -1, True)
+    wv = oracle.binary("div", wv, d_)
+    es_ = oracle.embedding(wi, to_oracle(scale_t))
+    wv = oracle.binary("mul", wv, es_)
+    assert_equal(tid, wi, "router expert ids")
+    assert_close(tw, wv, torch.float32, "router weights")
+
+
+# ------------------------------------------------------------------ moe_gather
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,H,E,K", [(512, 2816, 128, 8), (37, 64, 16, 4), (5, 24, 300, 2), (1, 8, 4, 1)])
+@pytest.mark.parametrize("idx", [np.int64, np.int32])
+def test_moe_gather_bit_exact(ops, oracle, dtype, T, H, E, K, idx):
+    r = rng(T * 7 + E)
+    ids = np.stack([r.permutation(E)[:K] for _ in range(T)]).astype(idx)
+    w = np.abs(normal(r, (T, K)))
+    x = from_f32(normal(r, (T, H)), dtype)
+    wt = from_f32(w, dtype)
+    tid = torch.from_numpy(ids).cuda()
+    tdt = torch.int64 if idx == np.int64 else torch.int32
+    px, pw, tok, off = ops.moe_gather(x, tid, wt, E, index_dtype=tdt)
+    ops.check_device_errors()
+    wpx, wpw, wtok, woff = oracle.moe_gather(to_oracle(x), ids, to_oracle(wt), E, index_dtype=idx)
+    assert_equal(off, woff, "expert_offsets")
+    assert_equal(tok, wtok, "token_ids")
+    assert_equal(pw, wpw, "packed_weights")
+    assert_equal(px, wpx, "packed_x")
+
+
+def test_moe_gather_batched_and_skewed(ops, oracle):
+    """Rank-3 inputs, and routes concentrated on few experts (long same-expert
+    runs inside a wave exercise the ballot ranking)."""
+    r = rng(12)
+    B, T, H, E, K = 3, 300, 40, 8, 2
+    ids = r.integers(0, 3, (B, T, K)).astype(np.int64)  # experts 0..2 only, repeats allowed
+    x = from_f32(normal(r, (B, T, H)), torch.bfloat16)
+    w = from_f32(np.abs(normal(r, (B, T, K))), torch.bfloat16)
+    got = ops.moe_gather(x, torch.from_numpy(ids).cuda(), w, E)
+    want = oracle.moe_gather(to_oracle(x), ids, to_oracle(w), E)
+    for g, wnt, name in zip(got, want, ["packed_x", "packed_weights", "token_ids", "offsets"]):
+        assert_equal(g, wnt, name)
+
+
+def test_moe_gather_bad_expert_sets_device_error(ops):
+    from sandyrt_amd._lib import SandyError
+    x = torch.zeros(2, 8, device="cuda")
+    ops.moe_gather(x, torch.tensor([[0], [9]], device="cuda"), torch.ones(2, 1, device="cuda"), 4)
+    with pytest.raises(SandyError, match="moe_gather topk expert id out of range"):
+        ops.check_device_errors()
+
+
+# ------------------------------------------------------------------ moe_matmul
+def oracle_matmul_experts(oracle, x, off, w, experts, transpose_rhs=True):
+    """Oracle on selected experts only (each expert's rows are independent)."""
+    out = {}
+    for e in experts:
+        lo, hi = int(off[e]), int(off[e + 1])
+        if hi == lo:
+            continue
+        sub_off = np.array([0, hi - lo], np.int64)
+        out[e] = oracle.moe_matmul(np.ascontiguousarray(x[lo:hi]), sub_off, np.ascontiguousarray(w[e:e + 1]), transpose_rhs)
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("transpose_rhs", [True, False])
+def test_moe_matmul_small(ops, oracle, dtype, transpose_rhs):
+    r = rng(21)
+    E, K, M = 6, 96, 40
+    counts = np.array([0, 5, 17, 1, 40, 70])
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    x = from_f32(normal(r, (int(off[-1]), K)), dtype)
+    w = from_f32(normal(r, (E, M, K) if transpose_rhs else (E, K, M), 0.2), dtype)
+    got = ops.moe_matmul(x, torch.from_numpy(off).cuda(), w, transpose_rhs)
+    want = oracle.moe_matmul(to_oracle(x), off, to_oracle(w), transpose_rhs)
+    assert_close(got, want, dtype, "moe_matmul")
+
+
+@pytest.mark.parametrize("shape", ["gate", "down"])
+def test_moe_matmul_config5(ops, oracle, shape):
+    """Config 5 grouped GEMM at full size (4096 routed rows, 128 experts);
+    the oracle checks 4 experts, torch fp32 per-expert GEMMs check them all."""
+    r = rng(4)
+    E = 128
+    K, M = (2816, 704) if shape == "gate" else (704, 2816)
+    ids = np.stack([r.permutation(E)[:8] for _ in range(512)])
+    counts = np.bincount(ids.reshape(-1), minlength=E)
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    g = torch.Generator(device="cuda").manual_seed(4)
+    x = torch.randn(4096, K, generator=g, device="cuda").to(torch.bfloat16)
+    w = (torch.randn(E, M, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    got = ops.moe_matmul(x, torch.from_numpy(off).cuda(), w, True)
+    xo, wo = to_oracle(x), None
+    for e in [0, 1, int(np.argmax(counts)), E - 1]:
+        lo, hi = int(off[e]), int(off[e + 1])
+        want = oracle.moe_matmul(np.ascontiguousarray(xo[lo:hi]), np.array([0, hi - lo], np.int64),
+                                 to_oracle(w[e:e + 1]), True)
+        assert_close(got[lo:hi], want, torch.bfloat16, f"expert {e}")
+    xf, wf = x.float(), w.float()
+    for e in range(E):
+        lo, hi = int(off[e]), int(off[e + 1])
+        ref = (xf[lo:hi] @ wf[e].t()).to(torch.bfloat16)
+        assert_close(got[lo:hi], to_oracle(ref), torch.bfloat16, f"expert {e} vs torch fp32")
+
+
+def test_moe_matmul_bad_offsets_sets_device_error(ops):
+    from sandyrt_amd._lib import SandyError
+    x = torch.zeros(4, 32, dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(2, 16, 32, dtype=torch.bfloat16, device="cuda")
+    ops.moe_matmul(x, torch.tensor([0, 3, 9], device="cuda"), w, True)
+    with pytest.raises(SandyError, match="moe_matmul invalid expert offsets"):
+        ops.check_device_errors()
+
+
+# ------------------------------------------------------------------ moe_scatter_sum
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,H,K", [(512, 2816, 8), (9, 24, 3), (4, 100, 2)])
+def test_moe_scatter_sum_bit_exact(ops, oracle, dtype, T, H, K):
+    r = rng(T + H)
+    tok = np.sort(r.integers(0, T, T * K)).astype(np.int64)
+    r.shuffle(tok)
+    p = from_f32(normal(r, (T * K, H)), dtype)
+    w = from_f32(np.abs(normal(r, (T * K,))), dtype)
+    got = ops.moe_scatter_sum(p, w, torch.from_numpy(tok).cuda(), T)
+    ops.check_device_errors()
+    assert_equal(got, oracle.moe_scatter_sum(to_oracle(p), to_oracle(w), tok, T), "moe_scatter_sum")
+
+
+def test_moe_scatter_sum_batched(ops, oracle):
+    r = rng(5)
+    B, N, T, H = 2, 30, 7, 64
+    tok = r.integers(0, T, (B, N)).astype(np.int32)
+    p = from_f32(normal(r, (B, N, H)), torch.bfloat16)
+    w = from_f32(normal(r, (B, N)), torch.bfloat16)
+    got = ops.moe_scatter_sum(p, w, torch.from_numpy(tok).cuda(), T)
+    assert_equal(got, oracle.moe_scatter_sum(to_oracle(p), to_oracle(w), tok, T), "batched combine")
+
+
+def test_moe_scatter_sum_bad_token_sets_device_error(ops):
+    from sandyrt_amd._lib import SandyError
+    p = torch.zeros(3, 8, device="cuda")
+    ops.moe_scatter_sum(p, torch.ones(3, device="cuda"), torch.tensor([0, 1, 5], device="cuda"), 2)
+    with pytest.raises(SandyError, match="moe_scatter_sum token id out of range"):
+        ops.check_device_errors()
+
+
+# ------------------------------------------------------------------ the whole block
+def test_moe_block_permute_unpermute_identity(ops, oracle):
+    """gather -> scatter_sum with unit weights returns K * x (fp32: exact)."""
+    r = rng(77)
+    T, H, E, K = 64, 128, 16, 4
+    ids = np.stack([r.permutation(E)[:K] for _ in range(T)])
+    x = from_f32(np.round(normal(r, (T, H)) * 8) / 8, torch.float32)
+    px, pw, tok, off = ops.moe_gather(x, torch.from_numpy(ids).cuda(), torch.ones(T, K, device="cuda"), E)
+    y = ops.moe_scatter_sum(px, pw, tok, T)
+    assert torch.equal(y, x * K)
