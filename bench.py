@@ -50,6 +50,9 @@ def parse():
     p.add_argument("--cpu-tokens", type=int, default=4096, help="C2 rows timed on the CPU")
     p.add_argument("--cpu-seqs", type=int, default=8, help="decode sequences timed on the CPU")
     p.add_argument("--only", default="", help="comma list of kernels to run (profiling)")
+    p.add_argument("--no-extras", action="store_true", help="skip the config-4/5 kernel table")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="also run a plain 256 MiB device copy (counter calibration for rocprofv3 --pmc)")
     return p.parse_args()
 
 
@@ -144,6 +147,130 @@ def build_workload(replicas):
     return kernels, bytes_per, keep, host
 
 
+GEM_B, GEM_HQ, GEM_HKV, GEM_D, GEM_HID, GEM_FF, GEM_VOCAB = 64, 8, 2, 256, 2560, 10240, 262144
+MOE_T, MOE_E, MOE_K, MOE_D, MOE_F = 512, 128, 8, 2816, 704
+
+
+def build_extras(replicas):
+    """Config 4 (Gemma decoder layer: paged decode D 256 + norm/GeGLU/softcap
+    groups at batch 64) and config 5 (MoE block) as prepared kernel calls.
+    Reported per kernel; not part of `value`."""
+    import numpy as np
+    import torch
+    from sandyrt_amd import _lib, ops
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    desc = _lib.desc
+    bf = torch.bfloat16
+    kernels, keep = {}, []
+    # ---- config 4
+    r = np.random.default_rng(3)
+    ctx = r.integers(1024, 8193, GEM_B).astype(np.int64)
+    nblk = (ctx + DEC_PAGE - 1) // DEC_PAGE
+    maxb = int(nblk.max())
+    pool = int(nblk.sum()) + 64
+    names = ["c4_paged_decode", "c4_rms_norm", "c4_geglu", "c4_softcap"]
+    for n in names:
+        kernels[n] = []
+    for rep in range(replicas):
+        g.manual_seed(3 + 1000 * rep)
+        kpool = torch.randn(pool, GEM_HKV, DEC_PAGE, GEM_D, generator=g, device=dev).to(bf)
+        vpool = torch.randn(pool, GEM_HKV, DEC_PAGE, GEM_D, generator=g, device=dev).to(bf)
+        qd = torch.randn(GEM_B, GEM_HQ, 1, GEM_D, generator=g, device=dev).to(bf)
+        od = torch.empty_like(qd)
+        perm = np.random.default_rng(3 + rep).permutation(pool).astype(np.int32)
+        table = np.zeros((GEM_B, maxb), np.int32)
+        off = 0
+        for b in range(GEM_B):
+            table[b, :nblk[b]] = perm[off:off + nblk[b]]
+            off += nblk[b]
+        tt = torch.from_numpy(table).to(dev)
+        pt = torch.from_numpy(ctx - 1).to(dev)
+        kc, vc = ops.PagedCache(kpool).struct(), ops.PagedCache(vpool).struct()
+        xg = torch.randn(GEM_B, GEM_HID, generator=g, device=dev).to(bf)
+        wg = torch.randn(GEM_HID, generator=g, device=dev).to(bf)
+        yg = torch.empty_like(xg)
+        gate = torch.randn(GEM_B, GEM_FF, generator=g, device=dev).to(bf)
+        up = torch.randn(GEM_B, GEM_FF, generator=g, device=dev).to(bf)
+        act = torch.empty_like(gate)
+        logits = (torch.randn(GEM_B, GEM_VOCAB, generator=g, device=dev) * 20).to(bf)
+        capped = torch.empty_like(logits)
+        d = {k: desc(v) for k, v in dict(qd=qd, od=od, tt=tt, pt=pt, xg=xg, wg=wg, yg=yg, gate=gate, up=up, act=act,
+                                         logits=logits, capped=capped).items()}
+        gnodes, gres = ops.gelu_mul_nodes()
+        snodes, sres = ops.softcap_nodes(30.0)
+        cg, cs = ops._nodes(gnodes), ops._nodes(snodes)
+        arr2 = (_lib.SandyTensor * 2)(d["gate"].contents, d["up"].contents)
+        arr1 = (_lib.SandyTensor * 1)(d["logits"].contents)
+        bc = (C.c_int32 * 2)(0, 0)
+        keep += [kpool, vpool, qd, od, tt, pt, kc, vc, xg, wg, yg, gate, up, act, logits, capped, d, cg, cs, arr2, arr1, bc]
+        kernels["c4_paged_decode"].append(Prepared("sandy_hip_paged_attention", d["qd"], kc, vc, d["tt"], d["pt"],
+                                                   C.c_int64(0), C.c_double(1.0), d["od"]))
+        kernels["c4_rms_norm"].append(Prepared("sandy_hip_norm", C.c_int32(0), d["xg"], d["wg"], None,
+                                               C.c_double(1e-6), d["yg"]))
+        kernels["c4_geglu"].append(Prepared("sandy_hip_elementwise", cg, C.c_int32(len(gnodes)), C.c_uint32(gres),
+                                            arr2, bc, C.c_int32(2), d["act"]))
+        kernels["c4_softcap"].append(Prepared("sandy_hip_elementwise", cs, C.c_int32(len(snodes)), C.c_uint32(sres),
+                                              arr1, bc, C.c_int32(1), d["capped"]))
+    bytes_per = {
+        "c4_paged_decode": int(ctx.sum()) * GEM_HKV * GEM_D * 2 * 2 + 2 * GEM_B * GEM_HQ * GEM_D * 2 + int(nblk.sum()) * 4,
+        "c4_rms_norm": 2 * GEM_B * GEM_HID * 2 + GEM_HID * 2,
+        "c4_geglu": 3 * GEM_B * GEM_FF * 2,
+        "c4_softcap": 2 * GEM_B * GEM_VOCAB * 2,
+    }
+    # ---- config 5 (one copy: the 1.5 GB of expert weights exceed the cache)
+    g.manual_seed(4)
+    logits = torch.randn(MOE_T, MOE_E, generator=g, device=dev)
+    probs = ops.softmax(logits)
+    tw, tid = ops.topk(probs, MOE_K)
+    x = torch.randn(MOE_T, MOE_D, generator=g, device=dev).to(bf)
+    wgate = (torch.randn(MOE_E, MOE_F, MOE_D, generator=g, device=dev) * 0.02).to(bf)
+    wup = (torch.randn(MOE_E, MOE_F, MOE_D, generator=g, device=dev) * 0.02).to(bf)
+    wdown = (torch.randn(MOE_E, MOE_D, MOE_F, generator=g, device=dev) * 0.02).to(bf)
+    twb = tw.to(bf)
+    px, pw, tok, offs = ops.moe_gather(x, tid, twb, MOE_E)
+    gate_o = torch.empty(MOE_T * MOE_K, MOE_F, dtype=bf, device=dev)
+    up_o, act_o = torch.empty_like(gate_o), torch.empty_like(gate_o)
+    down_o = torch.empty(MOE_T * MOE_K, MOE_D, dtype=bf, device=dev)
+    comb = torch.empty(MOE_T, MOE_D, dtype=bf, device=dev)
+    vals = torch.empty(MOE_T, MOE_K, device=dev)
+    idx = torch.empty(MOE_T, MOE_K, dtype=torch.int64, device=dev)
+    d = {k: desc(v) for k, v in dict(probs=probs, vals=vals, idx=idx, x=x, tid=tid, twb=twb, px=px, pw=pw, tok=tok,
+                                     offs=offs, wgate=wgate, wup=wup, wdown=wdown, gate_o=gate_o, up_o=up_o,
+                                     act_o=act_o, down_o=down_o, comb=comb).items()}
+    snodes, sres = ops.silu_mul_nodes()
+    cs = ops._nodes(snodes)
+    arr = (_lib.SandyTensor * 2)(d["gate_o"].contents, d["up_o"].contents)
+    bc = (C.c_int32 * 2)(0, 0)
+    keep += [logits, probs, tw, tid, x, wgate, wup, wdown, twb, px, pw, tok, offs, gate_o, up_o, act_o, down_o, comb,
+             vals, idx, d, cs, arr, bc]
+    kernels["c5_topk"] = [Prepared("sandy_hip_topk", d["probs"], C.c_int64(MOE_K), C.c_int64(-1), d["vals"], d["idx"])]
+    kernels["c5_moe_gather"] = [Prepared("sandy_hip_moe_gather", d["x"], d["tid"], d["twb"], C.c_int64(MOE_E),
+                                         C.c_int64(MOE_K), d["px"], d["pw"], d["tok"], d["offs"])]
+    kernels["c5_moe_matmul_gate"] = [Prepared("sandy_hip_moe_matmul", d["px"], d["offs"], d["wgate"], C.c_int32(1),
+                                              d["gate_o"])]
+    kernels["c5_moe_matmul_up"] = [Prepared("sandy_hip_moe_matmul", d["px"], d["offs"], d["wup"], C.c_int32(1),
+                                            d["up_o"])]
+    kernels["c5_swiglu"] = [Prepared("sandy_hip_elementwise", cs, C.c_int32(len(snodes)), C.c_uint32(sres), arr, bc,
+                                     C.c_int32(2), d["act_o"])]
+    kernels["c5_moe_matmul_down"] = [Prepared("sandy_hip_moe_matmul", d["act_o"], d["offs"], d["wdown"],
+                                              C.c_int32(1), d["down_o"])]
+    kernels["c5_moe_scatter_sum"] = [Prepared("sandy_hip_moe_scatter_sum", d["down_o"], d["pw"], d["tok"], d["comb"])]
+    rows = MOE_T * MOE_K
+    wbytes = MOE_E * MOE_F * MOE_D * 2
+    bytes_per.update({
+        "c5_topk": MOE_T * MOE_E * 4 + MOE_T * MOE_K * 12,
+        "c5_moe_gather": MOE_T * MOE_D * 2 + rows * MOE_D * 2,
+        "c5_moe_matmul_gate": wbytes + rows * MOE_D * 2 + rows * MOE_F * 2,
+        "c5_moe_matmul_up": wbytes + rows * MOE_D * 2 + rows * MOE_F * 2,
+        "c5_swiglu": 3 * rows * MOE_F * 2,
+        "c5_moe_matmul_down": wbytes + rows * MOE_F * 2 + rows * MOE_D * 2,
+        "c5_moe_scatter_sum": rows * MOE_D * 2 + MOE_T * MOE_D * 2,
+    })
+    return kernels, bytes_per, keep
+
+
 def time_kernels(kernels, iters, stream, torch):
     """Average launch duration of each kernel from HIP events on its stream
     around `iters` back-to-back launches rotating over the replicas."""
@@ -234,6 +361,17 @@ def main():
         kernels = {k: v for k, v in kernels.items() if k in args.only.split(",")}
         bytes_per = {k: v for k, v in bytes_per.items() if k in kernels}
     stream = torch.cuda.current_stream().cuda_stream
+    if args.calibrate_copy:
+        # 256 MiB identity copy through the generated element-wise kernel
+        # (16-byte loads/stores per lane, like every hot kernel here): the
+        # rocprofv3 FETCH_SIZE / WRITE_SIZE it reads give the counter scale.
+        from sandyrt_amd import ops as _ops
+        src = torch.ones(128 << 20, dtype=torch.bfloat16, device="cuda")
+        ident = [_ops.ScalarNode(0, _ops.LOAD, 0)]
+        for _ in range(4):
+            _ops.elementwise(ident, 0, [src])
+        torch.cuda.synchronize()
+        del src
     per_kernel_us = time_kernels(kernels, args.kernel_iters, stream, torch)
 
     order = list(kernels)
@@ -284,6 +422,20 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "cpu_baseline": None,
     }
+    if not args.no_extras and not args.only:
+        ek, eb, ekeep = build_extras(args.replicas)
+        eus = time_kernels(ek, args.kernel_iters, stream, torch)
+        _lib.take_device_errors()
+        line["extras"] = {n: {"us": round(eus[n], 2), "bytes": eb[n],
+                              "gbs": round(eb[n] / (eus[n] * 1e-6) / 1e9, 1),
+                              "frac": round(eb[n] / (eus[n] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)} for n in eus}
+        moe_us = sum(v for n, v in eus.items() if n.startswith("c5_"))
+        line["extras_summary"] = {
+            "c4_decode_tok_s": round(GEM_B / (eus["c4_paged_decode"] * 1e-6), 1),
+            "c5_moe_block_us": round(moe_us, 2),
+            "c5_moe_block_tok_s": round(MOE_T / (moe_us * 1e-6), 1),
+        }
+        del ekeep
     if not args.no_cpu and not args.only:
         line["cpu_baseline"] = cpu_baseline(host, bytes_per, args.cpu_tokens, args.cpu_seqs)
     print(json.dumps(line), flush=True)

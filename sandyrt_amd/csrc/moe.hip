@@ -388,15 +388,16 @@ __global__ __launch_bounds__(256) void moe_gemm_generic_kernel(const void* __res
     Vec8<T>::store1(out, (b * rows + r) * M + o, acc);
 }
 
+// One thread per (batch, expert): offsets must be non-negative, monotone and
+// within the row count.
 __global__ void validate_offsets_kernel(const void* __restrict__ offs, int32_t off_dt, int64_t experts, int64_t rows,
                                         int64_t batch, uint32_t* errw) {
-    const int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (b >= batch) return;
-    for (int64_t e = 0; e < experts; e++) {
-        const int64_t lo = load_index(offs, off_dt, b * (experts + 1) + e);
-        const int64_t hi = load_index(offs, off_dt, b * (experts + 1) + e + 1);
-        if (lo < 0 || hi < lo || hi > rows) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_OFFSETS));
-    }
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= batch * experts) return;
+    const int64_t b = t / experts, e = t % experts;
+    const int64_t lo = load_index(offs, off_dt, b * (experts + 1) + e);
+    const int64_t hi = load_index(offs, off_dt, b * (experts + 1) + e + 1);
+    if (lo < 0 || hi < lo || hi > rows) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_OFFSETS));
 }
 
 } // namespace
@@ -548,8 +549,7 @@ extern "C" int sandy_hip_moe_matmul(const SandyTensor* x, const SandyTensor* exp
     if (status) return status;
     const bool aligned = ((reinterpret_cast<uintptr_t>(base_ptr(*x)) | reinterpret_cast<uintptr_t>(base_ptr(*weight))) & 15) == 0;
     if (x->dtype == SANDY_BF16 && transpose_rhs && K % 32 == 0 && aligned) {
-        hipLaunchKernelGGL(validate_offsets_kernel, dim3(static_cast<unsigned>((batch + 63) / 64)), dim3(64), 0, stream,
-                           base_ptr(*expert_offsets), expert_offsets->dtype, experts, rows, batch, errw);
+        // every workgroup checks the offsets of its own expert
         dim3 grid(static_cast<unsigned>(batch * experts), static_cast<unsigned>((M + 63) / 64));
         // rows per expert: 16 rows per pass for decode-sized batches, 64 otherwise
         const int64_t avg = rows / experts;
@@ -562,7 +562,7 @@ extern "C" int sandy_hip_moe_matmul(const SandyTensor* x, const SandyTensor* exp
         else
             hipLaunchKernelGGL(moe_gemm_mfma_kernel<4>, grid, dim3(256), 0, stream, px, po_, expert_offsets->dtype, pw, po, rows, K, M, experts, batch, errw);
     } else {
-        hipLaunchKernelGGL(validate_offsets_kernel, dim3(static_cast<unsigned>((batch + 63) / 64)), dim3(64), 0, stream,
+        hipLaunchKernelGGL(validate_offsets_kernel, dim3(static_cast<unsigned>((batch * experts + 255) / 256)), dim3(256), 0, stream,
                            base_ptr(*expert_offsets), expert_offsets->dtype, experts, rows, batch, errw);
         const int64_t threads = batch * rows * M;
         dim3 grid(static_cast<unsigned>((threads + 255) / 256));
