@@ -390,6 +390,9 @@ def main():
 
     step_bytes = sum(bytes_per.values())
     value = step_bytes / step_s / 1e9
+    if not per_kernel_us:
+        per_kernel_us = {"add_rms_norm": float("nan")}
+        bytes_per = {"add_rms_norm": 0}
     dominant = max(per_kernel_us, key=per_kernel_us.get)
     achieved = bytes_per[dominant] / (per_kernel_us[dominant] * 1e-6) / 1e9
     traffic = None
@@ -422,19 +425,23 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "cpu_baseline": None,
     }
-    if not args.no_extras and not args.only:
+    want_extras = not args.no_extras and (not args.only or any(o.startswith(("c4_", "c5_")) for o in args.only.split(",")))
+    if want_extras:
         ek, eb, ekeep = build_extras(args.replicas)
+        if args.only:
+            ek = {k: v for k, v in ek.items() if k in args.only.split(",")}
         eus = time_kernels(ek, args.kernel_iters, stream, torch)
         _lib.take_device_errors()
         line["extras"] = {n: {"us": round(eus[n], 2), "bytes": eb[n],
                               "gbs": round(eb[n] / (eus[n] * 1e-6) / 1e9, 1),
                               "frac": round(eb[n] / (eus[n] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)} for n in eus}
         moe_us = sum(v for n, v in eus.items() if n.startswith("c5_"))
-        line["extras_summary"] = {
-            "c4_decode_tok_s": round(GEM_B / (eus["c4_paged_decode"] * 1e-6), 1),
-            "c5_moe_block_us": round(moe_us, 2),
-            "c5_moe_block_tok_s": round(MOE_T / (moe_us * 1e-6), 1),
-        }
+        if not args.only:
+            line["extras_summary"] = {
+                "c4_decode_tok_s": round(GEM_B / (eus["c4_paged_decode"] * 1e-6), 1),
+                "c5_moe_block_us": round(moe_us, 2),
+                "c5_moe_block_tok_s": round(MOE_T / (moe_us * 1e-6), 1),
+            }
         del ekeep
     if not args.no_cpu and not args.only:
         line["cpu_baseline"] = cpu_baseline(host, bytes_per, args.cpu_tokens, args.cpu_seqs)
