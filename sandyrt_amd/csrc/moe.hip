@@ -94,6 +94,44 @@ __global__ __launch_bounds__(256) void topk_rows_kernel(const void* __restrict__
     }
 }
 
+// Small rows (<= 256): one wave per row; each element's rank under (value
+// desc, index asc) is counted against the whole row staged in LDS, and the
+// elements with rank < k are written straight to their slot.  No serial
+// rounds: one pass of compares.
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void topk_rank_kernel(const void* __restrict__ x, void* __restrict__ values,
+                                                        void* __restrict__ indices, int32_t idx_dt, int64_t rows,
+                                                        int axis, int k) {
+    __shared__ float row_v[4][64 * NV];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+    if (row >= rows) return;
+    float v[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int c = lane + 64 * j;
+        v[j] = c < axis ? Vec8<T>::load1(x, row * axis + c) : 0.0f;
+        if (c < axis) row_v[wave][c] = v[j];
+    }
+    __builtin_amdgcn_wave_barrier();
+    int rank[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) rank[j] = 0;
+    for (int a = 0; a < axis; a++) {
+        const float o = row_v[wave][a];
+#pragma unroll
+        for (int j = 0; j < NV; j++) rank[j] += better(o, a, v[j], lane + 64 * j) ? 1 : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int c = lane + 64 * j;
+        if (c < axis && rank[j] < k) {
+            Vec8<T>::store1(values, row * k + rank[j], v[j]);
+            store_index(indices, idx_dt, row * k + rank[j], c);
+        }
+    }
+}
+
 // Any axis: one thread per (outer, inner) column, selection over the axis.
 template <typename T>
 __global__ __launch_bounds__(256) void topk_columns_kernel(const void* __restrict__ x, void* __restrict__ values,
@@ -127,6 +165,7 @@ __global__ __launch_bounds__(256) void topk_columns_kernel(const void* __restric
 // ---------------------------------------------------------------- moe_gather
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
+constexpr int kRouteStage = 4096;  // routes whose ids and weights are staged in LDS
 
 // One workgroup per batch.  Pass 1 counts routes per expert; pass 2 walks the
 // routes in order, 1024 at a time: inside a wave, lanes routed to the same
@@ -140,32 +179,72 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
     extern __shared__ int32_t lds[];
     int32_t* cursor = lds;                      // [E]
     int32_t* wcount = lds + experts;            // [kRouteWaves][E]
+    int32_t* sid = wcount + kRouteWaves * experts;          // staged ids  [kRouteStage]
+    float* sw = reinterpret_cast<float*>(sid + kRouteStage);  // staged weights [kRouteStage]
     const int b = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t routes = seq * top_k;
     const int64_t rb = static_cast<int64_t>(b) * routes;
+    const bool staged = routes <= kRouteStage;
     for (int64_t e = tid; e < experts; e += kRouteThreads) cursor[e] = 0;
-    __syncthreads();
-    for (int64_t r = tid; r < routes; r += kRouteThreads) {
-        const int64_t e = load_index(ids, ids_dt, rb + r);
-        if (e < 0 || e >= experts) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_EXPERT_ID));
-        else atomicAdd(&cursor[e], 1);
+    if (staged) {  // all loads independent: one memory round trip
+        for (int64_t r = tid; r < routes; r += kRouteThreads) {
+            int64_t e = load_index(ids, ids_dt, rb + r);
+            if (e < 0 || e >= experts) {
+                atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_EXPERT_ID));
+                e = -1;
+            }
+            sid[r] = static_cast<int32_t>(e);
+            sw[r] = load_any(w, w_dt, rb + r);
+        }
     }
     __syncthreads();
-    if (tid == 0) {  // exclusive scan -> offsets and starting cursors
-        int32_t run = 0;
-        for (int64_t e = 0; e < experts; e++) {
-            const int32_t c = cursor[e];
-            cursor[e] = run;
-            store_index(offsets, off_dt, static_cast<int64_t>(b) * (experts + 1) + e, run);
-            run += c;
+    for (int64_t r = tid; r < routes; r += kRouteThreads) {
+        int64_t e;
+        if (staged) e = sid[r];
+        else {
+            e = load_index(ids, ids_dt, rb + r);
+            if (e < 0 || e >= experts) {
+                atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_EXPERT_ID));
+                e = -1;
+            }
         }
-        store_index(offsets, off_dt, static_cast<int64_t>(b) * (experts + 1) + experts, run);
+        if (e >= 0) atomicAdd(&cursor[e], 1);
+    }
+    __syncthreads();
+    // exclusive scan of the counts -> offsets and starting cursors: each wave
+    // scans 64-expert segments with shuffles, segments chained serially
+    {
+        __shared__ int32_t seg_total;
+        if (tid == 0) seg_total = 0;
+        __syncthreads();
+        for (int64_t s0 = 0; s0 < experts; s0 += 64) {
+            if (wave == 0) {
+                const int64_t ex = s0 + lane;
+                const int32_t c = ex < experts ? cursor[ex] : 0;
+                int32_t incl = c;
+#pragma unroll
+                for (int d = 1; d < 64; d <<= 1) {
+                    const int32_t up = __shfl_up(incl, d, 64);
+                    if (lane >= d) incl += up;
+                }
+                const int32_t base = seg_total;
+                if (ex < experts) {
+                    cursor[ex] = base + incl - c;
+                    store_index(offsets, off_dt, static_cast<int64_t>(b) * (experts + 1) + ex, base + incl - c);
+                }
+                const int32_t tot = __shfl(incl, 63, 64);
+                if (lane == 0) seg_total = base + tot;
+            }
+            __syncthreads();
+        }
+        if (tid == 0) store_index(offsets, off_dt, static_cast<int64_t>(b) * (experts + 1) + experts, seg_total);
     }
     __syncthreads();
     for (int64_t c0 = 0; c0 < routes; c0 += kRouteThreads) {
         const int64_t r = c0 + tid;
-        int64_t e = r < routes ? load_index(ids, ids_dt, rb + r) : -1;
+        int64_t e = -1;
+        if (r < routes) e = staged ? sid[r] : load_index(ids, ids_dt, rb + r);
         if (e >= experts) e = -1;
         for (int64_t i = lane; i < experts; i += 64) wcount[wave * experts + i] = 0;
         __syncthreads();
@@ -174,7 +253,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         uint64_t pending = __ballot(e >= 0);
         while (pending) {
             const int leader = __ffsll(static_cast<long long>(pending)) - 1;
-            const int64_t le = __shfl(e, leader, 64);
+            const int64_t le = __builtin_amdgcn_readlane(static_cast<int>(e), leader);
             const uint64_t same = __ballot(e == le);
             if (e == le) rank = __popcll(same & ((1ull << lane) - 1ull));
             if (lane == leader) wcount[wave * experts + le] = __popcll(same);
@@ -196,7 +275,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
             const int32_t row = wcount[wave * experts + e] + rank;
             dest[rb + r] = row;
             const int64_t mb = static_cast<int64_t>(b) * routes;
-            store_any(packed_w, w_dt, mb + row, load_any(w, w_dt, rb + r));
+            store_any(packed_w, w_dt, mb + row, staged ? sw[r] : load_any(w, w_dt, rb + r));
             store_index(token_ids, tok_dt, mb + row, r / top_k);
         } else if (r < routes) {
             dest[rb + r] = -1;
@@ -228,52 +307,94 @@ __global__ __launch_bounds__(256) void moe_copy_rows_kernel(const char* __restri
 }
 
 // ---------------------------------------------------------------- moe_scatter_sum
-// One wave per (batch, token, 512-column chunk): finds the rows of its token
-// in row order with ballots and accumulates w * packed[row] with the
-// reference's two roundings (product, then sum rounded to the output dtype).
+// Workgroup = (batch, 4 tokens, 512-column chunk); wave = one token.  The
+// batch's token ids are staged in LDS once per workgroup; each wave collects
+// the rows of its token in row order with ballots, then processes them 8 at a
+// time: the 8 rows' loads are issued together and accumulated in row order
+// with the reference's two roundings (product, then sum rounded to the output
+// dtype) -- bit-identical to the CPU, no atomics.
+constexpr int kCombineStage = 8192;  // rows staged in LDS (32 KiB)
+constexpr int kCombineHits = 128;    // per-wave hit list
+
 template <typename T>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict__ packed,
                                                           const void* __restrict__ pw,
                                                           const void* __restrict__ tok, int32_t tok_dt,
                                                           void* __restrict__ out, int64_t batch, int64_t rows,
                                                           int64_t hidden, int64_t seq, uint32_t* errw) {
-    const int lane = threadIdx.x & 63;
+    __shared__ int32_t ids[kCombineStage];
+    __shared__ int32_t hit[4][kCombineHits];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t chunks = (hidden + 511) / 512;
-    const int64_t wid = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-    if (wid >= batch * seq * chunks) return;
-    const int64_t ch = wid % chunks;
-    const int64_t t = (wid / chunks) % seq;
-    const int64_t b = wid / (chunks * seq);
+    const int64_t tgroups = (seq + 3) / 4;
+    const int64_t ch = blockIdx.x % chunks;
+    const int64_t tg = (blockIdx.x / chunks) % tgroups;
+    const int64_t b = blockIdx.x / (chunks * tgroups);
+    const int64_t t = tg * 4 + wave;
+    const int64_t mb = b * rows;
+    const bool staged = rows <= kCombineStage;
+    if (staged) {
+        for (int64_t r = threadIdx.x; r < rows; r += 256) {
+            const int64_t v = load_index(tok, tok_dt, mb + r);
+            if ((v < 0 || v >= seq) && blockIdx.x % (chunks * tgroups) == 0)
+                atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_TOKEN_ID));
+            ids[r] = static_cast<int32_t>(v);
+        }
+    }
+    __syncthreads();
+    if (t >= seq) return;
     const int64_t c0 = ch * 512 + lane * 8;
     const bool vec = (hidden & 7) == 0;
+    const int32_t wdt = sizeof(typename Vec8<T>::elem) == 2 ? SANDY_BF16 : SANDY_F32;
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) acc[i] = 0.0f;
-    const int64_t mb = b * rows;
-    for (int64_t r0 = 0; r0 < rows; r0 += 64) {
-        const int64_t r = r0 + lane;
-        const int64_t tr = r < rows ? load_index(tok, tok_dt, mb + r) : -1;
-        if (r < rows && (tr < 0 || tr >= seq) && t == 0 && ch == 0)
-            atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_TOKEN_ID));
-        uint64_t hits = __ballot(tr == t);
-        while (hits) {
-            const int hl = __ffsll(static_cast<long long>(hits)) - 1;
-            hits &= hits - 1;
-            const int64_t row = r0 + hl;
-            const float wv = load_any(pw, sizeof(typename Vec8<T>::elem) == 2 ? SANDY_BF16 : SANDY_F32, mb + row);
-            const int64_t src = (mb + row) * hidden + c0;
-            if (c0 < hidden) {
-                float pv[8];
-                if (vec) {
-                    Vec8<T>::load(packed, src, pv);
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 8; i++) pv[i] = c0 + i < hidden ? Vec8<T>::load1(packed, src + i) : 0.0f;
+    int64_t r0 = 0;
+    while (r0 < rows) {
+        // collect up to kCombineHits rows of token t, in row order
+        int n = 0;
+        for (; r0 < rows && n + 64 <= kCombineHits; r0 += 64) {
+            const int64_t r = r0 + lane;
+            int64_t tr = -1;
+            if (r < rows) {
+                if (staged) tr = ids[r];
+                else {
+                    tr = load_index(tok, tok_dt, mb + r);
+                    if ((tr < 0 || tr >= seq) && t == 0 && ch == 0)
+                        atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_TOKEN_ID));
                 }
-#pragma unroll
-                for (int i = 0; i < 8; i++) acc[i] = Vec8<T>::round(__fadd_rn(acc[i], __fmul_rn(wv, pv[i])));
             }
+            const uint64_t hits = __ballot(tr == t);
+            if (tr == t) hit[wave][n + __popcll(hits & ((1ull << lane) - 1ull))] = static_cast<int32_t>(r);
+            n += __popcll(hits);
         }
+        __builtin_amdgcn_wave_barrier();
+        // accumulate the collected rows, 8 loads in flight at a time
+        for (int g = 0; g < n; g += 8) {
+            float pv[8][8];
+            float wv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const bool in = g + u < n;
+                const int64_t row = in ? hit[wave][g + u] : 0;
+                wv[u] = in ? load_any(pw, wdt, mb + row) : 0.0f;
+                const int64_t src = (mb + row) * hidden + c0;
+                if (in && c0 < hidden) {
+                    if (vec) {
+                        Vec8<T>::load(packed, src, pv[u]);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 8; i++) pv[u][i] = c0 + i < hidden ? Vec8<T>::load1(packed, src + i) : 0.0f;
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (g + u < n)
+#pragma unroll
+                    for (int i = 0; i < 8; i++) acc[i] = Vec8<T>::round(__fadd_rn(acc[i], __fmul_rn(wv[u], pv[u][i])));
+        }
+        __builtin_amdgcn_wave_barrier();
     }
     if (c0 < hidden) {
         const int64_t dst = (b * seq + t) * hidden + c0;
@@ -473,12 +594,16 @@ extern "C" int sandy_hip_topk(const SandyTensor* x, int64_t k, int64_t axis, con
 #define TOPK_LAUNCH(NV)                                                                                                 \
     if (bf) hipLaunchKernelGGL((topk_rows_kernel<BF16, NV>), grid, dim3(256), 0, stream, px, pv, pi, indices->dtype, outer, ax, kk); \
     else hipLaunchKernelGGL((topk_rows_kernel<F32, NV>), grid, dim3(256), 0, stream, px, pv, pi, indices->dtype, outer, ax, kk)
-        if (n <= 64) { TOPK_LAUNCH(1); }
-        else if (n <= 128) { TOPK_LAUNCH(2); }
-        else if (n <= 256) { TOPK_LAUNCH(4); }
+#define TOPK_RANK(NV)                                                                                                   \
+    if (bf) hipLaunchKernelGGL((topk_rank_kernel<BF16, NV>), grid, dim3(256), 0, stream, px, pv, pi, indices->dtype, outer, ax, kk); \
+    else hipLaunchKernelGGL((topk_rank_kernel<F32, NV>), grid, dim3(256), 0, stream, px, pv, pi, indices->dtype, outer, ax, kk)
+        if (n <= 64) { TOPK_RANK(1); }
+        else if (n <= 128) { TOPK_RANK(2); }
+        else if (n <= 256) { TOPK_RANK(4); }
         else if (n <= 512) { TOPK_LAUNCH(8); }
         else { TOPK_LAUNCH(16); }
 #undef TOPK_LAUNCH
+#undef TOPK_RANK
     } else {
         const int64_t threads = outer * inner;
         dim3 grid(static_cast<unsigned>((threads + 255) / 256));
@@ -524,8 +649,8 @@ extern "C" int sandy_hip_moe_gather(const SandyTensor* x, const SandyTensor* top
         return fail(e, SANDY_ERR_INVALID, "moe_gather metadata output shape mismatch");
     for (const SandyTensor* t : all)
         if (!contiguous(*t)) return fail(e, SANDY_ERR_UNSUPPORTED, "moe_gather requires contiguous tensors");
-    const size_t lds = static_cast<size_t>(num_experts) * (1 + kRouteWaves) * sizeof(int32_t);
-    if (lds > 64 * 1024) return fail(e, SANDY_ERR_UNSUPPORTED, "moe_gather supports up to %d experts", (64 * 1024 / 4) / (1 + kRouteWaves));
+    const size_t lds = static_cast<size_t>(num_experts) * (1 + kRouteWaves) * sizeof(int32_t) + 2 * kRouteStage * 4;
+    if (lds > 64 * 1024) return fail(e, SANDY_ERR_UNSUPPORTED, "moe_gather supports up to %d experts", (64 * 1024 / 4 - 2 * kRouteStage) / (1 + kRouteWaves));
     if (batch == 0) return ok(e);
     int status = 0;
     uint32_t* errw = device_error_word(e, &status);
@@ -648,8 +773,8 @@ extern "C" int sandy_hip_moe_scatter_sum(const SandyTensor* packed_out, const Sa
     int status = 0;
     uint32_t* errw = device_error_word(e, &status);
     if (status) return status;
-    const int64_t waves = batch * seq * ((hidden + 511) / 512);
-    dim3 grid(static_cast<unsigned>((waves + 3) / 4));
+    const int64_t blocks = batch * ((seq + 3) / 4) * ((hidden + 511) / 512);
+    dim3 grid(static_cast<unsigned>(blocks));
     const bool aligned = ((reinterpret_cast<uintptr_t>(base_ptr(*packed_out)) | reinterpret_cast<uintptr_t>(base_ptr(*out))) & 15) == 0;
     if (!aligned && hidden % 8 == 0) return fail(e, SANDY_ERR_UNSUPPORTED, "moe_scatter_sum needs 16-byte aligned rows");
     if (packed_out->dtype == SANDY_BF16)
