@@ -231,6 +231,103 @@ int sandy_hip_moe_scatter_sum(const SandyTensor* packed_out, const SandyTensor* 
                               const SandyTensor* token_ids, const SandyTensor* out,
                               void* stream, char* err, size_t err_cap);
 
+/* ---------------------------------------------------------------- device runtime
+ *
+ * A HIP device object with the reference Device's responsibilities
+ * (src/device/Device.h:27-66): buffers by id, paged tensor pools, stream and
+ * graph capture.  A Device::run on top of it calls the kernel entry points
+ * above with this object's stream and views.
+ *
+ * Paged pools keep their bookkeeping on the device: one pool allocation of
+ * pages ([pages, prefix, page_size, inner], the reference's page layout), an
+ * int32 block table [max_tensors, max_blocks] and int32 grow lengths
+ * [max_tensors].  Appends are one kernel launch (the reference issues one
+ * cudaMemcpyAsync per row, src/device/cuda/CudaPagedTensor.cpp:649-740), and
+ * sandy_hip_device_paged_append_step reads positions on the device, so a whole
+ * decode step (append + attention) can be captured in a HIP graph.
+ */
+typedef struct SandyHipDevice SandyHipDevice;
+
+typedef struct SandyPagedPoolDesc {     /* DevicePagedPoolDesc, src/device/DeviceTypes.h:36-42 */
+    int32_t dtype;
+    int32_t rank;
+    int64_t dims[SANDY_HIP_MAX_RANK];   /* template shape; dims[grow_dim] is ignored */
+    int64_t grow_dim;
+    int64_t page_size;                  /* power of two */
+    int64_t initial_pages;
+    int64_t max_pages;                  /* < 0: the pool grows on demand */
+    int64_t max_tensors;                /* rows of the device block table */
+    int64_t max_blocks;                 /* pages per tensor (block table columns) */
+} SandyPagedPoolDesc;
+
+typedef struct SandyPagedMeta {         /* DevicePagedTensorMeta, src/device/DeviceTypes.h:44-52 */
+    uint32_t pool;
+    int32_t dtype;
+    int32_t rank;
+    int32_t slot;                       /* row of the pool's block table */
+    int64_t dims[SANDY_HIP_MAX_RANK];   /* logical shape (grow dim = grow_length) */
+    int64_t grow_dim;
+    int64_t page_size;
+    int64_t grow_length;
+    int64_t page_count;
+    int64_t page_element_count;
+} SandyPagedMeta;
+
+/* Device lifetime.  The device owns one HIP stream (default priority). */
+int sandy_hip_device_create(int32_t ordinal, SandyHipDevice** out, char* err, size_t err_cap);
+void sandy_hip_device_destroy(SandyHipDevice* dev);
+void* sandy_hip_device_stream(SandyHipDevice* dev);
+int sandy_hip_device_synchronize(SandyHipDevice* dev, char* err, size_t err_cap);
+
+/* Buffers (Device::alloc/dealloc/load/read).  load and read synchronise. */
+int sandy_hip_device_alloc(SandyHipDevice* dev, uint64_t bytes, uint32_t* buffer, char* err, size_t err_cap);
+int sandy_hip_device_dealloc(SandyHipDevice* dev, uint32_t buffer, char* err, size_t err_cap);
+void* sandy_hip_device_buffer(SandyHipDevice* dev, uint32_t buffer);
+int sandy_hip_device_load(SandyHipDevice* dev, const void* host, uint64_t bytes, uint32_t* buffer, char* err,
+                          size_t err_cap);
+int sandy_hip_device_read(SandyHipDevice* dev, uint32_t buffer, uint64_t offset, uint64_t bytes, void* host,
+                          char* err, size_t err_cap);
+
+/* Paged tensors (Device::createPagedPool .. destroyPagedPool). */
+int sandy_hip_device_paged_pool_create(SandyHipDevice* dev, const SandyPagedPoolDesc* desc, uint32_t* pool,
+                                       char* err, size_t err_cap);
+int sandy_hip_device_paged_pool_destroy(SandyHipDevice* dev, uint32_t pool, char* err, size_t err_cap);
+int sandy_hip_device_paged_alloc(SandyHipDevice* dev, uint32_t pool, uint32_t* tensor, char* err, size_t err_cap);
+int sandy_hip_device_paged_dealloc(SandyHipDevice* dev, uint32_t tensor, char* err, size_t err_cap);
+int sandy_hip_device_paged_reserve(SandyHipDevice* dev, uint32_t tensor, int64_t page_count, char* err,
+                                   size_t err_cap);
+/* Appends a dense chunk (logical shape with the grow dim = chunk length) in
+ * one device copy; stream ordered, no host sync. */
+int sandy_hip_device_paged_append(SandyHipDevice* dev, uint32_t tensor, const SandyTensor* chunk, char* err,
+                                  size_t err_cap);
+/* Appends one grow row to each of `count` tensors of one pool: rows is
+ * [count, <template dims with the grow dim = 1>]; each tensor's position is
+ * read from its device-side length, which the kernel advances.  Pages for the
+ * new rows must already be reserved (sandy_hip_device_paged_reserve). */
+int sandy_hip_device_paged_append_step(SandyHipDevice* dev, uint32_t pool, const uint32_t* tensors, int32_t count,
+                                       const SandyTensor* rows, char* err, size_t err_cap);
+/* positions[i] = device length of tensors[i] - 1 (int32 or int64 output), for
+ * the position_offsets of decode attention inside a captured step. */
+int sandy_hip_device_paged_positions(SandyHipDevice* dev, uint32_t pool, const uint32_t* tensors, int32_t count,
+                                     const SandyTensor* positions, char* err, size_t err_cap);
+int sandy_hip_device_paged_meta(SandyHipDevice* dev, uint32_t tensor, SandyPagedMeta* meta, char* err,
+                                size_t err_cap);
+/* Reads the dense logical tensor (Device::read(DevicePagedTensorView)); synchronises. */
+int sandy_hip_device_paged_read(SandyHipDevice* dev, uint32_t tensor, void* host, uint64_t bytes, char* err,
+                                size_t err_cap);
+/* The pool as a SandyPagedCache, its block table [max_tensors, max_blocks]
+ * int32 and grow lengths [max_tensors] int32 (device-resident views). */
+int sandy_hip_device_paged_views(SandyHipDevice* dev, uint32_t pool, SandyPagedCache* cache,
+                                 SandyTensor* block_table, SandyTensor* lengths, char* err, size_t err_cap);
+/* Re-reads the device lengths into the host bookkeeping (after graph replays). */
+int sandy_hip_device_paged_sync(SandyHipDevice* dev, uint32_t pool, char* err, size_t err_cap);
+
+/* HIP graph capture of work on the device stream. */
+int sandy_hip_device_graph_begin(SandyHipDevice* dev, char* err, size_t err_cap);
+int sandy_hip_device_graph_end(SandyHipDevice* dev, uint32_t* graph, char* err, size_t err_cap);
+int sandy_hip_device_graph_launch(SandyHipDevice* dev, uint32_t graph, char* err, size_t err_cap);
+int sandy_hip_device_graph_destroy(SandyHipDevice* dev, uint32_t graph, char* err, size_t err_cap);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,6 +74,35 @@ class SandyScalarNode(C.Structure):
     ]
 
 
+class SandyPagedPoolDesc(C.Structure):
+    _fields_ = [
+        ("dtype", C.c_int32),
+        ("rank", C.c_int32),
+        ("dims", C.c_int64 * MAX_RANK),
+        ("grow_dim", C.c_int64),
+        ("page_size", C.c_int64),
+        ("initial_pages", C.c_int64),
+        ("max_pages", C.c_int64),
+        ("max_tensors", C.c_int64),
+        ("max_blocks", C.c_int64),
+    ]
+
+
+class SandyPagedMeta(C.Structure):
+    _fields_ = [
+        ("pool", C.c_uint32),
+        ("dtype", C.c_int32),
+        ("rank", C.c_int32),
+        ("slot", C.c_int32),
+        ("dims", C.c_int64 * MAX_RANK),
+        ("grow_dim", C.c_int64),
+        ("page_size", C.c_int64),
+        ("grow_length", C.c_int64),
+        ("page_count", C.c_int64),
+        ("page_element_count", C.c_int64),
+    ]
+
+
 T = C.POINTER(SandyTensor)
 P = C.POINTER(SandyPagedCache)
 ERR = C.c_char_p
@@ -98,6 +127,38 @@ SIGNATURES = {
     "sandy_hip_moe_scatter_sum": [T, T, T, T, C.c_void_p, ERR, C.c_size_t],
 }
 
+# device runtime entry points: name -> (argtypes without the trailing err/cap, restype)
+DEV = C.c_void_p
+U32P = C.POINTER(C.c_uint32)
+DEVICE_SIGNATURES = {
+    "sandy_hip_device_create": ([C.c_int32, C.POINTER(C.c_void_p)], C.c_int),
+    "sandy_hip_device_destroy": ([DEV], None),
+    "sandy_hip_device_stream": ([DEV], C.c_void_p),
+    "sandy_hip_device_synchronize": ([DEV], C.c_int),
+    "sandy_hip_device_alloc": ([DEV, C.c_uint64, U32P], C.c_int),
+    "sandy_hip_device_dealloc": ([DEV, C.c_uint32], C.c_int),
+    "sandy_hip_device_buffer": ([DEV, C.c_uint32], C.c_void_p),
+    "sandy_hip_device_load": ([DEV, C.c_void_p, C.c_uint64, U32P], C.c_int),
+    "sandy_hip_device_read": ([DEV, C.c_uint32, C.c_uint64, C.c_uint64, C.c_void_p], C.c_int),
+    "sandy_hip_device_paged_pool_create": ([DEV, C.POINTER(SandyPagedPoolDesc), U32P], C.c_int),
+    "sandy_hip_device_paged_pool_destroy": ([DEV, C.c_uint32], C.c_int),
+    "sandy_hip_device_paged_alloc": ([DEV, C.c_uint32, U32P], C.c_int),
+    "sandy_hip_device_paged_dealloc": ([DEV, C.c_uint32], C.c_int),
+    "sandy_hip_device_paged_reserve": ([DEV, C.c_uint32, C.c_int64], C.c_int),
+    "sandy_hip_device_paged_append": ([DEV, C.c_uint32, T], C.c_int),
+    "sandy_hip_device_paged_append_step": ([DEV, C.c_uint32, U32P, C.c_int32, T], C.c_int),
+    "sandy_hip_device_paged_positions": ([DEV, C.c_uint32, U32P, C.c_int32, T], C.c_int),
+    "sandy_hip_device_paged_meta": ([DEV, C.c_uint32, C.POINTER(SandyPagedMeta)], C.c_int),
+    "sandy_hip_device_paged_read": ([DEV, C.c_uint32, C.c_void_p, C.c_uint64], C.c_int),
+    "sandy_hip_device_paged_views": ([DEV, C.c_uint32, P, T, T], C.c_int),
+    "sandy_hip_device_paged_sync": ([DEV, C.c_uint32], C.c_int),
+    "sandy_hip_device_graph_begin": ([DEV], C.c_int),
+    "sandy_hip_device_graph_end": ([DEV, U32P], C.c_int),
+    "sandy_hip_device_graph_launch": ([DEV, C.c_uint32], C.c_int),
+    "sandy_hip_device_graph_destroy": ([DEV, C.c_uint32], C.c_int),
+}
+NO_ERR_ARGS = {"sandy_hip_device_destroy", "sandy_hip_device_stream", "sandy_hip_device_buffer"}
+
 _lib = None
 
 
@@ -115,12 +176,24 @@ def lib():
             fn = getattr(handle, name)
             fn.argtypes = argtypes
             fn.restype = C.c_int
+        for name, (argtypes, restype) in DEVICE_SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes + ([] if name in NO_ERR_ARGS else [ERR, C.c_size_t])
+            fn.restype = restype
         _lib = handle
     return _lib
 
 
 def exported_symbols():
-    return ["sandy_hip_version", *SIGNATURES.keys()]
+    return ["sandy_hip_version", *SIGNATURES.keys(), *DEVICE_SIGNATURES.keys()]
+
+
+def dcall(name: str, *args):
+    """Invoke a device-runtime entry point (error buffer appended)."""
+    buf = C.create_string_buffer(512)
+    rc = getattr(lib(), name)(*args, buf, C.c_size_t(512))
+    if rc != 0:
+        raise SandyError(rc, buf.value.decode(errors="replace"))
 
 
 def desc(t: torch.Tensor | None):

@@ -1,0 +1,699 @@
+// hip_device.hip -- the device object: buffers, paged tensor pools with
+// device-resident block tables and lengths, one stream, HIP graph capture.
+//
+// Mirrors the responsibilities of sandy::device::Device
+// (src/device/Device.h:27-66) and the CUDA backend's paged storage
+// (src/device/cuda/CudaPagedTensor.{h,cpp}).  Differences by design:
+//   - a pool is one allocation of pages, pages are int32 block ids (the
+//     reference allocates every page separately and keeps a void* page table
+//     per tensor, synchronised to the device incrementally);
+//   - each pool keeps an int32 block table [max_tensors, max_blocks] and int32
+//     grow lengths [max_tensors] on the device; a tensor is a row (slot);
+//   - an append is one kernel launch instead of one cudaMemcpyAsync per
+//     (prefix, grow) row (CudaPagedTensor.cpp:649-740); the step append reads
+//     and advances the lengths on the device, so a decode step needs no host
+//     bookkeeping and can be captured in a graph.
+// Error wording follows the reference (CpuDevice.cpp:444-554,
+// CudaPagedTensor.cpp:30-55,232-258, Device.cpp:13-19).
+#include "common.h"
+
+#include <algorithm>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace sandy_hip {
+namespace {
+
+constexpr int kMaxStepTensors = 512;
+
+struct PagedPool {
+    SandyPagedPoolDesc desc{};
+    int64_t prefix = 1, inner = 1;   // elements before / after the grow dim
+    int64_t page_elems = 0;          // prefix * page_size * inner
+    size_t elem = 0;
+    char* pages = nullptr;           // [capacity, prefix, page_size, inner]
+    int64_t capacity = 0;
+    int64_t used = 0;                // pages ever handed out (high-water mark)
+    std::vector<int32_t> free_pages;
+    int32_t* table = nullptr;        // device [max_tensors, max_blocks]
+    int32_t* host_table = nullptr;   // pinned mirror: source of the table updates
+    int32_t* lengths = nullptr;      // device [max_tensors]
+    std::vector<int32_t> free_slots;
+};
+
+struct PagedTensor {
+    uint32_t pool = 0;
+    int32_t slot = 0;
+    int64_t grow_length = 0;
+    std::vector<int32_t> pages;
+};
+
+struct StepArgs {
+    int32_t slots[kMaxStepTensors];
+};
+
+// chunk rows -> pages: one wave per (prefix, grow) row of the chunk
+__global__ __launch_bounds__(256) void paged_append_kernel(const char* __restrict__ src, char* __restrict__ pages,
+                                                           const int32_t* __restrict__ table_row,
+                                                           int32_t* __restrict__ length_slot, int64_t old_len,
+                                                           int64_t chunk_len, int64_t prefix, int64_t page_size,
+                                                           int64_t row_bytes, int64_t page_bytes) {
+    const int lane = threadIdx.x & 63;
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (r == 0 && threadIdx.x == 0) *length_slot = static_cast<int32_t>(old_len + chunk_len);
+    if (r >= prefix * chunk_len) return;
+    const int64_t p = r / chunk_len, g = r % chunk_len;
+    const int64_t dst_grow = old_len + g;
+    const int32_t blk = table_row[dst_grow / page_size];
+    const char* s = src + r * row_bytes;
+    char* d = pages + blk * page_bytes + (p * page_size + dst_grow % page_size) * row_bytes;
+    if ((row_bytes & 15) == 0 && ((reinterpret_cast<uintptr_t>(s) | reinterpret_cast<uintptr_t>(d)) & 15) == 0) {
+        for (int64_t o = lane * 16; o < row_bytes; o += 64 * 16)
+            *reinterpret_cast<uint4*>(d + o) = *reinterpret_cast<const uint4*>(s + o);
+    } else {
+        for (int64_t o = lane; o < row_bytes; o += 64) d[o] = s[o];
+    }
+}
+
+// one new grow row per tensor; position = device length; block per tensor
+__global__ __launch_bounds__(256) void paged_append_step_kernel(const char* __restrict__ rows, char* __restrict__ pages,
+                                                                const int32_t* __restrict__ table,
+                                                                int32_t* __restrict__ lengths, int64_t max_blocks,
+                                                                int64_t prefix, int64_t page_size, int64_t row_bytes,
+                                                                int64_t page_bytes, uint32_t* errw, StepArgs args) {
+    const int i = blockIdx.x;
+    const int32_t slot = args.slots[i];
+    const int32_t len = lengths[slot];
+    __syncthreads();  // every wave has read the length before it advances
+    const int32_t page = len / page_size;
+    const int32_t blk = page < max_blocks ? table[slot * max_blocks + page] : -1;
+    if (blk >= 0) {
+        const int lane = threadIdx.x & 63;
+        for (int64_t p = threadIdx.x >> 6; p < prefix; p += 4) {
+            const char* s = rows + (static_cast<int64_t>(i) * prefix + p) * row_bytes;
+            char* d = pages + blk * page_bytes + (p * page_size + len % page_size) * row_bytes;
+            if ((row_bytes & 15) == 0) {
+                for (int64_t o = lane * 16; o < row_bytes; o += 64 * 16)
+                    *reinterpret_cast<uint4*>(d + o) = *reinterpret_cast<const uint4*>(s + o);
+            } else {
+                for (int64_t o = lane; o < row_bytes; o += 64) d[o] = s[o];
+            }
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (blk >= 0) lengths[slot] = len + 1;
+        else atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));  // no page reserved for the row
+    }
+}
+
+__global__ void paged_positions_kernel(const int32_t* __restrict__ lengths, void* __restrict__ out, int32_t out_dt,
+                                       int32_t count, StepArgs args) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) store_index(out, out_dt, i, static_cast<int64_t>(lengths[args.slots[i]]) - 1);
+}
+
+} // namespace
+
+struct HipDeviceImpl {
+    int ordinal = 0;
+    hipStream_t stream = nullptr;
+    uint32_t next_id = 1;
+    std::map<uint32_t, std::pair<void*, size_t>> buffers;
+    std::map<uint32_t, std::unique_ptr<PagedPool>> pools;
+    std::map<uint32_t, PagedTensor> tensors;
+    std::map<uint32_t, hipGraphExec_t> graphs;
+    hipGraph_t capturing = nullptr;
+    std::mutex mu;
+};
+
+} // namespace sandy_hip
+
+struct SandyHipDevice {
+    sandy_hip::HipDeviceImpl impl;
+};
+
+using namespace sandy_hip;
+
+namespace {
+
+int set_device(SandyHipDevice* d, Err e) {
+    if (!d) return fail(e, SANDY_ERR_INVALID, "hip device is null");
+    SANDY_HIP_TRY(hipSetDevice(d->impl.ordinal), e, "hipSetDevice");
+    return SANDY_OK;
+}
+
+int64_t product(const int64_t* dims, int lo, int hi) {
+    int64_t p = 1;
+    for (int i = lo; i < hi; i++) p *= dims[i];
+    return p;
+}
+
+// CudaPagedTensor.cpp:30-55 validate_paged_pool_desc, Device.cpp:13-19
+int validate_pool(const SandyPagedPoolDesc& d, Err e) {
+    if (d.rank <= 0 || d.rank > SANDY_HIP_MAX_RANK) return fail(e, SANDY_ERR_INVALID, "paged tensor pool rank must be >= 1");
+    if (d.grow_dim < 0 || d.grow_dim >= d.rank) return fail(e, SANDY_ERR_INVALID, "paged tensor pool grow_dim out of range");
+    if (d.page_size <= 0) return fail(e, SANDY_ERR_INVALID, "paged tensor pool page_size must be > 0");
+    if ((d.page_size & (d.page_size - 1)) != 0)
+        return fail(e, SANDY_ERR_INVALID, "paged tensor pool page_size must be a power of two");
+    if (d.initial_pages < 0) return fail(e, SANDY_ERR_INVALID, "paged tensor pool initial page count must be >= 0");
+    if (d.max_pages >= 0 && d.initial_pages > d.max_pages)
+        return fail(e, SANDY_ERR_INVALID, "paged tensor pool initial page count exceeds max page count");
+    for (int i = 0; i < d.rank; i++)
+        if (i != d.grow_dim && d.dims[i] <= 0)
+            return fail(e, SANDY_ERR_INVALID, "paged tensor pool non-grow dimensions must be static and positive");
+    if (!is_float(d.dtype) && d.dtype != SANDY_I32 && d.dtype != SANDY_I64)
+        return fail(e, SANDY_ERR_INVALID, "paged tensor pool unsupported dtype");
+    if (d.max_tensors <= 0 || d.max_blocks <= 0)
+        return fail(e, SANDY_ERR_INVALID, "paged tensor pool needs max_tensors and max_blocks > 0");
+    return SANDY_OK;
+}
+
+// Grows the page allocation to hold at least `need` pages (doubling).  Any
+// captured graph that used the old allocation must be re-captured.
+int grow_pool(HipDeviceImpl& d, PagedPool& p, int64_t need, Err e) {
+    if (need <= p.capacity) return SANDY_OK;
+    if (p.desc.max_pages >= 0 && need > p.desc.max_pages)
+        return fail(e, SANDY_ERR_INVALID, "hip device paged pool capacity exceeded");
+    int64_t cap = std::max<int64_t>(need, std::max<int64_t>(16, 2 * p.capacity));
+    if (p.desc.max_pages >= 0) cap = std::min(cap, p.desc.max_pages);
+    char* fresh = nullptr;
+    SANDY_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&fresh), static_cast<size_t>(cap * p.page_elems) * p.elem), e,
+                  "paged pool allocation");
+    if (p.pages) {
+        SANDY_HIP_TRY(hipMemcpyAsync(fresh, p.pages, static_cast<size_t>(p.capacity * p.page_elems) * p.elem,
+                                     hipMemcpyDeviceToDevice, d.stream), e, "paged pool growth copy");
+        SANDY_HIP_TRY(hipStreamSynchronize(d.stream), e, "paged pool growth");
+        SANDY_HIP_TRY(hipFree(p.pages), e, "paged pool release");
+    }
+    p.pages = fresh;
+    p.capacity = cap;
+    return SANDY_OK;
+}
+
+int take_page(HipDeviceImpl& d, PagedPool& p, int32_t* page, Err e) {
+    if (!p.free_pages.empty()) {
+        *page = p.free_pages.back();
+        p.free_pages.pop_back();
+        return SANDY_OK;
+    }
+    if (p.used >= 0x7fffffff) return fail(e, SANDY_ERR_INVALID, "hip device paged pool page index overflow");
+    int st = grow_pool(d, p, p.used + 1, e);
+    if (st) return st;
+    *page = static_cast<int32_t>(p.used++);
+    return SANDY_OK;
+}
+
+// CpuDevice.cpp:444-463 reservePaged: append pages until page_count; the new
+// block-table entries are copied to the device on the stream.
+int reserve(HipDeviceImpl& d, PagedTensor& t, int64_t page_count, Err e) {
+    if (page_count < 0) return fail(e, SANDY_ERR_INVALID, "hip device paged tensor reserve page count must be >= 0");
+    PagedPool& p = *d.pools.at(t.pool);
+    if (page_count > p.desc.max_blocks)
+        return fail(e, SANDY_ERR_INVALID, "hip device paged tensor exceeds the pool's max_blocks");
+    const size_t first = t.pages.size();
+    while (static_cast<int64_t>(t.pages.size()) < page_count) {
+        int32_t page = 0;
+        int st = take_page(d, p, &page, e);
+        if (st) return st;
+        t.pages.push_back(page);
+    }
+    if (t.pages.size() > first) {
+        const size_t n = t.pages.size() - first;
+        // entries go through the pinned mirror, which stays valid until the copy runs
+        int32_t* src = p.host_table + static_cast<int64_t>(t.slot) * p.desc.max_blocks + first;
+        std::copy(t.pages.begin() + static_cast<std::ptrdiff_t>(first), t.pages.end(), src);
+        SANDY_HIP_TRY(hipMemcpyAsync(p.table + t.slot * p.desc.max_blocks + first, src, n * sizeof(int32_t),
+                                     hipMemcpyHostToDevice, d.stream), e, "block table update");
+    }
+    return SANDY_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+int sandy_hip_device_create(int32_t ordinal, SandyHipDevice** out, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    if (!out) return fail(e, SANDY_ERR_INVALID, "hip device output pointer is null");
+    int count = 0;
+    SANDY_HIP_TRY(hipGetDeviceCount(&count), e, "hipGetDeviceCount");
+    if (ordinal < 0 || ordinal >= count) return fail(e, SANDY_ERR_INVALID, "hip device ordinal %d out of range", ordinal);
+    auto* d = new SandyHipDevice();
+    d->impl.ordinal = ordinal;
+    hipError_t st = hipSetDevice(ordinal);
+    if (st == hipSuccess) st = hipStreamCreateWithFlags(&d->impl.stream, hipStreamNonBlocking);
+    if (st != hipSuccess) {
+        delete d;
+        return fail(e, SANDY_ERR_HIP, "hip device stream: %s", hipGetErrorString(st));
+    }
+    *out = d;
+    return ok(e);
+}
+
+void sandy_hip_device_destroy(SandyHipDevice* d) {
+    if (!d) return;
+    auto& m = d->impl;
+    hipSetDevice(m.ordinal);
+    hipStreamSynchronize(m.stream);
+    for (auto& g : m.graphs) hipGraphExecDestroy(g.second);
+    for (auto& b : m.buffers) hipFree(b.second.first);
+    for (auto& p : m.pools) {
+        hipFree(p.second->pages);
+        hipFree(p.second->table);
+        hipFree(p.second->lengths);
+        hipHostFree(p.second->host_table);
+    }
+    hipStreamDestroy(m.stream);
+    delete d;
+}
+
+void* sandy_hip_device_stream(SandyHipDevice* d) { return d ? d->impl.stream : nullptr; }
+
+int sandy_hip_device_synchronize(SandyHipDevice* d, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    SANDY_HIP_TRY(hipStreamSynchronize(d->impl.stream), e, "hipStreamSynchronize");
+    return ok(e);
+}
+
+int sandy_hip_device_alloc(SandyHipDevice* d, uint64_t bytes, uint32_t* buffer, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    if (d->impl.capturing) return fail(e, SANDY_ERR_INVALID, "%s is not allowed during graph capture", __func__);
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    void* p = nullptr;
+    SANDY_HIP_TRY(hipMalloc(&p, bytes ? bytes : 16), e, "hip device alloc");
+    const uint32_t id = d->impl.next_id++;
+    d->impl.buffers[id] = {p, bytes};
+    *buffer = id;
+    return ok(e);
+}
+
+int sandy_hip_device_dealloc(SandyHipDevice* d, uint32_t buffer, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    if (d->impl.capturing) return fail(e, SANDY_ERR_INVALID, "%s is not allowed during graph capture", __func__);
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto it = d->impl.buffers.find(buffer);
+    if (it == d->impl.buffers.end()) return fail(e, SANDY_ERR_INVALID, "hip device buffer not found");
+    SANDY_HIP_TRY(hipStreamSynchronize(d->impl.stream), e, "hipStreamSynchronize");
+    SANDY_HIP_TRY(hipFree(it->second.first), e, "hip device dealloc");
+    d->impl.buffers.erase(it);
+    return ok(e);
+}
+
+void* sandy_hip_device_buffer(SandyHipDevice* d, uint32_t buffer) {
+    if (!d) return nullptr;
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto it = d->impl.buffers.find(buffer);
+    return it == d->impl.buffers.end() ? nullptr : it->second.first;
+}
+
+int sandy_hip_device_load(SandyHipDevice* d, const void* host, uint64_t bytes, uint32_t* buffer, char* err,
+                          size_t err_cap) {
+    Err e{err, err_cap};
+    int st = sandy_hip_device_alloc(d, bytes, buffer, err, err_cap);
+    if (st) return st;
+    void* p = sandy_hip_device_buffer(d, *buffer);
+    SANDY_HIP_TRY(hipMemcpyAsync(p, host, bytes, hipMemcpyHostToDevice, d->impl.stream), e, "hip device load");
+    SANDY_HIP_TRY(hipStreamSynchronize(d->impl.stream), e, "hip device load");
+    return ok(e);
+}
+
+int sandy_hip_device_read(SandyHipDevice* d, uint32_t buffer, uint64_t offset, uint64_t bytes, void* host, char* err,
+                          size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    void* p = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(d->impl.mu);
+        auto it = d->impl.buffers.find(buffer);
+        if (it == d->impl.buffers.end()) return fail(e, SANDY_ERR_INVALID, "hip device buffer not found");
+        if (offset + bytes > it->second.second) return fail(e, SANDY_ERR_INVALID, "hip device read exceeds the buffer");
+        p = static_cast<char*>(it->second.first) + offset;
+    }
+    SANDY_HIP_TRY(hipMemcpyAsync(host, p, bytes, hipMemcpyDeviceToHost, d->impl.stream), e, "hip device read");
+    SANDY_HIP_TRY(hipStreamSynchronize(d->impl.stream), e, "hip device read");
+    return ok(e);
+}
+
+int sandy_hip_device_paged_pool_create(SandyHipDevice* d, const SandyPagedPoolDesc* desc, uint32_t* pool, char* err,
+                                       size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    if (d->impl.capturing) return fail(e, SANDY_ERR_INVALID, "%s is not allowed during graph capture", __func__);
+    if (!desc || !pool) return fail(e, SANDY_ERR_INVALID, "paged pool descriptor is null");
+    st = validate_pool(*desc, e);
+    if (st) return st;
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto p = std::make_unique<PagedPool>();
+    p->desc = *desc;
+    p->prefix = product(desc->dims, 0, static_cast<int>(desc->grow_dim));
+    p->inner = product(desc->dims, static_cast<int>(desc->grow_dim) + 1, desc->rank);
+    p->page_elems = p->prefix * desc->page_size * p->inner;
+    p->elem = dtype_size(desc->dtype);
+    SANDY_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p->table), static_cast<size_t>(desc->max_tensors * desc->max_blocks) * 4),
+                  e, "block table allocation");
+    SANDY_HIP_TRY(hipMalloc(reinterpret_cast<void**>(&p->lengths), static_cast<size_t>(desc->max_tensors) * 4), e,
+                  "length allocation");
+    SANDY_HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&p->host_table),
+                                static_cast<size_t>(desc->max_tensors * desc->max_blocks) * 4, hipHostMallocDefault),
+                  e, "pinned block table mirror");
+    SANDY_HIP_TRY(hipMemsetAsync(p->table, 0xff, static_cast<size_t>(desc->max_tensors * desc->max_blocks) * 4, d->impl.stream),
+                  e, "block table init");
+    SANDY_HIP_TRY(hipMemsetAsync(p->lengths, 0, static_cast<size_t>(desc->max_tensors) * 4, d->impl.stream), e, "length init");
+    st = grow_pool(d->impl, *p, std::max<int64_t>(1, desc->initial_pages), e);
+    if (st) return st;
+    for (int64_t s = desc->max_tensors - 1; s >= 0; s--) p->free_slots.push_back(static_cast<int32_t>(s));
+    SANDY_HIP_TRY(hipStreamSynchronize(d->impl.stream), e, "paged pool create");
+    const uint32_t id = d->impl.next_id++;
+    d->impl.pools[id] = std::move(p);
+    *pool = id;
+    return ok(e);
+}
+
+int sandy_hip_device_paged_pool_destroy(SandyHipDevice* d, uint32_t pool, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto it = d->impl.pools.find(pool);
+    if (it == d->impl.pools.end()) return fail(e, SANDY_ERR_INVALID, "hip device paged pool not found");
+    for (auto& t : d->impl.tensors)
+        if (t.second.pool == pool) return fail(e, SANDY_ERR_INVALID, "hip device paged pool still has tensors");
+    SANDY_HIP_TRY(hipStreamSynchronize(d->impl.stream), e, "hipStreamSynchronize");
+    hipFree(it->second->pages);
+    hipFree(it->second->table);
+    hipFree(it->second->lengths);
+    hipHostFree(it->second->host_table);
+    d->impl.pools.erase(it);
+    return ok(e);
+}
+
+int sandy_hip_device_paged_alloc(SandyHipDevice* d, uint32_t pool, uint32_t* tensor, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    if (d->impl.capturing) return fail(e, SANDY_ERR_INVALID, "%s is not allowed during graph capture", __func__);
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto it = d->impl.pools.find(pool);
+    if (it == d->impl.pools.end()) return fail(e, SANDY_ERR_INVALID, "hip device paged pool not found");
+    PagedPool& p = *it->second;
+    if (p.free_slots.empty()) return fail(e, SANDY_ERR_INVALID, "hip device paged pool has no free tensor slot");
+    PagedTensor t;
+    t.pool = pool;
+    t.slot = p.free_slots.back();
+    p.free_slots.pop_back();
+    SANDY_HIP_TRY(hipMemsetAsync(p.lengths + t.slot, 0, 4, d->impl.stream), e, "length reset");
+    const uint32_t id = d->impl.next_id++;
+    d->impl.tensors[id] = std::move(t);
+    *tensor = id;
+    return ok(e);
+}
+
+int sandy_hip_device_paged_dealloc(SandyHipDevice* d, uint32_t tensor, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    if (d->impl.capturing) return fail(e, SANDY_ERR_INVALID, "%s is not allowed during graph capture", __func__);
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto it = d->impl.tensors.find(tensor);
+    if (it == d->impl.tensors.end()) return fail(e, SANDY_ERR_INVALID, "hip device paged tensor not found");
+    PagedPool& p = *d->impl.pools.at(it->second.pool);
+    for (int32_t page : it->second.pages) p.free_pages.push_back(page);  // pages return to the free list
+    SANDY_HIP_TRY(hipMemsetAsync(p.table + it->second.slot * p.desc.max_blocks, 0xff,
+                                 static_cast<size_t>(p.desc.max_blocks) * 4, d->impl.stream), e, "block table reset");
+    p.free_slots.push_back(it->second.slot);
+    d->impl.tensors.erase(it);
+    return ok(e);
+}
+
+int sandy_hip_device_paged_reserve(SandyHipDevice* d, uint32_t tensor, int64_t page_count, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    if (d->impl.capturing) return fail(e, SANDY_ERR_INVALID, "%s is not allowed during graph capture", __func__);
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto it = d->impl.tensors.find(tensor);
+    if (it == d->impl.tensors.end()) return fail(e, SANDY_ERR_INVALID, "hip device paged tensor not found");
+    st = reserve(d->impl, it->second, page_count, e);
+    return st ? st : ok(e);
+}
+
+int sandy_hip_device_paged_append(SandyHipDevice* d, uint32_t tensor, const SandyTensor* chunk, char* err,
+                                  size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    if (d->impl.capturing) return fail(e, SANDY_ERR_INVALID, "%s is not allowed during graph capture", __func__);
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto it = d->impl.tensors.find(tensor);
+    if (it == d->impl.tensors.end()) return fail(e, SANDY_ERR_INVALID, "hip device paged tensor not found");
+    PagedTensor& t = it->second;
+    PagedPool& p = *d->impl.pools.at(t.pool);
+    if (!chunk || chunk->rank != p.desc.rank) return fail(e, SANDY_ERR_INVALID, "hip device paged append chunk rank mismatch");
+    for (int i = 0; i < p.desc.rank; i++)
+        if (i != p.desc.grow_dim && chunk->dims[i] != p.desc.dims[i])
+            return fail(e, SANDY_ERR_INVALID, "hip device paged append chunk shape mismatch");
+    if (chunk->dtype != p.desc.dtype) return fail(e, SANDY_ERR_INVALID, "hip device paged append dtype mismatch");
+    if (!contiguous(*chunk)) return fail(e, SANDY_ERR_INVALID, "hip device paged append requires a contiguous source view");
+    const int64_t chunk_len = chunk->dims[p.desc.grow_dim];
+    if (chunk_len <= 0) return fail(e, SANDY_ERR_INVALID, "hip device paged append grow dimension must be > 0");
+    const int64_t new_len = t.grow_length + chunk_len;
+    st = reserve(d->impl, t, (new_len + p.desc.page_size - 1) / p.desc.page_size, e);
+    if (st) return st;
+    const int64_t rows = p.prefix * chunk_len;
+    hipLaunchKernelGGL(paged_append_kernel, dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, d->impl.stream,
+                       static_cast<const char*>(base_ptr(*chunk)), p.pages, p.table + t.slot * p.desc.max_blocks,
+                       p.lengths + t.slot, t.grow_length, chunk_len, p.prefix, p.desc.page_size,
+                       static_cast<int64_t>(p.inner * p.elem), static_cast<int64_t>(p.page_elems * p.elem));
+    SANDY_HIP_TRY(hipGetLastError(), e, "paged append launch");
+    t.grow_length = new_len;
+    return ok(e);
+}
+
+int sandy_hip_device_paged_append_step(SandyHipDevice* d, uint32_t pool, const uint32_t* tensors, int32_t count,
+                                       const SandyTensor* rows, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto pit = d->impl.pools.find(pool);
+    if (pit == d->impl.pools.end()) return fail(e, SANDY_ERR_INVALID, "hip device paged pool not found");
+    PagedPool& p = *pit->second;
+    if (count <= 0 || count > kMaxStepTensors) return fail(e, SANDY_ERR_INVALID, "paged append step count out of range");
+    if (!rows || !contiguous(*rows) || rows->dtype != p.desc.dtype || numel(*rows) != count * p.prefix * p.inner)
+        return fail(e, SANDY_ERR_INVALID, "hip device paged append step rows shape mismatch");
+    uint32_t* errw = device_error_word(e, &st);
+    if (st) return st;
+    StepArgs args{};
+    for (int i = 0; i < count; i++) {
+        auto it = d->impl.tensors.find(tensors[i]);
+        if (it == d->impl.tensors.end() || it->second.pool != pool)
+            return fail(e, SANDY_ERR_INVALID, "hip device paged tensor not found");
+        PagedTensor& t = it->second;
+        // host bookkeeping advances in step with the device (graph replays: see paged_sync)
+        if (t.grow_length + 1 > static_cast<int64_t>(t.pages.size()) * p.desc.page_size && !d->impl.capturing) {
+            st = reserve(d->impl, t, (t.grow_length + p.desc.page_size) / p.desc.page_size, e);
+            if (st) return st;
+        }
+        t.grow_length += 1;
+        args.slots[i] = t.slot;
+    }
+    hipLaunchKernelGGL(paged_append_step_kernel, dim3(static_cast<unsigned>(count)), dim3(256), 0, d->impl.stream,
+                       static_cast<const char*>(base_ptr(*rows)), p.pages, p.table, p.lengths, p.desc.max_blocks,
+                       p.prefix, p.desc.page_size, static_cast<int64_t>(p.inner * p.elem),
+                       static_cast<int64_t>(p.page_elems * p.elem), errw, args);
+    SANDY_HIP_TRY(hipGetLastError(), e, "paged append step launch");
+    return ok(e);
+}
+
+int sandy_hip_device_paged_positions(SandyHipDevice* d, uint32_t pool, const uint32_t* tensors, int32_t count,
+                                     const SandyTensor* positions, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto pit = d->impl.pools.find(pool);
+    if (pit == d->impl.pools.end()) return fail(e, SANDY_ERR_INVALID, "hip device paged pool not found");
+    if (count <= 0 || count > kMaxStepTensors) return fail(e, SANDY_ERR_INVALID, "paged positions count out of range");
+    if (!positions || !is_index(positions->dtype) || numel(*positions) != count || !contiguous(*positions))
+        return fail(e, SANDY_ERR_INVALID, "paged positions output must be [count] i32 or i64");
+    StepArgs args{};
+    for (int i = 0; i < count; i++) {
+        auto it = d->impl.tensors.find(tensors[i]);
+        if (it == d->impl.tensors.end() || it->second.pool != pool)
+            return fail(e, SANDY_ERR_INVALID, "hip device paged tensor not found");
+        args.slots[i] = it->second.slot;
+    }
+    hipLaunchKernelGGL(paged_positions_kernel, dim3(static_cast<unsigned>((count + 255) / 256)), dim3(256), 0,
+                       d->impl.stream, pit->second->lengths, base_ptr(*positions), positions->dtype, count, args);
+    SANDY_HIP_TRY(hipGetLastError(), e, "paged positions launch");
+    return ok(e);
+}
+
+int sandy_hip_device_paged_meta(SandyHipDevice* d, uint32_t tensor, SandyPagedMeta* meta, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    if (!d || !meta) return fail(e, SANDY_ERR_INVALID, "paged meta arguments are null");
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto it = d->impl.tensors.find(tensor);
+    if (it == d->impl.tensors.end()) return fail(e, SANDY_ERR_INVALID, "hip device paged tensor not found");
+    const PagedTensor& t = it->second;
+    const PagedPool& p = *d->impl.pools.at(t.pool);
+    *meta = SandyPagedMeta{};
+    meta->pool = t.pool;
+    meta->dtype = p.desc.dtype;
+    meta->rank = p.desc.rank;
+    meta->slot = t.slot;
+    for (int i = 0; i < p.desc.rank; i++) meta->dims[i] = i == p.desc.grow_dim ? t.grow_length : p.desc.dims[i];
+    meta->grow_dim = p.desc.grow_dim;
+    meta->page_size = p.desc.page_size;
+    meta->grow_length = t.grow_length;
+    meta->page_count = static_cast<int64_t>(t.pages.size());
+    meta->page_element_count = p.page_elems;
+    return ok(e);
+}
+
+int sandy_hip_device_paged_read(SandyHipDevice* d, uint32_t tensor, void* host, uint64_t bytes, char* err,
+                                size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto it = d->impl.tensors.find(tensor);
+    if (it == d->impl.tensors.end()) return fail(e, SANDY_ERR_INVALID, "hip device paged tensor not found");
+    const PagedTensor& t = it->second;
+    const PagedPool& p = *d->impl.pools.at(t.pool);
+    const size_t row = static_cast<size_t>(p.inner) * p.elem;
+    const size_t need = static_cast<size_t>(p.prefix * t.grow_length) * row;
+    if (bytes < need) return fail(e, SANDY_ERR_INVALID, "hip device paged read buffer too small");
+    // CpuDevice.cpp:611-676: dense[prefix, grow, :] = page[prefix, grow % page_size, :]
+    char* out = static_cast<char*>(host);
+    SANDY_HIP_TRY(hipStreamSynchronize(d->impl.stream), e, "hipStreamSynchronize");
+    for (int64_t pr = 0; pr < p.prefix; pr++) {
+        for (int64_t g0 = 0; g0 < t.grow_length; g0 += p.desc.page_size) {
+            const int64_t n = std::min<int64_t>(p.desc.page_size, t.grow_length - g0);
+            const int32_t page = t.pages[static_cast<size_t>(g0 / p.desc.page_size)];
+            const char* src = p.pages + (static_cast<int64_t>(page) * p.page_elems + pr * p.desc.page_size * p.inner) * p.elem;
+            SANDY_HIP_TRY(hipMemcpy(out + (pr * t.grow_length + g0) * row, src, n * row, hipMemcpyDeviceToHost), e,
+                          "paged read");
+        }
+    }
+    return ok(e);
+}
+
+int sandy_hip_device_paged_views(SandyHipDevice* d, uint32_t pool, SandyPagedCache* cache, SandyTensor* block_table,
+                                 SandyTensor* lengths, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    if (!d) return fail(e, SANDY_ERR_INVALID, "hip device is null");
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto pit = d->impl.pools.find(pool);
+    if (pit == d->impl.pools.end()) return fail(e, SANDY_ERR_INVALID, "hip device paged pool not found");
+    const PagedPool& p = *pit->second;
+    if (cache) {
+        *cache = SandyPagedCache{};
+        cache->pool = p.pages;
+        cache->dtype = p.desc.dtype;
+        cache->page_size = p.desc.page_size;
+        cache->prefix = p.prefix;
+        cache->inner = p.inner;
+        cache->num_pages = p.capacity;
+    }
+    if (block_table) {
+        *block_table = SandyTensor{};
+        block_table->data = p.table;
+        block_table->dtype = SANDY_I32;
+        block_table->rank = 2;
+        block_table->dims[0] = p.desc.max_tensors;
+        block_table->dims[1] = p.desc.max_blocks;
+        block_table->strides[0] = p.desc.max_blocks;
+        block_table->strides[1] = 1;
+    }
+    if (lengths) {
+        *lengths = SandyTensor{};
+        lengths->data = p.lengths;
+        lengths->dtype = SANDY_I32;
+        lengths->rank = 1;
+        lengths->dims[0] = p.desc.max_tensors;
+        lengths->strides[0] = 1;
+    }
+    return ok(e);
+}
+
+int sandy_hip_device_paged_sync(SandyHipDevice* d, uint32_t pool, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto pit = d->impl.pools.find(pool);
+    if (pit == d->impl.pools.end()) return fail(e, SANDY_ERR_INVALID, "hip device paged pool not found");
+    PagedPool& p = *pit->second;
+    std::vector<int32_t> lens(static_cast<size_t>(p.desc.max_tensors));
+    SANDY_HIP_TRY(hipStreamSynchronize(d->impl.stream), e, "hipStreamSynchronize");
+    SANDY_HIP_TRY(hipMemcpy(lens.data(), p.lengths, lens.size() * 4, hipMemcpyDeviceToHost), e, "length read");
+    for (auto& t : d->impl.tensors)
+        if (t.second.pool == pool) t.second.grow_length = lens[static_cast<size_t>(t.second.slot)];
+    return ok(e);
+}
+
+int sandy_hip_device_graph_begin(SandyHipDevice* d, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    if (d->impl.capturing) return fail(e, SANDY_ERR_INVALID, "hip device is already capturing");
+    SANDY_HIP_TRY(hipStreamBeginCapture(d->impl.stream, hipStreamCaptureModeThreadLocal), e, "hipStreamBeginCapture");
+    d->impl.capturing = reinterpret_cast<hipGraph_t>(1);
+    return ok(e);
+}
+
+int sandy_hip_device_graph_end(SandyHipDevice* d, uint32_t* graph, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    if (!d->impl.capturing) return fail(e, SANDY_ERR_INVALID, "hip device is not capturing");
+    hipGraph_t g = nullptr;
+    d->impl.capturing = nullptr;
+    SANDY_HIP_TRY(hipStreamEndCapture(d->impl.stream, &g), e, "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    hipError_t rc = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (rc != hipSuccess) return fail(e, SANDY_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(rc));
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    const uint32_t id = d->impl.next_id++;
+    d->impl.graphs[id] = exec;
+    *graph = id;
+    return ok(e);
+}
+
+int sandy_hip_device_graph_launch(SandyHipDevice* d, uint32_t graph, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    auto it = d->impl.graphs.find(graph);
+    if (it == d->impl.graphs.end()) return fail(e, SANDY_ERR_INVALID, "hip device graph not found");
+    SANDY_HIP_TRY(hipGraphLaunch(it->second, d->impl.stream), e, "hipGraphLaunch");
+    return ok(e);
+}
+
+int sandy_hip_device_graph_destroy(SandyHipDevice* d, uint32_t graph, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    auto it = d->impl.graphs.find(graph);
+    if (it == d->impl.graphs.end()) return fail(e, SANDY_ERR_INVALID, "hip device graph not found");
+    SANDY_HIP_TRY(hipStreamSynchronize(d->impl.stream), e, "hipStreamSynchronize");
+    hipGraphExecDestroy(it->second);
+    d->impl.graphs.erase(it);
+    return ok(e);
+}
+
+} // extern "C"

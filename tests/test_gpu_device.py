@@ -1,0 +1,196 @@
+"""GPU tests of the device runtime (buffers, paged pools with device-side
+append, graph capture of a decode step) against the reference's CPU device
+semantics: CpuDevice::appendPaged / read(DevicePagedTensorView)
+(src/device/cpu/CpuDevice.cpp:465-676) and its validation errors."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import assert_close, from_f32, normal, rng, to_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture()
+def dev():
+    from sandyrt_amd.device import HipDevice
+    d = HipDevice(0)
+    yield d
+    d.close()
+
+
+def bf16_np(t):
+    return to_oracle(t)
+
+
+def test_buffers_roundtrip(dev):
+    from sandyrt_amd._lib import SandyError
+    a = np.arange(1000, dtype=np.float32)
+    b = dev.load(a)
+    assert np.frombuffer(dev.read(b, a.nbytes), np.float32).tolist() == a.tolist()
+    assert np.frombuffer(dev.read(b, 40, offset=400), np.float32).tolist() == a[100:110].tolist()
+    dev.dealloc(b)
+    with pytest.raises(SandyError, match="hip device buffer not found"):
+        dev.dealloc(b)
+
+
+def test_paged_pool_validation(dev):
+    from sandyrt_amd._lib import BF16, SandyError
+    with pytest.raises(SandyError, match="page_size must be a power of two"):
+        dev.create_paged_pool([1, 4, -1, 64], BF16, 2, 12)
+    with pytest.raises(SandyError, match="grow_dim out of range"):
+        dev.create_paged_pool([1, 4, -1, 64], BF16, 4, 16)
+    with pytest.raises(SandyError, match="non-grow dimensions must be static and positive"):
+        dev.create_paged_pool([1, 0, -1, 64], BF16, 2, 16)
+    pool = dev.create_paged_pool([1, 2, -1, 8], BF16, 2, 16, max_pages=2, max_tensors=4, max_blocks=8)
+    t = dev.alloc_paged(pool)
+    dev.append_paged(t, torch.zeros(1, 2, 32, 8, dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(SandyError, match="paged pool capacity exceeded"):
+        dev.append_paged(t, torch.zeros(1, 2, 1, 8, dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(SandyError, match="dtype mismatch"):
+        dev.append_paged(t, torch.zeros(1, 2, 1, 8, dtype=torch.float32, device="cuda"))
+
+
+def test_paged_append_and_read_match_cpu_semantics(dev):
+    """Chunks of any length appended to several tensors read back as the
+    concatenation along the grow dim (CpuDevice.cpp:465-554, 611-676)."""
+    from sandyrt_amd._lib import BF16
+    torch.cuda.synchronize()
+    pool = dev.create_paged_pool([1, 4, -1, 64], BF16, 2, 16, initial_pages=4, max_tensors=8, max_blocks=64)
+    r = rng(1)
+    tensors = [dev.alloc_paged(pool) for _ in range(3)]
+    want = {t: [] for t in tensors}
+    for step, lens in enumerate([(37, 1, 16), (1, 15, 1), (1, 1, 17), (40, 3, 1)]):
+        for t, n in zip(tensors, lens):
+            chunk = from_f32(normal(r, (1, 4, n, 64)), torch.bfloat16)
+            torch.cuda.synchronize()
+            dev.append_paged(t, chunk)
+            want[t].append(bf16_np(chunk))
+    dev.synchronize()
+    for t in tensors:
+        dense = np.concatenate(want[t], axis=2)
+        got = dev.read_paged(t, np.uint16)
+        assert got.shape == dense.shape
+        assert np.array_equal(got, dense)
+        m = dev.paged_meta(t)
+        assert m.grow_length == dense.shape[2] and m.page_count == (dense.shape[2] + 15) // 16
+    # freed pages are reused by the next tensor
+    dev.dealloc_paged(tensors[0])
+    t4 = dev.alloc_paged(pool)
+    chunk = from_f32(normal(r, (1, 4, 20, 64)), torch.bfloat16)
+    torch.cuda.synchronize()
+    dev.append_paged(t4, chunk)
+    assert np.array_equal(dev.read_paged(t4, np.uint16), bf16_np(chunk))
+
+
+def _decode_setup(dev, r, B, hq, hkv, D, ctx, P=16):
+    from sandyrt_amd._lib import BF16
+    kp = dev.create_paged_pool([1, hkv, -1, D], BF16, 2, P, max_tensors=B, max_blocks=256)
+    vp = dev.create_paged_pool([1, hkv, -1, D], BF16, 2, P, max_tensors=B, max_blocks=256)
+    ks = [dev.alloc_paged(kp) for _ in range(B)]
+    vs = [dev.alloc_paged(vp) for _ in range(B)]
+    dense_k, dense_v = [], []
+    for b in range(B):
+        k = from_f32(normal(r, (1, hkv, ctx[b], D)), torch.bfloat16)
+        v = from_f32(normal(r, (1, hkv, ctx[b], D)), torch.bfloat16)
+        torch.cuda.synchronize()
+        dev.append_paged(ks[b], k)
+        dev.append_paged(vs[b], v)
+        dense_k.append(bf16_np(k))
+        dense_v.append(bf16_np(v))
+    return kp, vp, ks, vs, dense_k, dense_v
+
+
+def _attend(dev, kp, vp, q, pos, out, B):
+    from sandyrt_amd import _lib
+    kc, table, _ = dev.paged_views(kp)
+    vc, _, _ = dev.paged_views(vp)
+    table.contents.dims[0] = B  # rows 0..B-1 are the tensors in allocation order
+    _lib.call("sandy_hip_paged_attention", _lib.desc(q), kc, vc, table, _lib.desc(pos), 0, 0.125, _lib.desc(out),
+              stream=dev.stream)
+
+
+def test_decode_step_append_positions_attention(dev, oracle):
+    """One decode step entirely on the device: append the new K/V row of every
+    sequence at its device-side length, derive positions, attend."""
+    r = rng(7)
+    B, hq, hkv, D = 4, 32, 4, 64
+    ctx = [1, 15, 16, 300]
+    kp, vp, ks, vs, dk, dv = _decode_setup(dev, r, B, hq, hkv, D, ctx)
+    newk = from_f32(normal(r, (B, hkv, 1, D)), torch.bfloat16)
+    newv = from_f32(normal(r, (B, hkv, 1, D)), torch.bfloat16)
+    q = from_f32(normal(r, (B, hq, 1, D)), torch.bfloat16)
+    pos = torch.zeros(B, dtype=torch.int32, device="cuda")
+    out = torch.empty_like(q)
+    torch.cuda.synchronize()
+    dev.append_step(kp, ks, newk)
+    dev.append_step(vp, vs, newv)
+    dev.positions(kp, ks, pos)
+    _attend(dev, kp, vp, q, pos, out, B)
+    dev.synchronize()
+    from sandyrt_amd import _lib
+    _lib.take_device_errors(stream=dev.stream)
+    assert pos.cpu().tolist() == [c for c in ctx]  # new length - 1
+    T = max(ctx) + 1
+    kd = np.zeros((B, hkv, T, D), np.uint16)
+    vd = np.zeros_like(kd)
+    for b in range(B):
+        kd[b, :, :ctx[b] + 1] = np.concatenate([dk[b][0], bf16_np(newk[b:b + 1])[0]], axis=1)
+        vd[b, :, :ctx[b] + 1] = np.concatenate([dv[b][0], bf16_np(newv[b:b + 1])[0]], axis=1)
+        assert np.array_equal(dev.read_paged(ks[b], np.uint16)[0], kd[b, :, :ctx[b] + 1])
+    want = oracle.attention(bf16_np(q), kd, vd, np.array(ctx, np.int64), 0, 0.125)
+    assert_close(out, want, torch.bfloat16, "device decode step")
+
+
+def test_graph_captured_decode_steps_match_eager(dev):
+    """A captured decode step (two appends, positions, attention) replayed
+    three times matches the same three steps run eagerly on a twin pool."""
+    r = rng(9)
+    B, hq, hkv, D = 3, 8, 2, 64
+    ctx = [5, 40, 100]
+    a = _decode_setup(dev, np.random.default_rng(1), B, hq, hkv, D, ctx)
+    b = _decode_setup(dev, np.random.default_rng(1), B, hq, hkv, D, ctx)
+    steps = 3
+    rows_k = [from_f32(normal(r, (B, hkv, 1, D)), torch.bfloat16) for _ in range(steps)]
+    rows_v = [from_f32(normal(r, (B, hkv, 1, D)), torch.bfloat16) for _ in range(steps)]
+    q = from_f32(normal(r, (B, hq, 1, D)), torch.bfloat16)
+    # graph inputs live in fixed buffers that are refilled between replays
+    gk = torch.empty_like(rows_k[0])
+    gv = torch.empty_like(rows_v[0])
+    pos_a = torch.zeros(B, dtype=torch.int32, device="cuda")
+    pos_b = torch.zeros(B, dtype=torch.int32, device="cuda")
+    out_a = torch.empty_like(q)
+    out_b = torch.empty_like(q)
+    for t in a[2] + a[3]:  # reserve pages for the captured steps
+        m = dev.paged_meta(t)
+        dev.reserve_paged(t, (m.grow_length + steps + 15) // 16)
+    # warm the attention workspace outside capture
+    dev.positions(a[0], a[2], pos_a)
+    _attend(dev, a[0], a[1], q, pos_a, out_a, B)
+    torch.cuda.synchronize()
+    dev.synchronize()
+    dev.graph_begin()
+    dev.append_step(a[0], a[2], gk)
+    dev.append_step(a[1], a[3], gv)
+    dev.positions(a[0], a[2], pos_a)
+    _attend(dev, a[0], a[1], q, pos_a, out_a, B)
+    graph = dev.graph_end()
+    for s in range(steps):
+        gk.copy_(rows_k[s])
+        gv.copy_(rows_v[s])
+        torch.cuda.synchronize()
+        dev.graph_launch(graph)
+        dev.synchronize()
+        got = out_a.clone()
+        dev.append_step(b[0], b[2], rows_k[s])
+        dev.append_step(b[1], b[3], rows_v[s])
+        dev.positions(b[0], b[2], pos_b)
+        _attend(dev, b[0], b[1], q, pos_b, out_b, B)
+        dev.synchronize()
+        assert torch.equal(got, out_b), f"replay {s} differs from eager"
+        assert torch.equal(pos_a, pos_b)
+    dev.paged_sync(a[0])
+    assert dev.paged_meta(a[2][2]).grow_length == ctx[2] + steps
+    dev.graph_destroy(graph)
