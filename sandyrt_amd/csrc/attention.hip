@@ -66,6 +66,8 @@ struct PagedArgs {
     float* ws_o;   // [B, Hq, max_splits, D]
     float* ws_ml;  // [B, Hq, max_splits, 2]
     uint32_t* errw;
+    uint32_t* counters;  // [B, Hkv] arrival counts of the fused merge
+    int32_t fused_merge;
 };
 
 __device__ __forceinline__ short4_t pack_p(const float (&p)[4]) {
@@ -118,12 +120,12 @@ __device__ __forceinline__ SplitRange split_range(const PagedArgs& a, int64_t po
 constexpr int kMaxSplitKeys = 2048;
 constexpr int kMaxSplitPages = kMaxSplitKeys / 16 + 2;
 
-template <int D, int NB>
+template <int D, int NB, int NT>
 __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     constexpr int kRow = 2 * D + 8;  // bytes per V row in LDS (8-byte pad: conflict-free transposed reads)
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar tile bookkeeping
     const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
     const int G = a.group;
 
@@ -213,20 +215,21 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
         }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        // branch-free update (keeps the load/wait schedule straight-line)
         const float m_new = fmaxf(m, mx);
-        if (m_new == -INFINITY) return;  // nothing visible yet: state unchanged
         float p[NB][4];
         float rs = 0.0f;
 #pragma unroll
         for (int n = 0; n < NB; n++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                p[n][i] = sv[n][i] == -INFINITY ? 0.0f : bf16_to_f32(f32_to_bf16(exp2f(sv[n][i] - m_new)));
+                const float e2 = exp2f(sv[n][i] - m_new);
+                p[n][i] = sv[n][i] == -INFINITY ? 0.0f : bf16_to_f32(f32_to_bf16(e2));
                 rs += p[n][i];
             }
         rs += __shfl_xor(rs, 16, 64);
         rs += __shfl_xor(rs, 32, 64);
-        const float alpha = m == -INFINITY ? 0.0f : exp2f(m - m_new);
+        const float alpha = m == -INFINITY ? (m_new == -INFINITY ? 1.0f : 0.0f) : exp2f(m - m_new);
         l = l * alpha + rs;
         m = m_new;
 #pragma unroll
@@ -270,18 +273,24 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
     auto load_batch = [&](TileRegs<D> (&buf)[NB], int it0) {
 #pragma unroll
         for (int n = 0; n < NB; n++) {
+            // unconditional: a tile past the split reads block 0 (blk -1) and is masked later
             const int64_t t = s_begin + 16 * wave + 64 * (it0 + n);
-            if (t < s_end) load_tile<D>(a, t, blk_of(it0 + n), kh, lane, buf[n]);
+            load_tile<D>(a, t, t < s_end ? blk_of(it0 + n) : -1, kh, lane, buf[n]);
         }
     };
-    const int my_tiles = static_cast<int>(max<int64_t>(0, (s_end - s_begin - 16 * wave + 63) / 64));
+    // NT tiles per wave, fully unrolled: every load is unconditional and every
+    // compute predicated, so the wait counts stay exact and the next batch's
+    // loads remain in flight while the current batch computes.
+    static_assert(NT % NB == 0, "tiles per wave must be a multiple of the batch");
     load_batch(bufA, 0);
-    for (int it = 0; it < my_tiles; it += 2 * NB) {
-        load_batch(bufB, it + NB);
+#pragma unroll
+    for (int it = 0; it < NT; it += 2 * NB) {
+        if (it + NB < NT) load_batch(bufB, it + NB);
         compute_batch(bufA, it);
-        if (it + NB >= my_tiles) break;
-        load_batch(bufA, it + 2 * NB);
-        compute_batch(bufB, it + NB);
+        if (it + NB < NT) {
+            if (it + 2 * NB < NT) load_batch(bufA, it + 2 * NB);
+            compute_batch(bufB, it + NB);
+        }
     }
 
     // ---- merge the 4 waves through LDS (reuses the V staging area)
@@ -317,13 +326,70 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
             }
         }
         const int h = kh * G + gg;
+        if (a.fused_merge && n_splits == 1) {
+            a.out[b * a.o_sb + h * a.o_sh + d] = f32_to_bf16(L > 0.0f ? O / L : 0.0f);
+            continue;
+        }
         const int64_t slot = (static_cast<int64_t>(b) * hq + h) * a.max_splits + split;
-        a.ws_o[slot * D + d] = O;
-        if (d == 0) {
-            a.ws_ml[slot * 2] = M;
-            a.ws_ml[slot * 2 + 1] = L;
+        if (a.fused_merge) {  // agent-coherent stores: visible to every XCD once complete
+            __hip_atomic_store(&a.ws_o[slot * D + d], O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (d == 0) {
+                __hip_atomic_store(&a.ws_ml[slot * 2], M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&a.ws_ml[slot * 2 + 1], L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        } else {
+            a.ws_o[slot * D + d] = O;
+            if (d == 0) {
+                a.ws_ml[slot * 2] = M;
+                a.ws_ml[slot * 2 + 1] = L;
+            }
         }
     }
+    if (!a.fused_merge || n_splits == 1) return;
+
+    // Fused merge: the partial stores above are agent-coherent; once they have
+    // completed, the last workgroup of this (sequence, kv head) to arrive reads
+    // every split's partial with agent-coherent loads and writes the output.
+    __shared__ int is_last;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(&a.counters[b * a.hkv + kh], 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        is_last = prev == static_cast<uint32_t>(n_splits - 1);
+    }
+    __syncthreads();
+    if (!is_last) return;
+    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
+        const int gg = idx / D, d = idx % D;
+        const int h = kh * G + gg;
+        const int64_t base = (static_cast<int64_t>(b) * hq + h) * a.max_splits;
+        float M = -INFINITY, L = 0.0f, O = 0.0f;
+        for (int s0 = 0; s0 < n_splits; s0 += 8) {
+            float ms[8], ls[8], os[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const bool in = s0 + u < n_splits;
+                const int64_t slot = base + (in ? s0 + u : 0);
+                ms[u] = in ? __hip_atomic_load(&a.ws_ml[slot * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
+                ls[u] = __hip_atomic_load(&a.ws_ml[slot * 2 + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                os[u] = __hip_atomic_load(&a.ws_o[slot * D + d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (ms[u] == -INFINITY) continue;
+                const float mn = fmaxf(M, ms[u]);
+                const float fo = M == -INFINITY ? 0.0f : exp2f(M - mn);
+                const float fs = exp2f(ms[u] - mn);
+                L = L * fo + ls[u] * fs;
+                O = O * fo + os[u] * fs;
+                M = mn;
+            }
+        }
+        a.out[b * a.o_sb + h * a.o_sh + d] = f32_to_bf16(L > 0.0f ? O / L : 0.0f);
+    }
+    if (threadIdx.x == 0)
+        __hip_atomic_store(&a.counters[b * a.hkv + kh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Combines the split partials of one (sequence, q head): log-sum-exp merge of
@@ -617,14 +683,13 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         a.group = static_cast<int32_t>(G);
         a.window = window;
         a.scale_log2 = sc * kLog2e;
-        // split size: ~4 workgroups per CU at the average context
-        const int nb = D == 64 ? (env_int("SANDY_PAGED_NB", 2) == 4 ? 4 : 2) : 1;
+        // split size = 64 keys x tiles per wave (NT); ~4 workgroups per CU at the average context
+        const int nb = D == 64 ? 2 : 1;
         const int64_t max_keys = max_blocks * P;
         int64_t split = env_int("SANDY_PAGED_SPLIT", 0);
         if (split <= 0) split = (max_keys * B * hkv) / 512;
-        split = std::min<int64_t>(kMaxSplitKeys, std::max<int64_t>(128, split));
-        split = (split + 64 * nb - 1) / (64 * nb) * (64 * nb);
-        if (split > kMaxSplitKeys) split = kMaxSplitKeys;
+        const int64_t nt = split <= 256 ? 4 : split <= 512 ? 8 : 16;
+        split = 64 * nt;
         a.split_keys = static_cast<int32_t>(split);
         a.max_splits = static_cast<int32_t>((max_keys + split - 1) / split);
         const size_t ws_o = static_cast<size_t>(B * hq * a.max_splits * D) * sizeof(float);
@@ -634,26 +699,32 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         a.ws_o = reinterpret_cast<float*>(ws);
         a.ws_ml = reinterpret_cast<float*>(ws + ws_o);
         a.errw = errw;
+        a.fused_merge = env_int("SANDY_PAGED_FUSED_MERGE", 0);
+        a.counters = static_cast<uint32_t*>(
+            device_counters(0, static_cast<size_t>(B * hkv) * sizeof(uint32_t), stream, e, &status));
+        if (status) return status;
         dim3 grid(static_cast<unsigned>(a.max_splits), static_cast<unsigned>(hkv), static_cast<unsigned>(B));
         const size_t lds_v = 4 * nb * 16 * (2 * D + 8);
         const size_t lds_r = (4 * G * D + 4 * G * 2) * sizeof(float);
         const size_t lds = std::max(lds_v, lds_r);
         dim3 mgrid(static_cast<unsigned>(hq), static_cast<unsigned>(B));
-        switch (D) {
-            case 64:
-                if (nb == 4) hipLaunchKernelGGL((paged_decode_mfma_kernel<64, 4>), grid, dim3(256), lds, stream, a);
-                else hipLaunchKernelGGL((paged_decode_mfma_kernel<64, 2>), grid, dim3(256), lds, stream, a);
-                hipLaunchKernelGGL(paged_decode_merge_kernel<64>, mgrid, dim3(64), 0, stream, a);
-                break;
-            case 128:
-                hipLaunchKernelGGL((paged_decode_mfma_kernel<128, 1>), grid, dim3(256), lds, stream, a);
-                hipLaunchKernelGGL(paged_decode_merge_kernel<128>, mgrid, dim3(64), 0, stream, a);
-                break;
-            default:
-                hipLaunchKernelGGL((paged_decode_mfma_kernel<256, 1>), grid, dim3(256), lds, stream, a);
-                hipLaunchKernelGGL(paged_decode_merge_kernel<256>, mgrid, dim3(64), 0, stream, a);
-                break;
+#define PD_LAUNCH(DD, NBB, NTT)                                                                          \
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<DD, NBB, NTT>), grid, dim3(256), lds, stream, a);        \
+    if (!a.fused_merge) hipLaunchKernelGGL(paged_decode_merge_kernel<DD>, mgrid, dim3(64), 0, stream, a)
+        if (D == 64) {
+            if (nt == 4) { PD_LAUNCH(64, 2, 4); }
+            else if (nt == 8) { PD_LAUNCH(64, 2, 8); }
+            else { PD_LAUNCH(64, 2, 16); }
+        } else if (D == 128) {
+            if (nt == 4) { PD_LAUNCH(128, 1, 4); }
+            else if (nt == 8) { PD_LAUNCH(128, 1, 8); }
+            else { PD_LAUNCH(128, 1, 16); }
+        } else {
+            if (nt == 4) { PD_LAUNCH(256, 1, 4); }
+            else if (nt == 8) { PD_LAUNCH(256, 1, 8); }
+            else { PD_LAUNCH(256, 1, 16); }
         }
+#undef PD_LAUNCH
         SANDY_HIP_TRY(hipGetLastError(), e, "paged attention launch");
         return ok(e);
     }

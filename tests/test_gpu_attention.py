@@ -184,10 +184,13 @@ def test_dense_attention_seeded_fuzz(ops, oracle):
         np.testing.assert_allclose(got.cpu().numpy(), want, atol=5e-4, err_msg=f"iteration {it}")
 
 
+@pytest.mark.parametrize("fused", ["0", "1"])
 @pytest.mark.parametrize("split", ["128", "512", "2048"])
-def test_paged_decode_split_sizes(ops, oracle, monkeypatch, split):
-    """Split partials merged by the merge kernel; repeated launches agree."""
+def test_paged_decode_split_sizes(ops, oracle, monkeypatch, split, fused):
+    """Split partials merged by the merge kernel or by the last workgroup of
+    each (sequence, kv head); repeated launches agree."""
     monkeypatch.setenv("SANDY_PAGED_SPLIT", split)
+    monkeypatch.setenv("SANDY_PAGED_FUSED_MERGE", fused)
     out1 = run_case(ops, oracle, 40, 5, 32, 4, 64, 16, [1, 300, 1500, 2049, 700], torch.bfloat16)
     out2 = run_case(ops, oracle, 40, 5, 32, 4, 64, 16, [1, 300, 1500, 2049, 700], torch.bfloat16)
     assert torch.equal(out1, out2)
