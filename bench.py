@@ -345,6 +345,19 @@ def cpu_baseline(host, bytes_per, n_tokens, n_seqs):
     }
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (FETCH_SIZE / WRITE_SIZE scaled by an identity copy), or None."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_bench_kernels.md")
+    if not os.path.exists(path):
+        return None
+    for row in open(path):
+        cells = [c.strip() for c in row.strip().strip("|").split("|")]
+        if len(cells) == 7 and cells[0] == kernel:
+            return int(cells[4])
+    return None
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -395,10 +408,7 @@ def main():
         bytes_per = {"add_rms_norm": 0}
     dominant = max(per_kernel_us, key=per_kernel_us.get)
     achieved = bytes_per[dominant] / (per_kernel_us[dominant] * 1e-6) / 1e9
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "hbm_traffic.json")
-    if os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get(dominant)
+    traffic = measured_traffic(dominant)
     kern = {n: {"us": round(per_kernel_us[n], 2), "bytes": bytes_per[n],
                 "gbs": round(bytes_per[n] / (per_kernel_us[n] * 1e-6) / 1e9, 1),
                 "frac": round(bytes_per[n] / (per_kernel_us[n] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)} for n in per_kernel_us}
