@@ -20,12 +20,16 @@
 //   - P^T leaves the S^T MFMA already in the B-operand layout of
 //     v_mfma_f32_16x16x16_bf16, and V tiles are transposed through LDS into A
 //     operands, so O^T += V^T P^T runs on MFMA with no register shuffles;
-//   - block ids, Q and the position are fetched together; each wave keeps
-//     two batches of tiles in flight (ping-pong) while computing;
-//   - the 4 waves merge in LDS and every split slot writes a (max, sum,
-//     O[D]) partial to a persistent workspace (empty slots write max = -inf);
-//     a small second kernel merges the slots (log-sum-exp) with one round of
-//     loads.  No host round trip and no allocation per call.
+//   - work units (sequence, split, kv head) are numbered over the active
+//     splits only, from a prefix scan of the positions, so workgroup ids --
+//     dealt round-robin to the 8 XCDs -- spread the real work evenly across
+//     XCDs and CUs whatever the context lengths; block ids and Q are then
+//     fetched together, and each wave keeps a ring of batches of tiles in
+//     flight while computing;
+//   - the 4 waves merge in LDS and every unit writes a (max, sum, O[D])
+//     partial to a persistent workspace; a small second kernel merges a
+//     sequence's splits (log-sum-exp), reading the position alongside the
+//     first partials.  No host round trip and no allocation per call.
 // The probabilities fed to the PV product are rounded to bf16 and the
 // normaliser sums those rounded values, so O / L stays a convex combination.
 #include "common.h"
@@ -66,8 +70,7 @@ struct PagedArgs {
     float* ws_o;   // [B, Hq, max_splits, D]
     float* ws_ml;  // [B, Hq, max_splits, 2]
     uint32_t* errw;
-    uint32_t* counters;  // [B, Hkv] arrival counts of the fused merge
-    int32_t fused_merge;
+    int32_t batch;
 };
 
 __device__ __forceinline__ short4_t pack_p(const float (&p)[4]) {
@@ -101,76 +104,131 @@ __device__ __forceinline__ void load_tile(const PagedArgs& a, int64_t t0, int32_
     }
 }
 
+// 32-bit load that the compiler keeps on the vector memory path (a plain
+// uniform load would become a scalar load, waited on together with the kernel
+// arguments before the loads that follow it are issued).
+__device__ __forceinline__ uint32_t load_u32_agent(const char* p) {
+    return __hip_atomic_load(reinterpret_cast<uint32_t*>(const_cast<char*>(p)), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Key range of one split of sequence b; shared by the attention and merge kernels.
 struct SplitRange {
     int64_t n_keys, min_key, key_begin;
     int n_splits;
 };
 
-__device__ __forceinline__ SplitRange split_range(const PagedArgs& a, int64_t pos) {
+__device__ __forceinline__ SplitRange split_range(const PagedArgs& a, int64_t pos, int split_keys) {
     SplitRange r;
     r.n_keys = min(pos + 1, a.max_blocks * static_cast<int64_t>(a.page_size));
     r.min_key = a.window > 0 ? max<int64_t>(0, pos + 1 - a.window) : 0;
     r.key_begin = (r.min_key >> 4) << 4;
     const int64_t span = max<int64_t>(0, r.n_keys - r.key_begin);
-    r.n_splits = max(1, static_cast<int>((span + a.split_keys - 1) / a.split_keys));
+    r.n_splits = max(1, static_cast<int>((span + split_keys - 1) / split_keys));
     return r;
 }
 
-constexpr int kMaxSplitKeys = 2048;
-constexpr int kMaxSplitPages = kMaxSplitKeys / 16 + 2;
 
-template <int D, int NB, int NT>
+
+// Position of sequence i as a 64-bit value in this lane (i must be < batch).
+__device__ __forceinline__ int64_t lane_position(const PagedArgs& a, int64_t i) {
+    const char* p = static_cast<const char*>(a.pos) + (a.pos_dt == SANDY_I32 ? 4 : 8) * i;
+    const uint32_t lo = load_u32_agent(p);
+    if (a.pos_dt == SANDY_I32) return static_cast<int32_t>(lo);
+    const uint32_t hi = load_u32_agent(p + 4);
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Work unit of one workgroup: (sequence, split, kv head).  The active units
+// (sequence b contributes hkv * n_splits(b), none when its position is
+// negative) are numbered in sequence order, and workgroup `lin` takes unit
+// `lin`; workgroups past the last unit have nothing to do.  Consecutive
+// workgroup ids are dealt round-robin to the 8 XCDs, so the active work
+// spreads evenly over XCDs and CUs whatever the context lengths are, and the
+// idle workgroups are the last ones dispatched.  Every wave computes the
+// same answer from the positions (a 64-lane prefix scan per 64 sequences).
+struct Unit {
+    int b, kh, split;
+    int64_t pos;
+    bool active;
+};
+
+__device__ __forceinline__ Unit find_unit(const PagedArgs& a, int lin, int split_keys, int lane) {
+    int base = 0;
+    for (int c0 = 0; c0 < a.batch; c0 += 64) {
+        const int bi = c0 + lane;
+        const int64_t p = lane_position(a, bi < a.batch ? bi : 0);
+        const bool live = bi < a.batch && p >= 0;
+        const int units = live ? a.hkv * split_range(a, p, split_keys).n_splits : 0;
+        int incl = units;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += t;
+        }
+        const int total = __builtin_amdgcn_readlane(incl, 63);
+        if (lin < base + total) {
+            const int bl = __builtin_ctzll(__ballot(lin < base + incl));
+            const int r = lin - base - __builtin_amdgcn_readlane(incl - units, bl);
+            Unit u;
+            u.b = c0 + bl;
+            u.split = r / a.hkv;
+            u.kh = r - u.split * a.hkv;
+            const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(p), bl);
+            const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(p) >> 32), bl);
+            u.pos = static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+            u.active = true;
+            return u;
+        }
+        base += total;
+    }
+    Unit u{};
+    u.active = false;
+    return u;
+}
+
+template <int D, int NB, int NT, int S>
 __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     constexpr int kRow = 2 * D + 8;  // bytes per V row in LDS (8-byte pad: conflict-free transposed reads)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar tile bookkeeping
-    const int split = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
     const int G = a.group;
 
     const int g = lane & 15;
     const int j = lane >> 4;
-    const int tiles_pw = a.split_keys >> 6;  // tiles per wave (<= 32)
+    constexpr int kSplit = 64 * NT;  // keys per split (the host passes split_keys == kSplit)
+    const int tiles_pw = NT;
 
-    // Issue the position, this wave's block ids and Q together.  With no
-    // sliding window the split starts at split * split_keys whatever the
-    // position, so the block-id loads need not wait for it.
-    const int64_t pos = load_index(a.pos, a.pos_dt, b);
-    int32_t blkv = -1;  // lane i: block id of this wave's tile i
-    auto load_ids = [&](int64_t sb) {
-        const int64_t t = sb + 16 * wave + 64 * lane;
+    const Unit unit = find_unit(a, blockIdx.x, kSplit, lane);
+    if (!unit.active) return;
+    const int b = unit.b, kh = unit.kh, split = unit.split;
+    const int64_t pos = unit.pos;
+    const SplitRange sr = split_range(a, pos, kSplit);
+    const int64_t min_key = sr.min_key;
+
+    // Issue this wave's block ids and Q together (branch-free vector loads).
+    // lane i: block id of this wave's tile i (valid where ids_in)
+    int32_t blkv;
+    bool ids_in;
+    {
+        const int64_t t = sr.key_begin + static_cast<int64_t>(split) * kSplit + 16 * wave + 64 * lane;
         const int64_t page = t >> a.log2_page;
-        blkv = (lane < tiles_pw && page < a.max_blocks) ? a.table[b * a.table_stride + page] : -1;
-    };
-    if (a.window == 0) load_ids(static_cast<int64_t>(split) * a.split_keys);
-    // Q^T as B operands: column g, d = 32 kk + 8 j .. + 7
+        ids_in = lane < tiles_pw && page < a.max_blocks;
+        blkv = a.table[b * a.table_stride + (ids_in ? page : 0)];  // max_blocks >= 1
+    }
+    // Q^T as B operands: column g, d = 32 kk + 8 j .. + 7.  Pad columns
+    // (g >= G) load head 0 again: every column is independent through the
+    // softmax and PV products, and pad columns are never stored.
     uint4 qv[D / 32];
-    if (g < G) {
-        const uint4* qp = reinterpret_cast<const uint4*>(a.q + b * a.q_sb + (kh * G + g) * a.q_sh + 8 * j);
+    {
+        const uint4* qp = reinterpret_cast<const uint4*>(a.q + b * a.q_sb + (kh * G + (g < G ? g : 0)) * a.q_sh + 8 * j);
 #pragma unroll
         for (int kk = 0; kk < D / 32; kk++) qv[kk] = qp[kk * 4];
-    } else {
-#pragma unroll
-        for (int kk = 0; kk < D / 32; kk++) qv[kk] = make_uint4(0, 0, 0, 0);
     }
-    if (pos < 0 && threadIdx.x == 0 && split == 0 && kh == 0)
-        atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
-    const SplitRange sr = split_range(a, pos);
-    const int n_splits = sr.n_splits;
-    const int64_t min_key = sr.min_key;
-    if (pos < 0 || split >= n_splits) {
-        // empty split slot: mark it so the merge needs no position
-        for (int gg = threadIdx.x; gg < G; gg += 256) {
-            const int64_t slot = (static_cast<int64_t>(b) * a.hq + kh * G + gg) * a.max_splits + split;
-            a.ws_ml[slot * 2] = -INFINITY;
-            a.ws_ml[slot * 2 + 1] = 0.0f;
-        }
-        return;
-    }
-    const int64_t s_begin = sr.key_begin + static_cast<int64_t>(split) * a.split_keys;
-    const int64_t s_end = min(sr.n_keys, s_begin + a.split_keys);
-    if (a.window != 0) load_ids(s_begin);
+    const int64_t s_begin = sr.key_begin + static_cast<int64_t>(split) * kSplit;
+    const int64_t s_end = min(sr.n_keys, s_begin + kSplit);
+    if (!ids_in) blkv = -1;
     {
         const int64_t t = s_begin + 16 * wave + 64 * lane;
         const bool used = lane < tiles_pw && t < s_end;
@@ -267,9 +325,11 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
         __builtin_amdgcn_wave_barrier();
     };
 
-    // Ping-pong batches of NB tiles: the next batch's loads are in flight
-    // while the current batch is computed.  Wave w owns tiles w, w+4, ...
-    TileRegs<D> bufA[NB], bufB[NB];
+    // A ring of S batches of NB tiles per wave: while batch i is computed the
+    // loads of batches i+1 .. i+S-1 are in flight (S * NB * 4 KB per wave at
+    // D = 64), which is what keeps HBM busy at the low wave counts of decode.
+    // Wave w owns tiles w, w+4, ...
+    TileRegs<D> ring[S][NB];
     auto load_batch = [&](TileRegs<D> (&buf)[NB], int it0) {
 #pragma unroll
         for (int n = 0; n < NB; n++) {
@@ -279,18 +339,17 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
         }
     };
     // NT tiles per wave, fully unrolled: every load is unconditional and every
-    // compute predicated, so the wait counts stay exact and the next batch's
+    // compute predicated, so the wait counts stay exact and the later batches'
     // loads remain in flight while the current batch computes.
     static_assert(NT % NB == 0, "tiles per wave must be a multiple of the batch");
-    load_batch(bufA, 0);
+    constexpr int kBatches = NT / NB;
 #pragma unroll
-    for (int it = 0; it < NT; it += 2 * NB) {
-        if (it + NB < NT) load_batch(bufB, it + NB);
-        compute_batch(bufA, it);
-        if (it + NB < NT) {
-            if (it + 2 * NB < NT) load_batch(bufA, it + 2 * NB);
-            compute_batch(bufB, it + NB);
-        }
+    for (int i = 0; i < S - 1; i++)
+        if (i < kBatches) load_batch(ring[i], i * NB);
+#pragma unroll
+    for (int i = 0; i < kBatches; i++) {
+        if (i + S - 1 < kBatches) load_batch(ring[(i + S - 1) % S], (i + S - 1) * NB);
+        compute_batch(ring[i % S], i * NB);
     }
 
     // ---- merge the 4 waves through LDS (reuses the V staging area)
@@ -326,98 +385,51 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
             }
         }
         const int h = kh * G + gg;
-        if (a.fused_merge && n_splits == 1) {
-            a.out[b * a.o_sb + h * a.o_sh + d] = f32_to_bf16(L > 0.0f ? O / L : 0.0f);
-            continue;
-        }
         const int64_t slot = (static_cast<int64_t>(b) * hq + h) * a.max_splits + split;
-        if (a.fused_merge) {  // agent-coherent stores: visible to every XCD once complete
-            __hip_atomic_store(&a.ws_o[slot * D + d], O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (d == 0) {
-                __hip_atomic_store(&a.ws_ml[slot * 2], M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(&a.ws_ml[slot * 2 + 1], L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        } else {
-            a.ws_o[slot * D + d] = O;
-            if (d == 0) {
-                a.ws_ml[slot * 2] = M;
-                a.ws_ml[slot * 2 + 1] = L;
-            }
+        a.ws_o[slot * D + d] = O;
+        if (d == 0) {
+            a.ws_ml[slot * 2] = M;
+            a.ws_ml[slot * 2 + 1] = L;
         }
     }
-    if (!a.fused_merge || n_splits == 1) return;
-
-    // Fused merge: the partial stores above are agent-coherent; once they have
-    // completed, the last workgroup of this (sequence, kv head) to arrive reads
-    // every split's partial with agent-coherent loads and writes the output.
-    __shared__ int is_last;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&a.counters[b * a.hkv + kh], 1u, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        is_last = prev == static_cast<uint32_t>(n_splits - 1);
-    }
-    __syncthreads();
-    if (!is_last) return;
-    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
-        const int gg = idx / D, d = idx % D;
-        const int h = kh * G + gg;
-        const int64_t base = (static_cast<int64_t>(b) * hq + h) * a.max_splits;
-        float M = -INFINITY, L = 0.0f, O = 0.0f;
-        for (int s0 = 0; s0 < n_splits; s0 += 8) {
-            float ms[8], ls[8], os[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const bool in = s0 + u < n_splits;
-                const int64_t slot = base + (in ? s0 + u : 0);
-                ms[u] = in ? __hip_atomic_load(&a.ws_ml[slot * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
-                ls[u] = __hip_atomic_load(&a.ws_ml[slot * 2 + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                os[u] = __hip_atomic_load(&a.ws_o[slot * D + d], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                if (ms[u] == -INFINITY) continue;
-                const float mn = fmaxf(M, ms[u]);
-                const float fo = M == -INFINITY ? 0.0f : exp2f(M - mn);
-                const float fs = exp2f(ms[u] - mn);
-                L = L * fo + ls[u] * fs;
-                O = O * fo + os[u] * fs;
-                M = mn;
-            }
-        }
-        a.out[b * a.o_sb + h * a.o_sh + d] = f32_to_bf16(L > 0.0f ? O / L : 0.0f);
-    }
-    if (threadIdx.x == 0)
-        __hip_atomic_store(&a.counters[b * a.hkv + kh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Combines the split partials of one (sequence, q head): log-sum-exp merge of
-// (max, sum, O[D]) over all max_splits slots (empty slots carry max = -inf),
-// every load issued at once -- one memory round trip, no position read.
+// (max, sum, O[D]) over the sequence's splits.  The position is loaded with
+// the first slots' partials (one memory round trip for up to 8 splits); slots
+// at or past the sequence's split count hold stale data and are skipped by
+// index, and a split whose keys were all masked carries max = -inf.
 template <int D>
 __global__ __launch_bounds__(64) void paged_decode_merge_kernel(PagedArgs a) {
     const int h = blockIdx.x, b = blockIdx.y;
     constexpr int PER = D / 64;  // head dims per thread
     const int64_t base = (static_cast<int64_t>(b) * a.hq + h) * a.max_splits;
+    const int64_t pos_v = lane_position(a, b);
     float M = -INFINITY, L = 0.0f, O[PER];
 #pragma unroll
     for (int i = 0; i < PER; i++) O[i] = 0.0f;
+    int n_splits = -1;  // known once the position has arrived
     for (int s0 = 0; s0 < a.max_splits; s0 += 8) {
         float ms[8], ls[8], os[8][PER];
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const bool in = s0 + u < a.max_splits;
-            const int64_t slot = base + (in ? s0 + u : 0);
+            const int64_t slot = base + (s0 + u < a.max_splits ? s0 + u : 0);
             const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + slot * 2);
-            ms[u] = in ? ml.x : -INFINITY;
+            ms[u] = ml.x;
             ls[u] = ml.y;
 #pragma unroll
             for (int i = 0; i < PER; i++) os[u][i] = a.ws_o[slot * D + threadIdx.x + 64 * i];
         }
+        if (n_splits < 0) {
+            const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(pos_v));
+            const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(pos_v) >> 32));
+            const int64_t pos = static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+            n_splits = pos < 0 ? 0 : split_range(a, pos, a.split_keys).n_splits;
+            if (pos < 0 && h == 0 && threadIdx.x == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
+        }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            if (ms[u] == -INFINITY) continue;  // empty slot: its O was never written
+            if (s0 + u >= n_splits || ms[u] == -INFINITY) continue;
             const float mn = fmaxf(M, ms[u]);
             const float fo = M == -INFINITY ? 0.0f : exp2f(M - mn);
             const float fs = exp2f(ms[u] - mn);
@@ -426,6 +438,7 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(PagedArgs a) {
             for (int i = 0; i < PER; i++) O[i] = O[i] * fo + os[u][i] * fs;
             M = mn;
         }
+        if (s0 + 8 >= n_splits) break;
     }
 #pragma unroll
     for (int i = 0; i < PER; i++)
@@ -656,6 +669,7 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
                            reinterpret_cast<uintptr_t>(vc->pool)) & 15u) == 0 &&
                          q->strides[0] % 8 == 0 && q->strides[1] % 8 == 0;
     const bool mfma = q->dtype == SANDY_BF16 && (D == 64 || D == 128 || D == 256) && G <= 16 && P % 16 == 0 &&
+                      table->dims[1] > 0 &&
                       aligned && env_int("SANDY_PAGED_GENERIC", 0) == 0;
     if (mfma) {
         PagedArgs a{};
@@ -683,11 +697,12 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         a.group = static_cast<int32_t>(G);
         a.window = window;
         a.scale_log2 = sc * kLog2e;
-        // split size = 64 keys x tiles per wave (NT); ~4 workgroups per CU at the average context
+        // split size = 64 keys x tiles per wave (NT): about 2048 work units at
+        // the longest context (~4-8 per CU once the active ones are dealt out)
         const int nb = D == 64 ? 2 : 1;
         const int64_t max_keys = max_blocks * P;
         int64_t split = env_int("SANDY_PAGED_SPLIT", 0);
-        if (split <= 0) split = (max_keys * B * hkv) / 512;
+        if (split <= 0) split = (max_keys * B * hkv) / 2048;
         const int64_t nt = split <= 256 ? 4 : split <= 512 ? 8 : 16;
         split = 64 * nt;
         a.split_keys = static_cast<int32_t>(split);
@@ -699,31 +714,35 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         a.ws_o = reinterpret_cast<float*>(ws);
         a.ws_ml = reinterpret_cast<float*>(ws + ws_o);
         a.errw = errw;
-        a.fused_merge = env_int("SANDY_PAGED_FUSED_MERGE", 0);
-        a.counters = static_cast<uint32_t*>(
-            device_counters(0, static_cast<size_t>(B * hkv) * sizeof(uint32_t), stream, e, &status));
-        if (status) return status;
-        dim3 grid(static_cast<unsigned>(a.max_splits), static_cast<unsigned>(hkv), static_cast<unsigned>(B));
+        a.batch = static_cast<int32_t>(B);
+        // one workgroup per possible (sequence, split, kv head); the active ones come first
+        dim3 grid(static_cast<unsigned>(a.max_splits * hkv * B));
         const size_t lds_v = 4 * nb * 16 * (2 * D + 8);
         const size_t lds_r = (4 * G * D + 4 * G * 2) * sizeof(float);
         const size_t lds = std::max(lds_v, lds_r);
         dim3 mgrid(static_cast<unsigned>(hq), static_cast<unsigned>(B));
-#define PD_LAUNCH(DD, NBB, NTT)                                                                          \
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<DD, NBB, NTT>), grid, dim3(256), lds, stream, a);        \
-    if (!a.fused_merge) hipLaunchKernelGGL(paged_decode_merge_kernel<DD>, mgrid, dim3(64), 0, stream, a)
-        if (D == 64) {
-            if (nt == 4) { PD_LAUNCH(64, 2, 4); }
-            else if (nt == 8) { PD_LAUNCH(64, 2, 8); }
-            else { PD_LAUNCH(64, 2, 16); }
-        } else if (D == 128) {
-            if (nt == 4) { PD_LAUNCH(128, 1, 4); }
-            else if (nt == 8) { PD_LAUNCH(128, 1, 8); }
-            else { PD_LAUNCH(128, 1, 16); }
-        } else {
-            if (nt == 4) { PD_LAUNCH(256, 1, 4); }
-            else if (nt == 8) { PD_LAUNCH(256, 1, 8); }
-            else { PD_LAUNCH(256, 1, 16); }
-        }
+        // ring depth: batches in flight per wave (bounded by the tile registers)
+        int stages = env_int("SANDY_PAGED_STAGES", 0);
+        if (stages <= 0) stages = 2;
+        stages = std::min(stages, D == 256 ? 3 : 4);
+#define PD_LAUNCH(DD, NBB, NTT, SS)                                                                      \
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<DD, NBB, NTT, SS>), grid, dim3(256), lds, stream, a)
+#define PD_STAGES(DD, NBB, NTT)                                \
+    if (stages <= 2) { PD_LAUNCH(DD, NBB, NTT, 2); }           \
+    else if (stages == 3 || DD == 256) { PD_LAUNCH(DD, NBB, NTT, 3); } \
+    else { PD_LAUNCH(DD, NBB, NTT, DD == 256 ? 3 : 4); }
+#define PD_SPLITS(DD, NBB)                                     \
+    if (nt == 4) { PD_STAGES(DD, NBB, 4) }                     \
+    else if (nt == 8) { PD_STAGES(DD, NBB, 8) }                \
+    else { PD_STAGES(DD, NBB, 16) }
+        if (D == 64) { PD_SPLITS(64, 2) }
+        else if (D == 128) { PD_SPLITS(128, 1) }
+        else { PD_SPLITS(256, 1) }
+        if (D == 64) hipLaunchKernelGGL(paged_decode_merge_kernel<64>, mgrid, dim3(64), 0, stream, a);
+        else if (D == 128) hipLaunchKernelGGL(paged_decode_merge_kernel<128>, mgrid, dim3(64), 0, stream, a);
+        else hipLaunchKernelGGL(paged_decode_merge_kernel<256>, mgrid, dim3(64), 0, stream, a);
+#undef PD_SPLITS
+#undef PD_STAGES
 #undef PD_LAUNCH
         SANDY_HIP_TRY(hipGetLastError(), e, "paged attention launch");
         return ok(e);

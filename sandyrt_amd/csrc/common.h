@@ -99,8 +99,6 @@ uint32_t* device_error_word(Err e, int* status);
 // need zeroed memory keep it zero themselves.
 void* device_workspace(int slot, size_t bytes, hipStream_t stream, Err e, int* status);
 
-// Zero-initialised companion area (counters); re-zeroed only when grown.
-void* device_counters(int slot, size_t bytes, hipStream_t stream, Err e, int* status);
 
 // ---------------------------------------------------------------- device helpers
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }

@@ -184,13 +184,34 @@ def test_dense_attention_seeded_fuzz(ops, oracle):
         np.testing.assert_allclose(got.cpu().numpy(), want, atol=5e-4, err_msg=f"iteration {it}")
 
 
-@pytest.mark.parametrize("fused", ["0", "1"])
+@pytest.mark.parametrize("stages", ["2", "3", "4"])
 @pytest.mark.parametrize("split", ["128", "512", "2048"])
-def test_paged_decode_split_sizes(ops, oracle, monkeypatch, split, fused):
-    """Split partials merged by the merge kernel or by the last workgroup of
-    each (sequence, kv head); repeated launches agree."""
+def test_paged_decode_split_sizes(ops, oracle, monkeypatch, split, stages):
+    """Every split size and load-ring depth merges to the oracle's result;
+    repeated launches agree bit for bit."""
     monkeypatch.setenv("SANDY_PAGED_SPLIT", split)
-    monkeypatch.setenv("SANDY_PAGED_FUSED_MERGE", fused)
+    monkeypatch.setenv("SANDY_PAGED_STAGES", stages)
     out1 = run_case(ops, oracle, 40, 5, 32, 4, 64, 16, [1, 300, 1500, 2049, 700], torch.bfloat16)
     out2 = run_case(ops, oracle, 40, 5, 32, 4, 64, 16, [1, 300, 1500, 2049, 700], torch.bfloat16)
     assert torch.equal(out1, out2)
+
+
+@pytest.mark.parametrize("pos_dtype", [torch.int32, torch.int64])
+def test_paged_decode_negative_position(ops, oracle, pos_dtype):
+    """A negative position raises the reference's error when the device
+    errors are read; the other sequences are still attended correctly and the
+    bad row comes out zero (it owns no work unit)."""
+    from sandyrt_amd._lib import SandyError
+    r = rng(91)
+    ctx = [100, 50, 700, 1]
+    q, kpool, vpool, table, pos = make_paged(r, 4, 8, 2, 64, 16, ctx, 80, torch.bfloat16)
+    bad = pos.copy()
+    bad[1] = -3
+    out = ops.paged_attention(q, ops.PagedCache(kpool), ops.PagedCache(vpool), torch.from_numpy(table).cuda(),
+                              torch.from_numpy(bad).to(pos_dtype).cuda(), window=0, scale=-1.0)
+    with pytest.raises(SandyError, match="attention position_offsets must be non-negative"):
+        ops.check_device_errors()
+    sel = np.array([0, 2, 3])
+    want = oracle_paged(oracle, q[sel], kpool, vpool, table[sel], pos[sel], 0, -1.0)
+    assert_close(out[sel], want, torch.bfloat16, "rows with valid positions")
+    assert torch.count_nonzero(out[1]).item() == 0
