@@ -13,8 +13,9 @@
 // address math and a cudaMallocAsync of the split partials on every call
 // (CudaAttentionKernels.cu:247-404,469-563).  Here one 256-thread workgroup
 // owns (split of keys, kv head, sequence) and the whole GQA group of q heads:
-//   - K tiles of 16 keys are read from their page with 128-bit loads straight
-//     into MFMA A operands; S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (the head
+//   - K tiles of 16 keys are read from their page with 128-bit buffer loads
+//     (a resource per tile; tiles past the unit get an empty range and
+//     cost no memory traffic) straight into MFMA A operands; S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (the head
 //     group padded to 16 columns);
 //   - online softmax in the exp2 domain, per q head (one MFMA column);
 //   - P^T leaves the S^T MFMA already in the B-operand layout of
@@ -26,10 +27,11 @@
 //     XCDs and CUs whatever the context lengths; block ids and Q are then
 //     fetched together, and each wave keeps a ring of batches of tiles in
 //     flight while computing;
-//   - the 4 waves merge in LDS and every unit writes a (max, sum, O[D])
-//     partial to a persistent workspace; a small second kernel merges a
-//     sequence's splits (log-sum-exp), reading the position alongside the
-//     first partials.  No host round trip and no allocation per call.
+//   - the 4 waves merge in LDS; a sequence of one split is written as final
+//     output, otherwise every unit writes a (max, sum, O[D]) partial to a
+//     persistent workspace and a small second kernel merges the sequence's
+//     splits (log-sum-exp), reading the position alongside the first
+//     partials.  No host round trip and no allocation per call.
 // The probabilities fed to the PV product are rounded to bf16 and the
 // normaliser sums those rounded values, so O / L stays a convex combination.
 #include "common.h"
@@ -63,14 +65,16 @@ struct PagedArgs {
     int32_t page_size;
     int32_t log2_page;
     int32_t hq, hkv, group;
+    int32_t batch;
     int64_t window;
     float scale_log2;  // scale * log2(e)
-    int32_t split_keys;
-    int32_t max_splits;
-    float* ws_o;   // [B, Hq, max_splits, D]
-    float* ws_ml;  // [B, Hq, max_splits, 2]
+    int32_t split_keys;  // split-unit schedule: keys per split
+    int32_t max_splits;  // split-unit schedule: slots per (sequence, q head)
+    // partial (O[D], max, sum) slots: [B, Hq, max_splits] for the split-unit
+    // schedule, [workgroups, 2, G] for the balanced one
+    float* ws_o;
+    float* ws_ml;
     uint32_t* errw;
-    int32_t batch;
 };
 
 __device__ __forceinline__ short4_t pack_p(const float (&p)[4]) {
@@ -86,137 +90,74 @@ struct TileRegs {
     uint4 v[D / 32];
 };
 
-// Loads one 16-key tile of K and V (this lane: key lane%16, 8 dims per MFMA
-// k-step) from block `blk` (already validated; -1 = skip).
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kBufferWord3 = 0x00020000;  // gfx9 buffer resource word 3: raw dword access
+
+// Loads one 16-key tile of K and V of kv head kh from block `blk` (this
+// lane: key lane%16, 8 dims per MFMA k-step) through buffer resources that
+// span exactly the tile.  blk < 0 gives an empty range: the loads return
+// zeros without touching memory, so tiles past a piece cost no bandwidth and
+// every load can stay unconditional.
 template <int D>
-__device__ __forceinline__ void load_tile(const PagedArgs& a, int64_t t0, int32_t blk, int kh, int lane,
+__device__ __forceinline__ void load_tile(const PagedArgs& a, int32_t blk, int64_t in_page, int kh, int lane,
                                           TileRegs<D>& r) {
-    const int64_t safe = blk < 0 ? 0 : blk;
-    const int64_t in_page = t0 & (a.page_size - 1);
-    const int64_t row = safe * a.page_elems + static_cast<int64_t>(kh) * a.page_size * D +
-                        (in_page + (lane & 15)) * D + 8 * (lane >> 4);
-    const uint4* kp = reinterpret_cast<const uint4*>(a.k_pool + row);
-    const uint4* vp = reinterpret_cast<const uint4*>(a.v_pool + row);
+    const int64_t off = blk < 0 ? 0 : static_cast<int64_t>(blk) * a.page_elems + (static_cast<int64_t>(kh) * a.page_size + in_page) * D;
+    const int bytes = blk < 0 ? 0 : 32 * D;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.k_pool + off), 0, bytes, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.v_pool + off), 0, bytes, kBufferWord3);
+    const int voff = ((lane & 15) * D + 8 * (lane >> 4)) * 2;
 #pragma unroll
     for (int kk = 0; kk < D / 32; kk++) {
-        r.k[kk] = kp[kk * 4];  // + 32 elements per step
-        r.v[kk] = vp[kk * 4];
+        r.k[kk] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, voff + 64 * kk, 0, 0));
+        r.v[kk] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, voff + 64 * kk, 0, 0));
     }
 }
 
-// 32-bit load that the compiler keeps on the vector memory path (a plain
-// uniform load would become a scalar load, waited on together with the kernel
-// arguments before the loads that follow it are issued).
-__device__ __forceinline__ uint32_t load_u32_agent(const char* p) {
-    return __hip_atomic_load(reinterpret_cast<uint32_t*>(const_cast<char*>(p)), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Key range of one split of sequence b; shared by the attention and merge kernels.
+// Keys of sequence b: [key_begin, n_keys) in 16-key tiles from key_begin
+// (min_key is the first unmasked key under a sliding window).
 struct SplitRange {
     int64_t n_keys, min_key, key_begin;
-    int n_splits;
+    int n_tiles;
 };
 
-__device__ __forceinline__ SplitRange split_range(const PagedArgs& a, int64_t pos, int split_keys) {
+__device__ __forceinline__ SplitRange seq_range(const PagedArgs& a, int64_t pos) {
     SplitRange r;
     r.n_keys = min(pos + 1, a.max_blocks * static_cast<int64_t>(a.page_size));
     r.min_key = a.window > 0 ? max<int64_t>(0, pos + 1 - a.window) : 0;
     r.key_begin = (r.min_key >> 4) << 4;
     const int64_t span = max<int64_t>(0, r.n_keys - r.key_begin);
-    r.n_splits = max(1, static_cast<int>((span + split_keys - 1) / split_keys));
+    r.n_tiles = static_cast<int>((span + 15) >> 4);
     return r;
 }
 
-
-
 // Position of sequence i as a 64-bit value in this lane (i must be < batch).
+// Plain loads: positions are read-only here and stay in L2.
 __device__ __forceinline__ int64_t lane_position(const PagedArgs& a, int64_t i) {
-    const char* p = static_cast<const char*>(a.pos) + (a.pos_dt == SANDY_I32 ? 4 : 8) * i;
-    const uint32_t lo = load_u32_agent(p);
-    if (a.pos_dt == SANDY_I32) return static_cast<int32_t>(lo);
-    const uint32_t hi = load_u32_agent(p + 4);
+    return a.pos_dt == SANDY_I32 ? static_cast<int64_t>(static_cast<const int32_t*>(a.pos)[i])
+                                 : static_cast<const int64_t*>(a.pos)[i];
+}
+
+__device__ __forceinline__ int64_t lane_read64(int64_t v, int l) {
+    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(v), l);
+    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32), l);
     return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-// Work unit of one workgroup: (sequence, split, kv head).  The active units
-// (sequence b contributes hkv * n_splits(b), none when its position is
-// negative) are numbered in sequence order, and workgroup `lin` takes unit
-// `lin`; workgroups past the last unit have nothing to do.  Consecutive
-// workgroup ids are dealt round-robin to the 8 XCDs, so the active work
-// spreads evenly over XCDs and CUs whatever the context lengths are, and the
-// idle workgroups are the last ones dispatched.  Every wave computes the
-// same answer from the positions (a 64-lane prefix scan per 64 sequences).
-struct Unit {
-    int b, kh, split;
-    int64_t pos;
-    bool active;
-};
-
-__device__ __forceinline__ Unit find_unit(const PagedArgs& a, int lin, int split_keys, int lane) {
-    int base = 0;
-    for (int c0 = 0; c0 < a.batch; c0 += 64) {
-        const int bi = c0 + lane;
-        const int64_t p = lane_position(a, bi < a.batch ? bi : 0);
-        const bool live = bi < a.batch && p >= 0;
-        const int units = live ? a.hkv * split_range(a, p, split_keys).n_splits : 0;
-        int incl = units;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int t = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += t;
-        }
-        const int total = __builtin_amdgcn_readlane(incl, 63);
-        if (lin < base + total) {
-            const int bl = __builtin_ctzll(__ballot(lin < base + incl));
-            const int r = lin - base - __builtin_amdgcn_readlane(incl - units, bl);
-            Unit u;
-            u.b = c0 + bl;
-            u.split = r / a.hkv;
-            u.kh = r - u.split * a.hkv;
-            const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(p), bl);
-            const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(p) >> 32), bl);
-            u.pos = static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-            u.active = true;
-            return u;
-        }
-        base += total;
-    }
-    Unit u{};
-    u.active = false;
-    return u;
-}
-
+// One piece of work: tiles [tile_a, tile_b) of (sequence b, kv head kh) for
+// the whole GQA group, at most 4 * NT tiles.  The 4 waves take tiles tile_a + wave + 4i; each keeps
+// a ring of S batches of NB tiles in flight while it computes (S*NB*4 KB per
+// wave at D = 64), with S^T = K Q^T and O^T += V^T P^T on MFMA and the online
+// softmax in the exp2 domain.  The waves merge through LDS and the piece ends
+// as the final output rows (final_out) or as partial slots slot0 + g*stride.
 template <int D, int NB, int NT, int S>
-__global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+__device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* smem, int lane, int wave, int b,
+                                             int kh, const SplitRange& sr, int64_t tile_a, int64_t tile_b,
+                                             bool final_out, int64_t slot0, int64_t slot_stride) {
     constexpr int kRow = 2 * D + 8;  // bytes per V row in LDS (8-byte pad: conflict-free transposed reads)
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar tile bookkeeping
     const int G = a.group;
-
     const int g = lane & 15;
     const int j = lane >> 4;
-    constexpr int kSplit = 64 * NT;  // keys per split (the host passes split_keys == kSplit)
-    const int tiles_pw = NT;
 
-    const Unit unit = find_unit(a, blockIdx.x, kSplit, lane);
-    if (!unit.active) return;
-    const int b = unit.b, kh = unit.kh, split = unit.split;
-    const int64_t pos = unit.pos;
-    const SplitRange sr = split_range(a, pos, kSplit);
-    const int64_t min_key = sr.min_key;
-
-    // Issue this wave's block ids and Q together (branch-free vector loads).
-    // lane i: block id of this wave's tile i (valid where ids_in)
-    int32_t blkv;
-    bool ids_in;
-    {
-        const int64_t t = sr.key_begin + static_cast<int64_t>(split) * kSplit + 16 * wave + 64 * lane;
-        const int64_t page = t >> a.log2_page;
-        ids_in = lane < tiles_pw && page < a.max_blocks;
-        blkv = a.table[b * a.table_stride + (ids_in ? page : 0)];  // max_blocks >= 1
-    }
     // Q^T as B operands: column g, d = 32 kk + 8 j .. + 7.  Pad columns
     // (g >= G) load head 0 again: every column is independent through the
     // softmax and PV products, and pad columns are never stored.
@@ -226,136 +167,134 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
 #pragma unroll
         for (int kk = 0; kk < D / 32; kk++) qv[kk] = qp[kk * 4];
     }
-    const int64_t s_begin = sr.key_begin + static_cast<int64_t>(split) * kSplit;
-    const int64_t s_end = min(sr.n_keys, s_begin + kSplit);
-    if (!ids_in) blkv = -1;
-    {
-        const int64_t t = s_begin + 16 * wave + 64 * lane;
-        const bool used = lane < tiles_pw && t < s_end;
-        const bool ok = blkv >= 0 && blkv < a.num_pages;
-        if (used && !ok) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
-        if (!ok) blkv = -1;
-    }
-    auto blk_of = [&](int it) -> int32_t { return __builtin_amdgcn_readlane(blkv, it); };
 
     float m = -INFINITY, l = 0.0f;
     f32x4_t acc[D / 16];
 #pragma unroll
     for (int t = 0; t < D / 16; t++) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
     unsigned char* vl = smem + wave * NB * 16 * kRow;  // this wave's V tiles
 
-    // A batch of NB 16-key tiles: S^T on MFMA, one online-softmax update for
-    // the whole batch (one cross-lane max and sum), V^T through LDS, PV on MFMA.
-    auto compute_batch = [&](const TileRegs<D> (&buf)[NB], int it0) {
-        const int64_t tb = s_begin + 16 * wave + 64 * it0;
-        bool live_n[NB];
-#pragma unroll
-        for (int n = 0; n < NB; n++) live_n[n] = tb + 64 * n < s_end && blk_of(it0 + n) >= 0;
-        float sv[NB][4];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int n = 0; n < NB; n++) {
-            const int64_t t0 = tb + 64 * n;
-            const bool live = live_n[n];
-            f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kk = 0; kk < D / 32; kk++)
-                sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, buf[n].k[kk]),
-                                                             __builtin_bit_cast(bf16x8_t, qv[kk]), sc, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int64_t key = t0 + 4 * j + i;
-                const bool valid = live && key < s_end && key >= min_key;
-                sv[n][i] = valid ? sc[i] * a.scale_log2 : -INFINITY;
-                mx = fmaxf(mx, sv[n][i]);
-            }
+    {
+        const int64_t c0 = tile_a;  // tile_b - tile_a <= 4 * NT: one pass of the ring
+        // lane i: block id of this wave's tile i (-1: none / invalid)
+        int32_t blkv;
+        {
+            const int64_t tile = c0 + wave + 4 * lane;
+            const int64_t page = (sr.key_begin + 16 * tile) >> a.log2_page;
+            const bool in = lane < NT && tile < tile_b && page < a.max_blocks;
+            const int32_t id = a.table[b * a.table_stride + (in ? page : 0)];  // max_blocks >= 1
+            const bool ok = id >= 0 && id < a.num_pages;
+            if (in && !ok) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
+            blkv = in && ok ? id : -1;
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        // branch-free update (keeps the load/wait schedule straight-line)
-        const float m_new = fmaxf(m, mx);
-        float p[NB][4];
-        float rs = 0.0f;
-#pragma unroll
-        for (int n = 0; n < NB; n++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float e2 = exp2f(sv[n][i] - m_new);
-                p[n][i] = sv[n][i] == -INFINITY ? 0.0f : bf16_to_f32(f32_to_bf16(e2));
-                rs += p[n][i];
-            }
-        rs += __shfl_xor(rs, 16, 64);
-        rs += __shfl_xor(rs, 32, 64);
-        const float alpha = m == -INFINITY ? (m_new == -INFINITY ? 1.0f : 0.0f) : exp2f(m - m_new);
-        l = l * alpha + rs;
-        m = m_new;
-#pragma unroll
-        for (int t = 0; t < D / 16; t++) acc[t] *= alpha;
+        auto blk_of = [&](int it) -> int32_t { return __builtin_amdgcn_readlane(blkv, it); };
+        auto key0_of = [&](int it) -> int64_t { return sr.key_begin + 16 * (c0 + wave + 4 * it); };
 
-        // V tiles -> LDS (row = key; masked keys zeroed so they cannot inject NaN)
+        // A batch of NB tiles: S^T on MFMA, one online-softmax update for the
+        // whole batch (one cross-lane max and sum), V^T through LDS, PV on MFMA.
+        auto compute_batch = [&](const TileRegs<D> (&buf)[NB], int it0) {
+            bool live_n[NB];
+            bool any = false;
 #pragma unroll
-        for (int n = 0; n < NB; n++) {
-            const int64_t t0 = tb + 64 * n;
-            const bool live = live_n[n];
-            const int64_t vkey = t0 + (lane & 15);
-            const bool vvalid = live && vkey < s_end && vkey >= min_key;
-            unsigned char* row = vl + (n * 16 + (lane & 15)) * kRow + 16 * j;
-#pragma unroll
-            for (int kk = 0; kk < D / 32; kk++) {
-                uint4 v = vvalid ? buf[n].v[kk] : make_uint4(0, 0, 0, 0);
-                uint2* dst = reinterpret_cast<uint2*>(row + 64 * kk);
-                dst[0] = make_uint2(v.x, v.y);
-                dst[1] = make_uint2(v.z, v.w);
+            for (int n = 0; n < NB; n++) {
+                live_n[n] = blk_of(it0 + n) >= 0;
+                any = any || live_n[n];
             }
-        }
-        __builtin_amdgcn_wave_barrier();
+            if (!any) return;  // wave-uniform
+            float sv[NB][4];
+            float mx = -INFINITY;
 #pragma unroll
-        for (int n = 0; n < NB; n++) {
-            const short4_t pb = pack_p(p[n]);
+            for (int n = 0; n < NB; n++) {
+                const int64_t t0 = key0_of(it0 + n);
+                f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int t = 0; t < D / 16; t++) {
-                short4_t va;
-                const unsigned char* col = vl + n * 16 * kRow + 2 * (16 * t + (lane & 15));
+                for (int kk = 0; kk < D / 32; kk++)
+                    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, buf[n].k[kk]),
+                                                                 __builtin_bit_cast(bf16x8_t, qv[kk]), sc, 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 4; i++) va[i] = *reinterpret_cast<const short*>(col + (4 * j + i) * kRow);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, acc[t], 0, 0, 0);
+                for (int i = 0; i < 4; i++) {
+                    const int64_t key = t0 + 4 * j + i;
+                    const bool valid = live_n[n] && key < sr.n_keys && key >= sr.min_key;
+                    sv[n][i] = valid ? sc[i] * a.scale_log2 : -INFINITY;
+                    mx = fmaxf(mx, sv[n][i]);
+                }
             }
-        }
-        __builtin_amdgcn_wave_barrier();
-    };
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float m_new = fmaxf(m, mx);
+            float p[NB][4];
+            float rs = 0.0f;
+#pragma unroll
+            for (int n = 0; n < NB; n++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float e2 = exp2f(sv[n][i] - m_new);
+                    p[n][i] = sv[n][i] == -INFINITY ? 0.0f : bf16_to_f32(f32_to_bf16(e2));
+                    rs += p[n][i];
+                }
+            rs += __shfl_xor(rs, 16, 64);
+            rs += __shfl_xor(rs, 32, 64);
+            const float alpha = m == -INFINITY ? (m_new == -INFINITY ? 1.0f : 0.0f) : exp2f(m - m_new);
+            l = l * alpha + rs;
+            m = m_new;
+#pragma unroll
+            for (int t = 0; t < D / 16; t++) acc[t] *= alpha;
 
-    // A ring of S batches of NB tiles per wave: while batch i is computed the
-    // loads of batches i+1 .. i+S-1 are in flight (S * NB * 4 KB per wave at
-    // D = 64), which is what keeps HBM busy at the low wave counts of decode.
-    // Wave w owns tiles w, w+4, ...
-    TileRegs<D> ring[S][NB];
-    auto load_batch = [&](TileRegs<D> (&buf)[NB], int it0) {
+            // V tiles -> LDS (row = key; masked keys zeroed so they cannot inject NaN)
 #pragma unroll
-        for (int n = 0; n < NB; n++) {
-            // unconditional: a tile past the split reads block 0 (blk -1) and is masked later
-            const int64_t t = s_begin + 16 * wave + 64 * (it0 + n);
-            load_tile<D>(a, t, t < s_end ? blk_of(it0 + n) : -1, kh, lane, buf[n]);
+            for (int n = 0; n < NB; n++) {
+                const int64_t vkey = key0_of(it0 + n) + (lane & 15);
+                const bool vvalid = live_n[n] && vkey < sr.n_keys && vkey >= sr.min_key;
+                unsigned char* row = vl + (n * 16 + (lane & 15)) * kRow + 16 * j;
+#pragma unroll
+                for (int kk = 0; kk < D / 32; kk++) {
+                    uint4 v = vvalid ? buf[n].v[kk] : make_uint4(0, 0, 0, 0);
+                    uint2* dst = reinterpret_cast<uint2*>(row + 64 * kk);
+                    dst[0] = make_uint2(v.x, v.y);
+                    dst[1] = make_uint2(v.z, v.w);
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int n = 0; n < NB; n++) {
+                const short4_t pb = pack_p(p[n]);
+#pragma unroll
+                for (int t = 0; t < D / 16; t++) {
+                    short4_t va;
+                    const unsigned char* col = vl + n * 16 * kRow + 2 * (16 * t + (lane & 15));
+#pragma unroll
+                    for (int i = 0; i < 4; i++) va[i] = *reinterpret_cast<const short*>(col + (4 * j + i) * kRow);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, acc[t], 0, 0, 0);
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        };
+
+        TileRegs<D> ring[S][NB];
+        auto load_batch = [&](TileRegs<D> (&buf)[NB], int it0) {
+#pragma unroll
+            for (int n = 0; n < NB; n++)
+                load_tile<D>(a, blk_of(it0 + n), key0_of(it0 + n) & (a.page_size - 1), kh, lane, buf[n]);
+        };
+        // NT tiles per wave, fully unrolled: every load is unconditional (empty
+        // ranges past the piece), so the wait counts stay exact and the later
+        // batches' loads remain in flight while the current batch computes.
+        static_assert(NT % NB == 0, "tiles per wave must be a multiple of the batch");
+        constexpr int kBatches = NT / NB;
+#pragma unroll
+        for (int i = 0; i < S - 1; i++)
+            if (i < kBatches) load_batch(ring[i], i * NB);
+#pragma unroll
+        for (int i = 0; i < kBatches; i++) {
+            if (i + S - 1 < kBatches) load_batch(ring[(i + S - 1) % S], (i + S - 1) * NB);
+            compute_batch(ring[i % S], i * NB);
         }
-    };
-    // NT tiles per wave, fully unrolled: every load is unconditional and every
-    // compute predicated, so the wait counts stay exact and the later batches'
-    // loads remain in flight while the current batch computes.
-    static_assert(NT % NB == 0, "tiles per wave must be a multiple of the batch");
-    constexpr int kBatches = NT / NB;
-#pragma unroll
-    for (int i = 0; i < S - 1; i++)
-        if (i < kBatches) load_batch(ring[i], i * NB);
-#pragma unroll
-    for (int i = 0; i < kBatches; i++) {
-        if (i + S - 1 < kBatches) load_batch(ring[(i + S - 1) % S], (i + S - 1) * NB);
-        compute_batch(ring[i % S], i * NB);
     }
 
     // ---- merge the 4 waves through LDS (reuses the V staging area)
     __syncthreads();
-    float* red = reinterpret_cast<float*>(smem);   // [4][G][D]
-    float* ml = red + 4 * G * D;                    // [4][G][2]
+    float* red = reinterpret_cast<float*>(smem);  // [4][G][D]
+    float* ml = red + 4 * G * D;                   // [4][G][2]
     if (g < G) {
 #pragma unroll
         for (int t = 0; t < D / 16; t++)
@@ -367,7 +306,6 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
         }
     }
     __syncthreads();
-    const int hq = a.hq;
     for (int idx = threadIdx.x; idx < G * D; idx += 256) {
         const int gg = idx / D, d = idx % D;
         float M = -INFINITY;
@@ -384,27 +322,101 @@ __global__ __launch_bounds__(256) void paged_decode_mfma_kernel(PagedArgs a) {
                 L += ml[(w * G + gg) * 2 + 1] * f;
             }
         }
-        const int h = kh * G + gg;
-        const int64_t slot = (static_cast<int64_t>(b) * hq + h) * a.max_splits + split;
-        a.ws_o[slot * D + d] = O;
-        if (d == 0) {
-            a.ws_ml[slot * 2] = M;
-            a.ws_ml[slot * 2 + 1] = L;
+        if (final_out) {
+            a.out[b * a.o_sb + (kh * G + gg) * a.o_sh + d] = f32_to_bf16(L > 0.0f ? O / L : 0.0f);
+        } else {
+            const int64_t slot = slot0 + gg * slot_stride;
+            a.ws_o[slot * D + d] = O;
+            if (d == 0) {
+                a.ws_ml[slot * 2] = M;
+                a.ws_ml[slot * 2 + 1] = L;
+            }
         }
     }
+    __syncthreads();  // the next piece reuses the LDS
 }
 
-// Combines the split partials of one (sequence, q head): log-sum-exp merge of
-// (max, sum, O[D]) over the sequence's splits.  The position is loaded with
-// the first slots' partials (one memory round trip for up to 8 splits); slots
-// at or past the sequence's split count hold stale data and are skipped by
-// index, and a split whose keys were all masked carries max = -inf.
+// Writes zeros for sequence b's rows (negative position) and raises the flag.
 template <int D>
-__global__ __launch_bounds__(64) void paged_decode_merge_kernel(PagedArgs a) {
+__device__ __forceinline__ void zero_rows(const PagedArgs& a, int b, int h) {
+    for (int d = threadIdx.x; d < D; d += blockDim.x) a.out[b * a.o_sb + h * a.o_sh + d] = 0;
+    if (h == 0 && threadIdx.x == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
+}
+
+// ------------------------------------------------ split-unit schedule (any B)
+// Work units (sequence, split of 64*NT keys, kv head) are numbered over the
+// active splits only (a prefix scan of the positions, 64 sequences at a
+// time) and workgroup `lin` takes unit `lin`: consecutive workgroup ids are
+// dealt round-robin to the 8 XCDs, so the active work spreads evenly over
+// XCDs and CUs, and the idle workgroups are the last ones dispatched.
+struct Unit {
+    int b, kh, split;
+    int64_t pos;
+    bool active;
+};
+
+__device__ __forceinline__ Unit find_unit(const PagedArgs& a, int lin, int split_tiles, int lane) {
+    int base = 0;
+    for (int c0 = 0; c0 < a.batch; c0 += 64) {
+        const int bi = c0 + lane;
+        const int64_t p = lane_position(a, bi < a.batch ? bi : 0);
+        const bool live = bi < a.batch && p >= 0;
+        const int units = live ? a.hkv * ((seq_range(a, p).n_tiles + split_tiles - 1) / split_tiles) : 0;
+        int incl = units;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += t;
+        }
+        const int total = __builtin_amdgcn_readlane(incl, 63);
+        if (lin < base + total) {
+            const int bl = __builtin_ctzll(__ballot(lin < base + incl));
+            const int r = lin - base - __builtin_amdgcn_readlane(incl - units, bl);
+            Unit u;
+            u.b = c0 + bl;
+            u.split = r / a.hkv;
+            u.kh = r - u.split * a.hkv;
+            u.pos = lane_read64(p, bl);
+            u.active = true;
+            return u;
+        }
+        base += total;
+    }
+    Unit u{};
+    u.active = false;
+    return u;
+}
+
+template <int D, int NB, int NT, int S>
+__global__ __launch_bounds__(256) void paged_decode_units_kernel(PagedArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr int kSplitTiles = 4 * NT;  // the host passes split_keys == 16 * kSplitTiles
+    const Unit u = find_unit(a, blockIdx.x, kSplitTiles, lane);
+    if (!u.active) return;
+    const SplitRange sr = seq_range(a, u.pos);
+    const int64_t ta = static_cast<int64_t>(u.split) * kSplitTiles;
+    const int64_t tb = min<int64_t>(sr.n_tiles, ta + kSplitTiles);
+    const bool whole = sr.n_tiles <= kSplitTiles;
+    attend_piece<D, NB, NT, S>(a, smem, lane, wave, u.b, u.kh, sr, ta, tb, whole,
+                               (static_cast<int64_t>(u.b) * a.hq + u.kh * a.group) * a.max_splits + u.split,
+                               a.max_splits);
+}
+
+// Combines the split partials of one (sequence, q head) under the split-unit
+// schedule.  The position is loaded with the first slots' partials (one
+// memory round trip for up to 8 splits); slots at or past the sequence's
+// split count hold stale data and are skipped by index, and a split whose
+// keys were all masked carries max = -inf.  A sequence of one split was
+// written as final output by its workgroup.
+template <int D>
+__global__ __launch_bounds__(64) void paged_decode_units_merge_kernel(PagedArgs a) {
     const int h = blockIdx.x, b = blockIdx.y;
     constexpr int PER = D / 64;  // head dims per thread
     const int64_t base = (static_cast<int64_t>(b) * a.hq + h) * a.max_splits;
     const int64_t pos_v = lane_position(a, b);
+    const int split_tiles = a.split_keys >> 4;
     float M = -INFINITY, L = 0.0f, O[PER];
 #pragma unroll
     for (int i = 0; i < PER; i++) O[i] = 0.0f;
@@ -414,18 +426,20 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(PagedArgs a) {
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             const int64_t slot = base + (s0 + u < a.max_splits ? s0 + u : 0);
-            const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + slot * 2);
-            ms[u] = ml.x;
-            ls[u] = ml.y;
+            const float2 v = *reinterpret_cast<const float2*>(a.ws_ml + slot * 2);
+            ms[u] = v.x;
+            ls[u] = v.y;
 #pragma unroll
             for (int i = 0; i < PER; i++) os[u][i] = a.ws_o[slot * D + threadIdx.x + 64 * i];
         }
         if (n_splits < 0) {
-            const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(pos_v));
-            const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(pos_v) >> 32));
-            const int64_t pos = static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-            n_splits = pos < 0 ? 0 : split_range(a, pos, a.split_keys).n_splits;
-            if (pos < 0 && h == 0 && threadIdx.x == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
+            const int64_t pos = lane_read64(pos_v, 0);
+            if (pos < 0) {
+                zero_rows<D>(a, b, h);
+                return;
+            }
+            n_splits = (seq_range(a, pos).n_tiles + split_tiles - 1) / split_tiles;
+            if (n_splits <= 1) return;
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
@@ -443,6 +457,18 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(PagedArgs a) {
 #pragma unroll
     for (int i = 0; i < PER; i++)
         a.out[b * a.o_sb + h * a.o_sh + threadIdx.x + 64 * i] = f32_to_bf16(L > 0.0f ? O[i] / L : 0.0f);
+}
+
+// ------------------------------------------------ kernel selection (host)
+template <int D, int NB>
+const void* units_for(int nt) {
+    return nt == 4   ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 4, 2>)
+           : nt == 8 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 8, 2>)
+                     : reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 16, 2>);
+}
+
+const void* units_kernel(int D, int nt) {
+    return D == 64 ? units_for<64, 2>(nt) : D == 128 ? units_for<128, 1>(nt) : units_for<256, 1>(nt);
 }
 
 // ---------------------------------------------------------------- general kernel
@@ -697,53 +723,35 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         a.group = static_cast<int32_t>(G);
         a.window = window;
         a.scale_log2 = sc * kLog2e;
-        // split size = 64 keys x tiles per wave (NT): about 2048 work units at
-        // the longest context (~4-8 per CU once the active ones are dealt out)
-        const int nb = D == 64 ? 2 : 1;
-        const int64_t max_keys = max_blocks * P;
-        int64_t split = env_int("SANDY_PAGED_SPLIT", 0);
-        if (split <= 0) split = (max_keys * B * hkv) / 2048;
-        const int64_t nt = split <= 256 ? 4 : split <= 512 ? 8 : 16;
-        split = 64 * nt;
-        a.split_keys = static_cast<int32_t>(split);
-        a.max_splits = static_cast<int32_t>((max_keys + split - 1) / split);
-        const size_t ws_o = static_cast<size_t>(B * hq * a.max_splits * D) * sizeof(float);
-        const size_t ws_ml = static_cast<size_t>(B * hq * a.max_splits * 2) * sizeof(float);
-        char* ws = static_cast<char*>(device_workspace(0, ws_o + ws_ml, stream, e, &status));
-        if (status) return status;
-        a.ws_o = reinterpret_cast<float*>(ws);
-        a.ws_ml = reinterpret_cast<float*>(ws + ws_o);
-        a.errw = errw;
         a.batch = static_cast<int32_t>(B);
-        // one workgroup per possible (sequence, split, kv head); the active ones come first
-        dim3 grid(static_cast<unsigned>(a.max_splits * hkv * B));
+        a.errw = errw;
+        const int64_t max_keys = max_blocks * P;
+        const int nb = D == 64 ? 2 : 1;
         const size_t lds_v = 4 * nb * 16 * (2 * D + 8);
         const size_t lds_r = (4 * G * D + 4 * G * 2) * sizeof(float);
         const size_t lds = std::max(lds_v, lds_r);
         dim3 mgrid(static_cast<unsigned>(hq), static_cast<unsigned>(B));
-        // ring depth: batches in flight per wave (bounded by the tile registers)
-        int stages = env_int("SANDY_PAGED_STAGES", 0);
-        if (stages <= 0) stages = 2;
-        stages = std::min(stages, D == 256 ? 3 : 4);
-#define PD_LAUNCH(DD, NBB, NTT, SS)                                                                      \
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<DD, NBB, NTT, SS>), grid, dim3(256), lds, stream, a)
-#define PD_STAGES(DD, NBB, NTT)                                \
-    if (stages <= 2) { PD_LAUNCH(DD, NBB, NTT, 2); }           \
-    else if (stages == 3 || DD == 256) { PD_LAUNCH(DD, NBB, NTT, 3); } \
-    else { PD_LAUNCH(DD, NBB, NTT, DD == 256 ? 3 : 4); }
-#define PD_SPLITS(DD, NBB)                                     \
-    if (nt == 4) { PD_STAGES(DD, NBB, 4) }                     \
-    else if (nt == 8) { PD_STAGES(DD, NBB, 8) }                \
-    else { PD_STAGES(DD, NBB, 16) }
-        if (D == 64) { PD_SPLITS(64, 2) }
-        else if (D == 128) { PD_SPLITS(128, 1) }
-        else { PD_SPLITS(256, 1) }
-        if (D == 64) hipLaunchKernelGGL(paged_decode_merge_kernel<64>, mgrid, dim3(64), 0, stream, a);
-        else if (D == 128) hipLaunchKernelGGL(paged_decode_merge_kernel<128>, mgrid, dim3(64), 0, stream, a);
-        else hipLaunchKernelGGL(paged_decode_merge_kernel<256>, mgrid, dim3(64), 0, stream, a);
-#undef PD_SPLITS
-#undef PD_STAGES
-#undef PD_LAUNCH
+        void* args[] = {&a};
+        // split units of 64*NT keys; about 2048 units at the longest context
+        int64_t split = env_int("SANDY_PAGED_SPLIT", 0);
+        if (split <= 0) split = (max_keys * B * hkv) / 2048;
+        const int nt = split <= 256 ? 4 : split <= 512 ? 8 : 16;
+        split = 64 * nt;
+        a.split_keys = static_cast<int32_t>(split);
+        a.max_splits = static_cast<int32_t>((max_keys + split - 1) / split);
+        const size_t slots = static_cast<size_t>(B * hq * a.max_splits);
+        char* ws = static_cast<char*>(device_workspace(0, slots * (D + 2) * sizeof(float), stream, e, &status));
+        if (status) return status;
+        a.ws_o = reinterpret_cast<float*>(ws);
+        a.ws_ml = reinterpret_cast<float*>(ws + slots * D * sizeof(float));
+        const int64_t units = static_cast<int64_t>(a.max_splits) * hkv * B;
+        if (units > (1LL << 26)) return fail(e, SANDY_ERR_UNSUPPORTED, "paged attention batch too large");
+        SANDY_HIP_TRY(hipLaunchKernel(units_kernel(static_cast<int>(D), nt), dim3(static_cast<unsigned>(units)),
+                                      dim3(256), args, lds, stream), e, "paged attention launch");
+        const void* mfn = D == 64 ? reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<64>)
+                        : D == 128 ? reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<128>)
+                                   : reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<256>);
+        SANDY_HIP_TRY(hipLaunchKernel(mfn, mgrid, dim3(64), args, 0, stream), e, "paged attention merge launch");
         SANDY_HIP_TRY(hipGetLastError(), e, "paged attention launch");
         return ok(e);
     }
