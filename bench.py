@@ -47,6 +47,8 @@ def parse():
     p.add_argument("--replicas", type=int, default=4)
     p.add_argument("--kernel-iters", type=int, default=64)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--graph", action="store_true",
+                   help="replay the step as a captured HIP graph (measured slower than eager launches here)")
     p.add_argument("--cpu-tokens", type=int, default=4096, help="C2 rows timed on the CPU")
     p.add_argument("--cpu-seqs", type=int, default=8, help="decode sequences timed on the CPU")
     p.add_argument("--only", default="", help="comma list of kernels to run (profiling)")
@@ -389,14 +391,33 @@ def main():
 
     order = list(kernels)
     reps = args.replicas
+    if not args.graph:
+        def step(i):
+            for n in order:
+                kernels[n][i % reps](stream)
+    else:
+        # one HIP graph per replica holding the step's launches (captured
+        # after the warm calls above sized every workspace), replayed on the
+        # current stream: no host launch gaps between the step's kernels
+        graphs = []
+        cap = torch.cuda.Stream()
+        for r in range(reps):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr, stream=cap):
+                s_cap = torch.cuda.current_stream().cuda_stream
+                for n in order:
+                    kernels[n][r](s_cap)
+            graphs.append(gr)
+        torch.cuda.synchronize()
+
+        def step(i):
+            graphs[i % reps].replay()
     for i in range(args.warmup):
-        for n in order:
-            kernels[n][i % reps](stream)
+        step(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        for n in order:
-            kernels[n][i % reps](stream)
+        step(i)
     torch.cuda.synchronize()
     step_s = (time.perf_counter() - t0) / args.steps
     _lib.take_device_errors()
@@ -425,6 +446,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic N(0,1) (seeds 1 and 2), inputs resident in HBM, rotated over replicas",
+        "launch": "hip_graph (one captured step per replica)" if args.graph else "eager",
         "config": {"workload": "config2 TinyLlama fused groups (4096x2048 bf16) + config3 paged decode "
                                "(B32, ctx U[512,4096], 32q/4kv, D64, block 16, pool 32768)",
                    "tokens": T, "hidden": HID, "decode_batch": DEC_B, "replicas": args.replicas},
