@@ -137,6 +137,31 @@ __device__ __forceinline__ int64_t lane_position(const PagedArgs& a, int64_t i) 
                                  : static_cast<const int64_t*>(a.pos)[i];
 }
 
+// Position i as two raw 32-bit words fetched with relaxed agent-scope atomic
+// loads from branch-free addresses: they stay on the vector memory path, so
+// a uniform position travels with the loads issued after it instead of
+// being waited on (as a scalar load) before them.  join_position() combines
+// them at the first use.
+struct PosWords {
+    uint32_t lo, hi;
+};
+
+__device__ __forceinline__ PosWords vector_position(const PagedArgs& a, int64_t i) {
+    const bool i32 = a.pos_dt == SANDY_I32;
+    uint32_t* p = reinterpret_cast<uint32_t*>(const_cast<void*>(a.pos)) + (i32 ? i : 2 * i);
+    PosWords w;
+    w.lo = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    w.hi = __hip_atomic_load(p + (i32 ? 0 : 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return w;
+}
+
+__device__ __forceinline__ int64_t join_position(const PagedArgs& a, PosWords w) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(w.lo);
+    const uint32_t hi = a.pos_dt == SANDY_I32 ? static_cast<uint32_t>(static_cast<int32_t>(lo) >> 31)
+                                              : __builtin_amdgcn_readfirstlane(w.hi);
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 __device__ __forceinline__ int64_t lane_read64(int64_t v, int l) {
     const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(v), l);
     const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32), l);
@@ -415,12 +440,13 @@ __global__ __launch_bounds__(64) void paged_decode_units_merge_kernel(PagedArgs 
     const int h = blockIdx.x, b = blockIdx.y;
     constexpr int PER = D / 64;  // head dims per thread
     const int64_t base = (static_cast<int64_t>(b) * a.hq + h) * a.max_splits;
-    const int64_t pos_v = lane_position(a, b);
+    const PosWords pos_w = vector_position(a, b);
     const int split_tiles = a.split_keys >> 4;
     float M = -INFINITY, L = 0.0f, O[PER];
 #pragma unroll
     for (int i = 0; i < PER; i++) O[i] = 0.0f;
-    int n_splits = -1;  // known once the position has arrived
+    int64_t pos = -1;
+    int n_splits = -1;  // known once the position has arrived (after the first loads)
     for (int s0 = 0; s0 < a.max_splits; s0 += 8) {
         float ms[8], ls[8], os[8][PER];
 #pragma unroll
@@ -433,13 +459,8 @@ __global__ __launch_bounds__(64) void paged_decode_units_merge_kernel(PagedArgs 
             for (int i = 0; i < PER; i++) os[u][i] = a.ws_o[slot * D + threadIdx.x + 64 * i];
         }
         if (n_splits < 0) {
-            const int64_t pos = lane_read64(pos_v, 0);
-            if (pos < 0) {
-                zero_rows<D>(a, b, h);
-                return;
-            }
-            n_splits = (seq_range(a, pos).n_tiles + split_tiles - 1) / split_tiles;
-            if (n_splits <= 1) return;
+            pos = join_position(a, pos_w);
+            n_splits = pos < 0 ? 0 : (seq_range(a, pos).n_tiles + split_tiles - 1) / split_tiles;
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
@@ -454,6 +475,9 @@ __global__ __launch_bounds__(64) void paged_decode_units_merge_kernel(PagedArgs 
         }
         if (s0 + 8 >= n_splits) break;
     }
+    if (n_splits == 1) return;  // written as final output by its workgroup
+    if (pos < 0 && h == 0 && threadIdx.x == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
+    // (a negative position has no splits: L = 0 writes zeros)
 #pragma unroll
     for (int i = 0; i < PER; i++)
         a.out[b * a.o_sb + h * a.o_sh + threadIdx.x + 64 * i] = f32_to_bf16(L > 0.0f ? O[i] / L : 0.0f);
