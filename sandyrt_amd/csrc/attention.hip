@@ -412,8 +412,11 @@ __device__ __forceinline__ Unit find_unit(const PagedArgs& a, int lin, int split
     return u;
 }
 
-template <int D, int NB, int NT, int S>
-__global__ __launch_bounds__(256) void paged_decode_units_kernel(PagedArgs a) {
+// OCC: waves per SIMD the register allocation must allow (1 = no limit).  At
+// 5, config 3's shape still needs no scratch and every work unit of a 32 x
+// 4K-context step is resident at once (1280 workgroup slots).
+template <int D, int NB, int NT, int S, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void paged_decode_units_kernel(PagedArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -431,7 +434,7 @@ __global__ __launch_bounds__(256) void paged_decode_units_kernel(PagedArgs a) {
 
 // Combines the split partials of one (sequence, q head) under the split-unit
 // schedule.  The position is loaded with the first slots' partials (one
-// memory round trip for up to 8 splits); slots at or past the sequence's
+// memory round trip for up to 16 splits); slots at or past the sequence's
 // split count hold stale data and are skipped by index, and a split whose
 // keys were all masked carries max = -inf.  A sequence of one split was
 // written as final output by its workgroup.
@@ -447,10 +450,11 @@ __global__ __launch_bounds__(64) void paged_decode_units_merge_kernel(PagedArgs 
     for (int i = 0; i < PER; i++) O[i] = 0.0f;
     int64_t pos = -1;
     int n_splits = -1;  // known once the position has arrived (after the first loads)
-    for (int s0 = 0; s0 < a.max_splits; s0 += 8) {
-        float ms[8], ls[8], os[8][PER];
+    constexpr int R = 16;  // splits whose partials are loaded in one round trip
+    for (int s0 = 0; s0 < a.max_splits; s0 += R) {
+        float ms[R], ls[R], os[R][PER];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+        for (int u = 0; u < R; u++) {
             const int64_t slot = base + (s0 + u < a.max_splits ? s0 + u : 0);
             const float2 v = *reinterpret_cast<const float2*>(a.ws_ml + slot * 2);
             ms[u] = v.x;
@@ -463,7 +467,7 @@ __global__ __launch_bounds__(64) void paged_decode_units_merge_kernel(PagedArgs 
             n_splits = pos < 0 ? 0 : (seq_range(a, pos).n_tiles + split_tiles - 1) / split_tiles;
         }
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+        for (int u = 0; u < R; u++) {
             if (s0 + u >= n_splits || ms[u] == -INFINITY) continue;
             const float mn = fmaxf(M, ms[u]);
             const float fo = M == -INFINITY ? 0.0f : exp2f(M - mn);
@@ -473,7 +477,7 @@ __global__ __launch_bounds__(64) void paged_decode_units_merge_kernel(PagedArgs 
             for (int i = 0; i < PER; i++) O[i] = O[i] * fo + os[u][i] * fs;
             M = mn;
         }
-        if (s0 + 8 >= n_splits) break;
+        if (s0 + R >= n_splits) break;
     }
     if (n_splits == 1) return;  // written as final output by its workgroup
     if (pos < 0 && h == 0 && threadIdx.x == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
@@ -486,9 +490,10 @@ __global__ __launch_bounds__(64) void paged_decode_units_merge_kernel(PagedArgs 
 // ------------------------------------------------ kernel selection (host)
 template <int D, int NB>
 const void* units_for(int nt) {
-    return nt == 4   ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 4, 2>)
-           : nt == 8 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 8, 2>)
-                     : reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 16, 2>);
+    constexpr int kOcc4 = D == 64 ? 5 : 1;  // spill-free only for D = 64, four tiles per wave
+    return nt == 4   ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 4, 2, kOcc4>)
+           : nt == 8 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 8, 2, 1>)
+                     : reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 16, 2, 1>);
 }
 
 const void* units_kernel(int D, int nt) {
