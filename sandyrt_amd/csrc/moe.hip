@@ -505,6 +505,149 @@ __global__ __launch_bounds__(256) void moe_gemm_mfma_kernel(const uint16_t* __re
     }
 }
 
+// The same product with the weights read as whole 128-byte lines.  Loading
+// B operands straight into registers touches 16 weight rows x 64 bytes per
+// instruction; on gfx950 that pattern streams at about 3.2 TB/s against
+// 5.0 TB/s for 8 rows x 128 bytes.  Here each chunk of 64 k of the wave's
+// 16 * CT weight rows is loaded as full lines (lane: row 8i + lane/8, 16-byte
+// piece lane%8), written to a wave-private LDS tile whose pieces are
+// XOR-swizzled by (row / 2) % 8 (conflict-free 128-bit writes and reads), and
+// read back in the MFMA B layout; the k order inside a chunk is unchanged, so
+// the activation (A) loads are the same as above.  The tile is double
+// buffered in LDS: while chunk c multiplies out of one buffer, chunk c + 1's
+// loads are in flight and land in the other, so only one chunk of weights
+// lives in registers and two waves fit per SIMD at RT = CT = 4 (the
+// allocation is held to that: no accumulator registers, no scratch).
+template <int RT, int CT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void moe_gemm_lines_kernel(const uint16_t* __restrict__ x,
+                                                             const void* __restrict__ offs, int32_t off_dt,
+                                                             const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
+                                                             int64_t rows, int64_t K, int64_t M, int64_t experts,
+                                                             int64_t batch, uint32_t* errw) {
+    constexpr int kTileBytes = 16 * CT * 128;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[4 * 2 * kTileBytes];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t e = blockIdx.x % experts;
+    const int64_t b = blockIdx.x / experts;
+    const int64_t n0 = (static_cast<int64_t>(blockIdx.y) * 4 + wave) * 16 * CT;
+    const int64_t ob = b * (experts + 1);
+    const int64_t begin = load_index(offs, off_dt, ob + e);
+    const int64_t end = load_index(offs, off_dt, ob + e + 1);
+    if (begin < 0 || end < begin || end > rows) {
+        if (threadIdx.x == 0 && blockIdx.y == 0) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_OFFSETS));
+        return;
+    }
+    if (end == begin || n0 >= M) return;
+    unsigned char* tiles = lds + wave * 2 * kTileBytes;
+    auto swz = [](int row, int piece) { return row * 128 + ((piece ^ ((row >> 1) & 7)) << 4); };
+    const int64_t xb = b * rows * K, yb = b * rows * M;
+    const int64_t ksteps = K / 32;
+    const int64_t chunks = (ksteps + 1) / 2;  // 64 k per chunk
+    // Weights and activations through buffer resources: one scalar base, a
+    // 32-bit lane offset and a scalar offset per load; rows past the range
+    // read as zero (weight rows >= M, activation rows past this pass or >= end).
+    const int64_t wrows = min<int64_t>(16 * CT, M - n0);
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(w + (e * M + n0) * K), 0, static_cast<int>(wrows * K * 2), 0x00020000);
+    // full-line weight loads: instruction i covers tile rows 8i .. 8i + 7
+    const int wlane = static_cast<int>((lane >> 3) * K * 2 + (lane & 7) * 16);
+    const int wstep = static_cast<int>(8 * K * 2);
+    // tile row 8i + lane/8 swizzles by (4i + lane/16) % 8: one base for even i, one for odd i (+ i * 1024)
+    const int wbase[2] = {swz(lane >> 3, lane & 7), swz(8 + (lane >> 3), lane & 7) - 1024};
+    const bool w_hi = (lane & 7) >= 4;           // this lane's piece lies in the chunk's second k-step
+    int raddr[2][CT];
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int c = 0; c < CT; c++) raddr[u][c] = swz(16 * c + (lane & 15), 4 * u + (lane >> 4));
+
+    for (int64_t r0 = begin; r0 < end; r0 += 16 * RT) {
+        const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(x + xb + r0 * K), 0, static_cast<int>(min<int64_t>(end - r0, 16 * RT) * K * 2),
+            0x00020000);
+        const int xlane = static_cast<int>((lane & 15) * K * 2 + (lane >> 4) * 16);
+        f32x4_t acc[RT][CT];
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int c = 0; c < CT; c++) acc[t][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        uint4 wv[2 * CT], xA[2][RT], xB[2][RT];
+        auto load_w = [&](int64_t ch) {
+            const bool win = 2 * ch + (w_hi ? 1 : 0) < ksteps;
+#pragma unroll
+            for (int i = 0; i < 2 * CT; i++) {
+                const uint4 v = __builtin_bit_cast(
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wlane, static_cast<int>(i * wstep + ch * 128), 0));
+                wv[i] = win ? v : make_uint4(0, 0, 0, 0);
+            }
+        };
+        auto store_w = [&](int buf) {
+#pragma unroll
+            for (int i = 0; i < 2 * CT; i++)
+                *reinterpret_cast<uint4*>(tiles + buf * kTileBytes + wbase[i & 1] + i * 1024) = wv[i];
+        };
+        auto load_x = [&](uint4 (&xv)[2][RT], int64_t ch) {
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const bool in = 2 * ch + u < ksteps;
+#pragma unroll
+                for (int t = 0; t < RT; t++) {
+                    const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                        xres, xlane, static_cast<int>(16 * t * K * 2 + (2 * ch + u) * 64), 0));
+                    xv[u][t] = in ? v : make_uint4(0, 0, 0, 0);
+                }
+            }
+        };
+        auto mma = [&](int buf, const uint4 (&xv)[2][RT]) {
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int c = 0; c < CT; c++) {
+                    const uint4 bv = *reinterpret_cast<const uint4*>(tiles + buf * kTileBytes + raddr[u][c]);
+#pragma unroll
+                    for (int t = 0; t < RT; t++)
+                        acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xv[u][t]),
+                                                                            __builtin_bit_cast(bf16x8_t, bv),
+                                                                            acc[t][c], 0, 0, 0);
+                }
+        };
+        // chunk ch multiplies from buffer ch % 2 with activations xA (even) / xB (odd)
+        load_w(0);
+        load_x(xA, 0);
+        store_w(0);
+        __builtin_amdgcn_wave_barrier();
+        for (int64_t ch = 0; ch < chunks; ch += 2) {
+            if (ch + 1 < chunks) {
+                load_w(ch + 1);
+                load_x(xB, ch + 1);
+            }
+            mma(0, xA);
+            if (ch + 1 >= chunks) break;
+            store_w(1);
+            __builtin_amdgcn_wave_barrier();
+            if (ch + 2 < chunks) {
+                load_w(ch + 2);
+                load_x(xA, ch + 2);
+            }
+            mma(1, xB);
+            if (ch + 2 < chunks) store_w(0);
+            __builtin_amdgcn_wave_barrier();
+        }
+        __builtin_amdgcn_wave_barrier();
+        // acc[t][c][i]: row r0 + 16 t + 4 (lane/16) + i, column n0 + 16 c + lane%16
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int c = 0; c < CT; c++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int64_t rr = r0 + 16 * t + 4 * (lane >> 4) + i;
+                    const int64_t nc = n0 + 16 * c + (lane & 15);
+                    if (rr < end && nc < M) out[yb + rr * M + nc] = f32_to_bf16(acc[t][c][i]);
+                }
+    }
+}
+
 // Any dtype / layout: one thread per (row, column), float accumulation in k
 // order like the reference.
 template <typename T>
@@ -713,14 +856,22 @@ extern "C" int sandy_hip_moe_matmul(const SandyTensor* x, const SandyTensor* exp
         const auto* pw = static_cast<const uint16_t*>(base_ptr(*weight));
         auto* po = static_cast<uint16_t*>(base_ptr(*out));
         const void* po_ = base_ptr(*expert_offsets);
-        const int variant = env_int("SANDY_MOE_GEMM", avg <= 16 ? 0 : 7);
+        const int variant = env_int("SANDY_MOE_GEMM", avg <= 16 ? 8 : 9);
         auto grid_for = [&](int ct) {
             return dim3(static_cast<unsigned>(batch * experts), static_cast<unsigned>((M + 64 * ct - 1) / (64 * ct)));
         };
 #define GEMM_LAUNCH(RT, CT, KU)                                                                                      \
     hipLaunchKernelGGL((moe_gemm_mfma_kernel<RT, CT, KU>), grid_for(CT), dim3(256), 0, stream, px, po_,           \
                        expert_offsets->dtype, pw, po, rows, K, M, experts, batch, errw)
+#define LINES_LAUNCH(RT, CT)                                                                                        \
+    hipLaunchKernelGGL((moe_gemm_lines_kernel<RT, CT>), grid_for(CT), dim3(256), 0, stream, px, po_,               \
+                       expert_offsets->dtype, pw, po, rows, K, M, experts, batch, errw)
         switch (variant) {
+            case 8: LINES_LAUNCH(1, 2); break;
+            case 9: LINES_LAUNCH(4, 4); break;
+            case 10: LINES_LAUNCH(4, 2); break;
+            case 11: LINES_LAUNCH(2, 4); break;
+            case 12: LINES_LAUNCH(2, 2); break;
             case 0: GEMM_LAUNCH(1, 2, 4); break;
             case 1: GEMM_LAUNCH(4, 1, 4); break;
             case 2: GEMM_LAUNCH(4, 2, 2); break;
@@ -731,6 +882,7 @@ extern "C" int sandy_hip_moe_matmul(const SandyTensor* x, const SandyTensor* exp
             default: GEMM_LAUNCH(4, 4, 2); break;
         }
 #undef GEMM_LAUNCH
+#undef LINES_LAUNCH
     } else {
         hipLaunchKernelGGL(validate_offsets_kernel, dim3(static_cast<unsigned>((batch * experts + 255) / 256)), dim3(256), 0, stream,
                            base_ptr(*expert_offsets), expert_offsets->dtype, experts, rows, batch, errw);
