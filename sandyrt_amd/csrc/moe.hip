@@ -505,28 +505,29 @@ __global__ __launch_bounds__(256) void moe_gemm_mfma_kernel(const uint16_t* __re
     }
 }
 
-// The same product with the weights read as whole 128-byte lines.  Loading
-// B operands straight into registers touches 16 weight rows x 64 bytes per
-// instruction; on gfx950 that pattern streams at about 3.2 TB/s against
-// 5.0 TB/s for 8 rows x 128 bytes.  Here each chunk of 64 k of the wave's
-// 16 * CT weight rows is loaded as full lines (lane: row 8i + lane/8, 16-byte
-// piece lane%8), written to a wave-private LDS tile whose pieces are
-// XOR-swizzled by (row / 2) % 8 (conflict-free 128-bit writes and reads), and
-// read back in the MFMA B layout; the k order inside a chunk is unchanged, so
-// the activation (A) loads are the same as above.  The tile is double
-// buffered in LDS: while chunk c multiplies out of one buffer, chunk c + 1's
-// loads are in flight and land in the other, so only one chunk of weights
-// lives in registers and two waves fit per SIMD at RT = CT = 4 (the
-// allocation is held to that: no accumulator registers, no scratch).
+// The same product with both operands read as whole 128-byte lines.
+// Loading MFMA operands straight into registers touches 16 rows x 64 bytes
+// per instruction; on gfx950 that pattern streams at about 3.2 TB/s against
+// 5.0 TB/s for 8 rows x 128 bytes.  Per chunk of 64 k:
+//   - the workgroup loads the expert's 16 * RT activation rows once (every
+//     wave multiplies them) into a shared LDS tile;
+//   - each wave loads its 16 * CT weight rows into a private LDS tile;
+// both as full lines (8 rows x 128 bytes per instruction) into tiles whose
+// 16-byte pieces are XOR-swizzled by (row / 2) % 8, so 128-bit writes and
+// the MFMA-layout 128-bit reads are conflict-free; the k order inside a
+// chunk is unchanged.  Tiles are double buffered: chunk c + 1's loads are in
+// flight while chunk c multiplies, then land in the other buffer before the
+// workgroup barrier.  Two waves fit per SIMD at RT = CT = 4.
 template <int RT, int CT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void moe_gemm_lines_kernel(const uint16_t* __restrict__ x,
-                                                             const void* __restrict__ offs, int32_t off_dt,
-                                                             const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
-                                                             int64_t rows, int64_t K, int64_t M, int64_t experts,
-                                                             int64_t batch, uint32_t* errw) {
-    constexpr int kTileBytes = 16 * CT * 128;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[4 * 2 * kTileBytes];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void moe_gemm_lines_kernel(
+        const uint16_t* __restrict__ x, const void* __restrict__ offs, int32_t off_dt, const uint16_t* __restrict__ w,
+        uint16_t* __restrict__ out, int64_t rows, int64_t K, int64_t M, int64_t experts, int64_t batch,
+        uint32_t* errw) {
+    constexpr int kWTile = 16 * CT * 128;  // one wave's weight rows x 128 bytes
+    constexpr int kXTile = 16 * RT * 128;  // the workgroup's activation rows x 128 bytes
+    constexpr int kXPer = (16 * RT * 8 + 255) / 256;  // 16-byte activation pieces per thread
+    __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kXTile + 4 * 2 * kWTile];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t e = blockIdx.x % experts;
     const int64_t b = blockIdx.x / experts;
     const int64_t n0 = (static_cast<int64_t>(blockIdx.y) * 4 + wave) * 16 * CT;
@@ -534,45 +535,60 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     const int64_t begin = load_index(offs, off_dt, ob + e);
     const int64_t end = load_index(offs, off_dt, ob + e + 1);
     if (begin < 0 || end < begin || end > rows) {
-        if (threadIdx.x == 0 && blockIdx.y == 0) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_OFFSETS));
+        if (tid == 0 && blockIdx.y == 0) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_OFFSETS));
         return;
     }
-    if (end == begin || n0 >= M) return;
-    unsigned char* tiles = lds + wave * 2 * kTileBytes;
+    if (end == begin || static_cast<int64_t>(blockIdx.y) * 64 * CT >= M) return;  // workgroup-uniform exits only
+    const bool wave_live = n0 < M;
+    unsigned char* xt = lds;                           // [2][kXTile]
+    unsigned char* wt = lds + 2 * kXTile + wave * 2 * kWTile;  // [2][kWTile]
     auto swz = [](int row, int piece) { return row * 128 + ((piece ^ ((row >> 1) & 7)) << 4); };
     const int64_t xb = b * rows * K, yb = b * rows * M;
     const int64_t ksteps = K / 32;
     const int64_t chunks = (ksteps + 1) / 2;  // 64 k per chunk
-    // Weights and activations through buffer resources: one scalar base, a
-    // 32-bit lane offset and a scalar offset per load; rows past the range
-    // read as zero (weight rows >= M, activation rows past this pass or >= end).
-    const int64_t wrows = min<int64_t>(16 * CT, M - n0);
+    // Buffer resources: one scalar base, a 32-bit lane offset and a scalar
+    // offset per load; pieces past the range read as zero.
+    const int64_t wrows = wave_live ? min<int64_t>(16 * CT, M - n0) : 0;
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(w + (e * M + n0) * K), 0, static_cast<int>(wrows * K * 2), 0x00020000);
-    // full-line weight loads: instruction i covers tile rows 8i .. 8i + 7
+        const_cast<uint16_t*>(w + (e * M + (wave_live ? n0 : 0)) * K), 0, static_cast<int>(wrows * K * 2), 0x00020000);
+    // weight instruction i covers tile rows 8i .. 8i + 7 (lane: row 8i + lane/8, piece lane%8)
     const int wlane = static_cast<int>((lane >> 3) * K * 2 + (lane & 7) * 16);
     const int wstep = static_cast<int>(8 * K * 2);
     // tile row 8i + lane/8 swizzles by (4i + lane/16) % 8: one base for even i, one for odd i (+ i * 1024)
     const int wbase[2] = {swz(lane >> 3, lane & 7), swz(8 + (lane >> 3), lane & 7) - 1024};
-    const bool w_hi = (lane & 7) >= 4;           // this lane's piece lies in the chunk's second k-step
-    int raddr[2][CT];
+    const bool w_hi = (lane & 7) >= 4;  // this lane's weight piece lies in the chunk's second k-step
+    // activation piece q of this thread: tile row p / 8, piece p % 8 with p = tid + 256 q
+    int xaddr[kXPer], xoff[kXPer];
+    bool xlive[kXPer], x_hi[kXPer];
 #pragma unroll
-    for (int u = 0; u < 2; u++)
+    for (int q = 0; q < kXPer; q++) {
+        const int p = tid + 256 * q;
+        xlive[q] = p < 16 * RT * 8;
+        const int row = xlive[q] ? p >> 3 : 0;
+        xaddr[q] = swz(row, p & 7);
+        xoff[q] = static_cast<int>(row * K * 2 + (p & 7) * 16);
+        x_hi[q] = (p & 7) >= 4;
+    }
+    int raddr[2][CT], aaddr[2][RT];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
 #pragma unroll
         for (int c = 0; c < CT; c++) raddr[u][c] = swz(16 * c + (lane & 15), 4 * u + (lane >> 4));
+#pragma unroll
+        for (int t = 0; t < RT; t++) aaddr[u][t] = swz(16 * t + (lane & 15), 4 * u + (lane >> 4));
+    }
 
     for (int64_t r0 = begin; r0 < end; r0 += 16 * RT) {
         const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint16_t*>(x + xb + r0 * K), 0, static_cast<int>(min<int64_t>(end - r0, 16 * RT) * K * 2),
             0x00020000);
-        const int xlane = static_cast<int>((lane & 15) * K * 2 + (lane >> 4) * 16);
         f32x4_t acc[RT][CT];
 #pragma unroll
         for (int t = 0; t < RT; t++)
 #pragma unroll
             for (int c = 0; c < CT; c++) acc[t][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        uint4 wv[2 * CT], xA[2][RT], xB[2][RT];
-        auto load_w = [&](int64_t ch) {
+        uint4 wv[2 * CT], xv[kXPer];
+        auto load = [&](int64_t ch) {
             const bool win = 2 * ch + (w_hi ? 1 : 0) < ksteps;
 #pragma unroll
             for (int i = 0; i < 2 * CT; i++) {
@@ -580,71 +596,61 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
                     uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wlane, static_cast<int>(i * wstep + ch * 128), 0));
                 wv[i] = win ? v : make_uint4(0, 0, 0, 0);
             }
-        };
-        auto store_w = [&](int buf) {
 #pragma unroll
-            for (int i = 0; i < 2 * CT; i++)
-                *reinterpret_cast<uint4*>(tiles + buf * kTileBytes + wbase[i & 1] + i * 1024) = wv[i];
-        };
-        auto load_x = [&](uint4 (&xv)[2][RT], int64_t ch) {
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const bool in = 2 * ch + u < ksteps;
-#pragma unroll
-                for (int t = 0; t < RT; t++) {
-                    const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                        xres, xlane, static_cast<int>(16 * t * K * 2 + (2 * ch + u) * 64), 0));
-                    xv[u][t] = in ? v : make_uint4(0, 0, 0, 0);
-                }
+            for (int q = 0; q < kXPer; q++) {
+                const uint4 v = __builtin_bit_cast(
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[q], static_cast<int>(ch * 128), 0));
+                xv[q] = 2 * ch + (x_hi[q] ? 1 : 0) < ksteps ? v : make_uint4(0, 0, 0, 0);
             }
         };
-        auto mma = [&](int buf, const uint4 (&xv)[2][RT]) {
+        auto store = [&](int buf) {
 #pragma unroll
-            for (int u = 0; u < 2; u++)
+            for (int i = 0; i < 2 * CT; i++)
+                *reinterpret_cast<uint4*>(wt + buf * kWTile + wbase[i & 1] + i * 1024) = wv[i];
+#pragma unroll
+            for (int q = 0; q < kXPer; q++)
+                if (xlive[q]) *reinterpret_cast<uint4*>(xt + buf * kXTile + xaddr[q]) = xv[q];
+        };
+        auto mma = [&](int buf) {
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                uint4 av[RT];
+#pragma unroll
+                for (int t = 0; t < RT; t++) av[t] = *reinterpret_cast<const uint4*>(xt + buf * kXTile + aaddr[u][t]);
 #pragma unroll
                 for (int c = 0; c < CT; c++) {
-                    const uint4 bv = *reinterpret_cast<const uint4*>(tiles + buf * kTileBytes + raddr[u][c]);
+                    const uint4 bv = *reinterpret_cast<const uint4*>(wt + buf * kWTile + raddr[u][c]);
 #pragma unroll
                     for (int t = 0; t < RT; t++)
-                        acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xv[u][t]),
+                        acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[t]),
                                                                             __builtin_bit_cast(bf16x8_t, bv),
                                                                             acc[t][c], 0, 0, 0);
                 }
+            }
         };
-        // chunk ch multiplies from buffer ch % 2 with activations xA (even) / xB (odd)
-        load_w(0);
-        load_x(xA, 0);
-        store_w(0);
-        __builtin_amdgcn_wave_barrier();
-        for (int64_t ch = 0; ch < chunks; ch += 2) {
-            if (ch + 1 < chunks) {
-                load_w(ch + 1);
-                load_x(xB, ch + 1);
-            }
-            mma(0, xA);
-            if (ch + 1 >= chunks) break;
-            store_w(1);
-            __builtin_amdgcn_wave_barrier();
-            if (ch + 2 < chunks) {
-                load_w(ch + 2);
-                load_x(xA, ch + 2);
-            }
-            mma(1, xB);
-            if (ch + 2 < chunks) store_w(0);
-            __builtin_amdgcn_wave_barrier();
+        // chunk ch multiplies out of buffer ch % 2 while chunk ch + 1's loads are in flight
+        load(0);
+        store(0);
+        __syncthreads();
+        for (int64_t ch = 0; ch < chunks; ch++) {
+            if (ch + 1 < chunks) load(ch + 1);
+            if (wave_live) mma(static_cast<int>(ch & 1));
+            if (ch + 1 < chunks) store(static_cast<int>((ch + 1) & 1));
+            __syncthreads();
         }
-        __builtin_amdgcn_wave_barrier();
-        // acc[t][c][i]: row r0 + 16 t + 4 (lane/16) + i, column n0 + 16 c + lane%16
+        if (wave_live) {
+            // acc[t][c][i]: row r0 + 16 t + 4 (lane/16) + i, column n0 + 16 c + lane%16
 #pragma unroll
-        for (int t = 0; t < RT; t++)
+            for (int t = 0; t < RT; t++)
 #pragma unroll
-            for (int c = 0; c < CT; c++)
+                for (int c = 0; c < CT; c++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int64_t rr = r0 + 16 * t + 4 * (lane >> 4) + i;
-                    const int64_t nc = n0 + 16 * c + (lane & 15);
-                    if (rr < end && nc < M) out[yb + rr * M + nc] = f32_to_bf16(acc[t][c][i]);
-                }
+                    for (int i = 0; i < 4; i++) {
+                        const int64_t rr = r0 + 16 * t + 4 * (lane >> 4) + i;
+                        const int64_t nc = n0 + 16 * c + (lane & 15);
+                        if (rr < end && nc < M) out[yb + rr * M + nc] = f32_to_bf16(acc[t][c][i]);
+                    }
+        }
     }
 }
 
