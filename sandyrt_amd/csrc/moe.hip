@@ -411,103 +411,11 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
 // ---------------------------------------------------------------- moe_matmul
 // Grouped GEMM, bf16, transpose_rhs: out[row, n] = sum_k x[row, k] W[e, n, k].
 // Workgroup = (expert, 64 * CT output columns); wave w owns 16 * CT columns
-// and up to 16 * RT rows of the expert per pass.  A = x rows (lane: row
-// lane%16, k chunk 8 (lane/16)), B = W rows (lane: column lane%16, same k
-// chunk): both 16-byte loads along k; one activation load feeds CT weight
-// tiles.  Chunks of KU k-steps ping-pong: the next chunk's loads are in
-// flight while the current chunk feeds v_mfma_f32_16x16x32_bf16.  The weight
-// slice is streamed from HBM once per pass.
-template <int RT, int CT, int KU>
-__global__ __launch_bounds__(256) void moe_gemm_mfma_kernel(const uint16_t* __restrict__ x,
-                                                            const void* __restrict__ offs, int32_t off_dt,
-                                                            const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
-                                                            int64_t rows, int64_t K, int64_t M, int64_t experts,
-                                                            int64_t batch, uint32_t* errw) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t e = blockIdx.x % experts;
-    const int64_t b = blockIdx.x / experts;
-    const int64_t n0 = (static_cast<int64_t>(blockIdx.y) * 4 + wave) * 16 * CT;
-    const int64_t ob = b * (experts + 1);
-    const int64_t begin = load_index(offs, off_dt, ob + e);
-    const int64_t end = load_index(offs, off_dt, ob + e + 1);
-    if (begin < 0 || end < begin || end > rows) {
-        if (threadIdx.x == 0 && blockIdx.y == 0) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_OFFSETS));
-        return;
-    }
-    if (end == begin || n0 >= M) return;
-    const int64_t xb = b * rows * K, yb = b * rows * M;
-    const uint4* wrow[CT];
-    bool col_ok[CT];
-#pragma unroll
-    for (int c = 0; c < CT; c++) {
-        const int64_t ncol = n0 + 16 * c + (lane & 15);
-        col_ok[c] = ncol < M;
-        wrow[c] = reinterpret_cast<const uint4*>(w + (e * M + (col_ok[c] ? ncol : 0)) * K + 8 * (lane >> 4));
-    }
-    const int64_t ksteps = K / 32;
-    for (int64_t r0 = begin; r0 < end; r0 += 16 * RT) {
-        const uint4* xrow[RT];
-        bool row_ok[RT];
-#pragma unroll
-        for (int t = 0; t < RT; t++) {
-            const int64_t rr = r0 + 16 * t + (lane & 15);
-            row_ok[t] = rr < end;
-            xrow[t] = reinterpret_cast<const uint4*>(x + xb + (row_ok[t] ? rr : begin) * K + 8 * (lane >> 4));
-        }
-        f32x4_t acc[RT][CT];
-#pragma unroll
-        for (int t = 0; t < RT; t++)
-#pragma unroll
-            for (int c = 0; c < CT; c++) acc[t][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        uint4 bwA[KU][CT], axA[KU][RT], bwB[KU][CT], axB[KU][RT];
-        auto load_chunk = [&](uint4 (&bw)[KU][CT], uint4 (&ax)[KU][RT], int64_t ks) {
-#pragma unroll
-            for (int u = 0; u < KU; u++) {
-                const bool in = ks + u < ksteps;
-#pragma unroll
-                for (int c = 0; c < CT; c++)
-                    bw[u][c] = in && col_ok[c] ? wrow[c][(ks + u) * 4] : make_uint4(0, 0, 0, 0);
-#pragma unroll
-                for (int t = 0; t < RT; t++)
-                    ax[u][t] = in && row_ok[t] ? xrow[t][(ks + u) * 4] : make_uint4(0, 0, 0, 0);
-            }
-        };
-        auto mma_chunk = [&](const uint4 (&bw)[KU][CT], const uint4 (&ax)[KU][RT]) {
-#pragma unroll
-            for (int u = 0; u < KU; u++)
-#pragma unroll
-                for (int t = 0; t < RT; t++)
-#pragma unroll
-                    for (int c = 0; c < CT; c++)
-                        acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ax[u][t]),
-                                                                            __builtin_bit_cast(bf16x8_t, bw[u][c]),
-                                                                            acc[t][c], 0, 0, 0);
-        };
-        load_chunk(bwA, axA, 0);
-        for (int64_t ks = 0; ks < ksteps; ks += 2 * KU) {
-            if (ks + KU < ksteps) load_chunk(bwB, axB, ks + KU);
-            mma_chunk(bwA, axA);
-            if (ks + KU >= ksteps) break;
-            if (ks + 2 * KU < ksteps) load_chunk(bwA, axA, ks + 2 * KU);
-            mma_chunk(bwB, axB);
-        }
-        // acc[t][c][i]: row r0 + 16 t + 4 (lane/16) + i, column n0 + 16 c + lane%16
-#pragma unroll
-        for (int t = 0; t < RT; t++)
-#pragma unroll
-            for (int c = 0; c < CT; c++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int64_t rr = r0 + 16 * t + 4 * (lane >> 4) + i;
-                    const int64_t nc = n0 + 16 * c + (lane & 15);
-                    if (rr < end && col_ok[c]) out[yb + rr * M + nc] = f32_to_bf16(acc[t][c][i]);
-                }
-    }
-}
-
-// The same product with both operands read as whole 128-byte lines.
-// Loading MFMA operands straight into registers touches 16 rows x 64 bytes
-// per instruction; on gfx950 that pattern streams at about 3.2 TB/s against
+// and up to 16 * RT rows of the expert per pass (A = x rows, B = W rows on
+// v_mfma_f32_16x16x32_bf16); the weight slice is streamed from HBM once per
+// pass.  Both operands are read as whole 128-byte lines: loading MFMA
+// operands straight into registers touches 16 rows x 64 bytes per
+// instruction; on gfx950 that pattern streams at about 3.2 TB/s against
 // 5.0 TB/s for 8 rows x 128 bytes.  Per chunk of 64 k:
 //   - the workgroup loads the expert's 16 * RT activation rows once (every
 //     wave multiplies them) into a shared LDS tile;
@@ -856,38 +764,26 @@ extern "C" int sandy_hip_moe_matmul(const SandyTensor* x, const SandyTensor* exp
     const bool aligned = ((reinterpret_cast<uintptr_t>(base_ptr(*x)) | reinterpret_cast<uintptr_t>(base_ptr(*weight))) & 15) == 0;
     if (x->dtype == SANDY_BF16 && transpose_rhs && K % 32 == 0 && aligned) {
         // every workgroup checks the offsets of its own expert
-        // rows per expert: 16 rows per pass for decode-sized batches, 64 otherwise
         const int64_t avg = rows / experts;
         const auto* px = static_cast<const uint16_t*>(base_ptr(*x));
         const auto* pw = static_cast<const uint16_t*>(base_ptr(*weight));
         auto* po = static_cast<uint16_t*>(base_ptr(*out));
         const void* po_ = base_ptr(*expert_offsets);
-        const int variant = env_int("SANDY_MOE_GEMM", avg <= 16 ? 8 : 9);
+        // tile: 16 rows x 32 columns per wave for decode-sized batches, 64 x 64 otherwise
+        const int variant = env_int("SANDY_MOE_GEMM", avg <= 16 ? 0 : 1);
         auto grid_for = [&](int ct) {
             return dim3(static_cast<unsigned>(batch * experts), static_cast<unsigned>((M + 64 * ct - 1) / (64 * ct)));
         };
-#define GEMM_LAUNCH(RT, CT, KU)                                                                                      \
-    hipLaunchKernelGGL((moe_gemm_mfma_kernel<RT, CT, KU>), grid_for(CT), dim3(256), 0, stream, px, po_,           \
-                       expert_offsets->dtype, pw, po, rows, K, M, experts, batch, errw)
 #define LINES_LAUNCH(RT, CT)                                                                                        \
     hipLaunchKernelGGL((moe_gemm_lines_kernel<RT, CT>), grid_for(CT), dim3(256), 0, stream, px, po_,               \
                        expert_offsets->dtype, pw, po, rows, K, M, experts, batch, errw)
         switch (variant) {
-            case 8: LINES_LAUNCH(1, 2); break;
-            case 9: LINES_LAUNCH(4, 4); break;
-            case 10: LINES_LAUNCH(4, 2); break;
-            case 11: LINES_LAUNCH(2, 4); break;
-            case 12: LINES_LAUNCH(2, 2); break;
-            case 0: GEMM_LAUNCH(1, 2, 4); break;
-            case 1: GEMM_LAUNCH(4, 1, 4); break;
-            case 2: GEMM_LAUNCH(4, 2, 2); break;
-            case 3: GEMM_LAUNCH(4, 4, 1); break;
-            case 4: GEMM_LAUNCH(4, 2, 1); break;
-            case 5: GEMM_LAUNCH(2, 2, 2); break;
-            case 6: GEMM_LAUNCH(3, 2, 2); break;
-            default: GEMM_LAUNCH(4, 4, 2); break;
+            case 0: LINES_LAUNCH(1, 2); break;
+            case 2: LINES_LAUNCH(4, 2); break;
+            case 3: LINES_LAUNCH(2, 4); break;
+            case 4: LINES_LAUNCH(2, 2); break;
+            default: LINES_LAUNCH(4, 4); break;
         }
-#undef GEMM_LAUNCH
 #undef LINES_LAUNCH
     } else {
         hipLaunchKernelGGL(validate_offsets_kernel, dim3(static_cast<unsigned>((batch * experts + 255) / 256)), dim3(256), 0, stream,

@@ -124,7 +124,15 @@ def oracle_matmul_experts(oracle, x, off, w, experts, transpose_rhs=True):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("transpose_rhs", [True, False])
-def test_moe_matmul_small(ops, oracle, dtype, transpose_rhs):
+@pytest.mark.parametrize("tile", ["default", "0", "1", "2", "3", "4"])
+def test_moe_matmul_small(ops, oracle, monkeypatch, dtype, transpose_rhs, tile):
+    """Ragged experts (empty, 1 row, more rows than one pass), K with an odd
+    number of 32-wide steps, M not a multiple of a wave's columns; every tile
+    shape of the bf16 kernel."""
+    if tile != "default":
+        if dtype != torch.bfloat16 or not transpose_rhs:
+            pytest.skip("tile shapes apply to the bf16 transpose_rhs kernel")
+        monkeypatch.setenv("SANDY_MOE_GEMM", tile)
     r = rng(21)
     E, K, M = 6, 96, 40
     counts = np.array([0, 5, 17, 1, 40, 70])
