@@ -167,16 +167,59 @@ constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
 constexpr int kRouteStage = 4096;  // routes whose ids and weights are staged in LDS
 
-// One workgroup per batch.  Pass 1 counts routes per expert; pass 2 walks the
-// routes in order, 1024 at a time: inside a wave, lanes routed to the same
-// expert are ranked by ballot; waves are ordered through LDS prefix sums; a
-// per-expert cursor carries across chunks.  dest[r] receives the packed row
-// of route r (token-major route order r = token * top_k + slot).
+// Exclusive scan of the per-expert counts held in cursor[] -> expert offsets
+// (written out) and starting cursors: each wave-0 pass scans a 64-expert
+// segment with shuffles, segments chained serially.
+__device__ __forceinline__ void scan_expert_counts(int32_t* cursor, int64_t experts, void* offsets, int32_t off_dt,
+                                                   int b, int tid, int lane, int wave) {
+    __shared__ int32_t seg_total;
+    if (tid == 0) seg_total = 0;
+    __syncthreads();
+    for (int64_t s0 = 0; s0 < experts; s0 += 64) {
+        if (wave == 0) {
+            const int64_t ex = s0 + lane;
+            const int32_t c = ex < experts ? cursor[ex] : 0;
+            int32_t incl = c;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int32_t up = __shfl_up(incl, d, 64);
+                if (lane >= d) incl += up;
+            }
+            const int32_t base = seg_total;
+            if (ex < experts) {
+                cursor[ex] = base + incl - c;
+                store_index(offsets, off_dt, static_cast<int64_t>(b) * (experts + 1) + ex, base + incl - c);
+            }
+            const int32_t tot = __shfl(incl, 63, 64);
+            if (lane == 0) seg_total = base + tot;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) store_index(offsets, off_dt, static_cast<int64_t>(b) * (experts + 1) + experts, seg_total);
+}
+
+// One workgroup per batch.  dest[r] receives the packed row of route r
+// (token-major route order r = token * top_k + slot); rows of one expert are
+// in route order.
+//
+// BITS (all routes staged in LDS, no token listing an expert twice): a
+// token routes to an expert at most once, so the rank of route (token t,
+// expert e) among e's rows is the number of earlier tokens that chose e --
+// a prefix popcount over a per-expert token bitmask built with LDS atomic
+// ORs.  Every step is O(1) per route.  A repeated (token, expert) pair is
+// detected while the masks are built (the bit is already set) and sends the
+// workgroup to the general ranking below.
+//
+// General ranking: pass 1 counts routes per expert; pass 2 walks the routes
+// in order, 1024 at a time: inside a wave, lanes routed to the same expert
+// are ranked by ballot; waves are ordered through LDS prefix sums; a
+// per-expert cursor carries across chunks.
+template <bool BITS>
 __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         const void* __restrict__ ids, int32_t ids_dt, const void* __restrict__ w, int32_t w_dt, int64_t seq,
         int64_t top_k, int64_t experts, void* __restrict__ packed_w, void* __restrict__ token_ids, int32_t tok_dt,
         void* __restrict__ offsets, int32_t off_dt, int32_t* __restrict__ dest, uint32_t* errw) {
-    extern __shared__ int32_t lds[];
+    extern __shared__ __attribute__((aligned(16))) int32_t lds[];
     int32_t* cursor = lds;                      // [E]
     int32_t* wcount = lds + experts;            // [kRouteWaves][E]
     int32_t* sid = wcount + kRouteWaves * experts;          // staged ids  [kRouteStage]
@@ -199,6 +242,52 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         }
     }
     __syncthreads();
+    if constexpr (BITS) {
+        // [E][W] token bitmasks (64-bit words) and their exclusive prefix popcounts
+        const int64_t W = (seq + 63) / 64;
+        auto* mask = reinterpret_cast<unsigned long long*>(sw + kRouteStage + ((experts * (1 + kRouteWaves)) & 1));
+        int32_t* pref = reinterpret_cast<int32_t*>(mask + experts * W);
+        __shared__ int dup;
+        if (tid == 0) dup = 0;
+        for (int64_t i = tid; i < experts * W; i += kRouteThreads) mask[i] = 0ull;
+        __syncthreads();
+        for (int64_t r = tid; r < routes; r += kRouteThreads) {
+            const int e = sid[r];
+            if (e < 0) continue;
+            const int64_t t = r / top_k;
+            const unsigned long long bit = 1ull << (t & 63);
+            if (atomicOr(&mask[e * W + (t >> 6)], bit) & bit) dup = 1;
+        }
+        __syncthreads();
+        if (!dup) {
+            for (int64_t x = tid; x < experts; x += kRouteThreads) {
+                int32_t run = 0;
+                for (int64_t q = 0; q < W; q++) {
+                    pref[x * W + q] = run;
+                    run += __popcll(mask[x * W + q]);
+                }
+                cursor[x] = run;
+            }
+            __syncthreads();
+            scan_expert_counts(cursor, experts, offsets, off_dt, b, tid, lane, wave);
+            __syncthreads();
+            for (int64_t r = tid; r < routes; r += kRouteThreads) {
+                const int e = sid[r];
+                if (e < 0) {
+                    dest[rb + r] = -1;
+                    continue;
+                }
+                const int64_t t = r / top_k;
+                const unsigned long long m = mask[e * W + (t >> 6)];
+                const int32_t row = cursor[e] + pref[e * W + (t >> 6)] + __popcll(m & ((1ull << (t & 63)) - 1ull));
+                dest[rb + r] = row;
+                store_any(packed_w, w_dt, rb + row, sw[r]);
+                store_index(token_ids, tok_dt, rb + row, t);
+            }
+            return;
+        }
+        // a token lists an expert twice: the general ranking below
+    }
     for (int64_t r = tid; r < routes; r += kRouteThreads) {
         int64_t e;
         if (staged) e = sid[r];
@@ -212,34 +301,7 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         if (e >= 0) atomicAdd(&cursor[e], 1);
     }
     __syncthreads();
-    // exclusive scan of the counts -> offsets and starting cursors: each wave
-    // scans 64-expert segments with shuffles, segments chained serially
-    {
-        __shared__ int32_t seg_total;
-        if (tid == 0) seg_total = 0;
-        __syncthreads();
-        for (int64_t s0 = 0; s0 < experts; s0 += 64) {
-            if (wave == 0) {
-                const int64_t ex = s0 + lane;
-                const int32_t c = ex < experts ? cursor[ex] : 0;
-                int32_t incl = c;
-#pragma unroll
-                for (int d = 1; d < 64; d <<= 1) {
-                    const int32_t up = __shfl_up(incl, d, 64);
-                    if (lane >= d) incl += up;
-                }
-                const int32_t base = seg_total;
-                if (ex < experts) {
-                    cursor[ex] = base + incl - c;
-                    store_index(offsets, off_dt, static_cast<int64_t>(b) * (experts + 1) + ex, base + incl - c);
-                }
-                const int32_t tot = __shfl(incl, 63, 64);
-                if (lane == 0) seg_total = base + tot;
-            }
-            __syncthreads();
-        }
-        if (tid == 0) store_index(offsets, off_dt, static_cast<int64_t>(b) * (experts + 1) + experts, seg_total);
-    }
+    scan_expert_counts(cursor, experts, offsets, off_dt, b, tid, lane, wave);
     __syncthreads();
     for (int64_t c0 = 0; c0 < routes; c0 += kRouteThreads) {
         const int64_t r = c0 + tid;
@@ -714,10 +776,20 @@ extern "C" int sandy_hip_moe_gather(const SandyTensor* x, const SandyTensor* top
     if (status) return status;
     int32_t* dest = static_cast<int32_t*>(device_workspace(2, static_cast<size_t>(batch * routes) * sizeof(int32_t), stream, e, &status));
     if (status) return status;
-    hipLaunchKernelGGL(moe_route_kernel, dim3(static_cast<unsigned>(batch)), dim3(kRouteThreads), lds, stream,
-                       base_ptr(*topk_ids), topk_ids->dtype, base_ptr(*topk_weights), topk_weights->dtype, seq, top_k,
-                       num_experts, base_ptr(*packed_weights), base_ptr(*token_ids), token_ids->dtype,
-                       base_ptr(*expert_offsets), expert_offsets->dtype, dest, errw);
+    // token bitmask ranking when every route is staged and the masks fit
+    const int64_t words = (seq + 63) / 64;
+    const size_t lds_bits = lds + 4 + static_cast<size_t>(num_experts * words) * 12;
+    const bool bits = routes <= kRouteStage && lds_bits <= 64 * 1024 && env_int("SANDY_MOE_ROUTE_GENERAL", 0) == 0;
+    if (bits)
+        hipLaunchKernelGGL(moe_route_kernel<true>, dim3(static_cast<unsigned>(batch)), dim3(kRouteThreads), lds_bits,
+                           stream, base_ptr(*topk_ids), topk_ids->dtype, base_ptr(*topk_weights), topk_weights->dtype,
+                           seq, top_k, num_experts, base_ptr(*packed_weights), base_ptr(*token_ids), token_ids->dtype,
+                           base_ptr(*expert_offsets), expert_offsets->dtype, dest, errw);
+    else
+        hipLaunchKernelGGL(moe_route_kernel<false>, dim3(static_cast<unsigned>(batch)), dim3(kRouteThreads), lds,
+                           stream, base_ptr(*topk_ids), topk_ids->dtype, base_ptr(*topk_weights), topk_weights->dtype,
+                           seq, top_k, num_experts, base_ptr(*packed_weights), base_ptr(*token_ids), token_ids->dtype,
+                           base_ptr(*expert_offsets), expert_offsets->dtype, dest, errw);
     if (routes > 0 && hidden > 0) {
         const int64_t waves = batch * routes;
         const int64_t row_bytes = hidden * static_cast<int64_t>(dtype_size(x->dtype));

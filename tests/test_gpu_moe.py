@@ -68,9 +68,16 @@ def test_router_chain_config5(ops, oracle):
 
 # ------------------------------------------------------------------ moe_gather
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("T,H,E,K", [(512, 2816, 128, 8), (37, 64, 16, 4), (5, 24, 300, 2), (1, 8, 4, 1)])
+@pytest.mark.parametrize("T,H,E,K", [(512, 2816, 128, 8), (37, 64, 16, 4), (5, 24, 300, 2), (1, 8, 4, 1),
+                                     (700, 16, 64, 8), (130, 16, 8, 3)])
 @pytest.mark.parametrize("idx", [np.int64, np.int32])
-def test_moe_gather_bit_exact(ops, oracle, dtype, T, H, E, K, idx):
+@pytest.mark.parametrize("ranking", ["bitmask", "general"])
+def test_moe_gather_bit_exact(ops, oracle, monkeypatch, dtype, T, H, E, K, idx, ranking):
+    """Token bitmask ranking (the default when every route fits in LDS) and
+    the general ballot ranking give the reference's packing bit for bit;
+    700 x 8 routes exceed the staging area and always take the general path."""
+    if ranking == "general":
+        monkeypatch.setenv("SANDY_MOE_ROUTE_GENERAL", "1")
     r = rng(T * 7 + E)
     ids = np.stack([r.permutation(E)[:K] for _ in range(T)]).astype(idx)
     w = np.abs(normal(r, (T, K)))
