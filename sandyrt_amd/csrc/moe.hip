@@ -384,7 +384,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
                                                           const void* __restrict__ tok, int32_t tok_dt,
                                                           void* __restrict__ out, int64_t batch, int64_t rows,
                                                           int64_t hidden, int64_t seq, uint32_t* errw) {
-    __shared__ int32_t ids[kCombineStage];
+    __shared__ __attribute__((aligned(16))) int32_t ids[kCombineStage];
     __shared__ int32_t hit[4][kCombineHits];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t chunks = (hidden + 511) / 512;
@@ -396,11 +396,23 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
     const int64_t mb = b * rows;
     const bool staged = rows <= kCombineStage;
     if (staged) {
-        for (int64_t r = threadIdx.x; r < rows; r += 256) {
-            const int64_t v = load_index(tok, tok_dt, mb + r);
-            if ((v < 0 || v >= seq) && blockIdx.x % (chunks * tgroups) == 0)
-                atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_TOKEN_ID));
-            ids[r] = static_cast<int32_t>(v);
+        // 16 loads per thread in flight at once, then the LDS stores
+        constexpr int kBatch = 16;
+        for (int64_t r0 = threadIdx.x; r0 < rows; r0 += 256 * kBatch) {
+            int64_t v[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; u++) {
+                const int64_t r = r0 + 256 * u;
+                v[u] = load_index(tok, tok_dt, mb + (r < rows ? r : 0));
+            }
+#pragma unroll
+            for (int u = 0; u < kBatch; u++) {
+                const int64_t r = r0 + 256 * u;
+                if (r >= rows) break;
+                if ((v[u] < 0 || v[u] >= seq) && blockIdx.x % (chunks * tgroups) == 0)
+                    atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_TOKEN_ID));
+                ids[r] = static_cast<int32_t>(v[u]);
+            }
         }
     }
     __syncthreads();
@@ -411,27 +423,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) acc[i] = 0.0f;
-    int64_t r0 = 0;
-    while (r0 < rows) {
-        // collect up to kCombineHits rows of token t, in row order
-        int n = 0;
-        for (; r0 < rows && n + 64 <= kCombineHits; r0 += 64) {
-            const int64_t r = r0 + lane;
-            int64_t tr = -1;
-            if (r < rows) {
-                if (staged) tr = ids[r];
-                else {
-                    tr = load_index(tok, tok_dt, mb + r);
-                    if ((tr < 0 || tr >= seq) && t == 0 && ch == 0)
-                        atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_TOKEN_ID));
-                }
-            }
-            const uint64_t hits = __ballot(tr == t);
-            if (tr == t) hit[wave][n + __popcll(hits & ((1ull << lane) - 1ull))] = static_cast<int32_t>(r);
-            n += __popcll(hits);
-        }
-        __builtin_amdgcn_wave_barrier();
-        // accumulate the collected rows, 8 loads in flight at a time
+    // accumulate the n collected rows of hit[wave], 8 loads in flight at a time
+    auto accumulate = [&](int n) {
         for (int g = 0; g < n; g += 8) {
             float pv[8][8];
             float wv[8];
@@ -456,6 +449,71 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
 #pragma unroll
                     for (int i = 0; i < 8; i++) acc[i] = Vec8<T>::round(__fadd_rn(acc[i], __fmul_rn(wv[u], pv[u][i])));
         }
+        __builtin_amdgcn_wave_barrier();
+    };
+    int64_t r0 = 0;
+    if (staged && rows <= 64 * 256) {
+        // each lane scans its own run of `seg` consecutive rows (128-bit LDS
+        // reads) into a bit mask; a wave prefix sum of the hit counts places
+        // the hits in row order
+        const int64_t seg = ((rows + 255) / 256) * 4;  // multiple of 4, at most 256
+        const int64_t s0 = lane * seg;
+        int cnt = 0;
+        uint64_t mk[4] = {0, 0, 0, 0};
+        for (int64_t q = 0; q < seg; q += 4) {
+            const int64_t r = s0 + q;
+            if (r >= rows) break;
+            const int4 v = *reinterpret_cast<const int4*>(&ids[r]);  // rows past the end hold stale ids: masked
+            const int vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (r + i < rows && vv[i] == t) {
+                    mk[(q + i) >> 6] |= 1ull << ((q + i) & 63);
+                    cnt++;
+                }
+        }
+        int excl = cnt;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int up = __shfl_up(excl, d, 64);
+            if (lane >= d) excl += up;
+        }
+        const int n_all = __shfl(excl, 63, 64);
+        excl -= cnt;
+        if (n_all <= kCombineHits) {  // else: the chunked collection below
+#pragma unroll
+            for (int w4 = 0; w4 < 4; w4++) {
+                uint64_t m = mk[w4];
+                while (m) {
+                    hit[wave][excl++] = static_cast<int32_t>(s0 + 64 * w4 + __builtin_ctzll(m));
+                    m &= m - 1;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            accumulate(n_all);
+            r0 = rows;
+        }
+    }
+    while (r0 < rows) {
+        // collect up to kCombineHits rows of token t, in row order
+        int n = 0;
+        for (; r0 < rows && n + 64 <= kCombineHits; r0 += 64) {
+            const int64_t r = r0 + lane;
+            int64_t tr = -1;
+            if (r < rows) {
+                if (staged) tr = ids[r];
+                else {
+                    tr = load_index(tok, tok_dt, mb + r);
+                    if ((tr < 0 || tr >= seq) && t == 0 && ch == 0)
+                        atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_TOKEN_ID));
+                }
+            }
+            const uint64_t hits = __ballot(tr == t);
+            if (tr == t) hit[wave][n + __popcll(hits & ((1ull << lane) - 1ull))] = static_cast<int32_t>(r);
+            n += __popcll(hits);
+        }
+        __builtin_amdgcn_wave_barrier();
+        accumulate(n);
         __builtin_amdgcn_wave_barrier();
     }
     if (c0 < hidden) {
