@@ -150,6 +150,7 @@ def build_workload(replicas):
 
 
 GEM_B, GEM_HQ, GEM_HKV, GEM_D, GEM_HID, GEM_FF, GEM_VOCAB = 64, 8, 2, 256, 2560, 10240, 262144
+GPT2_VOCAB = 50257
 MOE_T, MOE_E, MOE_K, MOE_D, MOE_F = 512, 128, 8, 2816, 704
 
 
@@ -172,7 +173,7 @@ def build_extras(replicas):
     nblk = (ctx + DEC_PAGE - 1) // DEC_PAGE
     maxb = int(nblk.max())
     pool = int(nblk.sum()) + 64
-    names = ["c4_paged_decode", "c4_rms_norm", "c4_geglu", "c4_softcap"]
+    names = ["c4_paged_decode", "c4_rms_norm", "c4_geglu", "c4_softcap", "c4_greedy_argmax"]
     for n in names:
         kernels[n] = []
     for rep in range(replicas):
@@ -198,15 +199,20 @@ def build_extras(replicas):
         act = torch.empty_like(gate)
         logits = (torch.randn(GEM_B, GEM_VOCAB, generator=g, device=dev) * 20).to(bf)
         capped = torch.empty_like(logits)
+        amax_v = torch.empty(GEM_B, 1, dtype=bf, device=dev)
+        amax_i = torch.empty(GEM_B, 1, dtype=torch.int64, device=dev)
         d = {k: desc(v) for k, v in dict(qd=qd, od=od, tt=tt, pt=pt, xg=xg, wg=wg, yg=yg, gate=gate, up=up, act=act,
-                                         logits=logits, capped=capped).items()}
+                                         logits=logits, capped=capped, amax_v=amax_v, amax_i=amax_i).items()}
         gnodes, gres = ops.gelu_mul_nodes()
         snodes, sres = ops.softcap_nodes(30.0)
         cg, cs = ops._nodes(gnodes), ops._nodes(snodes)
         arr2 = (_lib.SandyTensor * 2)(d["gate"].contents, d["up"].contents)
         arr1 = (_lib.SandyTensor * 1)(d["logits"].contents)
         bc = (C.c_int32 * 2)(0, 0)
-        keep += [kpool, vpool, qd, od, tt, pt, kc, vc, xg, wg, yg, gate, up, act, logits, capped, d, cg, cs, arr2, arr1, bc]
+        keep += [kpool, vpool, qd, od, tt, pt, kc, vc, xg, wg, yg, gate, up, act, logits, capped, amax_v, amax_i, d, cg,
+                 cs, arr2, arr1, bc]
+        kernels["c4_greedy_argmax"].append(Prepared("sandy_hip_topk", d["logits"], C.c_int64(1), C.c_int64(-1),
+                                                    d["amax_v"], d["amax_i"]))
         kernels["c4_paged_decode"].append(Prepared("sandy_hip_paged_attention", d["qd"], kc, vc, d["tt"], d["pt"],
                                                    C.c_int64(0), C.c_double(1.0), d["od"]))
         kernels["c4_rms_norm"].append(Prepared("sandy_hip_norm", C.c_int32(0), d["xg"], d["wg"], None,
@@ -220,7 +226,17 @@ def build_extras(replicas):
         "c4_rms_norm": 2 * GEM_B * GEM_HID * 2 + GEM_HID * 2,
         "c4_geglu": 3 * GEM_B * GEM_FF * 2,
         "c4_softcap": 2 * GEM_B * GEM_VOCAB * 2,
+        "c4_greedy_argmax": GEM_B * GEM_VOCAB * 2 + GEM_B * 10,
     }
+    # ---- config 1: greedy token selection over GPT-2's fp32 vocabulary
+    g.manual_seed(1)
+    c1_logits = torch.randn(1, GPT2_VOCAB, generator=g, device=dev)
+    c1_v = torch.empty(1, 1, device=dev)
+    c1_i = torch.empty(1, 1, dtype=torch.int64, device=dev)
+    d1 = {k: desc(v) for k, v in dict(l=c1_logits, v=c1_v, i=c1_i).items()}
+    keep += [c1_logits, c1_v, c1_i, d1]
+    kernels["c1_greedy_argmax"] = [Prepared("sandy_hip_topk", d1["l"], C.c_int64(1), C.c_int64(-1), d1["v"], d1["i"])]
+    bytes_per["c1_greedy_argmax"] = GPT2_VOCAB * 4 + 12
     # ---- config 5 (one copy: the 1.5 GB of expert weights exceed the cache)
     g.manual_seed(4)
     logits = torch.randn(MOE_T, MOE_E, generator=g, device=dev)
@@ -457,7 +473,7 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "cpu_baseline": None,
     }
-    want_extras = not args.no_extras and (not args.only or any(o.startswith(("c4_", "c5_")) for o in args.only.split(",")))
+    want_extras = not args.no_extras and (not args.only or any(o.startswith(("c1_", "c4_", "c5_")) for o in args.only.split(",")))
     if want_extras:
         ek, eb, ekeep = build_extras(args.replicas)
         if args.only:

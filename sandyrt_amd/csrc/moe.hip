@@ -162,6 +162,127 @@ __global__ __launch_bounds__(256) void topk_columns_kernel(const void* __restric
     }
 }
 
+// Long rows (inner == 1, axis > 1024, k <= 16): greedy token selection over a
+// vocabulary is the case that matters.  Phase 1: workgroup (chunk of 4096,
+// row) keeps its 16 elements per thread in registers (loads coalesced per
+// step) and runs k rounds of a block argmax, each round taking the best item
+// strictly after the previous pick in (value desc, index asc) order;
+// phase 2: one workgroup per row merges the chunks' candidates the same way.
+constexpr int kWideChunk = 4096;
+constexpr int kWideMaxK = 16;
+
+__device__ __forceinline__ void take_if_better(float& v, int64_t& i, float ov, int64_t oi) {
+    if (oi >= 0 && (i < 0 || better(ov, oi, v, i))) {
+        v = ov;
+        i = oi;
+    }
+}
+
+// Best (value, index) over the workgroup's 256 threads (index < 0: none);
+// every thread returns the result.
+__device__ __forceinline__ void block_best(float& v, int64_t& i, float* sv, int64_t* si) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o, 64);
+        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(i), o, 64);
+        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(static_cast<uint64_t>(i) >> 32), o, 64);
+        take_if_better(v, i, ov, static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo));
+    }
+    if (lane == 0) {
+        sv[wave] = v;
+        si[wave] = i;
+    }
+    __syncthreads();
+    v = sv[0];
+    i = si[0];
+#pragma unroll
+    for (int w = 1; w < 4; w++) take_if_better(v, i, sv[w], si[w]);
+    __syncthreads();
+}
+
+// VEC: 8-element (16- or 32-byte) loads, thread t covering elements
+// 8t .. 8t + 7 and 2048 + 8t .. of its chunk; else 16 strided scalar loads.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void topk_wide_chunks_kernel(const void* __restrict__ x, int64_t n, int64_t chunks,
+                                                               int k, float* __restrict__ cv, int64_t* __restrict__ ci) {
+    __shared__ float sv[4];
+    __shared__ int64_t si[4];
+    const int64_t c = blockIdx.x, row = blockIdx.y;
+    float v[16];
+    int64_t id[16];
+    if constexpr (VEC) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int64_t i0 = c * kWideChunk + 2048 * h + 8 * threadIdx.x;
+            float part[8];
+            Vec8<T>::load(x, row * n + (i0 < n ? i0 : 0), part);  // n % 8 == 0: a vector is all in or all out
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                v[8 * h + q] = part[q];
+                id[8 * h + q] = i0 + q;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            id[j] = c * kWideChunk + threadIdx.x + 256 * j;
+            v[j] = Vec8<T>::load1(x, row * n + (id[j] < n ? id[j] : 0));
+        }
+    }
+    float pv = 0.0f;
+    int64_t pi = -1;
+    bool done = false;
+    float* ov = cv + (row * chunks + c) * k;
+    int64_t* oi = ci + (row * chunks + c) * k;
+    for (int r = 0; r < k; r++) {
+        float bv = 0.0f;
+        int64_t bi = -1;
+        if (!done) {
+#pragma unroll
+            for (int j = 0; j < 16; j++)
+                if (id[j] < n && (pi < 0 || better(pv, pi, v[j], id[j]))) take_if_better(bv, bi, v[j], id[j]);
+        }
+        block_best(bv, bi, sv, si);
+        if (threadIdx.x == 0) {
+            ov[r] = bv;
+            oi[r] = bi;
+        }
+        done = bi < 0;  // the chunk has fewer than k items: the rest stay empty
+        pv = bv;
+        pi = bi;
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void topk_wide_merge_kernel(const float* __restrict__ cv, const int64_t* __restrict__ ci,
+                                                              int64_t chunks, int k, void* __restrict__ values,
+                                                              void* __restrict__ indices, int32_t idx_dt) {
+    __shared__ float sv[4];
+    __shared__ int64_t si[4];
+    const int64_t row = blockIdx.x;
+    const int64_t m = chunks * k;
+    const float* rv = cv + row * m;
+    const int64_t* ri = ci + row * m;
+    float pv = 0.0f;
+    int64_t pi = -1;
+    for (int r = 0; r < k; r++) {
+        float bv = 0.0f;
+        int64_t bi = -1;
+        for (int64_t j = threadIdx.x; j < m; j += 256) {
+            const int64_t idx = ri[j];
+            if (idx >= 0 && (pi < 0 || better(pv, pi, rv[j], idx))) take_if_better(bv, bi, rv[j], idx);
+        }
+        block_best(bv, bi, sv, si);
+        if (threadIdx.x == 0) {
+            Vec8<T>::store1(values, row * k + r, bv);
+            store_index(indices, idx_dt, row * k + r, bi);
+        }
+        pv = bv;
+        pi = bi;
+    }
+}
+
 // ---------------------------------------------------------------- moe_gather
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
@@ -781,6 +902,29 @@ extern "C" int sandy_hip_topk(const SandyTensor* x, int64_t k, int64_t axis, con
         else { TOPK_LAUNCH(16); }
 #undef TOPK_LAUNCH
 #undef TOPK_RANK
+    } else if (inner == 1 && k <= kWideMaxK && outer <= 65535) {
+        const int64_t chunks = (n + kWideChunk - 1) / kWideChunk;
+        int status = 0;
+        char* ws = static_cast<char*>(
+            device_workspace(3, static_cast<size_t>(outer * chunks * k) * (sizeof(float) + sizeof(int64_t)), stream, e,
+                             &status));
+        if (status) return status;
+        int64_t* ci = reinterpret_cast<int64_t*>(ws);
+        float* cv = reinterpret_cast<float*>(ci + outer * chunks * k);
+        const int kk = static_cast<int>(k);
+        dim3 g1(static_cast<unsigned>(chunks), static_cast<unsigned>(outer));
+        const bool vec = n % 8 == 0 && (reinterpret_cast<uintptr_t>(px) & 31) == 0;
+        if (bf) {
+            if (vec) hipLaunchKernelGGL((topk_wide_chunks_kernel<BF16, true>), g1, dim3(256), 0, stream, px, n, chunks, kk, cv, ci);
+            else hipLaunchKernelGGL((topk_wide_chunks_kernel<BF16, false>), g1, dim3(256), 0, stream, px, n, chunks, kk, cv, ci);
+            hipLaunchKernelGGL(topk_wide_merge_kernel<BF16>, dim3(static_cast<unsigned>(outer)), dim3(256), 0, stream, cv, ci,
+                               chunks, kk, pv, pi, indices->dtype);
+        } else {
+            if (vec) hipLaunchKernelGGL((topk_wide_chunks_kernel<F32, true>), g1, dim3(256), 0, stream, px, n, chunks, kk, cv, ci);
+            else hipLaunchKernelGGL((topk_wide_chunks_kernel<F32, false>), g1, dim3(256), 0, stream, px, n, chunks, kk, cv, ci);
+            hipLaunchKernelGGL(topk_wide_merge_kernel<F32>, dim3(static_cast<unsigned>(outer)), dim3(256), 0, stream, cv, ci,
+                               chunks, kk, pv, pi, indices->dtype);
+        }
     } else {
         const int64_t threads = outer * inner;
         dim3 grid(static_cast<unsigned>((threads + 255) / 256));

@@ -20,8 +20,12 @@ def ops():
 
 # ------------------------------------------------------------------ top-k
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("shape,k", [((512, 128), 8), ((7, 64), 64), ((3, 1000), 17), ((4, 3000), 5), ((1, 1), 1)])
+@pytest.mark.parametrize("shape,k", [((512, 128), 8), ((7, 64), 64), ((3, 1000), 17), ((4, 3000), 5), ((1, 1), 1),
+                                     ((1, 50257), 1), ((2, 262144), 1), ((3, 4097), 16), ((2, 5000), 17),
+                                     ((1, 1025), 1), ((5, 9000), 3)])
 def test_topk_bit_exact(ops, oracle, dtype, shape, k):
+    """Row kernels (axis <= 1024), the two-phase long-row kernels (chunk
+    candidates then a merge; k <= 16) and the column fallback (k = 17)."""
     r = rng(shape[-1] + k)
     xf = np.round(normal(r, shape) * 3) / 3  # frequent ties: index order decides
     x = from_f32(xf, dtype)
@@ -29,6 +33,24 @@ def test_topk_bit_exact(ops, oracle, dtype, shape, k):
     wv, wi = oracle.topk(to_oracle(x), k)
     assert_equal(i, wi, "topk indices")
     assert_equal(v, wv, "topk values")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_greedy_argmax_ties_take_lowest_id(ops, dtype):
+    """Greedy selection over a vocabulary (Sampler.cpp:69-79: stable sort by
+    logit, so equal maxima resolve to the lowest token id), with the maximum
+    repeated across chunk boundaries."""
+    r = rng(3)
+    x = from_f32(normal(r, (3, 262144)), dtype)
+    x[0, 70000] = 30.0
+    x[0, 4095] = 30.0
+    x[0, 200000] = 30.0
+    x[1, 262143] = 31.0
+    x[2, 8191] = 29.0
+    x[2, 8192] = 29.0
+    v, i = ops.topk(x, 1)
+    assert i[:, 0].cpu().tolist() == [4095, 262143, 8191]
+    assert v[:, 0].float().cpu().tolist() == [30.0, 31.0, 29.0]
 
 
 def test_topk_middle_axis_and_i32(ops, oracle):
