@@ -20,7 +20,9 @@
 //   - online softmax in the exp2 domain, per q head (one MFMA column);
 //   - P^T leaves the S^T MFMA already in the B-operand layout of
 //     v_mfma_f32_16x16x16_bf16, and V tiles are transposed through LDS into A
-//     operands, so O^T += V^T P^T runs on MFMA with no register shuffles;
+//     operands with gfx950's transposing ds_read_b64_tr_b16 (one read per
+//     16 x 4 operand), so O^T += V^T P^T runs on MFMA with no register
+//     shuffles;
 //   - work units (sequence, split, kv head) are numbered over the active
 //     splits only, from a prefix scan of the positions, so workgroup ids --
 //     dealt round-robin to the 8 XCDs -- spread the real work evenly across
@@ -285,10 +287,13 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
                 const short4_t pb = pack_p(p[n]);
 #pragma unroll
                 for (int t = 0; t < D / 16; t++) {
-                    short4_t va;
-                    const unsigned char* col = vl + n * 16 * kRow + 2 * (16 * t + (lane & 15));
-#pragma unroll
-                    for (int i = 0; i < 4; i++) va[i] = *reinterpret_cast<const short*>(col + (4 * j + i) * kRow);
+                    // ds_read_b64_tr_b16: in each 16-lane group, lane i gets element i % 4 of the
+                    // 8-byte pieces addressed by lanes 4m + i / 4 (m = 0..3), so pointing lane i at
+                    // key 4j + i / 4, dims 16t + 4(i % 4) .. + 3 yields V[4j + m][16t + i], m = 0..3
+                    const int i = lane & 15;
+                    const unsigned char* src = vl + (n * 16 + 4 * j + (i >> 2)) * kRow + 2 * (16 * t + 4 * (i & 3));
+                    const short4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (short4_t __attribute__((address_space(3)))*)((unsigned char __attribute__((address_space(3)))*)src));
                     acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, acc[t], 0, 0, 0);
                 }
             }
