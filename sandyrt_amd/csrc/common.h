@@ -138,7 +138,11 @@ struct Vec8<BF16> {
         r.y = pack_bf16x2(v[2], v[3]);
         r.z = pack_bf16x2(v[4], v[5]);
         r.w = pack_bf16x2(v[6], v[7]);
-        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p) + i) = r;
+        // streamed output: non-temporal, so it does not sit dirty in L2 until the
+        // end-of-kernel write-back (measured: shorter kernel tails on gfx950)
+        typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
+        __builtin_nontemporal_store(u32x4_nt{r.x, r.y, r.z, r.w},
+                                    reinterpret_cast<u32x4_nt*>(static_cast<uint16_t*>(p) + i));
     }
     // value as it will read back after a store (rounded to bf16)
     __device__ __forceinline__ static float round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
@@ -160,9 +164,10 @@ struct Vec8<F32> {
         v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     }
     __device__ __forceinline__ static void store(void* p, int64_t i, const float (&v)[8]) {
-        float4* q = reinterpret_cast<float4*>(static_cast<float*>(p) + i);
-        q[0] = make_float4(v[0], v[1], v[2], v[3]);
-        q[1] = make_float4(v[4], v[5], v[6], v[7]);
+        typedef float f32x4_nt __attribute__((ext_vector_type(4)));  // streamed output, as for bf16
+        f32x4_nt* q = reinterpret_cast<f32x4_nt*>(static_cast<float*>(p) + i);
+        __builtin_nontemporal_store(f32x4_nt{v[0], v[1], v[2], v[3]}, q);
+        __builtin_nontemporal_store(f32x4_nt{v[4], v[5], v[6], v[7]}, q + 1);
     }
     __device__ __forceinline__ static float round(float f) { return f; }
     __device__ __forceinline__ static float load1(const void* p, int64_t i) { return static_cast<const float*>(p)[i]; }

@@ -79,11 +79,14 @@ __device__ __forceinline__ void st8_bf16(void* p, i64 i, const float* v) {
   r.y = (unsigned)f2bf(v[2]) | ((unsigned)f2bf(v[3]) << 16);
   r.z = (unsigned)f2bf(v[4]) | ((unsigned)f2bf(v[5]) << 16);
   r.w = (unsigned)f2bf(v[6]) | ((unsigned)f2bf(v[7]) << 16);
-  *(uint4*)((u16*)p + i) = r;
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store(u32x4{r.x, r.y, r.z, r.w}, (u32x4*)((u16*)p + i));
 }
 __device__ __forceinline__ void st8_f32(void* p, i64 i, const float* v) {
-  float4* q = (float4*)((float*)p + i);
-  q[0] = make_float4(v[0], v[1], v[2], v[3]); q[1] = make_float4(v[4], v[5], v[6], v[7]);
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  f32x4* q = (f32x4*)((float*)p + i);
+  __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, q);
+  __builtin_nontemporal_store(f32x4{v[4], v[5], v[6], v[7]}, q + 1);
 }
 )";
 
