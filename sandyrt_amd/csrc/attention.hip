@@ -353,10 +353,10 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
             }
         }
         if (final_out) {
-            a.out[b * a.o_sb + (kh * G + gg) * a.o_sh + d] = f32_to_bf16(L > 0.0f ? O / L : 0.0f);
+            __builtin_nontemporal_store(f32_to_bf16(L > 0.0f ? O / L : 0.0f), &a.out[b * a.o_sb + (kh * G + gg) * a.o_sh + d]);
         } else {
             const int64_t slot = slot0 + gg * slot_stride;
-            a.ws_o[slot * D + d] = O;
+            __builtin_nontemporal_store(O, &a.ws_o[slot * D + d]);  // read by the merge kernel from another XCD
             if (d == 0) {
                 a.ws_ml[slot * 2] = M;
                 a.ws_ml[slot * 2 + 1] = L;

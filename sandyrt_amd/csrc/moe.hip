@@ -482,8 +482,9 @@ __global__ __launch_bounds__(256) void moe_copy_rows_kernel(const char* __restri
     const char* src = x + (b * seq + r / top_k) * row_bytes;
     char* dst = packed + (b * routes + row) * row_bytes;
     if (aligned) {
+        typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));
         for (int64_t o = lane * 16; o < row_bytes; o += 64 * 16)
-            *reinterpret_cast<uint4*>(dst + o) = *reinterpret_cast<const uint4*>(src + o);
+            __builtin_nontemporal_store(*reinterpret_cast<const u32x4_nt*>(src + o), reinterpret_cast<u32x4_nt*>(dst + o));
     } else {
         for (int64_t o = lane; o < row_bytes; o += 64) dst[o] = src[o];
     }
@@ -797,7 +798,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
                     for (int i = 0; i < 4; i++) {
                         const int64_t rr = r0 + 16 * t + 4 * (lane >> 4) + i;
                         const int64_t nc = n0 + 16 * c + (lane & 15);
-                        if (rr < end && nc < M) out[yb + rr * M + nc] = f32_to_bf16(acc[t][c][i]);
+                        if (rr < end && nc < M) __builtin_nontemporal_store(f32_to_bf16(acc[t][c][i]), &out[yb + rr * M + nc]);
                     }
         }
     }
