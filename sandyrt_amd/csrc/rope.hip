@@ -259,8 +259,9 @@ extern "C" int sandy_hip_rope(const SandyTensor* x, const SandyTensor* position_
             groups = static_cast<int>(outer);
             per = 1;
         } else {
-            // enough threads to fill 256 CUs (~128K), each reusing its sincos over per heads
-            const int64_t want = 131072;
+            // threads (each reusing its sincos over `per` heads): numel / 32 within
+            // [32K, 128K] -- measured best for C2's q (128K) and k (32K) on gfx950
+            const int64_t want = std::min<int64_t>(131072, std::max<int64_t>(32768, total / 32));
             groups = static_cast<int>(std::min<int64_t>(outer, std::max<int64_t>(1, want / std::max<int64_t>(1, base_threads))));
             per = static_cast<int>((outer + groups - 1) / groups);
             groups = static_cast<int>((outer + per - 1) / per);
