@@ -31,9 +31,13 @@
 //     flight while computing;
 //   - the 4 waves merge in LDS; a sequence of one split is written as final
 //     output, otherwise every unit writes a (max, sum, O[D]) partial to a
-//     persistent workspace and a small second kernel merges the sequence's
-//     splits (log-sum-exp), reading the position alongside the first
-//     partials.  No host round trip and no allocation per call.
+//     persistent workspace, written through to the agent's coherence point,
+//     and the last of the sequence's workgroups for that kv head (an
+//     arrival counter) merges the splits (log-sum-exp) and writes the rows
+//     -- one launch.  The two-launch form (partials, then a merge kernel
+//     reading the position alongside the first partials) is kept behind
+//     SANDY_PAGED_FUSED_MERGE=0.  No host round trip and no allocation per
+//     call.
 // The probabilities fed to the PV product are rounded to bf16 and the
 // normaliser sums those rounded values, so O / L stays a convex combination.
 #include "common.h"
@@ -77,6 +81,8 @@ struct PagedArgs {
     float* ws_o;
     float* ws_ml;
     uint32_t* errw;
+    uint32_t* counters;  // [B, Hkv] arrivals for the fused merge (zero between launches)
+    int32_t fused;       // merge in the last-arriving workgroup of each (sequence, kv head)
 };
 
 __device__ __forceinline__ short4_t pack_p(const float (&p)[4]) {
@@ -179,7 +185,7 @@ __device__ __forceinline__ int64_t lane_read64(int64_t v, int l) {
 template <int D, int NB, int NT, int S>
 __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* smem, int lane, int wave, int b,
                                              int kh, const SplitRange& sr, int64_t tile_a, int64_t tile_b,
-                                             bool final_out, int64_t slot0, int64_t slot_stride) {
+                                             bool final_out, int64_t slot0, int64_t slot_stride, bool coherent) {
     constexpr int kRow = 2 * D + 8;  // bytes per V row in LDS (8-byte pad: conflict-free transposed reads)
     const int G = a.group;
     const int g = lane & 15;
@@ -336,30 +342,39 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
         }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < G * D; idx += 256) {
-        const int gg = idx / D, d = idx % D;
+    for (int idx = threadIdx.x; idx < G * D / 2; idx += 256) {  // two dims per thread
+        const int gg = idx / (D / 2), d = 2 * (idx % (D / 2));
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < 4; w++) M = fmaxf(M, ml[(w * G + gg) * 2]);
-        float O = 0.0f, L = 0.0f;
+        float O0 = 0.0f, O1 = 0.0f, L = 0.0f;
         if (M != -INFINITY) {
 #pragma unroll
             for (int w = 0; w < 4; w++) {
                 const float mw = ml[(w * G + gg) * 2];
                 if (mw == -INFINITY) continue;
                 const float f = exp2f(mw - M);
-                O += red[(w * G + gg) * D + d] * f;
+                O0 += red[(w * G + gg) * D + d] * f;
+                O1 += red[(w * G + gg) * D + d + 1] * f;
                 L += ml[(w * G + gg) * 2 + 1] * f;
             }
         }
         if (final_out) {
-            __builtin_nontemporal_store(f32_to_bf16(L > 0.0f ? O / L : 0.0f), &a.out[b * a.o_sb + (kh * G + gg) * a.o_sh + d]);
+            const uint32_t pair = static_cast<uint32_t>(f32_to_bf16(L > 0.0f ? O0 / L : 0.0f)) |
+                                  (static_cast<uint32_t>(f32_to_bf16(L > 0.0f ? O1 / L : 0.0f)) << 16);
+            __builtin_nontemporal_store(pair, reinterpret_cast<uint32_t*>(&a.out[b * a.o_sb + (kh * G + gg) * a.o_sh + d]));
         } else {
             const int64_t slot = slot0 + gg * slot_stride;
-            __builtin_nontemporal_store(O, &a.ws_o[slot * D + d]);  // read by the merge kernel from another XCD
-            if (d == 0) {
-                a.ws_ml[slot * 2] = M;
-                a.ws_ml[slot * 2 + 1] = L;
+            const uint64_t ov = static_cast<uint64_t>(__float_as_uint(O0)) | (static_cast<uint64_t>(__float_as_uint(O1)) << 32);
+            const uint64_t mv = static_cast<uint64_t>(__float_as_uint(M)) | (static_cast<uint64_t>(__float_as_uint(L)) << 32);
+            uint64_t* po = reinterpret_cast<uint64_t*>(&a.ws_o[slot * D + d]);
+            uint64_t* pm = reinterpret_cast<uint64_t*>(&a.ws_ml[slot * 2]);
+            if (coherent) {  // written through for a workgroup on another XCD (fused merge)
+                __hip_atomic_store(po, ov, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (d == 0) __hip_atomic_store(pm, mv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {  // read by the merge kernel
+                __builtin_nontemporal_store(ov, po);
+                if (d == 0) __builtin_nontemporal_store(mv, pm);
             }
         }
     }
@@ -383,6 +398,7 @@ struct Unit {
     int b, kh, split;
     int64_t pos;
     bool active;
+    int total;  // active units (set when !active)
 };
 
 __device__ __forceinline__ Unit find_unit(const PagedArgs& a, int lin, int split_tiles, int lane) {
@@ -414,7 +430,28 @@ __device__ __forceinline__ Unit find_unit(const PagedArgs& a, int lin, int split
     }
     Unit u{};
     u.active = false;
+    u.total = base;
     return u;
+}
+
+// The i-th sequence (in order) whose position is negative, or -1.  Such a
+// sequence owns no work unit; under the fused merge an idle workgroup (there
+// is at least one per such sequence) writes its zero rows and raises the
+// error flag, which the merge kernel does otherwise.
+__device__ __forceinline__ int negative_sequence(const PagedArgs& a, int i, int lane) {
+    int base = 0;
+    for (int c0 = 0; c0 < a.batch; c0 += 64) {
+        const int bi = c0 + lane;
+        const int64_t p = lane_position(a, bi < a.batch ? bi : 0);
+        const uint64_t neg = __ballot(bi < a.batch && p < 0);
+        const int cnt = __popcll(neg);
+        if (i < base + cnt) {
+            const int rank = __popcll(neg & ((1ull << lane) - 1));
+            return c0 + __builtin_ctzll(__ballot(((neg >> lane) & 1) && rank == i - base));
+        }
+        base += cnt;
+    }
+    return -1;
 }
 
 // OCC: waves per SIMD the register allocation must allow (1 = no limit).  At
@@ -427,14 +464,74 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     constexpr int kSplitTiles = 4 * NT;  // the host passes split_keys == 16 * kSplitTiles
     const Unit u = find_unit(a, blockIdx.x, kSplitTiles, lane);
-    if (!u.active) return;
+    if (!u.active) {
+        if (a.fused) {
+            const int nb = negative_sequence(a, static_cast<int>(blockIdx.x) - u.total, lane);
+            if (nb >= 0) {
+                for (int idx = threadIdx.x; idx < a.hq * D; idx += 256) a.out[nb * a.o_sb + (idx / D) * a.o_sh + idx % D] = 0;
+                if (threadIdx.x == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
+            }
+        }
+        return;
+    }
     const SplitRange sr = seq_range(a, u.pos);
     const int64_t ta = static_cast<int64_t>(u.split) * kSplitTiles;
     const int64_t tb = min<int64_t>(sr.n_tiles, ta + kSplitTiles);
-    const bool whole = sr.n_tiles <= kSplitTiles;
-    attend_piece<D, NB, NT, S>(a, smem, lane, wave, u.b, u.kh, sr, ta, tb, whole,
-                               (static_cast<int64_t>(u.b) * a.hq + u.kh * a.group) * a.max_splits + u.split,
-                               a.max_splits);
+    const int n_splits = (sr.n_tiles + kSplitTiles - 1) / kSplitTiles;
+    const bool whole = n_splits == 1;
+    const int64_t slot0 = (static_cast<int64_t>(u.b) * a.hq + u.kh * a.group) * a.max_splits;
+    attend_piece<D, NB, NT, S>(a, smem, lane, wave, u.b, u.kh, sr, ta, tb, whole, slot0 + u.split, a.max_splits,
+                               a.fused != 0);
+    if (!a.fused || whole) return;
+
+    // Fused merge.  The partials above were written through to the agent's
+    // coherence point; once every thread's stores have completed (the
+    // barrier waits for them), the workgroup counts itself in, and the last
+    // of the sequence's n_splits workgroups for this kv head reads every
+    // split's partial with agent-scope loads, writes the output rows and
+    // re-arms the counter for the next launch.
+    __shared__ int is_last;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's write-through stores acknowledged
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t* ctr = a.counters + static_cast<int64_t>(u.b) * a.hkv + u.kh;
+        const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        is_last = prev == static_cast<uint32_t>(n_splits - 1);
+        if (is_last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!is_last) return;
+    const int G = a.group;
+    for (int idx = threadIdx.x; idx < G * D / 2; idx += 256) {
+        const int gg = idx / (D / 2), d = 2 * (idx % (D / 2));
+        float M = -INFINITY, L = 0.0f, O0 = 0.0f, O1 = 0.0f;
+        for (int s0 = 0; s0 < n_splits; s0 += 8) {
+            uint64_t mv[8], ov[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const int64_t slot = slot0 + gg * a.max_splits + (s0 + q < n_splits ? s0 + q : 0);
+                mv[q] = __hip_atomic_load(reinterpret_cast<uint64_t*>(&a.ws_ml[slot * 2]), __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+                ov[q] = __hip_atomic_load(reinterpret_cast<uint64_t*>(&a.ws_o[slot * D + d]), __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const float ms = __uint_as_float(static_cast<uint32_t>(mv[q]));
+                if (s0 + q >= n_splits || ms == -INFINITY) continue;
+                const float mn = fmaxf(M, ms);
+                const float fo = M == -INFINITY ? 0.0f : exp2f(M - mn);
+                const float fs = exp2f(ms - mn);
+                L = L * fo + __uint_as_float(static_cast<uint32_t>(mv[q] >> 32)) * fs;
+                O0 = O0 * fo + __uint_as_float(static_cast<uint32_t>(ov[q])) * fs;
+                O1 = O1 * fo + __uint_as_float(static_cast<uint32_t>(ov[q] >> 32)) * fs;
+                M = mn;
+            }
+        }
+        const uint32_t pair = static_cast<uint32_t>(f32_to_bf16(L > 0.0f ? O0 / L : 0.0f)) |
+                              (static_cast<uint32_t>(f32_to_bf16(L > 0.0f ? O1 / L : 0.0f)) << 16);
+        *reinterpret_cast<uint32_t*>(&a.out[u.b * a.o_sb + (u.kh * G + gg) * a.o_sh + d]) = pair;
+    }
 }
 
 // Combines the split partials of one (sequence, q head) under the split-unit
@@ -727,7 +824,8 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
 
     const bool aligned = ((reinterpret_cast<uintptr_t>(base_ptr(*q)) | reinterpret_cast<uintptr_t>(kc->pool) |
                            reinterpret_cast<uintptr_t>(vc->pool)) & 15u) == 0 &&
-                         q->strides[0] % 8 == 0 && q->strides[1] % 8 == 0;
+                         q->strides[0] % 8 == 0 && q->strides[1] % 8 == 0 && out->strides[0] % 2 == 0 &&
+                         out->strides[1] % 2 == 0 && (reinterpret_cast<uintptr_t>(base_ptr(*out)) & 3u) == 0;
     const bool mfma = q->dtype == SANDY_BF16 && (D == 64 || D == 128 || D == 256) && G <= 16 && P % 16 == 0 &&
                       table->dims[1] > 0 &&
                       aligned && env_int("SANDY_PAGED_GENERIC", 0) == 0;
@@ -759,6 +857,12 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         a.scale_log2 = sc * kLog2e;
         a.batch = static_cast<int32_t>(B);
         a.errw = errw;
+        a.fused = env_int("SANDY_PAGED_FUSED_MERGE", 1);
+        if (a.fused) {
+            a.counters = static_cast<uint32_t*>(
+                device_counters(0, static_cast<size_t>(B * hkv) * sizeof(uint32_t), stream, e, &status));
+            if (status) return status;
+        }
         const int64_t max_keys = max_blocks * P;
         const int nb = D == 64 ? 2 : 1;
         const size_t lds_v = 4 * nb * 16 * (2 * D + 8);
@@ -766,9 +870,10 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         const size_t lds = std::max(lds_v, lds_r);
         dim3 mgrid(static_cast<unsigned>(hq), static_cast<unsigned>(B));
         void* args[] = {&a};
-        // split units of 64*NT keys; about 2048 units at the longest context
+        // split units of 64*NT keys; about 1024 units at the longest context
+        // (measured best with the fused merge: config 3 at 512 keys, config 4 at 1024)
         int64_t split = env_int("SANDY_PAGED_SPLIT", 0);
-        if (split <= 0) split = (max_keys * B * hkv) / 2048;
+        if (split <= 0) split = (max_keys * B * hkv) / 1024;
         const int nt = split <= 256 ? 4 : split <= 512 ? 8 : 16;
         split = 64 * nt;
         a.split_keys = static_cast<int32_t>(split);
@@ -785,7 +890,8 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         const void* mfn = D == 64 ? reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<64>)
                         : D == 128 ? reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<128>)
                                    : reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<256>);
-        SANDY_HIP_TRY(hipLaunchKernel(mfn, mgrid, dim3(64), args, 0, stream), e, "paged attention merge launch");
+        if (!a.fused)
+            SANDY_HIP_TRY(hipLaunchKernel(mfn, mgrid, dim3(64), args, 0, stream), e, "paged attention merge launch");
         SANDY_HIP_TRY(hipGetLastError(), e, "paged attention launch");
         return ok(e);
     }

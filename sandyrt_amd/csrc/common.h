@@ -99,6 +99,10 @@ uint32_t* device_error_word(Err e, int* status);
 // need zeroed memory keep it zero themselves.
 void* device_workspace(int slot, size_t bytes, hipStream_t stream, Err e, int* status);
 
+// Zero-initialised per-device counters; zeroed when (re)allocated, kept zero
+// afterwards by the kernels that use them.
+void* device_counters(int slot, size_t bytes, hipStream_t stream, Err e, int* status);
+
 
 // ---------------------------------------------------------------- device helpers
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }

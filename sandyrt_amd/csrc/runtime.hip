@@ -19,6 +19,8 @@ struct DeviceState {
     uint32_t* error_word = nullptr;
     void* ws[kSlots] = {};
     size_t ws_bytes[kSlots] = {};
+    void* ctr[kSlots] = {};
+    size_t ctr_bytes[kSlots] = {};
 };
 
 std::mutex g_mu;
@@ -78,6 +80,34 @@ void* device_workspace(int slot, size_t bytes, hipStream_t stream, Err e, int* s
     }
     (void)stream;
     return s.ws[slot];
+}
+
+void* device_counters(int slot, size_t bytes, hipStream_t stream, Err e, int* status) {
+    int dev = 0;
+    *status = current_device(e, &dev);
+    if (*status) return nullptr;
+    if (bytes == 0) bytes = 256;
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceState& s = g_dev[dev];
+    if (s.ctr_bytes[slot] < bytes) {
+        if (s.ctr[slot]) {
+            hipDeviceSynchronize();
+            hipFree(s.ctr[slot]);
+            s.ctr[slot] = nullptr;
+            s.ctr_bytes[slot] = 0;
+        }
+        size_t grown = bytes + bytes / 4;
+        hipError_t st = hipMalloc(&s.ctr[slot], grown);
+        if (st == hipSuccess) st = hipMemset(s.ctr[slot], 0, grown);
+        if (st == hipSuccess) st = hipDeviceSynchronize();
+        if (st != hipSuccess) {
+            *status = fail(e, SANDY_ERR_HIP, "counter allocation of %zu bytes: %s", grown, hipGetErrorString(st));
+            return nullptr;
+        }
+        s.ctr_bytes[slot] = grown;
+    }
+    (void)stream;
+    return s.ctr[slot];
 }
 
 } // namespace sandy_hip

@@ -184,24 +184,30 @@ def test_dense_attention_seeded_fuzz(ops, oracle):
         np.testing.assert_allclose(got.cpu().numpy(), want, atol=5e-4, err_msg=f"iteration {it}")
 
 
+@pytest.mark.parametrize("fused", ["0", "1"])
 @pytest.mark.parametrize("split", ["128", "256", "512", "2048"])
-def test_paged_decode_split_sizes(ops, oracle, monkeypatch, split):
+def test_paged_decode_split_sizes(ops, oracle, monkeypatch, split, fused):
     """Every split size (one split per sequence written as final output,
-    several merged) matches the oracle; repeated launches agree bit for bit."""
+    several merged by the merge kernel or by the last workgroup of each
+    sequence and kv head) matches the oracle; repeated launches agree bit
+    for bit."""
     monkeypatch.setenv("SANDY_PAGED_SPLIT", split)
+    monkeypatch.setenv("SANDY_PAGED_FUSED_MERGE", fused)
     out1 = run_case(ops, oracle, 40, 5, 32, 4, 64, 16, [1, 300, 1500, 2049, 700], torch.bfloat16)
     out2 = run_case(ops, oracle, 40, 5, 32, 4, 64, 16, [1, 300, 1500, 2049, 700], torch.bfloat16)
     assert torch.equal(out1, out2)
 
 
+@pytest.mark.parametrize("fused", ["0", "1"])
 @pytest.mark.parametrize("split", ["128", "2048"])
 @pytest.mark.parametrize("pos_dtype", [torch.int32, torch.int64])
-def test_paged_decode_negative_position(ops, oracle, monkeypatch, pos_dtype, split):
+def test_paged_decode_negative_position(ops, oracle, monkeypatch, pos_dtype, split, fused):
     """A negative position raises the reference's error when the device
     errors are read; the other sequences are still attended correctly and the
     bad row comes out zero (it owns no work unit)."""
     from sandyrt_amd._lib import SandyError
     monkeypatch.setenv("SANDY_PAGED_SPLIT", split)
+    monkeypatch.setenv("SANDY_PAGED_FUSED_MERGE", fused)
     r = rng(91)
     ctx = [100, 50, 700, 1]
     q, kpool, vpool, table, pos = make_paged(r, 4, 8, 2, 64, 16, ctx, 80, torch.bfloat16)
