@@ -798,7 +798,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
                     for (int i = 0; i < 4; i++) {
                         const int64_t rr = r0 + 16 * t + 4 * (lane >> 4) + i;
                         const int64_t nc = n0 + 16 * c + (lane & 15);
-                        if (rr < end && nc < M) __builtin_nontemporal_store(f32_to_bf16(acc[t][c][i]), &out[yb + rr * M + nc]);
+                        if (rr < end && nc < M) out[yb + rr * M + nc] = f32_to_bf16(acc[t][c][i]);  // 2-byte: L2 combines them
                     }
         }
     }
