@@ -454,9 +454,9 @@ __device__ __forceinline__ int negative_sequence(const PagedArgs& a, int i, int 
     return -1;
 }
 
-// OCC: waves per SIMD the register allocation must allow (1 = no limit).  At
-// 5, config 3's shape still needs no scratch and every work unit of a 32 x
-// 4K-context step is resident at once (1280 workgroup slots).
+// OCC: waves per SIMD the register allocation must allow (1 = no limit).  The
+// D = 64 four-tile kernel (256-key splits) is held to 5, where it needs no
+// scratch and 1280 of its workgroups are resident at once.
 template <int D, int NB, int NT, int S, int OCC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void paged_decode_units_kernel(PagedArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
