@@ -151,17 +151,9 @@ def oracle_matmul_experts(oracle, x, off, w, experts, transpose_rhs=True):
     return out
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("transpose_rhs", [True, False])
-@pytest.mark.parametrize("tile", ["default", "0", "1", "2", "3", "4"])
-def test_moe_matmul_small(ops, oracle, monkeypatch, dtype, transpose_rhs, tile):
+def _moe_matmul_ragged(ops, oracle, dtype, transpose_rhs):
     """Ragged experts (empty, 1 row, more rows than one pass), K with an odd
-    number of 32-wide steps, M not a multiple of a wave's columns; every tile
-    shape of the bf16 kernel."""
-    if tile != "default":
-        if dtype != torch.bfloat16 or not transpose_rhs:
-            pytest.skip("tile shapes apply to the bf16 transpose_rhs kernel")
-        monkeypatch.setenv("SANDY_MOE_GEMM", tile)
+    number of 32-wide steps, M not a multiple of a wave's columns."""
     r = rng(21)
     E, K, M = 6, 96, 40
     counts = np.array([0, 5, 17, 1, 40, 70])
@@ -171,6 +163,19 @@ def test_moe_matmul_small(ops, oracle, monkeypatch, dtype, transpose_rhs, tile):
     got = ops.moe_matmul(x, torch.from_numpy(off).cuda(), w, transpose_rhs)
     want = oracle.moe_matmul(to_oracle(x), off, to_oracle(w), transpose_rhs)
     assert_close(got, want, dtype, "moe_matmul")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("transpose_rhs", [True, False])
+def test_moe_matmul_small(ops, oracle, dtype, transpose_rhs):
+    _moe_matmul_ragged(ops, oracle, dtype, transpose_rhs)
+
+
+@pytest.mark.parametrize("tile", ["0", "1", "2", "3", "4"])
+def test_moe_matmul_tile_shapes(ops, oracle, monkeypatch, tile):
+    """Every tile shape of the bf16 grouped-GEMM kernel on the ragged case."""
+    monkeypatch.setenv("SANDY_MOE_GEMM", tile)
+    _moe_matmul_ragged(ops, oracle, torch.bfloat16, True)
 
 
 @pytest.mark.parametrize("shape", ["gate", "down"])
