@@ -231,6 +231,26 @@ int sandy_hip_moe_scatter_sum(const SandyTensor* packed_out, const SandyTensor* 
                               const SandyTensor* token_ids, const SandyTensor* out,
                               void* stream, char* err, size_t err_cap);
 
+/* ---------------------------------------------------------------- dense matmul */
+
+/* MatMulKernelOp (src/ir/KernelIR.h:447-471; replaces launch_cuda_matmul,
+ * src/device/cuda/CudaMatMulKernels.cu:221-292, and its cuBLAS call at
+ * 173-216).  lhs [.., M, K] (or [.., K, M] when transpose_lhs), rhs [.., K, N]
+ * (or [.., N, K] when transpose_rhs), out [batch.., M, N]; batch dims
+ * broadcast as in src/core/ShapeUtil.cpp:39-71 (1, equal, or a multiple:
+ * grouped heads).  Same float dtype everywhere, contiguous views.  bf16 with
+ * transpose_rhs runs on MFMA (fp32 accumulation); every other case keeps the
+ * reference's per-output k order. */
+int sandy_hip_matmul(const SandyTensor* lhs, const SandyTensor* rhs, int32_t transpose_lhs,
+                     int32_t transpose_rhs, const SandyTensor* out, void* stream, char* err, size_t err_cap);
+
+/* LinearKernelOp (src/ir/KernelIR.h:426-445; CPU semantics src/core/
+ * TensorCalc.cpp:722-773 -- the reference's CUDA device rejects it,
+ * src/device/cuda/CudaDevice.cpp:536-537): out[.., o] = bias[o] +
+ * sum_i x[.., i] * weight[o, i]. */
+int sandy_hip_linear(const SandyTensor* x, const SandyTensor* weight, const SandyTensor* bias,
+                     const SandyTensor* out, void* stream, char* err, size_t err_cap);
+
 /* ---------------------------------------------------------------- device runtime
  *
  * A HIP device object with the reference Device's responsibilities

@@ -255,17 +255,26 @@ class Oracle:
                    C.c_int(dtype_code(token_ids)), C.c_int(dtype_code(packed_out)), b, rows, hidden, seq, _p(out))
         return out[0] if squeeze else out
 
-    def matmul(self, lhs, rhs, transpose_rhs=False):
-        squeeze = lhs.ndim == 2
-        if squeeze:
-            lhs = lhs[None]
-        b, m, k = lhs.shape
-        rhs_batched = rhs.ndim == 3
-        n = rhs.shape[-2] if transpose_rhs else rhs.shape[-1]
-        out = np.empty((b, m, n), dtype=lhs.dtype)
-        self._call("matmul", _p(lhs), _p(np.ascontiguousarray(rhs)), _p(out), C.c_int(dtype_code(lhs)), b, m, k, n,
-                   C.c_int(int(rhs_batched)), C.c_int(int(transpose_rhs)))
-        return out[0] if squeeze else out
+    @staticmethod
+    def matmul_shape(lshape, rshape, transpose_lhs=False, transpose_rhs=False):
+        """output shape of matmul (ShapeUtil.cpp:39-71 batch broadcast)"""
+        lb, rb = list(lshape[:-2]), list(rshape[:-2])
+        rank = max(len(lb), len(rb))
+        lb = [1] * (rank - len(lb)) + lb
+        rb = [1] * (rank - len(rb)) + rb
+        batch = [a if a == b or b == 1 or (a > b and a % b == 0) else b for a, b in zip(lb, rb)]
+        m = lshape[-1] if transpose_lhs else lshape[-2]
+        n = rshape[-2] if transpose_rhs else rshape[-1]
+        return tuple(batch) + (m, n)
+
+    def matmul(self, lhs, rhs, transpose_lhs=False, transpose_rhs=False):
+        lhs, rhs = np.ascontiguousarray(lhs), np.ascontiguousarray(rhs)
+        out = np.empty(self.matmul_shape(lhs.shape, rhs.shape, transpose_lhs, transpose_rhs), dtype=lhs.dtype)
+        ld = (C.c_int64 * lhs.ndim)(*lhs.shape)
+        rd = (C.c_int64 * rhs.ndim)(*rhs.shape)
+        self._call("matmul", _p(lhs), ld, C.c_int(lhs.ndim), _p(rhs), rd, C.c_int(rhs.ndim),
+                   C.c_int(int(transpose_lhs)), C.c_int(int(transpose_rhs)), _p(out), C.c_int(dtype_code(lhs)))
+        return out
 
     def linear(self, x, weight, bias):
         rows = x.size // x.shape[-1]

@@ -5,6 +5,7 @@
 // reference sources where they lie; never part of the product path.
 //
 // Signatures mirror sandy_oracle.h (prefix ref_ instead of oracle_).
+#include "ShapeUtil.h"
 #include "TensorCalc.h"
 
 #include <cstdint>
@@ -168,12 +169,20 @@ int ref_unary(int op, const void* x, void* out, int dtype, int64_t n) {
     return -1;
 }
 
-int ref_matmul(const void* lhs, const void* rhs, void* out, int dtype, int64_t batch, int64_t m,
-               int64_t k, int64_t n, int rhs_batched, int transpose_rhs) {
-    std::vector<int64_t> rdims = transpose_rhs ? std::vector<int64_t>{n, k} : std::vector<int64_t>{k, n};
-    if (rhs_batched) rdims.insert(rdims.begin(), batch);
-    return ret(sandy::core::matmul(in(lhs, {batch, m, k}, dtype), in(rhs, rdims, dtype), false,
-                                   transpose_rhs != 0, outref(out, {batch, m, n}, dtype)));
+int ref_matmul(const void* lhs, const int64_t* ldims, int lrank, const void* rhs, const int64_t* rdims, int rrank,
+               int transpose_lhs, int transpose_rhs, void* out, int dtype) {
+    std::vector<int64_t> ld(ldims, ldims + lrank), rd(rdims, rdims + rrank);
+    std::vector<int64_t> lb(ld.begin(), ld.end() - 2), rb(rd.begin(), rd.end() - 2);
+    auto bs = sandy::core::matmul_batch_shape(Shape(lb), Shape(rb));
+    if (!bs) {
+        g_err = bs.error();
+        return -1;
+    }
+    std::vector<int64_t> od = bs.take().dims();
+    od.push_back(ld[lrank - (transpose_lhs ? 1 : 2)]);
+    od.push_back(rd[rrank - (transpose_rhs ? 2 : 1)]);
+    return ret(sandy::core::matmul(in(lhs, ld, dtype), in(rhs, rd, dtype), transpose_lhs != 0, transpose_rhs != 0,
+                                   outref(out, od, dtype)));
 }
 
 int ref_linear(const void* x, const void* w, const void* b, void* out, int dtype, int64_t rows,

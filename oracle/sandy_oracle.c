@@ -476,20 +476,77 @@ int oracle_moe_scatter_sum(const void* packed_out, const void* packed_weights,
     return 0;
 }
 
-/* TensorCalc.cpp:804-919 matmul (plain loop path): out[b, m, n] = sum_k
- * lhs[b, m, k] * rhs[(b), k, n] (or rhs[(b), n, k] when transpose_rhs) */
-int oracle_matmul(const void* lhs, const void* rhs, void* out, int dtype,
-                  int64_t batch, int64_t m, int64_t k, int64_t n,
-                  int rhs_batched, int transpose_rhs) {
+/* ShapeUtil.cpp:39-71 matmul_batch_shape: right-aligned; equal dims, a 1, or
+ * one dim a multiple of the other (grouped heads) */
+static int batch_shape(const int64_t* l, int lr, const int64_t* r, int rr, int64_t* out) {
+    int orank = lr > rr ? lr : rr;
+    for (int i = 0; i < orank; i++) {
+        int li = lr - 1 - i, ri = rr - 1 - i;
+        int64_t a = li >= 0 ? l[li] : 1, b = ri >= 0 ? r[ri] : 1, o;
+        if (a == b) o = a;
+        else if (a == 1) o = b;
+        else if (b == 1) o = a;
+        else if (a > b && a % b == 0) o = a;
+        else if (b > a && b % a == 0) o = b;
+        else return -1;
+        out[orank - 1 - i] = o;
+    }
+    return orank;
+}
+
+/* TensorCalc.cpp:213-240 matmul_batch_offset: a source dim of 1 broadcasts; a
+ * smaller source dim d serves batch/d consecutive output coordinates */
+static int64_t batch_offset(int64_t index, const int64_t* bshape, int brank, const int64_t* sdims, int srank) {
+    int sb = srank - 2;
+    if (sb <= 0) return 0;
+    int64_t strides[16], s = 1;
+    for (int d = srank - 1; d >= 0; d--) {
+        strides[d] = s;
+        s *= sdims[d];
+    }
+    int64_t off = 0, rem = index;
+    int shift = brank - sb;
+    for (int bd = brank - 1; bd >= 0; bd--) {
+        int64_t dim = bshape[bd], coord = rem % dim;
+        rem /= dim;
+        int sd = bd - shift;
+        if (sd < 0 || sdims[sd] == 1) continue;
+        if (sdims[sd] != dim) coord /= dim / sdims[sd];
+        off += coord * strides[sd];
+    }
+    return off;
+}
+
+/* TensorCalc.cpp:804-919 matmul (plain loop path): for every output batch,
+ * out[m, n] = sum over k in order of lhs[m, k] * rhs[k, n] (operands read
+ * transposed when asked), float accumulation, row-major contiguous operands
+ * of rank >= 2 */
+int oracle_matmul(const void* lhs, const int64_t* ldims, int lrank, const void* rhs, const int64_t* rdims,
+                  int rrank, int transpose_lhs, int transpose_rhs, void* out, int dtype) {
     if (!is_float(dtype)) return fail("matmul lhs unsupported dtype");
-    for (int64_t b = 0; b < batch; b++) {
-        int64_t lb = b * m * k, rb = rhs_batched ? b * k * n : 0, ob = b * m * n;
+    if (lrank < 2) return fail("matmul lhs must have rank >= 2");
+    if (rrank < 2) return fail("matmul rhs must have rank >= 2");
+    if (lrank > 14 || rrank > 14) return fail("matmul rank too large");
+    int64_t m = ldims[lrank - (transpose_lhs ? 1 : 2)], lk = ldims[lrank - (transpose_lhs ? 2 : 1)];
+    int64_t rk = rdims[rrank - (transpose_rhs ? 1 : 2)], n = rdims[rrank - (transpose_rhs ? 2 : 1)];
+    if (lk != rk) return fail("matmul contracting dimension mismatch");
+    int64_t bshape[16];
+    int brank = batch_shape(ldims, lrank - 2, rdims, rrank - 2, bshape);
+    if (brank < 0) return fail("cannot broadcast matmul batch shapes");
+    int64_t batches = 1;
+    for (int i = 0; i < brank; i++) batches *= bshape[i];
+    int64_t lrs = ldims[lrank - 1], rrs = rdims[rrank - 1];  /* row strides */
+    for (int64_t b = 0; b < batches; b++) {
+        int64_t lb = batch_offset(b, bshape, brank, ldims, lrank);
+        int64_t rb = batch_offset(b, bshape, brank, rdims, rrank);
+        int64_t ob = b * m * n;
         for (int64_t r = 0; r < m; r++) {
             for (int64_t c = 0; c < n; c++) {
                 float acc = 0.0f;
-                for (int64_t i = 0; i < k; i++) {
-                    int64_t ri = transpose_rhs ? c * k + i : i * n + c;
-                    float prod = ld(lhs, dtype, lb + r * k + i) * ld(rhs, dtype, rb + ri);
+                for (int64_t i = 0; i < lk; i++) {
+                    int64_t li = transpose_lhs ? i * lrs + r : r * lrs + i;
+                    int64_t ri = transpose_rhs ? c * rrs + i : i * rrs + c;
+                    float prod = ld(lhs, dtype, lb + li) * ld(rhs, dtype, rb + ri);
                     acc += prod;
                 }
                 st(out, dtype, ob + r * n + c, acc);

@@ -88,9 +88,8 @@ int oracle_moe_scatter_sum(const void* packed_out, const void* packed_weights,
                            const void* token_ids, int tok_dtype, int dtype,
                            int64_t batch, int64_t rows, int64_t hidden, int64_t seq,
                            void* out);
-int oracle_matmul(const void* lhs, const void* rhs, void* out, int dtype,
-                  int64_t batch, int64_t m, int64_t k, int64_t n,
-                  int rhs_batched, int transpose_rhs);
+int oracle_matmul(const void* lhs, const int64_t* ldims, int lrank, const void* rhs, const int64_t* rdims,
+                  int rrank, int transpose_lhs, int transpose_rhs, void* out, int dtype);
 int oracle_linear(const void* x, const void* weight, const void* bias, void* out, int dtype,
                   int64_t rows, int64_t in_features, int64_t out_features);
 

@@ -54,6 +54,8 @@ inline int64_t numel(const SandyTensor& t) {
 }
 
 inline bool contiguous(const SandyTensor& t) {
+    for (int i = 0; i < t.rank; i++)
+        if (t.dims[i] == 0) return true;  // empty: no element is addressed
     int64_t s = 1;
     for (int i = t.rank - 1; i >= 0; i--) {
         if (t.dims[i] != 1 && t.strides[i] != s) return false;

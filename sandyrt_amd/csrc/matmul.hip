@@ -1,0 +1,547 @@
+// matmul.hip -- dense matmul and linear (the projections and the lm-head).
+//
+// Semantics (src/core/TensorCalc.cpp):
+//   matmul 804-919   for every batch of the broadcast batch shape
+//                    (ShapeUtil.cpp:39-71; a smaller batch dim d serves
+//                    batch/d consecutive output coordinates, TensorCalc.cpp:
+//                    213-240), out[m, n] = sum over k in order of
+//                    lhs[m, k] * rhs[k, n], either operand read transposed;
+//                    float accumulation
+//   linear 722-773   out[r, o] = bias[o] + sum over i in order of
+//                    x[r, i] * w[o, i]
+// Validation follows launch_cuda_matmul (src/device/cuda/
+// CudaMatMulKernels.cu:78-141): same float dtype, contiguous views, rank >= 2,
+// matching contracting dims and the exact output shape.
+//
+// The reference hands both to cuBLAS (cublasGemmEx, CudaMatMulKernels.cu:
+// 173-216; its CUDA linear is not implemented, CudaDevice.cpp:536-537).
+// Here there are two kernels:
+//   - gemm_lines_kernel: bf16 with the weight read row-major as [n, k]
+//     (transpose_rhs, the layout of every projection and the lm-head) on
+//     v_mfma_f32_16x16x32_bf16.  Decode-sized products are weight streams
+//     (tens of rows against megabytes of weights), so the kernel splits K
+//     over workgroups when the column tiles alone cannot fill the chip, and
+//     the last-arriving workgroup of each output tile sums the fp32 partials
+//     in split order (deterministic) -- one launch, no second reduction pass;
+//   - gemm_simt_kernel: every other case (f32, either operand transposed,
+//     unaligned shapes).  Register-tiled FMA-free float loops that keep the
+//     reference's k order per output, so f32 results are bit-identical to the
+//     CPU path.
+#include "common.h"
+
+#include <algorithm>
+#include <cstdlib>
+
+namespace sandy_hip {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+int env_int(const char* name, int dflt) {
+    const char* v = std::getenv(name);
+    return v && *v ? std::atoi(v) : dflt;
+}
+
+// Element offsets of batch index b in each operand.  For each output batch
+// dim d (innermost first): coordinate c = b mod dims[d]; an operand adds
+// (c / div[d]) * stride[d] (stride 0 where it broadcasts a size-1 or absent
+// dim; div = out dim / operand dim for a grouped dim).
+struct BatchMap {
+    int32_t rank;
+    int64_t dims[SANDY_HIP_MAX_RANK];
+    int64_t l_stride[SANDY_HIP_MAX_RANK], l_div[SANDY_HIP_MAX_RANK];
+    int64_t r_stride[SANDY_HIP_MAX_RANK], r_div[SANDY_HIP_MAX_RANK];
+};
+
+__device__ __forceinline__ void batch_offsets(const BatchMap& m, int64_t b, int64_t& lo, int64_t& ro) {
+    lo = 0;
+    ro = 0;
+    for (int d = m.rank - 1; d >= 0; d--) {
+        const int64_t c = b % m.dims[d];
+        b /= m.dims[d];
+        lo += (c / m.l_div[d]) * m.l_stride[d];
+        ro += (c / m.r_div[d]) * m.r_stride[d];
+    }
+}
+
+struct GemmArgs {
+    const uint16_t* a;     // [.., M, K]
+    const uint16_t* w;     // [.., N, K]
+    const uint16_t* bias;  // [N] or null
+    uint16_t* out;         // [batch, M, N]
+    int64_t M, N, K;
+    int32_t col_tiles, row_tiles, splits, split_chunks;
+    float* part;           // [tiles, splits, 4 waves, RT * CT * 64 lanes * 4]
+    uint32_t* counters;    // [tiles] arrivals (zero between launches)
+    BatchMap bm;
+};
+
+// Workgroup = (column tile of 64 * CT, row tile of 16 * RT, batch, K split);
+// wave w owns columns n0 = (tile * 4 + w) * 16 * CT .. + 16 * CT.  Per chunk
+// of 64 k the workgroup stages its activation rows once in LDS and each wave
+// its own weight rows, both as whole 128-byte lines (8 rows x 128 bytes per
+// load instruction: on gfx950 that streams at about 5.0 TB/s against 3.2 TB/s
+// for MFMA-layout half lines) into tiles whose 16-byte pieces are XOR-swizzled
+// by (row / 2) % 8, so the 128-bit LDS writes and the MFMA-layout 128-bit
+// reads are conflict-free.  Tiles are double buffered: chunk c + 1's loads
+// are in flight while chunk c multiplies.  Loads go through buffer resources
+// whose range checks return zero past the operand's last row; every offset is
+// in the checked vector offset.
+template <int RT, int CT, int OCC, bool SPLIT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void gemm_lines_kernel(GemmArgs g) {
+    constexpr int kWTile = 16 * CT * 128;
+    constexpr int kXTile = 16 * RT * 128;
+    constexpr int kXPer = (16 * RT * 8 + 255) / 256;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kXTile + 4 * 2 * kWTile];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ct = static_cast<int>(blockIdx.x) / g.splits;
+    const int split = static_cast<int>(blockIdx.x) % g.splits;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 16 * RT;
+    const int64_t bz = blockIdx.z;
+    int64_t lo, ro;
+    batch_offsets(g.bm, bz, lo, ro);
+    const int64_t M = g.M, N = g.N, K = g.K;
+    const int64_t n0 = (static_cast<int64_t>(ct) * 4 + wave) * 16 * CT;
+    const bool wave_live = n0 < N;
+    unsigned char* xt = lds;
+    unsigned char* wt = lds + 2 * kXTile + wave * 2 * kWTile;
+    auto swz = [](int row, int piece) { return row * 128 + ((piece ^ ((row >> 1) & 7)) << 4); };
+    const int64_t ksteps = K / 32;
+    const int64_t chunks = (ksteps + 1) / 2;
+    const int64_t c_begin = static_cast<int64_t>(split) * g.split_chunks;
+    const int64_t c_end = min<int64_t>(chunks, c_begin + g.split_chunks);
+
+    const int64_t wrows = wave_live ? min<int64_t>(16 * CT, N - n0) : 0;
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(g.w + ro + (wave_live ? n0 : 0) * K), 0, static_cast<int>(wrows * K * 2), 0x00020000);
+    const int64_t xrows = min<int64_t>(16 * RT, M - r0);
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(g.a + lo + r0 * K), 0, static_cast<int>(xrows * K * 2), 0x00020000);
+    // weight load i covers tile rows 8i .. 8i + 7 (lane: row 8i + lane/8, piece lane%8)
+    const int wlane = static_cast<int>((lane >> 3) * K * 2 + (lane & 7) * 16);
+    const int wstep = static_cast<int>(8 * K * 2);
+    // tile row 8i + lane/8 swizzles by (4i + lane/16) % 8: one base for even i, one for odd i (+ i * 1024)
+    const int wbase[2] = {swz(lane >> 3, lane & 7), swz(8 + (lane >> 3), lane & 7) - 1024};
+    const bool w_hi = (lane & 7) >= 4;  // this lane's piece lies in the chunk's second k-step
+    int xaddr[kXPer], xoff[kXPer];
+    bool xlive[kXPer], x_hi[kXPer];
+#pragma unroll
+    for (int q = 0; q < kXPer; q++) {
+        const int p = tid + 256 * q;
+        xlive[q] = p < 16 * RT * 8;
+        const int row = xlive[q] ? p >> 3 : 0;
+        xaddr[q] = swz(row, p & 7);
+        xoff[q] = static_cast<int>(row * K * 2 + (p & 7) * 16);
+        x_hi[q] = (p & 7) >= 4;
+    }
+    int raddr[2][CT], aaddr[2][RT];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+#pragma unroll
+        for (int c = 0; c < CT; c++) raddr[u][c] = swz(16 * c + (lane & 15), 4 * u + (lane >> 4));
+#pragma unroll
+        for (int t = 0; t < RT; t++) aaddr[u][t] = swz(16 * t + (lane & 15), 4 * u + (lane >> 4));
+    }
+
+    f32x4_t acc[RT][CT];
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int c = 0; c < CT; c++) acc[t][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    uint4 wv[2 * CT], xv[kXPer];
+    auto load = [&](int64_t ch) {
+        const bool win = 2 * ch + (w_hi ? 1 : 0) < ksteps;
+        const int kb = static_cast<int>(ch * 128);
+#pragma unroll
+        for (int i = 0; i < 2 * CT; i++) {
+            const uint4 v = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wlane + i * wstep + kb, 0, 0));
+            wv[i] = win ? v : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int q = 0; q < kXPer; q++) {
+            const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[q] + kb, 0, 0));
+            xv[q] = 2 * ch + (x_hi[q] ? 1 : 0) < ksteps ? v : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 2 * CT; i++) *reinterpret_cast<uint4*>(wt + buf * kWTile + wbase[i & 1] + i * 1024) = wv[i];
+#pragma unroll
+        for (int q = 0; q < kXPer; q++)
+            if (xlive[q]) *reinterpret_cast<uint4*>(xt + buf * kXTile + xaddr[q]) = xv[q];
+    };
+    auto mma = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            uint4 av[RT];
+#pragma unroll
+            for (int t = 0; t < RT; t++) av[t] = *reinterpret_cast<const uint4*>(xt + buf * kXTile + aaddr[u][t]);
+#pragma unroll
+            for (int c = 0; c < CT; c++) {
+                const uint4 bv = *reinterpret_cast<const uint4*>(wt + buf * kWTile + raddr[u][c]);
+#pragma unroll
+                for (int t = 0; t < RT; t++)
+                    acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[t]),
+                                                                        __builtin_bit_cast(bf16x8_t, bv), acc[t][c],
+                                                                        0, 0, 0);
+            }
+        }
+    };
+    if (c_begin < c_end) {
+        load(c_begin);
+        store(0);
+        __syncthreads();
+        for (int64_t ch = c_begin; ch < c_end; ch++) {
+            const int cur = static_cast<int>((ch - c_begin) & 1);
+            if (ch + 1 < c_end) load(ch + 1);
+            if (wave_live) mma(cur);
+            if (ch + 1 < c_end) store(cur ^ 1);
+            __syncthreads();
+        }
+    }
+
+    // acc[t][c][i]: row r0 + 16 t + 4 (lane / 16) + i, column n0 + 16 c + lane % 16
+    const int64_t ob = bz * M * N;
+    auto emit = [&](int t, int c, const f32x4_t& v) {
+        const int64_t nc = n0 + 16 * c + (lane & 15);
+        if (nc >= N) return;
+        const float bias = g.bias ? bf16_to_f32(g.bias[nc]) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int64_t rr = r0 + 16 * t + 4 * (lane >> 4) + i;
+            if (rr < M) g.out[ob + rr * N + nc] = f32_to_bf16(v[i] + bias);  // 2-byte: L2 combines them
+        }
+    };
+    if (!SPLIT || g.splits == 1) {
+        if (wave_live)
+#pragma unroll
+            for (int t = 0; t < RT; t++)
+#pragma unroll
+                for (int c = 0; c < CT; c++) emit(t, c, acc[t][c]);
+        return;
+    }
+
+    // Split-K: write this split's partial tile through to the agent's
+    // coherence point, count in, and let the last of the tile's workgroups
+    // sum the splits in order 0 .. splits-1 and write the output.
+    const int64_t tile = (bz * g.row_tiles + blockIdx.y) * g.col_tiles + ct;
+    constexpr int kWaveFloats = RT * CT * 64 * 4;
+    float* pbase = g.part + (tile * g.splits) * 4 * kWaveFloats + wave * kWaveFloats;
+    if (wave_live) {
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int c = 0; c < CT; c++) {
+                uint64_t* p = reinterpret_cast<uint64_t*>(pbase + split * 4 * kWaveFloats + ((t * CT + c) * 64 + lane) * 4);
+                const uint64_t w0 = static_cast<uint64_t>(__float_as_uint(acc[t][c][0])) |
+                                    (static_cast<uint64_t>(__float_as_uint(acc[t][c][1])) << 32);
+                const uint64_t w1 = static_cast<uint64_t>(__float_as_uint(acc[t][c][2])) |
+                                    (static_cast<uint64_t>(__float_as_uint(acc[t][c][3])) << 32);
+                __hip_atomic_store(p, w0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(p + 1, w1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+    }
+    __shared__ int is_last;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's write-through stores acknowledged
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t* ctr = g.counters + tile;
+        const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        is_last = prev == static_cast<uint32_t>(g.splits - 1);
+        if (is_last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!is_last || !wave_live) return;
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int c = 0; c < CT; c++) {
+            f32x4_t sum = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            for (int s = 0; s < g.splits; s++) {
+                uint64_t* p = reinterpret_cast<uint64_t*>(pbase + s * 4 * kWaveFloats + ((t * CT + c) * 64 + lane) * 4);
+                const uint64_t w0 = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t w1 = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                sum[0] += __uint_as_float(static_cast<uint32_t>(w0));
+                sum[1] += __uint_as_float(static_cast<uint32_t>(w0 >> 32));
+                sum[2] += __uint_as_float(static_cast<uint32_t>(w1));
+                sum[3] += __uint_as_float(static_cast<uint32_t>(w1 >> 32));
+            }
+            emit(t, c, sum);
+        }
+}
+
+// Any dtype, either operand transposed: 64 x 64 output tile per workgroup,
+// 4 x 4 outputs per thread, k staged 16 at a time through LDS.  Each output
+// is acc = (bias or 0) then acc = acc + a * b over k in order (no FMA
+// contraction), the reference's loop exactly.
+template <typename T>
+__global__ __launch_bounds__(256) void gemm_simt_kernel(const void* __restrict__ lhs, const void* __restrict__ rhs,
+                                                        const void* __restrict__ bias, void* __restrict__ out,
+                                                        int64_t M, int64_t N, int64_t K, int32_t tl, int32_t tr,
+                                                        int64_t lrs, int64_t rrs, BatchMap bm) {
+    constexpr int kT = 64, kK = 16;
+    __shared__ float As[kK][kT + 4];
+    __shared__ float Bs[kK][kT + 4];
+    const int tid = threadIdx.x;
+    const int tx = tid & 15, ty = tid >> 4;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kT, n0 = static_cast<int64_t>(blockIdx.x) * kT;
+    const int64_t bz = blockIdx.z;
+    int64_t lo, ro;
+    batch_offsets(bm, bz, lo, ro);
+    float acc[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int64_t n = n0 + tx + 16 * j;
+        const float b0 = bias && n < N ? Vec8<T>::load1(bias, n) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i][j] = b0;
+    }
+    for (int64_t k0 = 0; k0 < K; k0 += kK) {
+        // 1024 elements of each operand tile, 4 per thread; the fast index
+        // follows the operand's contiguous dimension
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int e = tid + 256 * q;
+            int mm, kk;
+            if (tl) { mm = e & 63; kk = e >> 6; } else { kk = e & 15; mm = e >> 4; }
+            const int64_t gm = m0 + mm, gk = k0 + kk;
+            float v = 0.0f;
+            if (gm < M && gk < K) v = Vec8<T>::load1(lhs, lo + (tl ? gk * lrs + gm : gm * lrs + gk));
+            As[kk][mm] = v;
+            int nn;
+            if (tr) { kk = e & 15; nn = e >> 4; } else { nn = e & 63; kk = e >> 6; }
+            const int64_t gn = n0 + nn, gk2 = k0 + kk;
+            float w = 0.0f;
+            if (gn < N && gk2 < K) w = Vec8<T>::load1(rhs, ro + (tr ? gn * rrs + gk2 : gk2 * rrs + gn));
+            Bs[kk][nn] = w;
+        }
+        __syncthreads();
+        const int kn = static_cast<int>(min<int64_t>(kK, K - k0));
+        for (int kk = 0; kk < kn; kk++) {
+            float av[4], bv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) av[i] = As[kk][ty + 16 * i];
+#pragma unroll
+            for (int j = 0; j < 4; j++) bv[j] = Bs[kk][tx + 16 * j];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = __fadd_rn(acc[i][j], __fmul_rn(av[i], bv[j]));
+        }
+        __syncthreads();
+    }
+    const int64_t ob = bz * M * N;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int64_t m = m0 + ty + 16 * i;
+        if (m >= M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int64_t n = n0 + tx + 16 * j;
+            if (n < N) Vec8<T>::store1(out, ob + m * N + n, acc[i][j]);
+        }
+    }
+}
+
+// --------------------------------------------------------------------- host
+struct Plan {
+    int64_t M, N, K, batches;
+    int64_t lrs, rrs;  // row strides (last dims) of lhs and rhs
+    BatchMap bm;
+};
+
+// Fills the plan from operand shapes with the reference's rules; returns an
+// error message or null.
+const char* plan_matmul(const SandyTensor& l, const SandyTensor& r, const SandyTensor& o, bool tl, bool tr, Plan& p) {
+    const int lr = l.rank, rr = r.rank;
+    if (lr < 2) return "matmul lhs must have rank >= 2";
+    if (rr < 2) return "matmul rhs must have rank >= 2";
+    p.M = l.dims[lr - (tl ? 1 : 2)];
+    const int64_t lk = l.dims[lr - (tl ? 2 : 1)];
+    const int64_t rk = r.dims[rr - (tr ? 1 : 2)];
+    p.N = r.dims[rr - (tr ? 2 : 1)];
+    if (p.M < 0 || p.N < 0 || lk < 0 || rk < 0) return "matmul matrix dimensions must be static";
+    if (lk != rk) return "matmul contracting dimension mismatch";
+    p.K = lk;
+    const int lb = lr - 2, rb = rr - 2;
+    const int brank = std::max(lb, rb);
+    if (o.rank != brank + 2) return "matmul output shape mismatch";
+    BatchMap& m = p.bm;
+    m.rank = brank;
+    p.batches = 1;
+    // contiguous strides of each operand's batch dims
+    int64_t ls[SANDY_HIP_MAX_RANK], rs[SANDY_HIP_MAX_RANK];
+    int64_t s = l.dims[lr - 1] * l.dims[lr - 2];
+    for (int d = lb - 1; d >= 0; d--) { ls[d] = s; s *= l.dims[d]; }
+    s = r.dims[rr - 1] * r.dims[rr - 2];
+    for (int d = rb - 1; d >= 0; d--) { rs[d] = s; s *= r.dims[d]; }
+    for (int i = 0; i < brank; i++) {
+        const int li = lb - brank + i, ri = rb - brank + i;
+        const int64_t a = li >= 0 ? l.dims[li] : 1, b = ri >= 0 ? r.dims[ri] : 1;
+        int64_t d;
+        if (a == b) d = a;
+        else if (a == 1) d = b;
+        else if (b == 1) d = a;
+        else if (a > b && a % b == 0) d = a;
+        else if (b > a && b % a == 0) d = b;
+        else return "cannot broadcast matmul batch shapes";
+        m.dims[i] = d;
+        m.l_stride[i] = (li >= 0 && a != 1) ? ls[li] : 0;
+        m.l_div[i] = (li >= 0 && a != 1) ? d / a : 1;
+        m.r_stride[i] = (ri >= 0 && b != 1) ? rs[ri] : 0;
+        m.r_div[i] = (ri >= 0 && b != 1) ? d / b : 1;
+        if (o.dims[i] != d) return "matmul output shape mismatch";
+        p.batches *= d;
+    }
+    if (o.dims[brank] != p.M || o.dims[brank + 1] != p.N) return "matmul output shape mismatch";
+    p.lrs = l.dims[lr - 1];
+    p.rrs = r.dims[rr - 1];
+    return nullptr;
+}
+
+int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const SandyTensor* bias, const SandyTensor& o,
+           bool tl, bool tr, hipStream_t stream, Err e, const char* what) {
+    if (p.batches == 0 || p.M == 0 || p.N == 0) return ok(e);
+    if (p.batches > 65535) return fail(e, SANDY_ERR_UNSUPPORTED, "%s batch count exceeds 65535", what);
+    const void* pl = base_ptr(l);
+    const void* pr = base_ptr(r);
+    const void* pb = bias ? base_ptr(*bias) : nullptr;
+    void* po = base_ptr(o);
+    const bool aligned = ((reinterpret_cast<uintptr_t>(pl) | reinterpret_cast<uintptr_t>(pr)) & 15) == 0;
+    const bool lines = l.dtype == SANDY_BF16 && !tl && tr && p.K % 32 == 0 && p.K > 0 && aligned &&
+                       p.K <= (int64_t{1} << 21) && env_int("SANDY_GEMM_SIMT", 0) == 0;
+    if (lines) {
+        GemmArgs g{};
+        g.a = static_cast<const uint16_t*>(pl);
+        g.w = static_cast<const uint16_t*>(pr);
+        g.bias = static_cast<const uint16_t*>(pb);
+        g.out = static_cast<uint16_t*>(po);
+        g.M = p.M;
+        g.N = p.N;
+        g.K = p.K;
+        g.bm = p.bm;
+        // tile: rows per workgroup follow M; 64 columns per wave for large products
+        int variant = env_int("SANDY_GEMM_TILE", -1);
+        if (variant < 0) variant = p.M <= 16 ? 0 : p.M <= 32 ? 1 : p.M <= 64 ? 2 : 3;
+        static const int kRT[] = {1, 2, 4, 4, 2, 1};
+        static const int kCT[] = {1, 1, 1, 4, 2, 2};
+        if (variant > 5) variant = 3;
+        const int RT = kRT[variant], CT = kCT[variant];
+        const int64_t rows_per = 16 * RT;
+        const int64_t row_tiles = (p.M + rows_per - 1) / rows_per;
+        const int64_t col_tiles = (p.N + 64 * CT - 1) / (64 * CT);
+        const int64_t chunks = (p.K / 32 + 1) / 2;
+        if (row_tiles > 65535 || col_tiles > (1 << 20))
+            return fail(e, SANDY_ERR_UNSUPPORTED, "%s shape exceeds the launch grid", what);
+        const int64_t tiles = row_tiles * col_tiles * p.batches;
+        // split K while the tiles alone leave the chip short of workgroups,
+        // keeping at least min_chunks chunks of 64 k per split
+        const int64_t target = env_int("SANDY_GEMM_TARGET_WG", 1024);
+        const int64_t min_chunks = std::max(1, env_int("SANDY_GEMM_MIN_CHUNKS", 4));
+        int64_t splits = env_int("SANDY_GEMM_SPLIT", 0);
+        if (splits <= 0) splits = std::min<int64_t>((target + tiles - 1) / tiles, chunks / min_chunks);
+        if (variant == 3) splits = 1;  // the 64 x 256 tile is built without the split-K epilogue
+        splits = std::max<int64_t>(1, std::min<int64_t>(splits, chunks));
+        const int64_t split_chunks = (chunks + splits - 1) / splits;
+        splits = (chunks + split_chunks - 1) / split_chunks;  // no empty splits
+        g.col_tiles = static_cast<int32_t>(col_tiles);
+        g.row_tiles = static_cast<int32_t>(row_tiles);
+        g.splits = static_cast<int32_t>(splits);
+        g.split_chunks = static_cast<int32_t>(split_chunks);
+        if (col_tiles * splits > 0x7fffffff) return fail(e, SANDY_ERR_UNSUPPORTED, "%s shape exceeds the launch grid", what);
+        if (splits > 1) {
+            int status = 0;
+            const size_t part = static_cast<size_t>(tiles * splits) * 4 * RT * CT * 64 * 4 * sizeof(float);
+            g.part = static_cast<float*>(device_workspace(4, part, stream, e, &status));
+            if (status) return status;
+            g.counters = static_cast<uint32_t*>(device_counters(1, static_cast<size_t>(tiles) * sizeof(uint32_t), stream, e, &status));
+            if (status) return status;
+        }
+        const dim3 grid(static_cast<unsigned>(col_tiles * splits), static_cast<unsigned>(row_tiles),
+                        static_cast<unsigned>(p.batches));
+        switch (variant) {
+            case 0: hipLaunchKernelGGL((gemm_lines_kernel<1, 1, 4, true>), grid, dim3(256), 0, stream, g); break;
+            case 1: hipLaunchKernelGGL((gemm_lines_kernel<2, 1, 4, true>), grid, dim3(256), 0, stream, g); break;
+            case 2: hipLaunchKernelGGL((gemm_lines_kernel<4, 1, 2, true>), grid, dim3(256), 0, stream, g); break;
+            case 4: hipLaunchKernelGGL((gemm_lines_kernel<2, 2, 2, true>), grid, dim3(256), 0, stream, g); break;
+            case 5: hipLaunchKernelGGL((gemm_lines_kernel<1, 2, 4, true>), grid, dim3(256), 0, stream, g); break;
+            default: hipLaunchKernelGGL((gemm_lines_kernel<4, 4, 2, false>), grid, dim3(256), 0, stream, g); break;
+        }
+    } else {
+        const int64_t gy = (p.M + 63) / 64, gx = (p.N + 63) / 64;
+        if (gy > 65535 || gx > 0x7fffffff) return fail(e, SANDY_ERR_UNSUPPORTED, "%s shape exceeds the launch grid", what);
+        const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy), static_cast<unsigned>(p.batches));
+        if (l.dtype == SANDY_BF16)
+            hipLaunchKernelGGL(gemm_simt_kernel<BF16>, grid, dim3(256), 0, stream, pl, pr, pb, po, p.M, p.N, p.K,
+                               static_cast<int32_t>(tl), static_cast<int32_t>(tr), p.lrs, p.rrs, p.bm);
+        else
+            hipLaunchKernelGGL(gemm_simt_kernel<F32>, grid, dim3(256), 0, stream, pl, pr, pb, po, p.M, p.N, p.K,
+                               static_cast<int32_t>(tl), static_cast<int32_t>(tr), p.lrs, p.rrs, p.bm);
+    }
+    SANDY_HIP_TRY(hipGetLastError(), e, what);
+    return ok(e);
+}
+
+} // namespace
+} // namespace sandy_hip
+
+using namespace sandy_hip;
+
+extern "C" int sandy_hip_matmul(const SandyTensor* lhs, const SandyTensor* rhs, int32_t transpose_lhs,
+                                int32_t transpose_rhs, const SandyTensor* out, void* stream_, char* err,
+                                size_t err_cap) {
+    Err e{err, err_cap};
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    if (!valid_rank(lhs) || !valid_rank(rhs) || !valid_rank(out))
+        return fail(e, SANDY_ERR_INVALID, "matmul requires lhs, rhs and out");
+    if (lhs->dtype != rhs->dtype || lhs->dtype != out->dtype)
+        return fail(e, SANDY_ERR_INVALID, "matmul operands must have same dtype");
+    if (!is_float(lhs->dtype)) return fail(e, SANDY_ERR_INVALID, "matmul unsupported dtype");
+    if (!contiguous(*lhs) || !contiguous(*rhs) || !contiguous(*out))
+        return fail(e, SANDY_ERR_UNSUPPORTED, "matmul requires contiguous tensor views");
+    Plan p{};
+    if (const char* msg = plan_matmul(*lhs, *rhs, *out, transpose_lhs != 0, transpose_rhs != 0, p))
+        return fail(e, SANDY_ERR_INVALID, "%s", msg);
+    return launch(p, *lhs, *rhs, nullptr, *out, transpose_lhs != 0, transpose_rhs != 0, stream, e, "matmul");
+}
+
+extern "C" int sandy_hip_linear(const SandyTensor* x, const SandyTensor* weight, const SandyTensor* bias,
+                                const SandyTensor* out, void* stream_, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    if (!valid_rank(x) || !valid_rank(weight) || !valid_rank(bias) || !valid_rank(out))
+        return fail(e, SANDY_ERR_INVALID, "linear requires input, weight, bias and out");
+    if (!is_float(x->dtype)) return fail(e, SANDY_ERR_INVALID, "linear input unsupported dtype");
+    if (weight->dtype != x->dtype || bias->dtype != x->dtype || out->dtype != x->dtype)
+        return fail(e, SANDY_ERR_INVALID, "linear operands must have same dtype");
+    if (x->rank < 1 || weight->rank != 2 || bias->rank != 1)
+        return fail(e, SANDY_ERR_INVALID, "linear expects input [..., in], weight [out, in], bias [out]");
+    const int64_t in_f = x->dims[x->rank - 1], out_f = weight->dims[0];
+    if (weight->dims[1] != in_f) return fail(e, SANDY_ERR_INVALID, "linear input/weight feature mismatch");
+    if (bias->dims[0] != out_f) return fail(e, SANDY_ERR_INVALID, "linear bias shape mismatch");
+    if (out->rank != x->rank || out->dims[x->rank - 1] != out_f)
+        return fail(e, SANDY_ERR_INVALID, "linear output shape mismatch");
+    for (int i = 0; i + 1 < x->rank; i++)
+        if (out->dims[i] != x->dims[i]) return fail(e, SANDY_ERR_INVALID, "linear output shape mismatch");
+    if (!contiguous(*x) || !contiguous(*weight) || !contiguous(*bias) || !contiguous(*out))
+        return fail(e, SANDY_ERR_UNSUPPORTED, "linear requires contiguous tensor views");
+    // rows of x flattened: [rows, in] times weight^T
+    SandyTensor x2 = *x, o2 = *out;
+    int64_t rows = 1;
+    for (int i = 0; i + 1 < x->rank; i++) rows *= x->dims[i];
+    x2.rank = 2;
+    x2.dims[0] = rows;
+    x2.dims[1] = in_f;
+    x2.strides[0] = in_f;
+    x2.strides[1] = 1;
+    o2.rank = 2;
+    o2.dims[0] = rows;
+    o2.dims[1] = out_f;
+    o2.strides[0] = out_f;
+    o2.strides[1] = 1;
+    Plan p{};
+    if (const char* msg = plan_matmul(x2, *weight, o2, false, true, p)) return fail(e, SANDY_ERR_INVALID, "%s", msg);
+    return launch(p, x2, *weight, bias, o2, false, true, stream, e, "linear");
+}

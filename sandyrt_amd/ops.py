@@ -269,3 +269,43 @@ def moe_scatter_sum(packed_out, packed_weights, token_ids, seq: int, out=None):
     out = torch.empty(shape, dtype=packed_out.dtype, device=packed_out.device) if out is None else out
     call("sandy_hip_moe_scatter_sum", desc(packed_out), desc(packed_weights), desc(token_ids), desc(out))
     return out
+
+
+def _matmul_shape(lshape, rshape, transpose_lhs, transpose_rhs):
+    """Output shape of matmul: batch dims broadcast right-aligned (equal, 1,
+    or one a multiple of the other -- ShapeUtil.cpp:39-71)."""
+    if len(lshape) < 2 or len(rshape) < 2:
+        raise SandyError("matmul operands must have rank >= 2")
+    lb, rb = list(lshape[:-2]), list(rshape[:-2])
+    rank = max(len(lb), len(rb))
+    lb = [1] * (rank - len(lb)) + lb
+    rb = [1] * (rank - len(rb)) + rb
+    batch = []
+    for a, b in zip(lb, rb):
+        if a == b or b == 1 or (a > b and a % b == 0):
+            batch.append(a)
+        elif a == 1 or (b > a and b % a == 0):
+            batch.append(b)
+        else:
+            raise SandyError(f"cannot broadcast matmul batch shapes {list(lshape[:-2])} and {list(rshape[:-2])}")
+    m = lshape[-1] if transpose_lhs else lshape[-2]
+    n = rshape[-2] if transpose_rhs else rshape[-1]
+    return batch + [m, n]
+
+
+def matmul(lhs, rhs, transpose_lhs: bool = False, transpose_rhs: bool = False, out=None):
+    """MatMulKernelOp (TensorCalc.cpp:804-919; CudaMatMulKernels.cu:221-292)."""
+    _require_gpu(lhs, rhs)
+    if out is None:
+        shape = _matmul_shape(list(lhs.shape), list(rhs.shape), transpose_lhs, transpose_rhs)
+        out = torch.empty(shape, dtype=lhs.dtype, device=lhs.device)
+    call("sandy_hip_matmul", desc(lhs), desc(rhs), int(bool(transpose_lhs)), int(bool(transpose_rhs)), desc(out))
+    return out
+
+
+def linear(x, weight, bias, out=None):
+    """LinearKernelOp (TensorCalc.cpp:722-773): bias + x @ weight^T."""
+    _require_gpu(x, weight, bias)
+    out = torch.empty(list(x.shape[:-1]) + [weight.shape[0]], dtype=x.dtype, device=x.device) if out is None else out
+    call("sandy_hip_linear", desc(x), desc(weight), desc(bias), desc(out))
+    return out

@@ -96,6 +96,11 @@ def cases(rng):
     out.append(("unary_sqrt_f32", "unary", dict(op="sqrt", x=np.abs(n(40)))))
     out.append(("unary_relu_f32", "unary", dict(op="relu", x=n(40))))
     out.append(("matmul_f32", "matmul", dict(lhs=n(2, 3, 16), rhs=n(16, 5), transpose_rhs=False)))
+    out.append(("matmul_bf16_t", "matmul", dict(lhs=bf(n(5, 64)), rhs=bf(n(24, 64) * 0.2), transpose_rhs=True)))
+    out.append(("matmul_f32_tlhs", "matmul", dict(lhs=n(16, 6), rhs=n(3, 16, 7), transpose_lhs=True)))
+    out.append(("matmul_f32_grouped_heads", "matmul", dict(lhs=n(2, 8, 3, 16), rhs=n(2, 2, 16, 5))))
+    out.append(("matmul_bf16_bcast", "matmul", dict(lhs=bf(n(4, 1, 3, 32)), rhs=bf(n(3, 5, 32)), transpose_rhs=True)))
+    out.append(("linear_bf16", "linear", dict(x=bf(n(4, 48)), weight=bf(n(9, 48) * 0.2), bias=bf(n(9)))))
     out.append(("linear_f32", "linear", dict(x=n(3, 16), weight=n(8, 16), bias=n(8))))
     return out
 

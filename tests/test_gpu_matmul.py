@@ -1,0 +1,202 @@
+"""GPU parity of dense matmul and linear against the oracle
+(src/core/TensorCalc.cpp matmul 804-919, linear 722-773; validation of
+launch_cuda_matmul, src/device/cuda/CudaMatMulKernels.cu:78-141).
+
+f32 and every layout other than bf16 x [n, k] weights keep the reference's k
+order per output: compared bit-exactly.  bf16 with transposed rhs runs on
+MFMA with fp32 accumulation in another order: compared at the bf16
+tolerance (2e-2)."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import assert_close, assert_equal, from_f32, normal, rng, to_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from sandyrt_amd import ops
+    return ops
+
+
+class env:
+    """Temporarily set SANDY_* tuning variables (read on every call)."""
+
+    def __init__(self, **kw):
+        self.kw = {k: str(v) for k, v in kw.items()}
+
+    def __enter__(self):
+        self.old = {k: os.environ.get(k) for k in self.kw}
+        os.environ.update(self.kw)
+
+    def __exit__(self, *a):
+        for k, v in self.old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+def f32(a):
+    return torch.tensor(a, dtype=torch.float32, device="cuda")
+
+
+# ---------------------------------------------------------------- known answers
+def test_matmul_reference_known_answers(ops):
+    """The reference's device tests (test/engine/CudaDeviceTest.cpp:1145-1198,
+    1200-1253, 1331-1384, 1386-1471)."""
+    lhs = f32([[1, 2, 3], [4, 5, 6]])
+    assert ops.matmul(lhs, f32([[7, 8], [9, 10], [11, 12]])).cpu().tolist() == [[58, 64], [139, 154]]
+    assert ops.matmul(lhs, f32([[7, 8, 9], [10, 11, 12]]), transpose_rhs=True).cpu().tolist() == [[50, 68], [122, 167]]
+    # a [1, 2] view at storage offset 4 of a [1, 3, 2] buffer
+    base = f32([1, 2, 3, 4, 5, 6])
+    view = base[4:6].view(1, 2)
+    assert view.storage_offset() == 4
+    assert ops.matmul(view, f32([[1, 0], [0, 1]])).cpu().tolist() == [[5, 6]]
+    gl = f32([1, 0, 0, 0, 1, 0, 0, 0, 1, 1, 1, 0, 1, 2, 0, 0, 1, 1, 2, 0, 1, 1, 0, 1]).view(1, 4, 2, 3)
+    gr = f32([10, 100, 20, 200, 30, 300, 1, 10, 2, 20, 3, 30]).view(1, 2, 3, 2)
+    assert ops.matmul(gl, gr).cpu().flatten().tolist() == [10, 100, 20, 200, 30, 300, 30, 300, 5, 50, 5, 50, 5, 50, 4, 40]
+
+
+def test_matmul_validation_errors(ops):
+    from sandyrt_amd._lib import SandyError
+    a = torch.zeros(2, 3, device="cuda")
+    with pytest.raises(SandyError, match="contracting dimension mismatch"):
+        ops.matmul(a, torch.zeros(4, 2, device="cuda"), out=torch.zeros(2, 2, device="cuda"))
+    with pytest.raises(SandyError, match="operands must have same dtype"):
+        ops.matmul(a, torch.zeros(3, 2, device="cuda", dtype=torch.bfloat16), out=torch.zeros(2, 2, device="cuda"))
+    with pytest.raises(SandyError, match="output shape mismatch"):
+        ops.matmul(a, torch.zeros(3, 2, device="cuda"), out=torch.zeros(2, 3, device="cuda"))
+    with pytest.raises(SandyError, match="contiguous"):
+        ops.matmul(torch.zeros(3, 2, device="cuda").t(), torch.zeros(3, 2, device="cuda"),
+                   out=torch.zeros(2, 2, device="cuda"))
+    with pytest.raises(SandyError, match="unsupported dtype"):
+        ops.matmul(torch.zeros(2, 3, device="cuda", dtype=torch.int32), torch.zeros(3, 2, device="cuda", dtype=torch.int32),
+                   out=torch.zeros(2, 2, device="cuda", dtype=torch.int32))
+    with pytest.raises(SandyError, match="rank >= 2"):
+        ops.matmul(torch.zeros(3, device="cuda"), torch.zeros(3, 2, device="cuda"), out=torch.zeros(2, device="cuda"))
+    with pytest.raises(SandyError, match="linear bias shape mismatch"):
+        ops.linear(a, torch.zeros(4, 3, device="cuda"), torch.zeros(5, device="cuda"))
+
+
+# ---------------------------------------------------------------- exact-order paths
+# bf16 with a transposed rhs and a plain lhs runs on MFMA: covered by the tolerance tests below
+EXACT_LAYOUTS = [(dt, tl, tr) for dt in (torch.float32, torch.bfloat16)
+                 for tl, tr in ((False, False), (True, False), (False, True), (True, True))
+                 if not (dt == torch.bfloat16 and tr and not tl)]
+
+
+@pytest.mark.parametrize("dtype,tl,tr", EXACT_LAYOUTS)
+@pytest.mark.parametrize("lshape,rshape", [((70, 33), (33, 90)), ((2, 4, 17, 40), (2, 1, 40, 9)),
+                                           ((3, 1, 5, 64), (2, 64, 130)), ((1, 8), (8, 1))])
+def test_matmul_exact_order_bit_exact(ops, oracle, dtype, tl, tr, lshape, rshape):
+    """f32 everywhere and bf16 outside the MFMA layout: same k order as the
+    reference, so results are bit-identical (batch broadcast and grouped heads
+    included)."""
+    r = rng(sum(lshape) + sum(rshape) + 2 * tl + tr)
+    lhs = normal(r, lshape)
+    rhs = normal(r, rshape)
+    if tl:
+        lhs = np.swapaxes(lhs, -1, -2).copy()
+    if tr:
+        rhs = np.swapaxes(rhs, -1, -2).copy()
+    L, R = from_f32(lhs, dtype), from_f32(rhs, dtype)
+    got = ops.matmul(L, R, transpose_lhs=tl, transpose_rhs=tr)
+    want = oracle.matmul(to_oracle(L), to_oracle(R), transpose_lhs=tl, transpose_rhs=tr)
+    assert_equal(got, want, "matmul")
+
+
+def test_matmul_bf16_simt_fallback_for_unaligned_k(ops, oracle):
+    """bf16 with [n, k] weights but K not a multiple of 32 takes the exact-order
+    kernel: bit-exact."""
+    r = rng(5)
+    L = from_f32(normal(r, (9, 40)), torch.bfloat16)
+    R = from_f32(normal(r, (33, 40)), torch.bfloat16)
+    assert_equal(ops.matmul(L, R, transpose_rhs=True), oracle.matmul(to_oracle(L), to_oracle(R), transpose_rhs=True),
+                 "matmul bf16 K=40")
+
+
+def test_matmul_empty(ops):
+    out = ops.matmul(torch.zeros(0, 64, device="cuda", dtype=torch.bfloat16),
+                     torch.zeros(32, 64, device="cuda", dtype=torch.bfloat16), transpose_rhs=True)
+    assert out.shape == (0, 32)
+    out = ops.matmul(torch.zeros(3, 0, device="cuda"), torch.zeros(0, 4, device="cuda"))
+    assert out.cpu().tolist() == [[0.0] * 4] * 3
+
+
+# ---------------------------------------------------------------- MFMA path
+# (M, N, K): decode rows against projection-like weights, ragged N, odd k-steps
+MFMA_SHAPES = [(1, 256, 64), (7, 200, 96), (16, 512, 2048), (32, 2048, 512), (33, 300, 160), (64, 1000, 256),
+               (100, 520, 224), (256, 640, 1024)]
+
+
+@pytest.mark.parametrize("m,n,k", MFMA_SHAPES)
+def test_matmul_bf16_mfma_matches_oracle(ops, oracle, m, n, k):
+    r = rng(m * 7 + n + k)
+    L = from_f32(normal(r, (m, k)), torch.bfloat16)
+    W = from_f32(normal(r, (n, k), 0.05), torch.bfloat16)
+    got = ops.matmul(L, W, transpose_rhs=True)
+    want = oracle.matmul(to_oracle(L), to_oracle(W), transpose_rhs=True)
+    assert_close(got, want, torch.bfloat16, f"matmul {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("variant", range(6))
+@pytest.mark.parametrize("split", [1, 3, 8])
+def test_matmul_bf16_every_tile_and_split(ops, oracle, variant, split):
+    """Every tile shape of the MFMA kernel, with and without split K (the 64 x
+    256 tile never splits)."""
+    r = rng(variant * 10 + split)
+    m, n, k = 45, 600, 1024
+    L = from_f32(normal(r, (m, k)), torch.bfloat16)
+    W = from_f32(normal(r, (n, k), 0.05), torch.bfloat16)
+    want = oracle.matmul(to_oracle(L), to_oracle(W), transpose_rhs=True)
+    with env(SANDY_GEMM_TILE=variant, SANDY_GEMM_SPLIT=split):
+        got = ops.matmul(L, W, transpose_rhs=True)
+        again = ops.matmul(L, W, transpose_rhs=True)
+    assert_close(got, want, torch.bfloat16, f"variant {variant} split {split}")
+    assert torch.equal(got, again), "split-K result is not deterministic"
+
+
+def test_matmul_bf16_split_counters_rearm(ops, oracle):
+    """Back-to-back split-K launches of different shapes: each launch leaves its
+    arrival counters at zero for the next."""
+    r = rng(11)
+    cases = [(32, 2048, 2048), (8, 700, 512), (32, 2048, 2048), (1, 64, 4096)]
+    outs = []
+    for m, n, k in cases:
+        L = from_f32(normal(r, (m, k)), torch.bfloat16)
+        W = from_f32(normal(r, (n, k), 0.05), torch.bfloat16)
+        outs.append((ops.matmul(L, W, transpose_rhs=True), L, W))
+    for got, L, W in outs:
+        assert_close(got, oracle.matmul(to_oracle(L), to_oracle(W), transpose_rhs=True), torch.bfloat16, "rearm")
+
+
+def test_matmul_bf16_mfma_batched_grouped_heads(ops, oracle):
+    """Batched [n, k] rhs with grouped-head broadcast on the MFMA kernel."""
+    r = rng(12)
+    L = from_f32(normal(r, (2, 8, 5, 64)), torch.bfloat16)
+    R = from_f32(normal(r, (2, 2, 48, 64)), torch.bfloat16)
+    got = ops.matmul(L, R, transpose_rhs=True)
+    want = oracle.matmul(to_oracle(L), to_oracle(R), transpose_rhs=True)
+    assert_close(got, want, torch.bfloat16, "grouped heads")
+
+
+# ---------------------------------------------------------------- linear
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("xshape,out_f", [((5, 768), 2304), ((2, 3, 64), 96), ((1, 40), 7), ((16,), 8)])
+def test_linear_matches_oracle(ops, oracle, dtype, xshape, out_f):
+    r = rng(len(xshape) + out_f)
+    in_f = xshape[-1]
+    x = from_f32(normal(r, xshape), dtype)
+    w = from_f32(normal(r, (out_f, in_f), 0.02), dtype)
+    b = from_f32(normal(r, (out_f,)), dtype)
+    got = ops.linear(x, w, b)
+    want = oracle.linear(to_oracle(x), to_oracle(w), to_oracle(b))
+    if dtype == torch.float32 or in_f % 32:
+        assert_equal(got, want, "linear exact order")  # acc starts at bias, k in order
+    else:
+        assert_close(got, want, dtype, "linear")

@@ -235,6 +235,45 @@ def test_moe_matmul_matches_segmented_gemm(oracle):
         np.testing.assert_allclose(y[off[e]:off[e + 1]], x[off[e]:off[e + 1]] @ w[e].T, rtol=1e-5, atol=1e-5)
 
 
+# matmul known answers: the reference's own device tests
+# (test/engine/CudaDeviceTest.cpp:1145-1198, 1331-1384, 1386-1471)
+MATMUL_LHS = np.arange(1, 7, dtype=np.float32).reshape(2, 3)
+GROUPED_LHS = np.array([1, 0, 0, 0, 1, 0, 0, 0, 1, 1, 1, 0, 1, 2, 0, 0, 1, 1, 2, 0, 1, 1, 0, 1],
+                       np.float32).reshape(1, 4, 2, 3)
+GROUPED_RHS = np.array([10, 100, 20, 200, 30, 300, 1, 10, 2, 20, 3, 30], np.float32).reshape(1, 2, 3, 2)
+GROUPED_OUT = [10, 100, 20, 200, 30, 300, 30, 300, 5, 50, 5, 50, 5, 50, 4, 40]
+
+
+def test_matmul_known_answers(oracle):
+    rhs = np.arange(7, 13, dtype=np.float32)
+    assert oracle.matmul(MATMUL_LHS, rhs.reshape(3, 2)).ravel().tolist() == [58, 64, 139, 154]
+    assert oracle.matmul(MATMUL_LHS, rhs.reshape(2, 3), transpose_rhs=True).ravel().tolist() == [50, 68, 122, 167]
+    # lhs heads 0-1 use rhs head 0, heads 2-3 rhs head 1 (grouped batch broadcast)
+    assert oracle.matmul(GROUPED_LHS, GROUPED_RHS).ravel().tolist() == GROUPED_OUT
+
+
+@pytest.mark.parametrize("tl,tr", [(False, False), (True, False), (False, True), (True, True)])
+def test_matmul_matches_float64_with_broadcast(oracle, tl, tr):
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((3, 1, 4, 24, 10)).astype(np.float32)  # [.., k, m] when transposed
+    b = rng.standard_normal((2, 1, 24, 6)).astype(np.float32)
+    lhs = a if tl else np.swapaxes(a, -1, -2).copy()
+    rhs = np.swapaxes(b, -1, -2).copy() if tr else b
+    got = oracle.matmul(lhs, rhs, transpose_lhs=tl, transpose_rhs=tr)
+    want = np.swapaxes(a, -1, -2).astype(np.float64) @ b.astype(np.float64)  # [3, 2, 4, 10, 6]
+    assert got.shape == (3, 2, 4, 10, 6)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+
+
+def test_linear_is_bias_plus_matmul(oracle):
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((5, 40)).astype(np.float32)
+    w = rng.standard_normal((7, 40)).astype(np.float32)
+    b = rng.standard_normal(7).astype(np.float32)
+    np.testing.assert_allclose(oracle.linear(x, w, b), x.astype(np.float64) @ w.T.astype(np.float64) + b,
+                               rtol=1e-5, atol=1e-5)
+
+
 def test_elementwise_dag_silu_gate(oracle):
     """silu(g) * u as lowered by BuiltinLowering.cpp:142-158: (0.5 g)(1 + tanh(0.5 g))"""
     rng = np.random.default_rng(5)
@@ -297,3 +336,8 @@ def test_oracle_fuzz_against_reference_build(oracle, ref, seed):
         t = cv(np.round(rng.standard_normal((9, 128)) * 4) / 4)
         for a, e in zip(oracle.topk(t, 8), ref.topk(t, 8)):
             assert bits_equal(a, e)
+        lm = cv(rng.standard_normal((2, 4, 5, 40)))
+        rm = cv(rng.standard_normal((2, 1, 40, 7)))
+        assert bits_equal(oracle.matmul(lm, rm), ref.matmul(lm, rm))
+        assert bits_equal(oracle.matmul(lm, np.swapaxes(rm, -1, -2).copy(), transpose_rhs=True),
+                          ref.matmul(lm, np.swapaxes(rm, -1, -2).copy(), transpose_rhs=True))
