@@ -15,14 +15,16 @@
 //
 // The reference hands both to cuBLAS (cublasGemmEx, CudaMatMulKernels.cu:
 // 173-216; its CUDA linear is not implemented, CudaDevice.cpp:536-537).
-// Here there are two kernels:
-//   - gemm_lines_kernel: bf16 with the weight read row-major as [n, k]
-//     (transpose_rhs, the layout of every projection and the lm-head) on
-//     v_mfma_f32_16x16x32_bf16.  Decode-sized products are weight streams
-//     (tens of rows against megabytes of weights), so the kernel splits K
-//     over workgroups when the column tiles alone cannot fill the chip, and
-//     the last-arriving workgroup of each output tile sums the fp32 partials
-//     in split order (deterministic) -- one launch, no second reduction pass;
+// Here there are three kernels:
+//   - bf16 with the weight read row-major as [n, k] (transpose_rhs, the
+//     layout of every projection and the lm-head) runs on
+//     v_mfma_f32_16x16x32_bf16 with fp32 accumulation:
+//       gemm_waves_kernel for decode-sized products (up to 64 rows): weight
+//         streams, HBM-bound, K split over the waves of a workgroup and, when
+//         the column tiles alone cannot fill the chip, over workgroups, with
+//         the last-arriving workgroup of each output tile summing the fp32
+//         partials in split order -- one launch, no second reduction pass;
+//       gemm_lines_kernel for larger row counts: 64 x 256 tiles;
 //   - gemm_simt_kernel: every other case (f32, either operand transposed,
 //     unaligned shapes).  Register-tiled FMA-free float loops that keep the
 //     reference's k order per output, so f32 results are bit-identical to the
@@ -77,26 +79,25 @@ struct GemmArgs {
     BatchMap bm;
 };
 
-// Workgroup = (column tile of 64 * CT, row tile of 16 * RT, batch, K split);
-// wave w owns columns n0 = (tile * 4 + w) * 16 * CT .. + 16 * CT.  Per chunk
-// of 64 k the workgroup stages its activation rows once in LDS and each wave
-// its own weight rows, both as whole 128-byte lines (8 rows x 128 bytes per
-// load instruction: on gfx950 that streams at about 5.0 TB/s against 3.2 TB/s
-// for MFMA-layout half lines) into tiles whose 16-byte pieces are XOR-swizzled
-// by (row / 2) % 8, so the 128-bit LDS writes and the MFMA-layout 128-bit
-// reads are conflict-free.  Tiles are double buffered: chunk c + 1's loads
-// are in flight while chunk c multiplies.  Loads go through buffer resources
-// whose range checks return zero past the operand's last row; every offset is
-// in the checked vector offset.
-template <int RT, int CT, int OCC, bool SPLIT>
+// Prefill-sized products: workgroup = 16 * RT rows x 64 * CT columns of one
+// batch; wave w owns columns n0 = (tile * 4 + w) * 16 * CT .. + 16 * CT.  Per
+// chunk of 64 k the workgroup stages its activation rows once in LDS and
+// each wave its own weight rows, both as whole 128-byte lines (8 rows x 128
+// bytes per load instruction: on gfx950 that streams at about 5.0 TB/s
+// against 3.2 TB/s for MFMA-layout half lines) into tiles whose 16-byte
+// pieces are XOR-swizzled by (row / 2) % 8, so the 128-bit LDS writes and the
+// MFMA-layout 128-bit reads are conflict-free.  Tiles are double buffered:
+// chunk c + 1's loads are in flight while chunk c multiplies.  Loads go
+// through buffer resources whose range checks return zero past the operand's
+// last row; every offset is in the checked vector offset.
+template <int RT, int CT, int OCC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void gemm_lines_kernel(GemmArgs g) {
     constexpr int kWTile = 16 * CT * 128;
     constexpr int kXTile = 16 * RT * 128;
     constexpr int kXPer = (16 * RT * 8 + 255) / 256;
     __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kXTile + 4 * 2 * kWTile];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int ct = static_cast<int>(blockIdx.x) / g.splits;
-    const int split = static_cast<int>(blockIdx.x) % g.splits;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ct = static_cast<int>(blockIdx.x);
     const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 16 * RT;
     const int64_t bz = blockIdx.z;
     int64_t lo, ro;
@@ -107,10 +108,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     unsigned char* xt = lds;
     unsigned char* wt = lds + 2 * kXTile + wave * 2 * kWTile;
     auto swz = [](int row, int piece) { return row * 128 + ((piece ^ ((row >> 1) & 7)) << 4); };
-    const int64_t ksteps = K / 32;
-    const int64_t chunks = (ksteps + 1) / 2;
-    const int64_t c_begin = static_cast<int64_t>(split) * g.split_chunks;
-    const int64_t c_end = min<int64_t>(chunks, c_begin + g.split_chunks);
+    // chunk indices are 32-bit (K <= 2^21): their compares stay on the scalar unit
+    const int ksteps = static_cast<int>(K / 32);
+    const int chunks = (ksteps + 1) / 2;
 
     const int64_t wrows = wave_live ? min<int64_t>(16 * CT, N - n0) : 0;
     const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
@@ -150,27 +150,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
         for (int c = 0; c < CT; c++) acc[t][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     uint4 wv[2 * CT], xv[kXPer];
-    auto load = [&](int64_t ch) {
-        const bool win = 2 * ch + (w_hi ? 1 : 0) < ksteps;
-        const int kb = static_cast<int>(ch * 128);
+    // the k-tail mask is applied when the registers are written to LDS
+    auto load = [&](int ch) {
+        const int kb = ch * 128;
 #pragma unroll
-        for (int i = 0; i < 2 * CT; i++) {
-            const uint4 v = __builtin_bit_cast(
-                uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wlane + i * wstep + kb, 0, 0));
-            wv[i] = win ? v : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int q = 0; q < kXPer; q++) {
-            const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[q] + kb, 0, 0));
-            xv[q] = 2 * ch + (x_hi[q] ? 1 : 0) < ksteps ? v : make_uint4(0, 0, 0, 0);
-        }
-    };
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 2 * CT; i++) *reinterpret_cast<uint4*>(wt + buf * kWTile + wbase[i & 1] + i * 1024) = wv[i];
+        for (int i = 0; i < 2 * CT; i++)
+            wv[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wlane + i * wstep + kb, 0, 0));
 #pragma unroll
         for (int q = 0; q < kXPer; q++)
-            if (xlive[q]) *reinterpret_cast<uint4*>(xt + buf * kXTile + xaddr[q]) = xv[q];
+            xv[q] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[q] + kb, 0, 0));
+    };
+    auto store = [&](int buf, int ch) {
+        const bool win = 2 * ch + (w_hi ? 1 : 0) < ksteps;
+#pragma unroll
+        for (int i = 0; i < 2 * CT; i++)
+            *reinterpret_cast<uint4*>(wt + buf * kWTile + wbase[i & 1] + i * 1024) = win ? wv[i] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < kXPer; q++)
+            if (xlive[q])
+                *reinterpret_cast<uint4*>(xt + buf * kXTile + xaddr[q]) =
+                    2 * ch + (x_hi[q] ? 1 : 0) < ksteps ? xv[q] : make_uint4(0, 0, 0, 0);
     };
     auto mma = [&](int buf) {
 #pragma unroll
@@ -189,20 +188,162 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
             }
         }
     };
-    if (c_begin < c_end) {
-        load(c_begin);
-        store(0);
+    load(0);
+    store(0, 0);
+    __syncthreads();
+    for (int ch = 0; ch < chunks; ch++) {
+        if (ch + 1 < chunks) load(ch + 1);
+        if (wave_live) mma(ch & 1);
+        if (ch + 1 < chunks) store((ch + 1) & 1, ch + 1);
         __syncthreads();
-        for (int64_t ch = c_begin; ch < c_end; ch++) {
-            const int cur = static_cast<int>((ch - c_begin) & 1);
-            if (ch + 1 < c_end) load(ch + 1);
-            if (wave_live) mma(cur);
-            if (ch + 1 < c_end) store(cur ^ 1);
-            __syncthreads();
+    }
+    if (!wave_live) return;
+    // acc[t][c][i]: row r0 + 16 t + 4 (lane / 16) + i, column n0 + 16 c + lane % 16
+    const int64_t ob = bz * M * N;
+#pragma unroll
+    for (int c = 0; c < CT; c++) {
+        const int64_t nc = n0 + 16 * c + (lane & 15);
+        if (nc >= N) continue;
+        const float bias = g.bias ? bf16_to_f32(g.bias[nc]) : 0.0f;
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int64_t rr = r0 + 16 * t + 4 * (lane >> 4) + i;
+                if (rr < M) g.out[ob + rr * N + nc] = f32_to_bf16(acc[t][c][i] + bias);  // 2-byte: L2 combines them
+            }
+    }
+}
+
+// Decode-shaped products (a few dozen rows against megabytes of weights):
+// workgroup = 16 * CT output columns x 16 * RT rows; its four waves take
+// consecutive quarters of the workgroup's K range and run independently --
+// no workgroup barrier inside the K loop -- so each wave keeps Q chunks of
+// its weight rows in flight on its own.  A wave loads its 16 * CT weight rows
+// as whole 128-byte lines into a private, swizzled, double-buffered LDS tile
+// (read back in MFMA layout) and its activation rows straight into MFMA
+// A-operand registers (they are L2-resident; every workgroup reads them).
+// The K loop is straight-line over CPS chunks so every register slot is
+// statically named and each LDS write waits only for its own chunk.  The
+// four partial accumulators are summed in wave order through LDS; when the
+// grid also splits K across workgroups, the last-arriving workgroup of each
+// tile sums the splits' fp32 partials in split order (deterministic).
+template <int RT, int CT, int Q, int CPS, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void gemm_waves_kernel(GemmArgs g) {
+    constexpr int kWTile = 16 * CT * 128;
+    constexpr int kAcc = RT * CT * 64 * 16;  // one wave's accumulators, bytes
+    constexpr int kLds = 4 * 2 * kWTile > 3 * kAcc ? 4 * 2 * kWTile : 3 * kAcc;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kLds];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ct = static_cast<int>(blockIdx.x) / g.splits;
+    const int split = static_cast<int>(blockIdx.x) % g.splits;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 16 * RT;
+    const int64_t bz = blockIdx.z;
+    int64_t lo, ro;
+    batch_offsets(g.bm, bz, lo, ro);
+    const int64_t M = g.M, N = g.N, K = g.K;
+    const int64_t n0 = static_cast<int64_t>(ct) * 16 * CT;
+    unsigned char* wt = lds + wave * 2 * kWTile;
+    auto swz = [](int row, int piece) { return row * 128 + ((piece ^ ((row >> 1) & 7)) << 4); };
+    const int ksteps = static_cast<int>(K / 32);
+    const int chunks = (ksteps + 1) / 2;
+    const int wg_begin = split * g.split_chunks;
+    const int wg_end = min(chunks, wg_begin + g.split_chunks);
+    const int c_begin = min(wg_end, wg_begin + wave * CPS);
+    const int c_end = min(wg_end, c_begin + CPS);
+
+    const int64_t wrows = min<int64_t>(16 * CT, N - n0);
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(g.w + ro + n0 * K), 0, static_cast<int>(wrows * K * 2), 0x00020000);
+    const int64_t xrows = min<int64_t>(16 * RT, M - r0);
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(g.a + lo + r0 * K), 0, static_cast<int>(xrows * K * 2), 0x00020000);
+    const int wlane = static_cast<int>((lane >> 3) * K * 2 + (lane & 7) * 16);
+    const int wstep = static_cast<int>(8 * K * 2);
+    const int wbase[2] = {swz(lane >> 3, lane & 7), swz(8 + (lane >> 3), lane & 7) - 1024};
+    // A operand of tile t, k-step u: row 16 t + lane % 16, 16-byte piece 4 u + lane / 16
+    int xoff[RT][2];
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+            xoff[t][u] = static_cast<int>((16 * t + (lane & 15)) * K * 2 + (4 * u + (lane >> 4)) * 16);
+    int raddr[2][CT];
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int c = 0; c < CT; c++) raddr[u][c] = swz(16 * c + (lane & 15), 4 * u + (lane >> 4));
+
+    f32x4_t acc[RT][CT];
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int c = 0; c < CT; c++) acc[t][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    uint4 wv[Q][2 * CT], xv[Q][RT][2];
+    // clamped re-reads past this wave's range: L2 hits, never multiplied
+    auto load = [&](int ch, int slot) {
+        const int kb = max(0, min(ch, c_end - 1)) * 128;
+#pragma unroll
+        for (int i = 0; i < 2 * CT; i++)
+            wv[slot][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wlane + i * wstep + kb, 0, 0));
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+                xv[slot][t][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[t][u] + kb, 0, 0));
+    };
+    auto store = [&](int slot, int buf) {
+#pragma unroll
+        for (int i = 0; i < 2 * CT; i++) *reinterpret_cast<uint4*>(wt + buf * kWTile + wbase[i & 1] + i * 1024) = wv[slot][i];
+    };
+    // the second k-step of a half chunk (odd K / 32) is skipped, so the
+    // registers past K never reach an MFMA
+    auto mma = [&](int slot, int buf, int ch) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            if (u == 1 && 2 * ch + 1 >= ksteps) break;
+#pragma unroll
+            for (int c = 0; c < CT; c++) {
+                const uint4 bv = *reinterpret_cast<const uint4*>(wt + buf * kWTile + raddr[u][c]);
+#pragma unroll
+                for (int t = 0; t < RT; t++)
+                    acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xv[slot][t][u]),
+                                                                        __builtin_bit_cast(bf16x8_t, bv), acc[t][c],
+                                                                        0, 0, 0);
+            }
         }
+    };
+#pragma unroll
+    for (int s = 0; s < Q; s++) load(c_begin + s, s);
+    store(0, 0);
+#pragma unroll
+    for (int u = 0; u < CPS; u++) {
+        const int c = c_begin + u;
+        if (c < c_end) mma(u % Q, u & 1, c);
+        if (c + 1 < c_end) store((u + 1) % Q, (u + 1) & 1);
+        load(c + Q, u % Q);
     }
 
-    // acc[t][c][i]: row r0 + 16 t + 4 (lane / 16) + i, column n0 + 16 c + lane % 16
+    // sum the four waves' partials in wave order (LDS reused after a barrier)
+    __syncthreads();
+    if (wave > 0) {
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int c = 0; c < CT; c++)
+                *reinterpret_cast<f32x4_t*>(lds + (wave - 1) * kAcc + ((t * CT + c) * 64 + lane) * 16) = acc[t][c];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int w = 0; w < 3; w++)
+#pragma unroll
+            for (int t = 0; t < RT; t++)
+#pragma unroll
+                for (int c = 0; c < CT; c++)
+                    acc[t][c] += *reinterpret_cast<const f32x4_t*>(lds + w * kAcc + ((t * CT + c) * 64 + lane) * 16);
+    }
+
     const int64_t ob = bz * M * N;
     auto emit = [&](int t, int c, const f32x4_t& v) {
         const int64_t nc = n0 + 16 * c + (lane & 15);
@@ -211,40 +352,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int64_t rr = r0 + 16 * t + 4 * (lane >> 4) + i;
-            if (rr < M) g.out[ob + rr * N + nc] = f32_to_bf16(v[i] + bias);  // 2-byte: L2 combines them
+            if (rr < M) g.out[ob + rr * N + nc] = f32_to_bf16(v[i] + bias);
         }
     };
-    if (!SPLIT || g.splits == 1) {
-        if (wave_live)
+    if (g.splits == 1) {
+        if (wave == 0)
 #pragma unroll
             for (int t = 0; t < RT; t++)
 #pragma unroll
                 for (int c = 0; c < CT; c++) emit(t, c, acc[t][c]);
         return;
     }
-
-    // Split-K: write this split's partial tile through to the agent's
-    // coherence point, count in, and let the last of the tile's workgroups
-    // sum the splits in order 0 .. splits-1 and write the output.
+    // split-K across workgroups: partials written through to the agent's coherence
+    // point, then the last-arriving workgroup of the tile sums them (wave 0 holds the tile)
     const int64_t tile = (bz * g.row_tiles + blockIdx.y) * g.col_tiles + ct;
-    constexpr int kWaveFloats = RT * CT * 64 * 4;
-    float* pbase = g.part + (tile * g.splits) * 4 * kWaveFloats + wave * kWaveFloats;
-    if (wave_live) {
+    constexpr int kTileFloats = RT * CT * 64 * 4;
+    float* pbase = g.part + tile * g.splits * kTileFloats;
+    if (wave == 0) {
 #pragma unroll
         for (int t = 0; t < RT; t++)
 #pragma unroll
             for (int c = 0; c < CT; c++) {
-                uint64_t* p = reinterpret_cast<uint64_t*>(pbase + split * 4 * kWaveFloats + ((t * CT + c) * 64 + lane) * 4);
-                const uint64_t w0 = static_cast<uint64_t>(__float_as_uint(acc[t][c][0])) |
-                                    (static_cast<uint64_t>(__float_as_uint(acc[t][c][1])) << 32);
-                const uint64_t w1 = static_cast<uint64_t>(__float_as_uint(acc[t][c][2])) |
-                                    (static_cast<uint64_t>(__float_as_uint(acc[t][c][3])) << 32);
-                __hip_atomic_store(p, w0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(p + 1, w1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                uint64_t* p = reinterpret_cast<uint64_t*>(pbase + split * kTileFloats + ((t * CT + c) * 64 + lane) * 4);
+                __hip_atomic_store(p, static_cast<uint64_t>(__float_as_uint(acc[t][c][0])) |
+                                          (static_cast<uint64_t>(__float_as_uint(acc[t][c][1])) << 32),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(p + 1, static_cast<uint64_t>(__float_as_uint(acc[t][c][2])) |
+                                              (static_cast<uint64_t>(__float_as_uint(acc[t][c][3])) << 32),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
     }
     __shared__ int is_last;
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's write-through stores acknowledged
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
         uint32_t* ctr = g.counters + tile;
@@ -253,20 +392,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         if (is_last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (!is_last || !wave_live) return;
+    if (!is_last || wave != 0) return;
 #pragma unroll
     for (int t = 0; t < RT; t++)
 #pragma unroll
         for (int c = 0; c < CT; c++) {
             f32x4_t sum = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            for (int s = 0; s < g.splits; s++) {
-                uint64_t* p = reinterpret_cast<uint64_t*>(pbase + s * 4 * kWaveFloats + ((t * CT + c) * 64 + lane) * 4);
-                const uint64_t w0 = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const uint64_t w1 = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                sum[0] += __uint_as_float(static_cast<uint32_t>(w0));
-                sum[1] += __uint_as_float(static_cast<uint32_t>(w0 >> 32));
-                sum[2] += __uint_as_float(static_cast<uint32_t>(w1));
-                sum[3] += __uint_as_float(static_cast<uint32_t>(w1 >> 32));
+            const int64_t off = ((t * CT + c) * 64 + lane) * 4;
+            for (int s0 = 0; s0 < g.splits; s0 += 8) {
+                uint64_t w0[8], w1[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const int s = s0 + q < g.splits ? s0 + q : s0;
+                    uint64_t* p = reinterpret_cast<uint64_t*>(pbase + s * kTileFloats + off);
+                    w0[q] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    w1[q] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    if (s0 + q >= g.splits) break;
+                    sum[0] += __uint_as_float(static_cast<uint32_t>(w0[q]));
+                    sum[1] += __uint_as_float(static_cast<uint32_t>(w0[q] >> 32));
+                    sum[2] += __uint_as_float(static_cast<uint32_t>(w1[q]));
+                    sum[3] += __uint_as_float(static_cast<uint32_t>(w1[q] >> 32));
+                }
             }
             emit(t, c, sum);
         }
@@ -412,7 +561,8 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
     const bool aligned = ((reinterpret_cast<uintptr_t>(pl) | reinterpret_cast<uintptr_t>(pr)) & 15) == 0;
     const bool lines = l.dtype == SANDY_BF16 && !tl && tr && p.K % 32 == 0 && p.K > 0 && aligned &&
                        p.K <= (int64_t{1} << 21) && env_int("SANDY_GEMM_SIMT", 0) == 0;
-    if (lines) {
+    const bool waves = lines && env_int("SANDY_GEMM_WAVES", p.M <= 64 ? 1 : 0) != 0;
+    if (waves) {
         GemmArgs g{};
         g.a = static_cast<const uint16_t*>(pl);
         g.w = static_cast<const uint16_t*>(pr);
@@ -422,38 +572,58 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
         g.N = p.N;
         g.K = p.K;
         g.bm = p.bm;
-        // tile: rows per workgroup follow M; 64 columns per wave for large products
-        int variant = env_int("SANDY_GEMM_TILE", -1);
-        if (variant < 0) variant = p.M <= 16 ? 0 : p.M <= 32 ? 1 : p.M <= 64 ? 2 : 3;
-        static const int kRT[] = {1, 2, 4, 4, 2, 1};
-        static const int kCT[] = {1, 1, 1, 4, 2, 2};
-        if (variant > 5) variant = 3;
-        const int RT = kRT[variant], CT = kCT[variant];
-        const int64_t rows_per = 16 * RT;
-        const int64_t row_tiles = (p.M + rows_per - 1) / rows_per;
-        const int64_t col_tiles = (p.N + 64 * CT - 1) / (64 * CT);
+        // tile: 16 * RT rows x 16 * CT columns (variants: RT 1 / 2 / 4 with
+        // CT 1, then (RT, CT) = (2, 2), (1, 2), (2, 4), (1, 4), (4, 2), (4, 4))
+        static const int kRT[] = {1, 2, 4, 2, 1, 2, 1, 4, 4};
+        static const int kCT[] = {1, 1, 1, 2, 2, 4, 4, 2, 4};
         const int64_t chunks = (p.K / 32 + 1) / 2;
-        if (row_tiles > 65535 || col_tiles > (1 << 20))
+        int variant = env_int("SANDY_GEMM_TILE", -1);
+        int cps = env_int("SANDY_GEMM_CPS", 0);
+        // K: at most 64 chunks (4096 k) per workgroup, split evenly; the
+        // per-wave run is rounded up to a built run length
+        const int64_t ksplits = (chunks + 63) / 64;
+        if (variant < 0 || variant > 8) {
+            // Measured on decode shapes (few long streams beat many short
+            // ones, and a cross-workgroup split costs its merge): the widest
+            // column tile that still gives about 120 workgroups, so the
+            // activation rows are re-read by as few workgroups as possible.
+            const int64_t rt = p.M <= 16 ? 1 : 2;
+            const int64_t rows = (p.M + 16 * rt - 1) / (16 * rt) * p.batches;
+            int ct = 1;
+            for (int c : {4, 2}) {
+                if ((p.N + 16 * c - 1) / (16 * c) * rows * ksplits >= 120) {
+                    ct = c;
+                    break;
+                }
+            }
+            static const int kPick[2][3] = {{0, 4, 6}, {1, 3, 5}};  // [RT 1/2][CT 1/2/4]
+            variant = kPick[rt == 1 ? 0 : 1][ct == 1 ? 0 : ct == 2 ? 1 : 2];
+        }
+        const int RT = kRT[variant], CT = kCT[variant];
+        const int64_t row_tiles = (p.M + 16 * RT - 1) / (16 * RT);
+        const int64_t col_tiles = (p.N + 16 * CT - 1) / (16 * CT);
+        if (row_tiles > 65535 || col_tiles > (1 << 24))
             return fail(e, SANDY_ERR_UNSUPPORTED, "%s shape exceeds the launch grid", what);
         const int64_t tiles = row_tiles * col_tiles * p.batches;
-        // split K while the tiles alone leave the chip short of workgroups,
-        // keeping at least min_chunks chunks of 64 k per split
-        const int64_t target = env_int("SANDY_GEMM_TARGET_WG", 1024);
-        const int64_t min_chunks = std::max(1, env_int("SANDY_GEMM_MIN_CHUNKS", 4));
-        int64_t splits = env_int("SANDY_GEMM_SPLIT", 0);
-        if (splits <= 0) splits = std::min<int64_t>((target + tiles - 1) / tiles, chunks / min_chunks);
-        if (variant == 3) splits = 1;  // the 64 x 256 tile is built without the split-K epilogue
-        splits = std::max<int64_t>(1, std::min<int64_t>(splits, chunks));
-        const int64_t split_chunks = (chunks + splits - 1) / splits;
-        splits = (chunks + split_chunks - 1) / split_chunks;  // no empty splits
+        if (cps <= 0) cps = static_cast<int>(((chunks + ksplits - 1) / ksplits + 3) / 4);
+        static const int kRuns[] = {2, 3, 4, 5, 6, 8, 10, 12, 16};
+        int run = 16;
+        for (int r : kRuns) {
+            if (r >= cps) {
+                run = r;
+                break;
+            }
+        }
+        cps = run;
+        const int64_t splits = (chunks + 4 * cps - 1) / (4 * cps);
         g.col_tiles = static_cast<int32_t>(col_tiles);
         g.row_tiles = static_cast<int32_t>(row_tiles);
         g.splits = static_cast<int32_t>(splits);
-        g.split_chunks = static_cast<int32_t>(split_chunks);
+        g.split_chunks = 4 * cps;
         if (col_tiles * splits > 0x7fffffff) return fail(e, SANDY_ERR_UNSUPPORTED, "%s shape exceeds the launch grid", what);
         if (splits > 1) {
             int status = 0;
-            const size_t part = static_cast<size_t>(tiles * splits) * 4 * RT * CT * 64 * 4 * sizeof(float);
+            const size_t part = static_cast<size_t>(tiles * splits) * RT * CT * 64 * 4 * sizeof(float);
             g.part = static_cast<float*>(device_workspace(4, part, stream, e, &status));
             if (status) return status;
             g.counters = static_cast<uint32_t*>(device_counters(1, static_cast<size_t>(tiles) * sizeof(uint32_t), stream, e, &status));
@@ -461,14 +631,50 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
         }
         const dim3 grid(static_cast<unsigned>(col_tiles * splits), static_cast<unsigned>(row_tiles),
                         static_cast<unsigned>(p.batches));
+#define WAVES_RUN(RT_, CT_, OCC_, R_) \
+    case R_: hipLaunchKernelGGL((gemm_waves_kernel<RT_, CT_, 2, R_, OCC_>), grid, dim3(256), 0, stream, g); break;
+#define WAVES_CPS(RT_, CT_, OCC_)                                                                          \
+    switch (cps) {                                                                                         \
+        WAVES_RUN(RT_, CT_, OCC_, 2) WAVES_RUN(RT_, CT_, OCC_, 3) WAVES_RUN(RT_, CT_, OCC_, 4)            \
+        WAVES_RUN(RT_, CT_, OCC_, 5) WAVES_RUN(RT_, CT_, OCC_, 6) WAVES_RUN(RT_, CT_, OCC_, 8)            \
+        WAVES_RUN(RT_, CT_, OCC_, 10) WAVES_RUN(RT_, CT_, OCC_, 12) WAVES_RUN(RT_, CT_, OCC_, 16)         \
+    }
         switch (variant) {
-            case 0: hipLaunchKernelGGL((gemm_lines_kernel<1, 1, 4, true>), grid, dim3(256), 0, stream, g); break;
-            case 1: hipLaunchKernelGGL((gemm_lines_kernel<2, 1, 4, true>), grid, dim3(256), 0, stream, g); break;
-            case 2: hipLaunchKernelGGL((gemm_lines_kernel<4, 1, 2, true>), grid, dim3(256), 0, stream, g); break;
-            case 4: hipLaunchKernelGGL((gemm_lines_kernel<2, 2, 2, true>), grid, dim3(256), 0, stream, g); break;
-            case 5: hipLaunchKernelGGL((gemm_lines_kernel<1, 2, 4, true>), grid, dim3(256), 0, stream, g); break;
-            default: hipLaunchKernelGGL((gemm_lines_kernel<4, 4, 2, false>), grid, dim3(256), 0, stream, g); break;
+            case 0: WAVES_CPS(1, 1, 4); break;
+            case 1: WAVES_CPS(2, 1, 4); break;
+            case 2: WAVES_CPS(4, 1, 2); break;
+            case 3: WAVES_CPS(2, 2, 2); break;
+            case 4: WAVES_CPS(1, 2, 4); break;
+            case 5: WAVES_CPS(2, 4, 2); break;
+            case 6: WAVES_CPS(1, 4, 2); break;
+            case 7: WAVES_CPS(4, 2, 2); break;
+            default: WAVES_CPS(4, 4, 2); break;
         }
+#undef WAVES_RUN
+#undef WAVES_CPS
+    } else if (lines) {
+        // 64 x 256 tiles for prefill-sized products (the K loop is rolled and
+        // the grid never splits K)
+        GemmArgs g{};
+        g.a = static_cast<const uint16_t*>(pl);
+        g.w = static_cast<const uint16_t*>(pr);
+        g.bias = static_cast<const uint16_t*>(pb);
+        g.out = static_cast<uint16_t*>(po);
+        g.M = p.M;
+        g.N = p.N;
+        g.K = p.K;
+        g.bm = p.bm;
+        const int64_t row_tiles = (p.M + 63) / 64;
+        const int64_t col_tiles = (p.N + 255) / 256;
+        if (row_tiles > 65535 || col_tiles > 0x7fffffff)
+            return fail(e, SANDY_ERR_UNSUPPORTED, "%s shape exceeds the launch grid", what);
+        g.col_tiles = static_cast<int32_t>(col_tiles);
+        g.row_tiles = static_cast<int32_t>(row_tiles);
+        g.splits = 1;
+        g.split_chunks = static_cast<int32_t>((p.K / 32 + 1) / 2);
+        const dim3 grid(static_cast<unsigned>(col_tiles), static_cast<unsigned>(row_tiles),
+                        static_cast<unsigned>(p.batches));
+        hipLaunchKernelGGL((gemm_lines_kernel<4, 4, 2>), grid, dim3(256), 0, stream, g);
     } else {
         const int64_t gy = (p.M + 63) / 64, gx = (p.N + 63) / 64;
         if (gy > 65535 || gx > 0x7fffffff) return fail(e, SANDY_ERR_UNSUPPORTED, "%s shape exceeds the launch grid", what);

@@ -677,7 +677,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
     constexpr int kXTile = 16 * RT * 128;  // the workgroup's activation rows x 128 bytes
     constexpr int kXPer = (16 * RT * 8 + 255) / 256;  // 16-byte activation pieces per thread
     __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kXTile + 4 * 2 * kWTile];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t e = blockIdx.x % experts;
     const int64_t b = blockIdx.x / experts;
     const int64_t n0 = (static_cast<int64_t>(blockIdx.y) * 4 + wave) * 16 * CT;

@@ -131,7 +131,7 @@ def test_matmul_empty(ops):
 # ---------------------------------------------------------------- MFMA path
 # (M, N, K): decode rows against projection-like weights, ragged N, odd k-steps
 MFMA_SHAPES = [(1, 256, 64), (7, 200, 96), (16, 512, 2048), (32, 2048, 512), (33, 300, 160), (64, 1000, 256),
-               (100, 520, 224), (256, 640, 1024)]
+               (3, 700, 2560), (40, 96, 5632), (100, 520, 224), (256, 640, 1024), (130, 300, 96)]
 
 
 @pytest.mark.parametrize("m,n,k", MFMA_SHAPES)
@@ -144,20 +144,21 @@ def test_matmul_bf16_mfma_matches_oracle(ops, oracle, m, n, k):
     assert_close(got, want, torch.bfloat16, f"matmul {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("variant", range(6))
-@pytest.mark.parametrize("split", [1, 3, 8])
-def test_matmul_bf16_every_tile_and_split(ops, oracle, variant, split):
-    """Every tile shape of the MFMA kernel, with and without split K (the 64 x
-    256 tile never splits)."""
-    r = rng(variant * 10 + split)
-    m, n, k = 45, 600, 1024
+@pytest.mark.parametrize("variant", range(9))
+@pytest.mark.parametrize("cps", [2, 5, 16])
+def test_matmul_bf16_wave_kernel_tiles_and_splits(ops, oracle, variant, cps):
+    """The decode kernel (four independent waves per workgroup splitting K)
+    for every tile and a short, odd and long run per wave: 1248 = 19.5
+    chunks of 64 gives split K, idle waves, partial runs and a half chunk."""
+    r = rng(variant * 100 + cps)
+    m, n, k = 45, 600, 1248
     L = from_f32(normal(r, (m, k)), torch.bfloat16)
     W = from_f32(normal(r, (n, k), 0.05), torch.bfloat16)
     want = oracle.matmul(to_oracle(L), to_oracle(W), transpose_rhs=True)
-    with env(SANDY_GEMM_TILE=variant, SANDY_GEMM_SPLIT=split):
+    with env(SANDY_GEMM_WAVES=1, SANDY_GEMM_TILE=variant, SANDY_GEMM_CPS=cps):
         got = ops.matmul(L, W, transpose_rhs=True)
         again = ops.matmul(L, W, transpose_rhs=True)
-    assert_close(got, want, torch.bfloat16, f"variant {variant} split {split}")
+    assert_close(got, want, torch.bfloat16, f"waves variant {variant} cps {cps}")
     assert torch.equal(got, again), "split-K result is not deterministic"
 
 
