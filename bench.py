@@ -52,7 +52,7 @@ def parse():
     p.add_argument("--cpu-tokens", type=int, default=4096, help="C2 rows timed on the CPU")
     p.add_argument("--cpu-seqs", type=int, default=8, help="decode sequences timed on the CPU")
     p.add_argument("--only", default="", help="comma list of kernels to run (profiling)")
-    p.add_argument("--no-extras", action="store_true", help="skip the config-4/5 kernel table")
+    p.add_argument("--no-extras", action="store_true", help="skip the per-kernel table of the other configs")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a plain 256 MiB device copy (counter calibration for rocprofv3 --pmc)")
     return p.parse_args()
@@ -151,12 +151,15 @@ def build_workload(replicas):
 
 GEM_B, GEM_HQ, GEM_HKV, GEM_D, GEM_HID, GEM_FF, GEM_VOCAB = 64, 8, 2, 256, 2560, 10240, 262144
 GPT2_VOCAB = 50257
+FFN, LLAMA_VOCAB = 5632, 32000
 MOE_T, MOE_E, MOE_K, MOE_D, MOE_F = 512, 128, 8, 2816, 704
 
 
 def build_extras(replicas):
     """Config 4 (Gemma decoder layer: paged decode D 256 + norm/GeGLU/softcap
-    groups at batch 64) and config 5 (MoE block) as prepared kernel calls.
+    groups at batch 64), config 5 (MoE block), config 1's greedy argmax, the
+    TinyLlama decode projections (dense GEMMs) at the config-3 batch and
+    config 2's SiLU gate at the model's FFN width, as prepared kernel calls.
     Reported per kernel; not part of `value`."""
     import numpy as np
     import torch
@@ -237,6 +240,41 @@ def build_extras(replicas):
     keep += [c1_logits, c1_v, c1_i, d1]
     kernels["c1_greedy_argmax"] = [Prepared("sandy_hip_topk", d1["l"], C.c_int64(1), C.c_int64(-1), d1["v"], d1["i"])]
     bytes_per["c1_greedy_argmax"] = GPT2_VOCAB * 4 + 12
+    # ---- TinyLlama decode projections at the config-3 batch (32 rows): the
+    # dense GEMMs of one decode step (q/k/v and gate/up fused as one weight
+    # each) and the lm-head, bf16 weights N(0, 0.02); replicas rotate so the
+    # weights stream from HBM
+    dense = {"c3_qkv_proj": (HQ * HD + 2 * HKV * HD, HID), "c3_o_proj": (HID, HID),
+             "c3_gate_up_proj": (2 * FFN, HID), "c3_down_proj": (HID, FFN), "c3_lm_head": (LLAMA_VOCAB, HID)}
+    for name, (n, k) in dense.items():
+        kernels[name] = []
+        reps = 1 if n * k * 2 * replicas > 512 * 2 ** 20 else replicas
+        for rep in range(reps):
+            g.manual_seed(7 + 100 * rep)
+            xin = torch.randn(DEC_B, k, generator=g, device=dev).to(bf)
+            w = (torch.randn(n, k, generator=g, device=dev) * 0.02).to(bf)
+            yo = torch.empty(DEC_B, n, dtype=bf, device=dev)
+            dd = {kk: desc(v) for kk, v in dict(x=xin, w=w, y=yo).items()}
+            keep += [xin, w, yo, dd]
+            kernels[name].append(Prepared("sandy_hip_matmul", dd["x"], dd["w"], C.c_int32(0), C.c_int32(1), dd["y"]))
+        bytes_per[name] = n * k * 2 + DEC_B * k * 2 + DEC_B * n * 2
+    # ---- config 2 SiLU-gate at the model's FFN width (the step above runs it at 2048)
+    kernels["c2_silu_gate_ffn"] = []
+    snodes, sres = ops.silu_mul_nodes()
+    csn = ops._nodes(snodes)
+    bc2 = (C.c_int32 * 2)(0, 0)
+    keep += [csn, bc2]
+    for rep in range(replicas):
+        g.manual_seed(11 + 100 * rep)
+        gt = torch.randn(T, FFN, generator=g, device=dev).to(bf)
+        ut = torch.randn(T, FFN, generator=g, device=dev).to(bf)
+        at = torch.empty_like(gt)
+        dd = {kk: desc(v) for kk, v in dict(g=gt, u=ut, a=at).items()}
+        arr = (_lib.SandyTensor * 2)(dd["g"].contents, dd["u"].contents)
+        keep += [gt, ut, at, dd, arr]
+        kernels["c2_silu_gate_ffn"].append(Prepared("sandy_hip_elementwise", csn, C.c_int32(len(snodes)),
+                                                    C.c_uint32(sres), arr, bc2, C.c_int32(2), dd["a"]))
+    bytes_per["c2_silu_gate_ffn"] = 3 * T * FFN * 2
     # ---- config 5 (one copy: the 1.5 GB of expert weights exceed the cache)
     g.manual_seed(4)
     logits = torch.randn(MOE_T, MOE_E, generator=g, device=dev)
@@ -473,7 +511,8 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "cpu_baseline": None,
     }
-    want_extras = not args.no_extras and (not args.only or any(o.startswith(("c1_", "c4_", "c5_")) for o in args.only.split(",")))
+    want_extras = not args.no_extras and (not args.only or any(o.startswith(("c1_", "c2_", "c3_", "c4_", "c5_"))
+                                                               for o in args.only.split(",")))
     if want_extras:
         ek, eb, ekeep = build_extras(args.replicas)
         if args.only:
@@ -489,6 +528,7 @@ def main():
                 "c4_decode_tok_s": round(GEM_B / (eus["c4_paged_decode"] * 1e-6), 1),
                 "c5_moe_block_us": round(moe_us, 2),
                 "c5_moe_block_tok_s": round(MOE_T / (moe_us * 1e-6), 1),
+                "c3_projections_us": round(sum(v for n, v in eus.items() if n.startswith("c3_") and n != "c3_lm_head"), 2),
             }
         del ekeep
     if not args.no_cpu and not args.only:
