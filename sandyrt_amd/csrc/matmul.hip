@@ -579,14 +579,14 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
         const int64_t chunks = (p.K / 32 + 1) / 2;
         int variant = env_int("SANDY_GEMM_TILE", -1);
         int cps = env_int("SANDY_GEMM_CPS", 0);
-        // K: at most 64 chunks (4096 k) per workgroup, split evenly; the
+        // K: at most 32 chunks (2048 k) per workgroup, split evenly; the
         // per-wave run is rounded up to a built run length
-        const int64_t ksplits = (chunks + 63) / 64;
+        const int64_t ksplits = (chunks + 31) / 32;
         if (variant < 0 || variant > 8) {
-            // Measured on decode shapes (few long streams beat many short
-            // ones, and a cross-workgroup split costs its merge): the widest
-            // column tile that still gives about 120 workgroups, so the
-            // activation rows are re-read by as few workgroups as possible.
+            // Measured on decode shapes with the weights streamed from HBM
+            // (few long streams beat many short ones): the widest column tile
+            // that still gives about 120 workgroups, so the activation rows
+            // are re-read by as few workgroups as possible.
             const int64_t rt = p.M <= 16 ? 1 : 2;
             const int64_t rows = (p.M + 16 * rt - 1) / (16 * rt) * p.batches;
             int ct = 1;
