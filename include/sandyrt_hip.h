@@ -330,6 +330,10 @@ int sandy_hip_device_paged_append_step(SandyHipDevice* dev, uint32_t pool, const
  * the position_offsets of decode attention inside a captured step. */
 int sandy_hip_device_paged_positions(SandyHipDevice* dev, uint32_t pool, const uint32_t* tensors, int32_t count,
                                      const SandyTensor* positions, char* err, size_t err_cap);
+/* lengths[i] = device length of tensors[i]: the position the next appended
+ * row takes (the position_id of a decode step, computed inside the step). */
+int sandy_hip_device_paged_lengths(SandyHipDevice* dev, uint32_t pool, const uint32_t* tensors, int32_t count,
+                                   const SandyTensor* lengths, char* err, size_t err_cap);
 int sandy_hip_device_paged_meta(SandyHipDevice* dev, uint32_t tensor, SandyPagedMeta* meta, char* err,
                                 size_t err_cap);
 /* Reads the dense logical tensor (Device::read(DevicePagedTensorView)); synchronises. */

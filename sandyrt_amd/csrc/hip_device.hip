@@ -111,9 +111,9 @@ __global__ __launch_bounds__(256) void paged_append_step_kernel(const char* __re
 }
 
 __global__ void paged_positions_kernel(const int32_t* __restrict__ lengths, void* __restrict__ out, int32_t out_dt,
-                                       int32_t count, StepArgs args) {
+                                       int32_t count, int32_t delta, StepArgs args) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < count) store_index(out, out_dt, i, static_cast<int64_t>(lengths[args.slots[i]]) - 1);
+    if (i < count) store_index(out, out_dt, i, static_cast<int64_t>(lengths[args.slots[i]]) + delta);
 }
 
 } // namespace
@@ -517,9 +517,10 @@ int sandy_hip_device_paged_append_step(SandyHipDevice* d, uint32_t pool, const u
     return ok(e);
 }
 
-int sandy_hip_device_paged_positions(SandyHipDevice* d, uint32_t pool, const uint32_t* tensors, int32_t count,
-                                     const SandyTensor* positions, char* err, size_t err_cap) {
-    Err e{err, err_cap};
+namespace {
+// out[i] = device length of tensors[i] + delta
+int paged_lengths_plus(SandyHipDevice* d, uint32_t pool, const uint32_t* tensors, int32_t count,
+                       const SandyTensor* positions, int32_t delta, Err e) {
     int st = set_device(d, e);
     if (st) return st;
     std::lock_guard<std::mutex> lock(d->impl.mu);
@@ -536,9 +537,20 @@ int sandy_hip_device_paged_positions(SandyHipDevice* d, uint32_t pool, const uin
         args.slots[i] = it->second.slot;
     }
     hipLaunchKernelGGL(paged_positions_kernel, dim3(static_cast<unsigned>((count + 255) / 256)), dim3(256), 0,
-                       d->impl.stream, pit->second->lengths, base_ptr(*positions), positions->dtype, count, args);
+                       d->impl.stream, pit->second->lengths, base_ptr(*positions), positions->dtype, count, delta, args);
     SANDY_HIP_TRY(hipGetLastError(), e, "paged positions launch");
     return ok(e);
+}
+} // namespace
+
+int sandy_hip_device_paged_positions(SandyHipDevice* d, uint32_t pool, const uint32_t* tensors, int32_t count,
+                                     const SandyTensor* positions, char* err, size_t err_cap) {
+    return paged_lengths_plus(d, pool, tensors, count, positions, -1, Err{err, err_cap});
+}
+
+int sandy_hip_device_paged_lengths(SandyHipDevice* d, uint32_t pool, const uint32_t* tensors, int32_t count,
+                                   const SandyTensor* lengths, char* err, size_t err_cap) {
+    return paged_lengths_plus(d, pool, tensors, count, lengths, 0, Err{err, err_cap});
 }
 
 int sandy_hip_device_paged_meta(SandyHipDevice* d, uint32_t tensor, SandyPagedMeta* meta, char* err, size_t err_cap) {

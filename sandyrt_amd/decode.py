@@ -1,0 +1,256 @@
+"""Greedy decode step of the TinyLlama model program, built from the C-ABI
+entry points and run eagerly or as one captured HIP graph.
+
+The step is the reference's `eval_token` program (src/models/tinyllama/
+eval_token.sandy.go and common.sandy.go:1-62): embedding, 22 blocks of
+RMSNorm -> q/k/v projections -> RoPE (split-half, theta 1e4) -> paged
+append -> paged decode attention -> o projection -> residual add ->
+RMSNorm -> SiLU-gated MLP -> residual add, then the final RMSNorm, the
+lm-head and greedy token selection (src/server/Sampler.cpp:69-79).
+
+Everything stays on the device between steps: the position of the new token
+is the device-side length of the layer-0 K cache (read inside the step),
+the appends advance the lengths, and the greedy token id is written where the
+next step's embedding reads it -- so a captured step replays with no host
+work and no host synchronisation (the reference syncs and copies per row,
+src/device/cuda/CudaPagedTensor.cpp:649-740, Engine.cpp:548-596).
+
+Layout choices (same arithmetic as the reference program):
+  * q/k/v weights are concatenated into one [q + k + v, hidden] matrix and
+    gate/up into one [2 * ffn, hidden] matrix, so each is one GEMM; the
+    q/k/v and gate/up outputs are contiguous views of those GEMM outputs.
+  * the residual add is fused into the next RMSNorm (sandy_hip_add_rms_norm).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib, ops
+from ._lib import BF16, desc
+from .device import HipDevice
+
+
+@dataclass
+class DecodeConfig:
+    layers: int = 22
+    hidden: int = 2048
+    heads: int = 32
+    kv_heads: int = 4
+    head_dim: int = 64
+    ffn: int = 5632
+    vocab: int = 32000
+    page_size: int = 32
+    eps: float = 1e-5
+    theta: float = 10000.0
+    max_context: int = 4096
+
+
+def random_weights(cfg: DecodeConfig, seed: int = 0, std: float = 0.02, device="cuda") -> dict:
+    """Random-init bf16 weights of the TinyLlama architecture (no checkpoint
+    is available offline).  Norm weights are 1 + N(0, std)."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+
+    def n(*shape, mean=0.0):
+        return (torch.randn(*shape, generator=g, device=device) * std + mean).to(torch.bfloat16)
+
+    qkv = (cfg.heads + 2 * cfg.kv_heads) * cfg.head_dim
+    w = {"embed": n(cfg.vocab, cfg.hidden, mean=0.0) * 50, "norm": n(cfg.hidden, mean=1.0),
+         "lm_head": n(cfg.vocab, cfg.hidden)}
+    for layer in range(cfg.layers):
+        w[f"{layer}.in_norm"] = n(cfg.hidden, mean=1.0)
+        w[f"{layer}.qkv"] = n(qkv, cfg.hidden)
+        w[f"{layer}.o"] = n(cfg.hidden, cfg.heads * cfg.head_dim)
+        w[f"{layer}.post_norm"] = n(cfg.hidden, mean=1.0)
+        w[f"{layer}.gate_up"] = n(2 * cfg.ffn, cfg.hidden)
+        w[f"{layer}.down"] = n(cfg.hidden, cfg.ffn)
+    return w
+
+
+class _Call:
+    """One C-ABI kernel entry point with its arguments bound once."""
+
+    def __init__(self, name, *args, stream):
+        self.fn = getattr(_lib.lib(), name)
+        self.args = args + (C.c_void_p(stream),)
+        self.buf = C.create_string_buffer(256)
+        self.name = name
+
+    def __call__(self):
+        if self.fn(*self.args, self.buf, C.c_size_t(256)):
+            raise _lib.SandyError(1, f"{self.name}: {self.buf.value.decode()}")
+
+
+class _DevCall:
+    """One device-runtime entry point (runs on the device's stream)."""
+
+    def __init__(self, name, *args):
+        self.fn = getattr(_lib.lib(), name)
+        self.args = args
+        self.buf = C.create_string_buffer(256)
+        self.name = name
+
+    def __call__(self):
+        if self.fn(*self.args, self.buf, C.c_size_t(256)):
+            raise _lib.SandyError(1, f"{self.name}: {self.buf.value.decode()}")
+
+
+class TinyLlamaDecoder:
+    """Owns the paged K/V caches of one sequence and the step's buffers; the
+    step program is a fixed list of bound calls on the device's stream."""
+
+    def __init__(self, dev: HipDevice, cfg: DecodeConfig, weights: dict):
+        self.dev, self.cfg, self.w = dev, cfg, weights
+        c = cfg
+        bf = torch.bfloat16
+        pages = (c.max_context + c.page_size - 1) // c.page_size
+        self.k_pools, self.v_pools, self.k_seq, self.v_seq = [], [], [], []
+        for _ in range(c.layers):
+            for pools, seqs in ((self.k_pools, self.k_seq), (self.v_pools, self.v_seq)):
+                p = dev.create_paged_pool([1, c.kv_heads, -1, c.head_dim], BF16, 2, c.page_size, initial_pages=pages,
+                                          max_pages=pages, max_tensors=1, max_blocks=pages)
+                t = dev.alloc_paged(p)
+                dev.reserve_paged(t, pages)
+                pools.append(p)
+                seqs.append(t)
+        dv = "cuda"
+        qkv = (c.heads + 2 * c.kv_heads) * c.head_dim
+        self.token = torch.zeros(1, 1, dtype=torch.int64, device=dv)  # greedy output -> next input
+        self.pos = torch.zeros(1, dtype=torch.int64, device=dv)
+        self.x0 = torch.empty(1, 1, c.hidden, dtype=bf, device=dv)
+        self.res = [torch.empty(1, c.hidden, dtype=bf, device=dv) for _ in range(2)]
+        self.h = torch.empty(1, c.hidden, dtype=bf, device=dv)
+        self.qkv = torch.empty(1, qkv, dtype=bf, device=dv)
+        self.qr = torch.empty(1, c.heads, 1, c.head_dim, dtype=bf, device=dv)
+        self.kr = torch.empty(1, c.kv_heads, 1, c.head_dim, dtype=bf, device=dv)
+        self.ctx = torch.empty(1, c.heads, 1, c.head_dim, dtype=bf, device=dv)
+        self.o = torch.empty(1, c.hidden, dtype=bf, device=dv)
+        self.gu = torch.empty(1, 2 * c.ffn, dtype=bf, device=dv)
+        self.act = torch.empty(1, c.ffn, dtype=bf, device=dv)
+        self.d = torch.empty(1, c.hidden, dtype=bf, device=dv)
+        self.logits = torch.empty(1, c.vocab, dtype=bf, device=dv)
+        self.top_v = torch.empty(1, 1, dtype=bf, device=dv)
+        self._keep = []
+        self.program = self._build()
+        self.graph = None
+
+    # ------------------------------------------------------------------ program
+    def _d(self, t):
+        p = desc(t)
+        self._keep.append(p)
+        return p
+
+    def _build(self):
+        c, w, dev, s = self.cfg, self.w, self.dev, self.dev.stream
+        d = self._d
+        prog = []
+        hq, hk, D = c.heads * c.head_dim, c.kv_heads * c.head_dim, c.head_dim
+        q_view = self.qkv[:, :hq].view(1, c.heads, 1, D)
+        k_view = self.qkv[:, hq:hq + hk].view(1, c.kv_heads, 1, D)
+        v_view = self.qkv[:, hq + hk:].view(1, c.kv_heads, 1, D)
+        gate, up = self.gu[:, :c.ffn], self.gu[:, c.ffn:]
+        h2d, ctx2d = self.h, self.ctx.view(1, hq)
+        ids0 = (C.c_uint32 * 1)(self.k_seq[0])
+        self._keep.append(ids0)
+        prog.append(_DevCall("sandy_hip_device_paged_lengths", dev.handle, C.c_uint32(self.k_pools[0]), ids0,
+                             C.c_int32(1), d(self.pos)))
+        prog.append(_Call("sandy_hip_gather", d(self.token), d(w["embed"]), d(self.x0), stream=s))
+        silu, sres = ops.silu_mul_nodes()
+        nodes = ops._nodes(silu)
+        arr = (_lib.SandyTensor * 2)(d(gate).contents, d(up).contents)
+        bc = (C.c_int32 * 2)(0, 0)
+        self._keep += [nodes, arr, bc]
+        x0 = self.x0.view(1, c.hidden)
+        # residual stream: block input x_l in buffer A (x0 for block 0), the
+        # residual after attention in buffer B
+        res_a, res_b = self.res
+        for layer in range(c.layers):
+            if layer == 0:
+                prog.append(_Call("sandy_hip_norm", C.c_int32(0), d(x0), d(w["0.in_norm"]), None, C.c_double(c.eps),
+                                  d(h2d), stream=s))
+                x_in = x0
+            else:
+                # x_l = previous residual + previous MLP output, then this block's input norm
+                prog.append(_Call("sandy_hip_add_rms_norm", d(self.d), d(res_b), d(w[f"{layer}.in_norm"]),
+                                  C.c_double(c.eps), d(res_a), d(h2d), stream=s))
+                x_in = res_a
+            prog.append(_Call("sandy_hip_matmul", d(h2d), d(w[f"{layer}.qkv"]), C.c_int32(0), C.c_int32(1),
+                              d(self.qkv), stream=s))
+            prog.append(_Call("sandy_hip_rope", d(q_view), d(self.pos), C.c_double(c.theta), C.c_int64(-1),
+                              C.c_int32(1), d(self.qr), stream=s))
+            prog.append(_Call("sandy_hip_rope", d(k_view), d(self.pos), C.c_double(c.theta), C.c_int64(-1),
+                              C.c_int32(1), d(self.kr), stream=s))
+            kid = (C.c_uint32 * 1)(self.k_seq[layer])
+            vid = (C.c_uint32 * 1)(self.v_seq[layer])
+            self._keep += [kid, vid]
+            prog.append(_DevCall("sandy_hip_device_paged_append_step", dev.handle, C.c_uint32(self.k_pools[layer]),
+                                 kid, C.c_int32(1), d(self.kr)))
+            prog.append(_DevCall("sandy_hip_device_paged_append_step", dev.handle, C.c_uint32(self.v_pools[layer]),
+                                 vid, C.c_int32(1), d(v_view)))
+            kc, table, _ = dev.paged_views(self.k_pools[layer])
+            vc, _, _ = dev.paged_views(self.v_pools[layer])
+            table.contents.dims[0] = 1
+            self._keep += [kc, vc, table]
+            prog.append(_Call("sandy_hip_paged_attention", d(self.qr), kc, vc, table, d(self.pos), C.c_int64(0),
+                              C.c_double(1.0 / (D ** 0.5)), d(self.ctx), stream=s))
+            prog.append(_Call("sandy_hip_matmul", d(ctx2d), d(w[f"{layer}.o"]), C.c_int32(0), C.c_int32(1),
+                              d(self.o), stream=s))
+            prog.append(_Call("sandy_hip_add_rms_norm", d(self.o), d(x_in), d(w[f"{layer}.post_norm"]),
+                              C.c_double(c.eps), d(res_b), d(h2d), stream=s))
+            prog.append(_Call("sandy_hip_matmul", d(h2d), d(w[f"{layer}.gate_up"]), C.c_int32(0), C.c_int32(1),
+                              d(self.gu), stream=s))
+            prog.append(_Call("sandy_hip_elementwise", nodes, C.c_int32(len(silu)), C.c_uint32(sres), arr, bc,
+                              C.c_int32(2), d(self.act), stream=s))
+            prog.append(_Call("sandy_hip_matmul", d(self.act), d(w[f"{layer}.down"]), C.c_int32(0), C.c_int32(1),
+                              d(self.d), stream=s))
+        prog.append(_Call("sandy_hip_add_rms_norm", d(self.d), d(res_b), d(w["norm"]), C.c_double(c.eps), d(res_a),
+                          d(h2d), stream=s))
+        prog.append(_Call("sandy_hip_matmul", d(h2d), d(w["lm_head"]), C.c_int32(0), C.c_int32(1), d(self.logits),
+                          stream=s))
+        prog.append(_Call("sandy_hip_topk", d(self.logits), C.c_int64(1), C.c_int64(-1), d(self.top_v),
+                          d(self.token), stream=s))
+        return prog
+
+    # ------------------------------------------------------------------ running
+    def prefill_cache(self, k_rows: list, v_rows: list):
+        """Append context K/V ([1, kv_heads, n, head_dim] per layer) as if
+        earlier tokens had been decoded."""
+        torch.cuda.synchronize()
+        for layer in range(self.cfg.layers):
+            self.dev.append_paged(self.k_seq[layer], k_rows[layer])
+            self.dev.append_paged(self.v_seq[layer], v_rows[layer])
+        self.dev.synchronize()
+
+    def set_token(self, token: int):
+        self.token.fill_(int(token))
+        torch.cuda.synchronize()
+
+    def step(self):
+        """One decode step, launched eagerly."""
+        for call in self.program:
+            call()
+
+    def capture(self):
+        """Capture one step as a HIP graph (run a warm step first: workspaces
+        and generated kernels must exist before capture)."""
+        self.dev.graph_begin()
+        try:
+            self.step()
+        finally:
+            self.graph = self.dev.graph_end()
+        return self.graph
+
+    def replay(self):
+        self.dev.graph_launch(self.graph)
+
+    def length(self) -> int:
+        self.dev.paged_sync(self.k_pools[0])
+        return self.dev.paged_meta(self.k_seq[0]).grow_length
+
+    def close(self):
+        if self.graph is not None:
+            self.dev.graph_destroy(self.graph)
+            self.graph = None

@@ -114,6 +114,13 @@ class HipDevice:
               desc(out))
         return out
 
+    def lengths(self, pool: int, tensors, out: torch.Tensor):
+        """out[i] = device length of tensors[i] (the next row's position)."""
+        ids = (C.c_uint32 * len(tensors))(*tensors)
+        dcall("sandy_hip_device_paged_lengths", self.handle, C.c_uint32(pool), ids, C.c_int32(len(tensors)),
+              desc(out))
+        return out
+
     def paged_meta(self, tensor: int) -> SandyPagedMeta:
         m = SandyPagedMeta()
         dcall("sandy_hip_device_paged_meta", self.handle, C.c_uint32(tensor), C.byref(m))
