@@ -251,6 +251,41 @@ int sandy_hip_matmul(const SandyTensor* lhs, const SandyTensor* rhs, int32_t tra
 int sandy_hip_linear(const SandyTensor* x, const SandyTensor* weight, const SandyTensor* bias,
                      const SandyTensor* out, void* stream, char* err, size_t err_cap);
 
+/* ---------------------------------------------------------------- safetensors weights
+ *
+ * EagerSafeTensorWeights (src/weight/SafeTensorWeights.h:29-48,
+ * SafeTensorWeights.cpp:44-117): header parsing with the reference's dtype
+ * table and error wording, tensors listed in name order (its descriptors()
+ * order).  Instead of holding the file in host memory, the data section is
+ * streamed through pinned staging buffers into one device arena in which
+ * every tensor starts at a 256-byte-aligned arena_offset.  Host-only except
+ * sandy_hip_safetensors_upload. */
+typedef struct SandySafetensors SandySafetensors;
+
+typedef struct SandySafetensorInfo {
+    char name[256];
+    int32_t dtype;                      /* SandyDType */
+    int32_t rank;
+    int64_t dims[SANDY_HIP_MAX_RANK];
+    uint64_t file_offset;               /* within the data section */
+    uint64_t nbytes;
+    uint64_t arena_offset;              /* where sandy_hip_safetensors_upload puts it */
+} SandySafetensorInfo;
+
+int sandy_hip_safetensors_open(const char* path, SandySafetensors** out, char* err, size_t err_cap);
+void sandy_hip_safetensors_close(SandySafetensors* st);
+int64_t sandy_hip_safetensors_count(const SandySafetensors* st);
+/* bytes of device memory the arena needs (sum of 256-aligned tensor sizes) */
+uint64_t sandy_hip_safetensors_arena_bytes(const SandySafetensors* st);
+int sandy_hip_safetensors_info(const SandySafetensors* st, int64_t index, SandySafetensorInfo* info, char* err,
+                               size_t err_cap);
+/* index of a tensor by name, -1 when absent (get_tensor returning null) */
+int64_t sandy_hip_safetensors_find(const SandySafetensors* st, const char* name);
+/* copies every tensor to arena + arena_offset (arena 256-byte aligned, at
+ * least arena_bytes); returns when the copies are complete */
+int sandy_hip_safetensors_upload(SandySafetensors* st, void* arena, uint64_t arena_bytes, void* stream, char* err,
+                                 size_t err_cap);
+
 /* ---------------------------------------------------------------- device runtime
  *
  * A HIP device object with the reference Device's responsibilities

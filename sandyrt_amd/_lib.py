@@ -88,6 +88,18 @@ class SandyPagedPoolDesc(C.Structure):
     ]
 
 
+class SandySafetensorInfo(C.Structure):
+    _fields_ = [
+        ("name", C.c_char * 256),
+        ("dtype", C.c_int32),
+        ("rank", C.c_int32),
+        ("dims", C.c_int64 * MAX_RANK),
+        ("file_offset", C.c_uint64),
+        ("nbytes", C.c_uint64),
+        ("arena_offset", C.c_uint64),
+    ]
+
+
 class SandyPagedMeta(C.Structure):
     _fields_ = [
         ("pool", C.c_uint32),
@@ -160,7 +172,19 @@ DEVICE_SIGNATURES = {
     "sandy_hip_device_graph_launch": ([DEV, C.c_uint32], C.c_int),
     "sandy_hip_device_graph_destroy": ([DEV, C.c_uint32], C.c_int),
 }
-NO_ERR_ARGS = {"sandy_hip_device_destroy", "sandy_hip_device_stream", "sandy_hip_device_buffer"}
+ST = C.c_void_p
+DEVICE_SIGNATURES.update({
+    "sandy_hip_safetensors_open": ([C.c_char_p, C.POINTER(C.c_void_p)], C.c_int),
+    "sandy_hip_safetensors_close": ([ST], None),
+    "sandy_hip_safetensors_count": ([ST], C.c_int64),
+    "sandy_hip_safetensors_arena_bytes": ([ST], C.c_uint64),
+    "sandy_hip_safetensors_info": ([ST, C.c_int64, C.POINTER(SandySafetensorInfo)], C.c_int),
+    "sandy_hip_safetensors_find": ([ST, C.c_char_p], C.c_int64),
+    "sandy_hip_safetensors_upload": ([ST, C.c_void_p, C.c_uint64, C.c_void_p], C.c_int),
+})
+NO_ERR_ARGS = {"sandy_hip_device_destroy", "sandy_hip_device_stream", "sandy_hip_device_buffer",
+               "sandy_hip_safetensors_close", "sandy_hip_safetensors_count", "sandy_hip_safetensors_arena_bytes",
+               "sandy_hip_safetensors_find"}
 
 _lib = None
 

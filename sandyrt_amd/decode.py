@@ -70,6 +70,33 @@ def random_weights(cfg: DecodeConfig, seed: int = 0, std: float = 0.02, device="
     return w
 
 
+def weights_from_safetensors(st, cfg: DecodeConfig) -> dict:
+    """Decoder weights from an uploaded checkpoint (sandyrt_amd.weights.
+    SafeTensors) under the program's scoped names, weight_scope "model" ->
+    "layers.{i}" -> "self_attn" / "mlp" (src/models/tinyllama/
+    eval_token.sandy.go:4-13, common.sandy.go:1-62); the lm-head is also
+    found at the top level, as Hugging Face checkpoints store it.  q/k/v and
+    gate/up are concatenated on the device once, here."""
+    def get(*names):
+        for n in names:
+            t = st.get_tensor(n)
+            if t is not None:
+                return t
+        raise KeyError(f"checkpoint has none of {names}")
+
+    w = {"embed": get("model.embed_tokens.weight"), "norm": get("model.norm.weight"),
+         "lm_head": get("model.lm_head.weight", "lm_head.weight")}
+    for i in range(cfg.layers):
+        p = f"model.layers.{i}."
+        w[f"{i}.in_norm"] = get(p + "input_layernorm.weight")
+        w[f"{i}.post_norm"] = get(p + "post_attention_layernorm.weight")
+        w[f"{i}.qkv"] = torch.cat([get(p + f"self_attn.{n}_proj.weight") for n in "qkv"], 0).contiguous()
+        w[f"{i}.o"] = get(p + "self_attn.o_proj.weight")
+        w[f"{i}.gate_up"] = torch.cat([get(p + "mlp.gate_proj.weight"), get(p + "mlp.up_proj.weight")], 0).contiguous()
+        w[f"{i}.down"] = get(p + "mlp.down_proj.weight")
+    return w
+
+
 class _Call:
     """One C-ABI kernel entry point with its arguments bound once."""
 
