@@ -129,6 +129,27 @@ struct Vec8;
 template <>
 struct Vec8<BF16> {
     using elem = uint16_t;
+    // raw 16-byte chunk: load early, unpack only when the values are needed,
+    // so independent work can run while the load is in flight
+    using raw = uint4;
+    __device__ __forceinline__ static raw load_raw(const void* p, int64_t i) {
+        return *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i);
+    }
+    // streamed input read once: non-temporal, so it does not displace reused data
+    __device__ __forceinline__ static raw load_raw_nt(const void* p, int64_t i) {
+        typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
+        const u32x4_nt v = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4_nt*>(static_cast<const uint16_t*>(p) + i));
+        return uint4{v.x, v.y, v.z, v.w};
+    }
+    __device__ __forceinline__ static void unpack(const raw& r, float (&v)[8]) {
+        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[2 * j] = __uint_as_float(w[j] << 16);
+            v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+        }
+    }
     __device__ __forceinline__ static void load(const void* p, int64_t i, float (&v)[8]) {
         uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i);
         uint32_t w[4] = {r.x, r.y, r.z, r.w};
@@ -163,6 +184,23 @@ struct Vec8<BF16> {
 template <>
 struct Vec8<F32> {
     using elem = float;
+    struct raw {
+        float4 a, b;
+    };
+    __device__ __forceinline__ static raw load_raw(const void* p, int64_t i) {
+        const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+        return raw{q[0], q[1]};
+    }
+    __device__ __forceinline__ static raw load_raw_nt(const void* p, int64_t i) {
+        typedef float f32x4_nt __attribute__((ext_vector_type(4)));
+        const f32x4_nt* q = reinterpret_cast<const f32x4_nt*>(static_cast<const float*>(p) + i);
+        const f32x4_nt a = __builtin_nontemporal_load(q), b = __builtin_nontemporal_load(q + 1);
+        return raw{float4{a.x, a.y, a.z, a.w}, float4{b.x, b.y, b.z, b.w}};
+    }
+    __device__ __forceinline__ static void unpack(const raw& r, float (&v)[8]) {
+        v[0] = r.a.x; v[1] = r.a.y; v[2] = r.a.z; v[3] = r.a.w;
+        v[4] = r.b.x; v[5] = r.b.y; v[6] = r.b.z; v[7] = r.b.w;
+    }
     __device__ __forceinline__ static void load(const void* p, int64_t i, float (&v)[8]) {
         const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
         float4 a = q[0], b = q[1];

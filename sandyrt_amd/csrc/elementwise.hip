@@ -19,12 +19,16 @@
 // Access modes per input: same-shape contiguous, right-aligned broadcast
 // (element index = linear % numel, CudaElementwiseKernels.cu:171-174), scalar
 // (numel 1) or strided (dims/strides passed at launch).  When the output and
-// every input allow it, a thread handles 8 consecutive elements with 128-bit
-// loads and stores; otherwise one element per thread.
+// every input allow it, threads walk the tensor in 8-element chunks with
+// 128-bit loads and stores, two chunks in flight per thread over a grid of at
+// most 4096 workgroups; contiguous inputs are read non-temporally (streamed
+// once; broadcast inputs are re-read and stay cached).  Otherwise one element
+// per thread.
 #include "common.h"
 
 #include <hip/hiprtc.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <sstream>
@@ -68,6 +72,18 @@ __device__ __forceinline__ void ld8_bf16(const void* p, i64 i, float* v) {
   uint4 r = *(const uint4*)((const u16*)p + i);
   unsigned w[4] = {r.x, r.y, r.z, r.w};
   for (int j = 0; j < 4; j++) { v[2*j] = __uint_as_float(w[j] << 16); v[2*j+1] = __uint_as_float(w[j] & 0xffff0000u); }
+}
+__device__ __forceinline__ void ldnt8_bf16(const void* p, i64 i, float* v) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 r = __builtin_nontemporal_load((const u32x4*)((const u16*)p + i));
+  unsigned w[4] = {r.x, r.y, r.z, r.w};
+  for (int j = 0; j < 4; j++) { v[2*j] = __uint_as_float(w[j] << 16); v[2*j+1] = __uint_as_float(w[j] & 0xffff0000u); }
+}
+__device__ __forceinline__ void ldnt8_f32(const void* p, i64 i, float* v) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const f32x4* q = (const f32x4*)((const float*)p + i);
+  f32x4 a = __builtin_nontemporal_load(q), b = __builtin_nontemporal_load(q + 1);
+  v[0]=a.x; v[1]=a.y; v[2]=a.z; v[3]=a.w; v[4]=b.x; v[5]=b.y; v[6]=b.z; v[7]=b.w;
 }
 __device__ __forceinline__ void ld8_f32(const void* p, i64 i, float* v) {
   const float4* q = (const float4*)((const float*)p + i); float4 a = q[0], b = q[1];
@@ -128,28 +144,44 @@ std::string generate(const SandyScalarNode* nodes, int count, uint32_t result, c
     s << kPrelude;
     s << "extern \"C\" __global__ __launch_bounds__(256) void sandy_ew(EwArgs a) {\n";
     if (vec) {
-        s << "  i64 base = ((i64)blockIdx.x * 256 + threadIdx.x) * 8;\n  if (base >= a.n) return;\n";
-        for (int i = 0; i < nin; i++) {
-            const char* ld = in_dt[i] == SANDY_BF16 ? "ld8_bf16" : "ld8_f32";
-            s << "  float in" << i << "[8];\n";
-            if (modes[i] == kContig)
-                s << "  " << ld << "(a.in[" << i << "], base, in" << i << ");\n";
-            else if (modes[i] == kBroadcast)
-                s << "  " << ld << "(a.in[" << i << "], base % a.numel[" << i << "], in" << i << ");\n";
-            else {  // scalar
-                s << "  { float v = " << (in_dt[i] == SANDY_BF16 ? "bf2f(((const u16*)a.in[" : "(((const float*)a.in[") << i
-                  << "])[0]); for (int k = 0; k < 8; k++) in" << i << "[k] = v; }\n";
+        // chunk j of 8 elements; a thread takes chunks c and c + 256 of each
+        // 512-chunk stride of the grid
+        s << "  const i64 chunks = a.n >> 3;\n";
+        s << "  for (i64 c0 = (i64)blockIdx.x * 512 + threadIdx.x; c0 < chunks; c0 += (i64)gridDim.x * 512) {\n";
+        s << "    const bool two = c0 + 256 < chunks;\n";
+        for (int u = 0; u < 2; u++) {
+            const std::string cidx = u == 0 ? "c0" : "(c0 + 256)";
+            for (int i = 0; i < nin; i++) s << "    float in" << i << "_" << u << "[8];\n";
+            if (u == 1) s << "    if (two) {\n";
+            for (int i = 0; i < nin; i++) {
+                const std::string nm = "in" + std::to_string(i) + "_" + std::to_string(u);
+                if (modes[i] == kContig)
+                    s << "    " << (in_dt[i] == SANDY_BF16 ? "ldnt8_bf16" : "ldnt8_f32") << "(a.in[" << i << "], "
+                      << cidx << " * 8, " << nm << ");\n";
+                else if (modes[i] == kBroadcast)
+                    s << "    " << (in_dt[i] == SANDY_BF16 ? "ld8_bf16" : "ld8_f32") << "(a.in[" << i << "], ("
+                      << cidx << " * 8) % a.numel[" << i << "], " << nm << ");\n";
+                else  // scalar
+                    s << "    { float v = " << (in_dt[i] == SANDY_BF16 ? "bf2f(((const u16*)a.in[" : "(((const float*)a.in[")
+                      << i << "])[0]); for (int k = 0; k < 8; k++) " << nm << "[k] = v; }\n";
             }
+            if (u == 1) s << "    }\n";
         }
-        s << "  float r[8];\n#pragma unroll\n  for (int k = 0; k < 8; k++) {\n";
-        for (int j = 0; j < count; j++) {
-            const auto& n = nodes[j];
-            s << "    const float s" << n.id << " = ";
-            if (n.op == 0) s << "in" << n.input_index << "[k];\n";
-            else s << node_expr(n) << ";\n";
+        for (int u = 0; u < 2; u++) {
+            const std::string cidx = u == 0 ? "c0" : "(c0 + 256)";
+            const std::string suf = "_" + std::to_string(u);
+            if (u == 1) s << "    if (!two) break;\n";
+            s << "    {\n    float r[8];\n#pragma unroll\n    for (int k = 0; k < 8; k++) {\n";
+            for (int j = 0; j < count; j++) {
+                const auto& n = nodes[j];
+                s << "      const float s" << n.id << " = ";
+                if (n.op == 0) s << "in" << n.input_index << suf << "[k];\n";
+                else s << node_expr(n) << ";\n";
+            }
+            s << "      r[k] = s" << result << ";\n    }\n";
+            s << "    " << (out_dt == SANDY_BF16 ? "st8_bf16" : "st8_f32") << "(a.out, " << cidx << " * 8, r);\n    }\n";
         }
-        s << "    r[k] = s" << result << ";\n  }\n";
-        s << "  " << (out_dt == SANDY_BF16 ? "st8_bf16" : "st8_f32") << "(a.out, base, r);\n}\n";
+        s << "  }\n}\n";
     } else {
         s << "  i64 lin = (i64)blockIdx.x * 256 + threadIdx.x;\n  if (lin >= a.n) return;\n";
         for (int i = 0; i < nin; i++) {
@@ -312,8 +344,12 @@ extern "C" int sandy_hip_elementwise(const SandyScalarNode* nodes, int32_t node_
             c = it->second;
         }
     }
-    const int64_t threads = vec ? n / 8 : n;
-    const unsigned blocks = static_cast<unsigned>((threads + 255) / 256);
+    // vectorised: 512 chunks of 8 per workgroup per grid stride, at most 4096
+    // workgroups (16 per CU); scalar: one element per thread
+    const int64_t threads = vec ? (n / 8 + 1) / 2 : n;
+    int64_t blocks64 = (threads + 255) / 256;
+    if (vec) blocks64 = std::min<int64_t>(blocks64, 4096);
+    const unsigned blocks = static_cast<unsigned>(blocks64);
     void* params[] = {&args};
     SANDY_HIP_TRY(hipModuleLaunchKernel(c.fn, blocks, 1, 1, 256, 1, 1, 0, stream, params, nullptr), e,
                   "elementwise launch");

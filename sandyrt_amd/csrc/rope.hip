@@ -10,16 +10,26 @@
 // The denominators theta^(2i/d) are evaluated on the host with the same
 // powf the CPU reference uses and passed as kernel arguments, so every angle
 // (a correctly rounded division on gfx950) equals the CPU's bit for bit; only
-// cos/sin differ, by the device libm's ulp error.  The reference CUDA kernel
+// cos/sin differ, within an ulp (evaluation below).  The reference CUDA kernel
 // evaluates powf per pair on the device and synchronises the host after every
 // launch to read an error flag (CudaRoPEKernels.cu:272-333); here a negative
 // position sets the sticky device error word instead.
 //
 // gfx950 design: when positions depend only on the sequence index, one thread
-// owns (sequence position, 8 pairs, a group of heads): it evaluates 8 sincos
-// once and reuses them for every head in its group, moving 2 x 16 B per head
-// with 128-bit loads/stores.  C2's q [1, 32, 4096, 64] therefore spends 1/4
-// of a sincos per element instead of one, and stays HBM-bound.
+// owns (sequence position, 8 pairs, a group of heads): it issues the loads of
+// up to four heads first (2 x 16 B each, 128-bit), evaluates its 8 sin/cos
+// pairs while they are in flight, and reuses them for every head of its
+// group.  C2's q [1, 32, 4096, 64] therefore spends 1/4 of a sin/cos per
+// element and stays HBM-bound.
+//
+// sin/cos: the angle (a float, bit-identical to the CPU's) is reduced by
+// Cody-Waite in double precision, r = a - k * pi/2 with pi/2 split in two
+// doubles (exact for the |a| < 2^20 that positions reach), then sin and cos
+// of |r| <= pi/4 are Taylor polynomials to r^11 / r^12 in float and the
+// quadrant k mod 4 selects and signs them.  Within 1 ulp of a correctly
+// rounded result, like the CPU's sinf/cosf, at a fraction of the cost of the
+// device libm's sincosf for large arguments (which made this kernel
+// compute-bound: 9.2 vs 7.8 us for C2's q).
 #include "common.h"
 
 #include <cmath>
@@ -32,6 +42,34 @@ constexpr int kMaxPairs = 256;  // rotary dims up to 512
 struct RopeArgs {
     float denom[kMaxPairs];
 };
+
+// sin and cos of a float angle: double-precision Cody-Waite reduction to
+// [-pi/4, pi/4], Taylor polynomials, quadrant select.
+__device__ __forceinline__ void rope_sincos(float a, float* s, float* c) {
+    const double k = __builtin_rint(static_cast<double>(a) * 0.63661977236758134308);  // 2 / pi
+    double rd = fma(-k, 1.5707963267948966192, static_cast<double>(a));               // pi/2 (head)
+    rd = fma(-k, 6.123233995736766036e-17, rd);                                        // pi/2 (tail)
+    const float r = static_cast<float>(rd);
+    const float r2 = r * r;
+    float sp = fmaf(r2, -2.5052108385441718775e-8f, 2.7557319223985890653e-6f);   // -1/11!, 1/9!
+    sp = fmaf(r2, sp, -1.9841269841269841270e-4f);                                 // -1/7!
+    sp = fmaf(r2, sp, 8.3333333333333333333e-3f);                                  // 1/5!
+    sp = fmaf(r2, sp, -1.6666666666666666667e-1f);                                 // -1/3!
+    const float sv = fmaf(r * r2, sp, r);
+    float cp = fmaf(r2, 2.0876756987868098979e-9f, -2.7557319223985890653e-7f);   // 1/12!, -1/10!
+    cp = fmaf(r2, cp, 2.4801587301587301587e-5f);                                  // 1/8!
+    cp = fmaf(r2, cp, -1.3888888888888888889e-3f);                                 // -1/6!
+    cp = fmaf(r2, cp, 4.1666666666666666667e-2f);                                  // 1/4!
+    cp = fmaf(r2, cp, -0.5f);
+    const float cv = fmaf(r2, cp, 1.0f);
+    const int q = static_cast<int>(k);
+    float ss = (q & 1) ? cv : sv;
+    float cc = (q & 1) ? sv : cv;
+    if (q & 2) ss = -ss;
+    if ((q + 1) & 2) cc = -cc;
+    *s = ss;
+    *c = cc;
+}
 
 // mode: 0 = position from sequence index, 1 = ids[0] + seq index,
 //       2 = ids[seq index], 3 = ids[vector]
@@ -48,104 +86,127 @@ __device__ __forceinline__ int64_t rope_position(int mode, const void* ids, int3
     return p;
 }
 
-// Split-half, 8 pairs per thread.  grid: (seq * chunks * groups) threads.
-template <typename T>
+// Split-half, 8 pairs per thread, loads of U heads issued before the sin/cos.
+// grid: (seq * chunks * groups) threads.  FULL: every group holds a multiple
+// of U heads and every pair rotates, so no guards (the per-load and per-pair
+// branches cost 15% of the kernel's time).
+template <typename T, int U, bool FULL>
 __global__ __launch_bounds__(256) void rope_split_kernel(
         const void* __restrict__ x, void* __restrict__ out, const void* __restrict__ ids, int32_t ids_dt, int mode,
         int64_t seq, int64_t outer, int dim, int rot_pairs, int groups, int per_group, RopeArgs args,
         uint32_t* errw) {
     const int half = dim >> 1;
-    const int chunks = half >> 3;
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t total = seq * chunks * groups;
-    if (t >= total) return;
+    const uint32_t chunks = static_cast<uint32_t>(half >> 3);
+    // 32-bit index math (the host keeps seq * chunks * groups below 2^31):
+    // 64-bit divisions by runtime values delayed the first load measurably
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= static_cast<uint32_t>(seq) * chunks * static_cast<uint32_t>(groups)) return;
     const int c = static_cast<int>(t % chunks);
-    const int64_t rest = t / chunks;
-    const int64_t s = rest % seq;
-    const int g = static_cast<int>(rest / seq);
+    const uint32_t rest = t / chunks;
+    const int64_t s = rest % static_cast<uint32_t>(seq);
+    const int g = static_cast<int>(rest / static_cast<uint32_t>(seq));
     const int64_t o_begin = static_cast<int64_t>(g) * per_group;
     const int64_t o_end = min(outer, o_begin + per_group);
     float cs[8], sn[8];
     int64_t pos = -1;
-    for (int64_t o = o_begin; o < o_end; o++) {
-        const int64_t vec = o * seq + s;
-        if (mode == 3 || pos < 0) {
-            pos = rope_position(mode, ids, ids_dt, vec, s, errw);
+    for (int64_t o0 = o_begin; o0 < o_end; o0 += U) {
+        // the position (possibly a load of position_ids) is read before the
+        // data loads: memory-load counters retire in order, so waiting for a
+        // later small load would also wait for every data load before it
+        const bool fresh = mode == 3 || pos < 0;  // mode 3 runs with one head per group
+        if (fresh) pos = rope_position(mode, ids, ids_dt, o0 * seq + s, s, errw);
+        typename Vec8<T>::raw ra_[U], rb_[U];
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            if (FULL || o0 + j < o_end) {
+                const int64_t base = ((o0 + j) * seq + s) * dim;
+                ra_[j] = Vec8<T>::load_raw(x, base + c * 8);
+                rb_[j] = Vec8<T>::load_raw(x, base + half + c * 8);
+            }
+        }
+        if (fresh) {
             const float fp = static_cast<float>(pos);
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const int p = c * 8 + i;
-                if (p < rot_pairs) {
-                    const float angle = fp / args.denom[p];
-                    sincosf(angle, &sn[i], &cs[i]);
+                if (FULL || p < rot_pairs) rope_sincos(fp / args.denom[p], &sn[i], &cs[i]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            if (!FULL && o0 + j >= o_end) break;
+            const int64_t base = ((o0 + j) * seq + s) * dim;
+            float a[8], b[8], ra[8], rb[8];
+            Vec8<T>::unpack(ra_[j], a);
+            Vec8<T>::unpack(rb_[j], b);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int p = c * 8 + i;
+                if (FULL || p < rot_pairs) {
+                    ra[i] = __fsub_rn(__fmul_rn(a[i], cs[i]), __fmul_rn(b[i], sn[i]));
+                    rb[i] = __fadd_rn(__fmul_rn(a[i], sn[i]), __fmul_rn(b[i], cs[i]));
+                } else {
+                    ra[i] = a[i];
+                    rb[i] = b[i];
                 }
             }
+            Vec8<T>::store(out, base + c * 8, ra);
+            Vec8<T>::store(out, base + half + c * 8, rb);
         }
-        const int64_t base = vec * dim;
-        float a[8], b[8];
-        Vec8<T>::load(x, base + c * 8, a);
-        Vec8<T>::load(x, base + half + c * 8, b);
-        float ra[8], rb[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int p = c * 8 + i;
-            if (p < rot_pairs) {
-                ra[i] = __fsub_rn(__fmul_rn(a[i], cs[i]), __fmul_rn(b[i], sn[i]));
-                rb[i] = __fadd_rn(__fmul_rn(a[i], sn[i]), __fmul_rn(b[i], cs[i]));
-            } else {
-                ra[i] = a[i];
-                rb[i] = b[i];
-            }
-        }
-        Vec8<T>::store(out, base + c * 8, ra);
-        Vec8<T>::store(out, base + half + c * 8, rb);
     }
 }
 
-// Interleaved, 4 pairs (8 elements) per thread.
-template <typename T>
+// Interleaved, 4 pairs (8 elements) per thread, loads of U heads first;
+// FULL as for the split-half kernel.
+template <typename T, int U, bool FULL>
 __global__ __launch_bounds__(256) void rope_interleaved_kernel(
         const void* __restrict__ x, void* __restrict__ out, const void* __restrict__ ids, int32_t ids_dt, int mode,
         int64_t seq, int64_t outer, int dim, int rot_pairs, int groups, int per_group, RopeArgs args,
         uint32_t* errw) {
-    const int chunks = dim >> 3;
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t total = seq * chunks * groups;
-    if (t >= total) return;
+    const uint32_t chunks = static_cast<uint32_t>(dim >> 3);
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= static_cast<uint32_t>(seq) * chunks * static_cast<uint32_t>(groups)) return;
     const int c = static_cast<int>(t % chunks);
-    const int64_t rest = t / chunks;
-    const int64_t s = rest % seq;
-    const int g = static_cast<int>(rest / seq);
+    const uint32_t rest = t / chunks;
+    const int64_t s = rest % static_cast<uint32_t>(seq);
+    const int g = static_cast<int>(rest / static_cast<uint32_t>(seq));
     const int64_t o_begin = static_cast<int64_t>(g) * per_group;
     const int64_t o_end = min(outer, o_begin + per_group);
     float cs[4], sn[4];
     int64_t pos = -1;
-    for (int64_t o = o_begin; o < o_end; o++) {
-        const int64_t vec = o * seq + s;
-        if (mode == 3 || pos < 0) {
-            pos = rope_position(mode, ids, ids_dt, vec, s, errw);
+    for (int64_t o0 = o_begin; o0 < o_end; o0 += U) {
+        const bool fresh = mode == 3 || pos < 0;  // position before the data loads, as above
+        if (fresh) pos = rope_position(mode, ids, ids_dt, o0 * seq + s, s, errw);
+        typename Vec8<T>::raw raw_[U];
+#pragma unroll
+        for (int j = 0; j < U; j++)
+            if (FULL || o0 + j < o_end) raw_[j] = Vec8<T>::load_raw(x, ((o0 + j) * seq + s) * dim + c * 8);
+        if (fresh) {
             const float fp = static_cast<float>(pos);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int p = c * 4 + i;
-                if (p < rot_pairs) sincosf(fp / args.denom[p], &sn[i], &cs[i]);
+                if (FULL || p < rot_pairs) rope_sincos(fp / args.denom[p], &sn[i], &cs[i]);
             }
         }
-        const int64_t base = vec * dim;
-        float a[8], r[8];
-        Vec8<T>::load(x, base + c * 8, a);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int p = c * 4 + i;
-            if (p < rot_pairs) {
-                r[2 * i] = __fsub_rn(__fmul_rn(a[2 * i], cs[i]), __fmul_rn(a[2 * i + 1], sn[i]));
-                r[2 * i + 1] = __fadd_rn(__fmul_rn(a[2 * i], sn[i]), __fmul_rn(a[2 * i + 1], cs[i]));
-            } else {
-                r[2 * i] = a[2 * i];
-                r[2 * i + 1] = a[2 * i + 1];
+        for (int j = 0; j < U; j++) {
+            if (!FULL && o0 + j >= o_end) break;
+            float a[8], r[8];
+            Vec8<T>::unpack(raw_[j], a);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int p = c * 4 + i;
+                if (FULL || p < rot_pairs) {
+                    r[2 * i] = __fsub_rn(__fmul_rn(a[2 * i], cs[i]), __fmul_rn(a[2 * i + 1], sn[i]));
+                    r[2 * i + 1] = __fadd_rn(__fmul_rn(a[2 * i], sn[i]), __fmul_rn(a[2 * i + 1], cs[i]));
+                } else {
+                    r[2 * i] = a[2 * i];
+                    r[2 * i + 1] = a[2 * i + 1];
+                }
             }
+            Vec8<T>::store(out, ((o0 + j) * seq + s) * dim + c * 8, r);
         }
-        Vec8<T>::store(out, base + c * 8, r);
     }
 }
 
@@ -192,7 +253,7 @@ __global__ __launch_bounds__(256) void rope_generic_kernel(
     }
     const int64_t pos = rope_position(mode, ids, ids_dt, vec, s, errw);
     float sn, cs;
-    sincosf(static_cast<float>(pos) / args.denom[p], &sn, &cs);
+    rope_sincos(static_cast<float>(pos) / args.denom[p], &sn, &cs);
     store_any(out, dt, o0, __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn)));
     store_any(out, dt, o1, __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, cs)));
 }
@@ -249,15 +310,15 @@ extern "C" int sandy_hip_rope(const SandyTensor* x, const SandyTensor* position_
     void* po = base_ptr(*out);
     const bool bf = x->dtype == SANDY_BF16;
     const bool aligned = ((reinterpret_cast<uintptr_t>(px) | reinterpret_cast<uintptr_t>(po)) & 15u) == 0;
-    const bool fast = contiguous(*x) && contiguous(*out) && aligned && dim <= 2 * kMaxPairs * 2 &&
+    bool fast = contiguous(*x) && contiguous(*out) && aligned && dim <= 2 * kMaxPairs * 2 &&
                       (split_half ? (dim / 2) % 8 == 0 : dim % 8 == 0);
+    int groups = 1, per = 1;
+    int64_t threads = 0;
     if (fast) {
         const int chunks = static_cast<int>(split_half ? dim / 16 : dim / 8);
         const int64_t base_threads = seq * chunks;
-        int groups = 1, per = 1;
         if (mode == 3) {
             groups = static_cast<int>(outer);
-            per = 1;
         } else {
             // threads (each reusing its sincos over `per` heads): numel / 32 within
             // [32K, 128K] -- measured best for C2's q (128K) and k (32K) on gfx950
@@ -266,15 +327,38 @@ extern "C" int sandy_hip_rope(const SandyTensor* x, const SandyTensor* position_
             per = static_cast<int>((outer + groups - 1) / groups);
             groups = static_cast<int>((outer + per - 1) / per);
         }
-        const int64_t threads = base_threads * groups;
+        threads = base_threads * groups;
+        if (threads + 255 >= (int64_t(1) << 31)) fast = false;  // the fast kernels index threads in 32 bits
+    }
+    if (fast) {
         dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+        // up to four heads' loads in flight per thread (mode 3 has one head per group)
+        const int u = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
+        const bool full = outer % per == 0 && per % u == 0 && rot_pairs == dim / 2;
+#define SANDY_ROPE_LAUNCH(KERNEL, T, U, F)                                                                        \
+    hipLaunchKernelGGL((KERNEL<T, U, F>), grid, dim3(256), 0, stream, px, po, ids, ids_dt, mode, seq, outer,     \
+                       static_cast<int>(dim), rot_pairs, groups, per, args, errw)
+#define SANDY_ROPE_F(KERNEL, T, U)                                 \
+    do {                                                           \
+        if (full) SANDY_ROPE_LAUNCH(KERNEL, T, U, true);           \
+        else SANDY_ROPE_LAUNCH(KERNEL, T, U, false);               \
+    } while (0)
+#define SANDY_ROPE_U(KERNEL, T)                         \
+    do {                                                \
+        if (u == 4) SANDY_ROPE_F(KERNEL, T, 4);         \
+        else if (u == 2) SANDY_ROPE_F(KERNEL, T, 2);    \
+        else SANDY_ROPE_F(KERNEL, T, 1);                \
+    } while (0)
         if (split_half) {
-            if (bf) hipLaunchKernelGGL(rope_split_kernel<BF16>, grid, dim3(256), 0, stream, px, po, ids, ids_dt, mode, seq, outer, static_cast<int>(dim), rot_pairs, groups, per, args, errw);
-            else hipLaunchKernelGGL(rope_split_kernel<F32>, grid, dim3(256), 0, stream, px, po, ids, ids_dt, mode, seq, outer, static_cast<int>(dim), rot_pairs, groups, per, args, errw);
+            if (bf) SANDY_ROPE_U(rope_split_kernel, BF16);
+            else SANDY_ROPE_U(rope_split_kernel, F32);
         } else {
-            if (bf) hipLaunchKernelGGL(rope_interleaved_kernel<BF16>, grid, dim3(256), 0, stream, px, po, ids, ids_dt, mode, seq, outer, static_cast<int>(dim), rot_pairs, groups, per, args, errw);
-            else hipLaunchKernelGGL(rope_interleaved_kernel<F32>, grid, dim3(256), 0, stream, px, po, ids, ids_dt, mode, seq, outer, static_cast<int>(dim), rot_pairs, groups, per, args, errw);
+            if (bf) SANDY_ROPE_U(rope_interleaved_kernel, BF16);
+            else SANDY_ROPE_U(rope_interleaved_kernel, F32);
         }
+#undef SANDY_ROPE_U
+#undef SANDY_ROPE_F
+#undef SANDY_ROPE_LAUNCH
     } else {
         Strided st{};
         st.rank = x->rank;
