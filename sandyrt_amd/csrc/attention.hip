@@ -182,23 +182,42 @@ __device__ __forceinline__ int64_t lane_read64(int64_t v, int l) {
 // wave at D = 64), with S^T = K Q^T and O^T += V^T P^T on MFMA and the online
 // softmax in the exp2 domain.  The waves merge through LDS and the piece ends
 // as the final output rows (final_out) or as partial slots slot0 + g*stride.
-template <int D, int NB, int NT, int S>
+// Q^T and this wave's block ids, issued by the caller before it knows the
+// sequence's position (static schedule); `id` is lane i's raw table entry for
+// tile tile_a + wave + 4i (-1 when past the table), validated here.
+template <int D>
+struct PieceInputs {
+    uint4 qv[D / 32];
+    int32_t id;
+};
+
+template <int D>
+__device__ __forceinline__ void load_q_columns(const PagedArgs& a, int b, int kh, int lane, uint4 (&qv)[D / 32]) {
+    // Q^T as B operands: column g, d = 32 kk + 8 j .. + 7.  Pad columns
+    // (g >= G) load head 0 again: every column is independent through the
+    // softmax and PV products, and pad columns are never stored.
+    const int G = a.group, g = lane & 15, j = lane >> 4;
+    const uint4* qp = reinterpret_cast<const uint4*>(a.q + b * a.q_sb + (kh * G + (g < G ? g : 0)) * a.q_sh + 8 * j);
+#pragma unroll
+    for (int kk = 0; kk < D / 32; kk++) qv[kk] = qp[kk * 4];
+}
+
+template <int D, int NB, int NT, int S, bool PRE = false>
 __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* smem, int lane, int wave, int b,
                                              int kh, const SplitRange& sr, int64_t tile_a, int64_t tile_b,
-                                             bool final_out, int64_t slot0, int64_t slot_stride, bool coherent) {
+                                             bool final_out, int64_t slot0, int64_t slot_stride, bool coherent,
+                                             const PieceInputs<D>* pre = nullptr) {
     constexpr int kRow = 2 * D + 8;  // bytes per V row in LDS (8-byte pad: conflict-free transposed reads)
     const int G = a.group;
     const int g = lane & 15;
     const int j = lane >> 4;
 
-    // Q^T as B operands: column g, d = 32 kk + 8 j .. + 7.  Pad columns
-    // (g >= G) load head 0 again: every column is independent through the
-    // softmax and PV products, and pad columns are never stored.
     uint4 qv[D / 32];
-    {
-        const uint4* qp = reinterpret_cast<const uint4*>(a.q + b * a.q_sb + (kh * G + (g < G ? g : 0)) * a.q_sh + 8 * j);
+    if constexpr (PRE) {
 #pragma unroll
-        for (int kk = 0; kk < D / 32; kk++) qv[kk] = qp[kk * 4];
+        for (int kk = 0; kk < D / 32; kk++) qv[kk] = pre->qv[kk];
+    } else {
+        load_q_columns<D>(a, b, kh, lane, qv);
     }
 
     float m = -INFINITY, l = 0.0f;
@@ -214,8 +233,12 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
         {
             const int64_t tile = c0 + wave + 4 * lane;
             const int64_t page = (sr.key_begin + 16 * tile) >> a.log2_page;
-            const bool in = lane < NT && tile < tile_b && page < a.max_blocks;
-            const int32_t id = a.table[b * a.table_stride + (in ? page : 0)];  // max_blocks >= 1
+            // a tile wholly below a sliding window's first key needs no data
+            const bool in = lane < NT && tile < tile_b && page < a.max_blocks &&
+                            sr.key_begin + 16 * tile + 15 >= sr.min_key;
+            int32_t id;
+            if constexpr (PRE) id = pre->id;
+            else id = a.table[b * a.table_stride + (in ? page : 0)];  // max_blocks >= 1
             const bool ok = id >= 0 && id < a.num_pages;
             if (in && !ok) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
             blkv = in && ok ? id : -1;
@@ -454,47 +477,20 @@ __device__ __forceinline__ int negative_sequence(const PagedArgs& a, int i, int 
     return -1;
 }
 
-// OCC: waves per SIMD the register allocation must allow (1 = no limit).  The
-// D = 64 four-tile kernel (256-key splits) is held to 5, where it needs no
-// scratch and 1280 of its workgroups are resident at once.
-template <int D, int NB, int NT, int S, int OCC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void paged_decode_units_kernel(PagedArgs a) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    constexpr int kSplitTiles = 4 * NT;  // the host passes split_keys == 16 * kSplitTiles
-    const Unit u = find_unit(a, blockIdx.x, kSplitTiles, lane);
-    if (!u.active) {
-        if (a.fused) {
-            const int nb = negative_sequence(a, static_cast<int>(blockIdx.x) - u.total, lane);
-            if (nb >= 0) {
-                for (int idx = threadIdx.x; idx < a.hq * D; idx += 256) a.out[nb * a.o_sb + (idx / D) * a.o_sh + idx % D] = 0;
-                if (threadIdx.x == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
-            }
-        }
-        return;
-    }
-    const SplitRange sr = seq_range(a, u.pos);
-    const int64_t ta = static_cast<int64_t>(u.split) * kSplitTiles;
-    const int64_t tb = min<int64_t>(sr.n_tiles, ta + kSplitTiles);
-    const int n_splits = (sr.n_tiles + kSplitTiles - 1) / kSplitTiles;
-    const bool whole = n_splits == 1;
-    const int64_t slot0 = (static_cast<int64_t>(u.b) * a.hq + u.kh * a.group) * a.max_splits;
-    attend_piece<D, NB, NT, S>(a, smem, lane, wave, u.b, u.kh, sr, ta, tb, whole, slot0 + u.split, a.max_splits,
-                               a.fused != 0);
-    if (!a.fused || whole) return;
-
-    // Fused merge.  The partials above were written through to the agent's
-    // coherence point; once every thread's stores have completed (the
-    // barrier waits for them), the workgroup counts itself in, and the last
-    // of the sequence's n_splits workgroups for this kv head reads every
-    // split's partial with agent-scope loads, writes the output rows and
-    // re-arms the counter for the next launch.
+// Fused split merge, run by every workgroup of a multi-split (sequence b,
+// kv head kh) after it wrote its partial.  The partials were written through
+// to the agent's coherence point; once every thread's stores have completed
+// (the barrier waits for them), the workgroup counts itself in, and the last
+// of the sequence's n_splits workgroups for this kv head reads every split's
+// partial with agent-scope loads, writes the output rows and re-arms the
+// counter for the next launch.
+template <int D>
+__device__ __forceinline__ void fused_merge(const PagedArgs& a, int b, int kh, int n_splits, int64_t slot0) {
     __shared__ int is_last;
     __builtin_amdgcn_s_waitcnt(0);  // this thread's write-through stores acknowledged
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t* ctr = a.counters + static_cast<int64_t>(u.b) * a.hkv + u.kh;
+        uint32_t* ctr = a.counters + static_cast<int64_t>(b) * a.hkv + kh;
         const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         is_last = prev == static_cast<uint32_t>(n_splits - 1);
         if (is_last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -530,8 +526,100 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         }
         const uint32_t pair = static_cast<uint32_t>(f32_to_bf16(L > 0.0f ? O0 / L : 0.0f)) |
                               (static_cast<uint32_t>(f32_to_bf16(L > 0.0f ? O1 / L : 0.0f)) << 16);
-        *reinterpret_cast<uint32_t*>(&a.out[u.b * a.o_sb + (u.kh * G + gg) * a.o_sh + d]) = pair;
+        *reinterpret_cast<uint32_t*>(&a.out[b * a.o_sb + (kh * G + gg) * a.o_sh + d]) = pair;
     }
+}
+
+// OCC: waves per SIMD the register allocation must allow (1 = no limit).  The
+// D = 64 four-tile kernel (256-key splits) is held to 5, where it needs no
+// scratch and 1280 of its workgroups are resident at once.
+template <int D, int NB, int NT, int S, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void paged_decode_units_kernel(PagedArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr int kSplitTiles = 4 * NT;  // the host passes split_keys == 16 * kSplitTiles
+    const Unit u = find_unit(a, blockIdx.x, kSplitTiles, lane);
+    if (!u.active) {
+        if (a.fused) {
+            const int nb = negative_sequence(a, static_cast<int>(blockIdx.x) - u.total, lane);
+            if (nb >= 0) {
+                for (int idx = threadIdx.x; idx < a.hq * D; idx += 256) a.out[nb * a.o_sb + (idx / D) * a.o_sh + idx % D] = 0;
+                if (threadIdx.x == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
+            }
+        }
+        return;
+    }
+    const SplitRange sr = seq_range(a, u.pos);
+    const int64_t ta = static_cast<int64_t>(u.split) * kSplitTiles;
+    const int64_t tb = min<int64_t>(sr.n_tiles, ta + kSplitTiles);
+    const int n_splits = (sr.n_tiles + kSplitTiles - 1) / kSplitTiles;
+    const bool whole = n_splits == 1;
+    const int64_t slot0 = (static_cast<int64_t>(u.b) * a.hq + u.kh * a.group) * a.max_splits;
+    attend_piece<D, NB, NT, S>(a, smem, lane, wave, u.b, u.kh, sr, ta, tb, whole, slot0 + u.split, a.max_splits,
+                               a.fused != 0);
+    if (!a.fused || whole) return;
+    fused_merge<D>(a, u.b, u.kh, n_splits, slot0);
+}
+
+// ------------------------------------------------ static schedule (fused merge)
+// Workgroup lin takes unit (split = lin / (B Hkv), b = lin / Hkv mod B,
+// kh = lin mod Hkv); splits are absolute ranges of 16 * kSplitTiles keys from
+// key 0.  The unit's block ids and Q columns therefore do not depend on the
+// sequence's position, and all three are requested at once: one memory round
+// trip before the K/V stream instead of two (position scan, then table).
+// Units past the sequence's last split exit when the position arrives.
+// Split-major numbering, rotated by the split, makes consecutive workgroups
+// (dealt round-robin to the XCDs) belong to different sequences and kv heads
+// and spreads each sequence's splits over the XCDs.
+template <int D, int NB, int NT, int S, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void paged_decode_static_kernel(PagedArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr int kSplitTiles = 4 * NT;  // the host passes split_keys == 16 * kSplitTiles
+    const int per_split = a.batch * a.hkv;
+    const int split = static_cast<int>(blockIdx.x) / per_split;
+    // rotated by the split so one sequence's splits land on successive XCDs
+    // (XCD = workgroup id mod 8): every XCD gets a share of every long
+    // sequence instead of a fixed subset of the sequences
+    int r = static_cast<int>(blockIdx.x) - split * per_split - split % per_split;
+    if (r < 0) r += per_split;
+    const int b = r / a.hkv;
+    const int kh = r - b * a.hkv;
+    const PosWords pw = vector_position(a, b);
+    PieceInputs<D> in;
+    load_q_columns<D>(a, b, kh, lane, in.qv);
+    {
+        const int64_t tile = static_cast<int64_t>(split) * kSplitTiles + wave + 4 * lane;
+        const int64_t page = (16 * tile) >> a.log2_page;
+        const bool ok = lane < NT && page < a.max_blocks;
+        const int32_t id = a.table[b * a.table_stride + (ok ? page : 0)];
+        in.id = ok ? id : -1;
+    }
+    const int64_t pos = join_position(a, pw);
+    if (pos < 0) {  // no keys: zero rows for this kv head's q heads, and the flag
+        if (split == 0) {
+            const int G = a.group;
+            for (int idx = threadIdx.x; idx < G * D; idx += 256)
+                a.out[b * a.o_sb + (kh * G + idx / D) * a.o_sh + idx % D] = 0;
+            if (kh == 0 && threadIdx.x == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
+        }
+        return;
+    }
+    SplitRange sr = seq_range(a, pos);
+    sr.key_begin = 0;  // absolute tiling; a sliding window only masks (and skips whole tiles)
+    sr.n_tiles = static_cast<int>((sr.n_keys + 15) >> 4);
+    const int n_splits = (sr.n_tiles + kSplitTiles - 1) / kSplitTiles;
+    if (split >= n_splits) return;
+    const int64_t ta = static_cast<int64_t>(split) * kSplitTiles;
+    const int64_t tb = min<int64_t>(sr.n_tiles, ta + kSplitTiles);
+    const bool whole = n_splits == 1;
+    const int64_t slot0 = (static_cast<int64_t>(b) * a.hq + kh * a.group) * a.max_splits;
+    attend_piece<D, NB, NT, S, true>(a, smem, lane, wave, b, kh, sr, ta, tb, whole, slot0 + split, a.max_splits, true,
+                                     &in);
+    if (whole) return;
+    fused_merge<D>(a, b, kh, n_splits, slot0);
 }
 
 // Combines the split partials of one (sequence, q head) under the split-unit
@@ -593,13 +681,27 @@ __global__ __launch_bounds__(64) void paged_decode_units_merge_kernel(PagedArgs 
 template <int D, int NB>
 const void* units_for(int nt) {
     constexpr int kOcc4 = D == 64 ? 5 : 1;  // spill-free only for D = 64, four tiles per wave
-    return nt == 4   ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 4, 2, kOcc4>)
+    return nt == 2   ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 2, 2, kOcc4>)
+           : nt == 4 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 4, 2, kOcc4>)
            : nt == 8 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 8, 2, 1>)
                      : reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 16, 2, 1>);
 }
 
 const void* units_kernel(int D, int nt) {
     return D == 64 ? units_for<64, 2>(nt) : D == 128 ? units_for<128, 1>(nt) : units_for<256, 1>(nt);
+}
+
+template <int D, int NB>
+const void* static_for(int nt) {
+    constexpr int kOcc4 = D == 64 ? 5 : 1;
+    return nt == 2   ? reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 2, 2, kOcc4>)
+           : nt == 4 ? reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 4, 2, kOcc4>)
+           : nt == 8 ? reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 8, 2, 1>)
+                     : reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 16, 2, 1>);
+}
+
+const void* static_kernel(int D, int nt) {
+    return D == 64 ? static_for<64, 2>(nt) : D == 128 ? static_for<128, 1>(nt) : static_for<256, 1>(nt);
 }
 
 // ---------------------------------------------------------------- general kernel
@@ -874,7 +976,7 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         // (measured best with the fused merge: config 3 at 512 keys, config 4 at 1024)
         int64_t split = env_int("SANDY_PAGED_SPLIT", 0);
         if (split <= 0) split = (max_keys * B * hkv) / 1024;
-        const int nt = split <= 256 ? 4 : split <= 512 ? 8 : 16;
+        const int nt = split <= 128 && D == 64 ? 2 : split <= 256 ? 4 : split <= 512 ? 8 : 16;
         split = 64 * nt;
         a.split_keys = static_cast<int32_t>(split);
         a.max_splits = static_cast<int32_t>((max_keys + split - 1) / split);
@@ -885,7 +987,14 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         a.ws_ml = reinterpret_cast<float*>(ws + slots * D * sizeof(float));
         const int64_t units = static_cast<int64_t>(a.max_splits) * hkv * B;
         if (units > (1LL << 26)) return fail(e, SANDY_ERR_UNSUPPORTED, "paged attention batch too large");
-        SANDY_HIP_TRY(hipLaunchKernel(units_kernel(static_cast<int>(D), nt), dim3(static_cast<unsigned>(units)),
+        // schedule: work units numbered over the active splits (default; best
+        // when context lengths vary) or the static
+        // split-major schedule (SANDY_PAGED_STATIC=1; one fewer memory round
+        // trip, best when the batch's contexts are about equal: 22.2 vs
+        // 25.1 us at 32 x 2304 keys, 26.4 vs 24.9 us at U[512, 4096])
+        const bool stat = a.fused && env_int("SANDY_PAGED_STATIC", 0) != 0;
+        SANDY_HIP_TRY(hipLaunchKernel(stat ? static_kernel(static_cast<int>(D), nt) : units_kernel(static_cast<int>(D), nt),
+                                      dim3(static_cast<unsigned>(units)),
                                       dim3(256), args, lds, stream), e, "paged attention launch");
         const void* mfn = D == 64 ? reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<64>)
                         : D == 128 ? reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<128>)
