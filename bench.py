@@ -54,6 +54,7 @@ def parse():
     p.add_argument("--cpu-seqs", type=int, default=8, help="decode sequences timed on the CPU")
     p.add_argument("--only", default="", help="comma list of kernels to run (profiling)")
     p.add_argument("--no-extras", action="store_true", help="skip the per-kernel table of the other configs")
+    p.add_argument("--no-decode-step", action="store_true", help="skip the whole-model decode tok/s measurement")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a plain 256 MiB device copy (counter calibration for rocprofv3 --pmc)")
     return p.parse_args()
@@ -363,6 +364,50 @@ def build_extras(replicas):
     return kernels, bytes_per, keep
 
 
+def decode_step_tok_s(batch, contexts, iters=10, seed=2):
+    """Whole TinyLlama-1.1B greedy decode step (22 layers: projections, RoPE,
+    paged append, paged decode attention, SiLU-gated MLP, lm-head, greedy
+    token; random bf16 weights, synthetic K/V history of the given context
+    lengths, block 16) for `batch` sequences, captured as one HIP graph and
+    replayed; returns (us per step, tokens/s, bytes per step)."""
+    import torch
+    from sandyrt_amd.decode import DecodeConfig, TinyLlamaDecoder, random_weights
+    from sandyrt_amd.device import HipDevice
+    cfg = DecodeConfig(page_size=DEC_PAGE, max_context=int(max(contexts)) + iters + 64)
+    w = random_weights(cfg, seed=seed)
+    dev = HipDevice(0)
+    dec = TinyLlamaDecoder(dev, cfg, w, batch=batch)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    for b, n in enumerate(contexts):
+        ks = [torch.randn(1, cfg.kv_heads, int(n), cfg.head_dim, generator=g, device="cuda").to(torch.bfloat16)
+              for _ in range(cfg.layers)]
+        vs = [torch.randn(1, cfg.kv_heads, int(n), cfg.head_dim, generator=g, device="cuda").to(torch.bfloat16)
+              for _ in range(cfg.layers)]
+        dec.prefill_cache(ks, vs, seq=b)
+    dec.set_token([int(t) for t in range(1, batch + 1)])
+    dec.step()  # warm: generated kernels and workspaces exist before capture
+    dev.synchronize()
+    dec.capture()
+    dec.replay()
+    dev.synchronize()
+    ts = dev.torch_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(ts)
+    for _ in range(iters):
+        dec.replay()
+    ev1.record(ts)
+    ev1.synchronize()
+    us = ev0.elapsed_time(ev1) / iters * 1e3
+    wbytes = sum(v.numel() * v.element_size() for n, v in w.items() if n != "embed") + batch * cfg.hidden * 2
+    kv = sum(int(n) + 1 for n in contexts) * cfg.layers * cfg.kv_heads * cfg.head_dim * 2 * 2
+    dec.close()
+    dev.close()
+    del dec, w
+    torch.cuda.empty_cache()
+    return us, batch / (us * 1e-6), wbytes + kv
+
+
 def time_kernels(kernels, iters, stream, torch):
     """Average launch duration of each kernel: `iters` back-to-back launches
     rotating over its replicas are captured once as a HIP graph and replayed,
@@ -555,7 +600,7 @@ def main():
                    "tokens": T, "hidden": HID, "decode_batch": DEC_B,
                    "replicas": {n: len(v) for n, v in kernels.items()}},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
-        "decode_tok_s": round(DEC_B / (per_kernel_us["paged_decode"] * 1e-6), 1) if "paged_decode" in per_kernel_us else None,
+        "decode_tok_s": None,
         "kernels": kern,
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
@@ -581,6 +626,22 @@ def main():
                 "c3_projections_us": round(sum(v for n, v in eus.items() if n.startswith("c3_") and n != "c3_lm_head"), 2),
             }
         del ekeep
+    if not args.only and not args.no_decode_step:
+        # decode tok/s: the whole TinyLlama step, at config 3's batch and
+        # contexts, and for one sequence (config 3's first context)
+        import numpy as np
+        ctx = np.random.default_rng(2).integers(512, 4097, DEC_B)
+        us32, tps32, by32 = decode_step_tok_s(DEC_B, ctx)
+        us1, tps1, by1 = decode_step_tok_s(1, ctx[:1])
+        line["decode_tok_s"] = round(tps32, 1)
+        line["decode_step"] = {
+            "model": "TinyLlama-1.1B shape (22 layers, d 2048, 32q/4kv, D 64, FFN 5632, vocab 32000), random bf16 "
+                     "weights, greedy, block 16, one captured HIP graph per step",
+            "batch32_config3_contexts": {"us_per_step": round(us32, 1), "tok_s": round(tps32, 1),
+                                         "gbs": round(by32 / (us32 * 1e-6) / 1e9, 1)},
+            "batch1_ctx%d" % int(ctx[0]): {"us_per_step": round(us1, 1), "tok_s": round(tps1, 1),
+                                           "gbs": round(by1 / (us1 * 1e-6) / 1e9, 1)},
+        }
     if not args.no_cpu and not args.only:
         line["cpu_baseline"] = cpu_baseline(host, bytes_per, args.cpu_tokens, args.cpu_seqs)
     print(json.dumps(line), flush=True)

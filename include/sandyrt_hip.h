@@ -361,6 +361,22 @@ int sandy_hip_device_paged_append(SandyHipDevice* dev, uint32_t tensor, const Sa
  * new rows must already be reserved (sandy_hip_device_paged_reserve). */
 int sandy_hip_device_paged_append_step(SandyHipDevice* dev, uint32_t pool, const uint32_t* tensors, int32_t count,
                                        const SandyTensor* rows, char* err, size_t err_cap);
+/* One decode step's q/k/v post-processing in one launch, for `count` <= 256
+ * sequences: qkv is the [count, (q_heads + 2 kv_heads) head_dim] bf16 output
+ * of the fused q/k/v projection.  q heads are rotated into q_out [count,
+ * q_heads, 1, head_dim]; k heads are rotated and appended as the next row of
+ * k_tensors[i] (pool k_pool), v heads appended to v_tensors[i] (v_pool), both
+ * lengths advanced on the device.  RoPE as sandy_hip_rope with full rotary
+ * (split_half or interleaved) and positions[i] for sequence i; appends as
+ * sandy_hip_device_paged_append_step.  Fuses two RoPEKernelOps
+ * (KernelIR.h:575-610) and two Engine::paged_append_op calls
+ * (src/engine/Engine.cpp:548-596) of the TinyLlama eval_token program
+ * (src/models/tinyllama/common.sandy.go:24-28); the
+ * reference has no single counterpart. */
+int sandy_hip_device_decode_qkv(SandyHipDevice* dev, uint32_t k_pool, const uint32_t* k_tensors, uint32_t v_pool,
+                                const uint32_t* v_tensors, int32_t count, const SandyTensor* qkv, int32_t q_heads,
+                                const SandyTensor* positions, double theta, int32_t split_half,
+                                const SandyTensor* q_out, char* err, size_t err_cap);
 /* positions[i] = device length of tensors[i] - 1 (int32 or int64 output), for
  * the position_offsets of decode attention inside a captured step. */
 int sandy_hip_device_paged_positions(SandyHipDevice* dev, uint32_t pool, const uint32_t* tensors, int32_t count,

@@ -974,9 +974,12 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         void* args[] = {&a};
         // split units of 64*NT keys; about 1024 units at the longest context
         // (measured best with the fused merge: config 3 at 512 keys, config 4 at 1024)
-        int64_t split = env_int("SANDY_PAGED_SPLIT", 0);
-        if (split <= 0) split = (max_keys * B * hkv) / 1024;
-        const int nt = split <= 128 && D == 64 ? 2 : split <= 256 ? 4 : split <= 512 ? 8 : 16;
+        // (the nearest size on a log scale: a table slightly longer than 4096
+        // keys keeps 512-key splits)
+        const int64_t forced = env_int("SANDY_PAGED_SPLIT", 0);
+        int64_t split = forced > 0 ? forced : (max_keys * B * hkv) / 1024;
+        const int nt = forced > 0 ? (split <= 128 && D == 64 ? 2 : split <= 256 ? 4 : split <= 512 ? 8 : 16)
+                                  : (split <= 362 ? 4 : split <= 724 ? 8 : 16);
         split = 64 * nt;
         a.split_keys = static_cast<int32_t>(split);
         a.max_splits = static_cast<int32_t>((max_keys + split - 1) / split);

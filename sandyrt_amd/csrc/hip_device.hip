@@ -18,6 +18,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <cmath>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -107,6 +108,87 @@ __global__ __launch_bounds__(256) void paged_append_step_kernel(const char* __re
     if (threadIdx.x == 0) {
         if (blk >= 0) lengths[slot] = len + 1;
         else atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));  // no page reserved for the row
+    }
+}
+
+// One decode step's q/k/v post-processing for `count` sequences in one
+// launch (workgroup b = sequence b): RoPE of the q heads into q_out, RoPE of
+// the k heads appended as the next row of sequence b's K tensor, the v heads
+// appended to its V tensor, both lengths advanced.  Same arithmetic as
+// sandy_hip_rope (host powf denominators, correctly rounded angle, rope_sincos,
+// bf16 round to nearest even) and the step append.
+constexpr int kMaxFusedStep = 256;
+constexpr int kMaxFusedPairs = 128;
+
+struct DecodeQkvArgs {
+    const uint16_t* qkv;
+    int64_t row_stride;  // elements between sequences' qkv rows
+    int32_t hq, hkv, d, split_half;
+    const void* pos;
+    int32_t pos_dt;
+    uint16_t* q_out;     // [count, hq, d]
+    char* k_pages;
+    char* v_pages;
+    const int32_t* k_table;
+    const int32_t* v_table;
+    int32_t* k_len;
+    int32_t* v_len;
+    int64_t k_max_blocks, v_max_blocks, page_size, page_bytes;
+    uint32_t* errw;
+    float denom[kMaxFusedPairs];
+    int32_t k_slots[kMaxFusedStep];
+    int32_t v_slots[kMaxFusedStep];
+};
+
+__global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a) {
+    const int b = blockIdx.x;
+    const int32_t ks = a.k_slots[b], vs = a.v_slots[b];
+    int64_t pos = load_index(a.pos, a.pos_dt, b);
+    const int32_t kl = a.k_len[ks], vl = a.v_len[vs];
+    __syncthreads();  // every thread has read the lengths before they advance
+    if (pos < 0) {
+        if (threadIdx.x == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_POSITION));
+        pos = 0;
+    }
+    const int32_t kblk = kl / a.page_size < a.k_max_blocks ? a.k_table[ks * a.k_max_blocks + kl / a.page_size] : -1;
+    const int32_t vblk = vl / a.page_size < a.v_max_blocks ? a.v_table[vs * a.v_max_blocks + vl / a.page_size] : -1;
+    const int half = a.d >> 1;
+    const uint16_t* row = a.qkv + b * a.row_stride;
+    const float fp = static_cast<float>(pos);
+    const int64_t row_bytes = static_cast<int64_t>(a.d) * 2;
+    for (int pi = threadIdx.x; pi < (a.hq + a.hkv) * half; pi += 256) {
+        const int head = pi / half, i = pi - head * half;
+        const int i0 = a.split_half ? i : 2 * i, i1 = a.split_half ? i + half : 2 * i + 1;
+        const float x0 = bf16_to_f32(row[head * a.d + i0]), x1 = bf16_to_f32(row[head * a.d + i1]);
+        float sn, cs;
+        rope_sincos(fp / a.denom[i], &sn, &cs);
+        const uint16_t r0 = f32_to_bf16(__fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn)));
+        const uint16_t r1 = f32_to_bf16(__fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs)));
+        if (head < a.hq) {
+            uint16_t* q = a.q_out + (static_cast<int64_t>(b) * a.hq + head) * a.d;
+            q[i0] = r0;
+            q[i1] = r1;
+        } else if (kblk >= 0) {
+            uint16_t* kd = reinterpret_cast<uint16_t*>(
+                a.k_pages + kblk * a.page_bytes + ((head - a.hq) * a.page_size + kl % a.page_size) * row_bytes);
+            kd[i0] = r0;
+            kd[i1] = r1;
+        }
+    }
+    if (vblk >= 0) {
+        const uint16_t* v = row + (a.hq + a.hkv) * a.d;
+        for (int e = threadIdx.x; e < a.hkv * a.d; e += 256) {
+            const int kh = e / a.d;
+            uint16_t* vd = reinterpret_cast<uint16_t*>(
+                a.v_pages + vblk * a.page_bytes + (kh * a.page_size + vl % a.page_size) * row_bytes);
+            vd[e - kh * a.d] = v[e];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (kblk >= 0) a.k_len[ks] = kl + 1;
+        if (vblk >= 0) a.v_len[vs] = vl + 1;
+        if (kblk < 0 || vblk < 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));  // no page reserved
     }
 }
 
@@ -514,6 +596,82 @@ int sandy_hip_device_paged_append_step(SandyHipDevice* d, uint32_t pool, const u
                        p.prefix, p.desc.page_size, static_cast<int64_t>(p.inner * p.elem),
                        static_cast<int64_t>(p.page_elems * p.elem), errw, args);
     SANDY_HIP_TRY(hipGetLastError(), e, "paged append step launch");
+    return ok(e);
+}
+
+int sandy_hip_device_decode_qkv(SandyHipDevice* d, uint32_t k_pool, const uint32_t* k_tensors, uint32_t v_pool,
+                                const uint32_t* v_tensors, int32_t count, const SandyTensor* qkv, int32_t q_heads,
+                                const SandyTensor* positions, double theta, int32_t split_half,
+                                const SandyTensor* q_out, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto kit = d->impl.pools.find(k_pool), vit = d->impl.pools.find(v_pool);
+    if (kit == d->impl.pools.end() || vit == d->impl.pools.end())
+        return fail(e, SANDY_ERR_INVALID, "hip device paged pool not found");
+    PagedPool& kp = *kit->second;
+    PagedPool& vp = *vit->second;
+    if (count <= 0 || count > kMaxFusedStep) return fail(e, SANDY_ERR_INVALID, "decode qkv count out of range");
+    if (kp.desc.dtype != SANDY_BF16 || vp.desc.dtype != SANDY_BF16 || kp.prefix != vp.prefix || kp.inner != vp.inner ||
+        kp.desc.page_size != vp.desc.page_size)
+        return fail(e, SANDY_ERR_INVALID, "decode qkv needs bf16 K and V pools of one geometry");
+    const int64_t hkv = kp.prefix, D = kp.inner;
+    if (D % 2 != 0 || D / 2 > kMaxFusedPairs) return fail(e, SANDY_ERR_UNSUPPORTED, "decode qkv head dimension unsupported");
+    if (q_heads <= 0 || q_heads % hkv != 0) return fail(e, SANDY_ERR_INVALID, "attention heads must be divisible by kv_heads");
+    if (!qkv || qkv->dtype != SANDY_BF16 || qkv->rank != 2 || qkv->dims[0] != count ||
+        qkv->dims[1] != (q_heads + 2 * hkv) * D || qkv->strides[1] != 1)
+        return fail(e, SANDY_ERR_INVALID, "decode qkv input must be [count, (q_heads + 2 kv_heads) head_dim] bf16");
+    if (!q_out || q_out->dtype != SANDY_BF16 || numel(*q_out) != count * q_heads * D || !contiguous(*q_out))
+        return fail(e, SANDY_ERR_INVALID, "decode qkv q output must be contiguous [count, q_heads, 1, head_dim] bf16");
+    if (!positions || !is_index(positions->dtype) || numel(*positions) != count || !contiguous(*positions))
+        return fail(e, SANDY_ERR_INVALID, "rope position_ids numel must match the sequence count");
+    const float th = static_cast<float>(theta);
+    if (th <= 0.0f) return fail(e, SANDY_ERR_INVALID, "rope theta must be > 0");
+    uint32_t* errw = device_error_word(e, &st);
+    if (st) return st;
+    DecodeQkvArgs a{};
+    for (int i = 0; i < count; i++) {
+        for (int which = 0; which < 2; which++) {
+            const uint32_t id = which ? v_tensors[i] : k_tensors[i];
+            auto it = d->impl.tensors.find(id);
+            if (it == d->impl.tensors.end() || it->second.pool != (which ? v_pool : k_pool))
+                return fail(e, SANDY_ERR_INVALID, "hip device paged tensor not found");
+            PagedTensor& t = it->second;
+            PagedPool& p = which ? vp : kp;
+            // host bookkeeping advances in step with the device, as for the step append
+            if (t.grow_length + 1 > static_cast<int64_t>(t.pages.size()) * p.desc.page_size && !d->impl.capturing) {
+                st = reserve(d->impl, t, (t.grow_length + p.desc.page_size) / p.desc.page_size, e);
+                if (st) return st;
+            }
+            t.grow_length += 1;
+            (which ? a.v_slots : a.k_slots)[i] = t.slot;
+        }
+    }
+    a.qkv = static_cast<const uint16_t*>(base_ptr(*qkv));
+    a.row_stride = qkv->strides[0];
+    a.hq = q_heads;
+    a.hkv = static_cast<int32_t>(hkv);
+    a.d = static_cast<int32_t>(D);
+    a.split_half = split_half ? 1 : 0;
+    a.pos = base_ptr(*positions);
+    a.pos_dt = positions->dtype;
+    a.q_out = static_cast<uint16_t*>(base_ptr(*q_out));
+    a.k_pages = kp.pages;
+    a.v_pages = vp.pages;
+    a.k_table = kp.table;
+    a.v_table = vp.table;
+    a.k_len = kp.lengths;
+    a.v_len = vp.lengths;
+    a.k_max_blocks = kp.desc.max_blocks;
+    a.v_max_blocks = vp.desc.max_blocks;
+    a.page_size = kp.desc.page_size;
+    a.page_bytes = static_cast<int64_t>(kp.page_elems * kp.elem);
+    a.errw = errw;
+    // the rope kernel's denominators: theta^(2i/d) in float, as the CPU reference
+    for (int i = 0; i < D / 2; i++) a.denom[i] = std::pow(th, static_cast<float>(2 * i) / static_cast<float>(D));
+    hipLaunchKernelGGL(decode_qkv_kernel, dim3(static_cast<unsigned>(count)), dim3(256), 0, d->impl.stream, a);
+    SANDY_HIP_TRY(hipGetLastError(), e, "decode qkv launch");
     return ok(e);
 }
 

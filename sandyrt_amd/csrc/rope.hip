@@ -43,34 +43,6 @@ struct RopeArgs {
     float denom[kMaxPairs];
 };
 
-// sin and cos of a float angle: double-precision Cody-Waite reduction to
-// [-pi/4, pi/4], Taylor polynomials, quadrant select.
-__device__ __forceinline__ void rope_sincos(float a, float* s, float* c) {
-    const double k = __builtin_rint(static_cast<double>(a) * 0.63661977236758134308);  // 2 / pi
-    double rd = fma(-k, 1.5707963267948966192, static_cast<double>(a));               // pi/2 (head)
-    rd = fma(-k, 6.123233995736766036e-17, rd);                                        // pi/2 (tail)
-    const float r = static_cast<float>(rd);
-    const float r2 = r * r;
-    float sp = fmaf(r2, -2.5052108385441718775e-8f, 2.7557319223985890653e-6f);   // -1/11!, 1/9!
-    sp = fmaf(r2, sp, -1.9841269841269841270e-4f);                                 // -1/7!
-    sp = fmaf(r2, sp, 8.3333333333333333333e-3f);                                  // 1/5!
-    sp = fmaf(r2, sp, -1.6666666666666666667e-1f);                                 // -1/3!
-    const float sv = fmaf(r * r2, sp, r);
-    float cp = fmaf(r2, 2.0876756987868098979e-9f, -2.7557319223985890653e-7f);   // 1/12!, -1/10!
-    cp = fmaf(r2, cp, 2.4801587301587301587e-5f);                                  // 1/8!
-    cp = fmaf(r2, cp, -1.3888888888888888889e-3f);                                 // -1/6!
-    cp = fmaf(r2, cp, 4.1666666666666666667e-2f);                                  // 1/4!
-    cp = fmaf(r2, cp, -0.5f);
-    const float cv = fmaf(r2, cp, 1.0f);
-    const int q = static_cast<int>(k);
-    float ss = (q & 1) ? cv : sv;
-    float cc = (q & 1) ? sv : cv;
-    if (q & 2) ss = -ss;
-    if ((q + 1) & 2) cc = -cc;
-    *s = ss;
-    *c = cc;
-}
-
 // mode: 0 = position from sequence index, 1 = ids[0] + seq index,
 //       2 = ids[seq index], 3 = ids[vector]
 __device__ __forceinline__ int64_t rope_position(int mode, const void* ids, int32_t ids_dt, int64_t vec, int64_t s,

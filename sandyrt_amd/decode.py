@@ -1,5 +1,6 @@
-"""Greedy decode step of the TinyLlama model program, built from the C-ABI
-entry points and run eagerly or as one captured HIP graph.
+"""Greedy decode step of the TinyLlama model program for a batch of
+sequences, built from the C-ABI entry points and run eagerly or as one
+captured HIP graph.
 
 The step is the reference's `eval_token` program (src/models/tinyllama/
 eval_token.sandy.go and common.sandy.go:1-62): embedding, 22 blocks of
@@ -16,6 +17,9 @@ work and no host synchronisation (the reference syncs and copies per row,
 src/device/cuda/CudaPagedTensor.cpp:649-740, Engine.cpp:548-596).
 
 Layout choices (same arithmetic as the reference program):
+  * RoPE of q and k and the two paged appends of each block run as one
+    launch (sandy_hip_device_decode_qkv); fused_qkv=False issues the
+    reference program's separate rope / append ops instead.
   * q/k/v weights are concatenated into one [q + k + v, hidden] matrix and
     gate/up into one [2 * ffn, hidden] matrix, so each is one GEMM; the
     q/k/v and gate/up outputs are contiguous views of those GEMM outputs.
@@ -126,40 +130,49 @@ class _DevCall:
 
 
 class TinyLlamaDecoder:
-    """Owns the paged K/V caches of one sequence and the step's buffers; the
-    step program is a fixed list of bound calls on the device's stream."""
+    """Owns the paged K/V caches of `batch` sequences and the step's buffers;
+    the step program is a fixed list of bound calls on the device's stream.
+    Sequence b owns row b of every layer's block table (its pool slot), so
+    the attention reads the pools' tables directly."""
 
-    def __init__(self, dev: HipDevice, cfg: DecodeConfig, weights: dict):
-        self.dev, self.cfg, self.w = dev, cfg, weights
-        c = cfg
+    def __init__(self, dev: HipDevice, cfg: DecodeConfig, weights: dict, batch: int = 1, fused_qkv: bool = True):
+        self.dev, self.cfg, self.w, self.batch, self.fused_qkv = dev, cfg, weights, batch, fused_qkv
+        c, B = cfg, batch
         bf = torch.bfloat16
         pages = (c.max_context + c.page_size - 1) // c.page_size
         self.k_pools, self.v_pools, self.k_seq, self.v_seq = [], [], [], []
         for _ in range(c.layers):
             for pools, seqs in ((self.k_pools, self.k_seq), (self.v_pools, self.v_seq)):
-                p = dev.create_paged_pool([1, c.kv_heads, -1, c.head_dim], BF16, 2, c.page_size, initial_pages=pages,
-                                          max_pages=pages, max_tensors=1, max_blocks=pages)
-                t = dev.alloc_paged(p)
-                dev.reserve_paged(t, pages)
+                p = dev.create_paged_pool([1, c.kv_heads, -1, c.head_dim], BF16, 2, c.page_size,
+                                          initial_pages=B * pages, max_pages=B * pages, max_tensors=B,
+                                          max_blocks=pages)
+                ids = []
+                for b in range(B):
+                    t = dev.alloc_paged(p)
+                    dev.reserve_paged(t, pages)
+                    if dev.paged_meta(t).slot != b:
+                        raise RuntimeError("paged pool slots are not allocated in order")
+                    ids.append(t)
                 pools.append(p)
-                seqs.append(t)
+                seqs.append(ids)
         dv = "cuda"
         qkv = (c.heads + 2 * c.kv_heads) * c.head_dim
-        self.token = torch.zeros(1, 1, dtype=torch.int64, device=dv)  # greedy output -> next input
-        self.pos = torch.zeros(1, dtype=torch.int64, device=dv)
-        self.x0 = torch.empty(1, 1, c.hidden, dtype=bf, device=dv)
-        self.res = [torch.empty(1, c.hidden, dtype=bf, device=dv) for _ in range(2)]
-        self.h = torch.empty(1, c.hidden, dtype=bf, device=dv)
-        self.qkv = torch.empty(1, qkv, dtype=bf, device=dv)
-        self.qr = torch.empty(1, c.heads, 1, c.head_dim, dtype=bf, device=dv)
-        self.kr = torch.empty(1, c.kv_heads, 1, c.head_dim, dtype=bf, device=dv)
-        self.ctx = torch.empty(1, c.heads, 1, c.head_dim, dtype=bf, device=dv)
-        self.o = torch.empty(1, c.hidden, dtype=bf, device=dv)
-        self.gu = torch.empty(1, 2 * c.ffn, dtype=bf, device=dv)
-        self.act = torch.empty(1, c.ffn, dtype=bf, device=dv)
-        self.d = torch.empty(1, c.hidden, dtype=bf, device=dv)
-        self.logits = torch.empty(1, c.vocab, dtype=bf, device=dv)
-        self.top_v = torch.empty(1, 1, dtype=bf, device=dv)
+        self.token = torch.zeros(B, 1, dtype=torch.int64, device=dv)  # greedy output -> next input
+        self.pos = torch.zeros(B, dtype=torch.int64, device=dv)
+        self.x0 = torch.empty(B, 1, c.hidden, dtype=bf, device=dv)
+        self.res = [torch.empty(B, c.hidden, dtype=bf, device=dv) for _ in range(2)]
+        self.h = torch.empty(B, c.hidden, dtype=bf, device=dv)
+        self.qkv = torch.empty(B, qkv, dtype=bf, device=dv)
+        self.qr = torch.empty(B, c.heads, 1, c.head_dim, dtype=bf, device=dv)
+        self.kr = torch.empty(B, c.kv_heads, 1, c.head_dim, dtype=bf, device=dv)
+        self.vr = torch.empty(B, c.kv_heads, 1, c.head_dim, dtype=bf, device=dv)
+        self.ctx = torch.empty(B, c.heads, 1, c.head_dim, dtype=bf, device=dv)
+        self.o = torch.empty(B, c.hidden, dtype=bf, device=dv)
+        self.gu = torch.empty(B, 2 * c.ffn, dtype=bf, device=dv)
+        self.act = torch.empty(B, c.ffn, dtype=bf, device=dv)
+        self.d = torch.empty(B, c.hidden, dtype=bf, device=dv)
+        self.logits = torch.empty(B, c.vocab, dtype=bf, device=dv)
+        self.top_v = torch.empty(B, 1, dtype=bf, device=dv)
         self._keep = []
         self.program = self._build()
         self.graph = None
@@ -171,26 +184,36 @@ class TinyLlamaDecoder:
         return p
 
     def _build(self):
-        c, w, dev, s = self.cfg, self.w, self.dev, self.dev.stream
+        c, w, dev, s, B = self.cfg, self.w, self.dev, self.dev.stream, self.batch
         d = self._d
         prog = []
         hq, hk, D = c.heads * c.head_dim, c.kv_heads * c.head_dim, c.head_dim
-        q_view = self.qkv[:, :hq].view(1, c.heads, 1, D)
-        k_view = self.qkv[:, hq:hq + hk].view(1, c.kv_heads, 1, D)
-        v_view = self.qkv[:, hq + hk:].view(1, c.kv_heads, 1, D)
+
+        def per_position(t, heads):
+            # [B, heads, D] rows of the qkv output (or of a [B, heads, 1, D]
+            # buffer) seen as [1, heads, B, D]: the sequence axis is the RoPE
+            # sequence, so position_ids[b] rotates every head of sequence b
+            return t.reshape(B, heads, D).permute(1, 0, 2).unsqueeze(0)
+
+        q_in = per_position(self.qkv[:, :hq], c.heads)
+        k_in = per_position(self.qkv[:, hq:hq + hk], c.kv_heads)
+        v_view = self.qkv[:, hq + hk:].view(B, c.kv_heads, 1, D)
+        q_out, k_out = per_position(self.qr, c.heads), per_position(self.kr, c.kv_heads)
         gate, up = self.gu[:, :c.ffn], self.gu[:, c.ffn:]
-        h2d, ctx2d = self.h, self.ctx.view(1, hq)
-        ids0 = (C.c_uint32 * 1)(self.k_seq[0])
+        h2d, ctx2d = self.h, self.ctx.view(B, hq)
+        ids0 = (C.c_uint32 * B)(*self.k_seq[0])
         self._keep.append(ids0)
         prog.append(_DevCall("sandy_hip_device_paged_lengths", dev.handle, C.c_uint32(self.k_pools[0]), ids0,
-                             C.c_int32(1), d(self.pos)))
+                             C.c_int32(B), d(self.pos)))
         prog.append(_Call("sandy_hip_gather", d(self.token), d(w["embed"]), d(self.x0), stream=s))
         silu, sres = ops.silu_mul_nodes()
         nodes = ops._nodes(silu)
         arr = (_lib.SandyTensor * 2)(d(gate).contents, d(up).contents)
         bc = (C.c_int32 * 2)(0, 0)
-        self._keep += [nodes, arr, bc]
-        x0 = self.x0.view(1, c.hidden)
+        copy_nodes = ops._nodes([ops.ScalarNode(0, ops.LOAD, 0)])
+        v_arr = (_lib.SandyTensor * 1)(d(v_view).contents)
+        self._keep += [nodes, arr, bc, copy_nodes, v_arr]
+        x0 = self.x0.view(B, c.hidden)
         # residual stream: block input x_l in buffer A (x0 for block 0), the
         # residual after attention in buffer B
         res_a, res_b = self.res
@@ -206,20 +229,33 @@ class TinyLlamaDecoder:
                 x_in = res_a
             prog.append(_Call("sandy_hip_matmul", d(h2d), d(w[f"{layer}.qkv"]), C.c_int32(0), C.c_int32(1),
                               d(self.qkv), stream=s))
-            prog.append(_Call("sandy_hip_rope", d(q_view), d(self.pos), C.c_double(c.theta), C.c_int64(-1),
-                              C.c_int32(1), d(self.qr), stream=s))
-            prog.append(_Call("sandy_hip_rope", d(k_view), d(self.pos), C.c_double(c.theta), C.c_int64(-1),
-                              C.c_int32(1), d(self.kr), stream=s))
-            kid = (C.c_uint32 * 1)(self.k_seq[layer])
-            vid = (C.c_uint32 * 1)(self.v_seq[layer])
+            kid = (C.c_uint32 * B)(*self.k_seq[layer])
+            vid = (C.c_uint32 * B)(*self.v_seq[layer])
             self._keep += [kid, vid]
-            prog.append(_DevCall("sandy_hip_device_paged_append_step", dev.handle, C.c_uint32(self.k_pools[layer]),
-                                 kid, C.c_int32(1), d(self.kr)))
-            prog.append(_DevCall("sandy_hip_device_paged_append_step", dev.handle, C.c_uint32(self.v_pools[layer]),
-                                 vid, C.c_int32(1), d(v_view)))
+            if self.fused_qkv:
+                # RoPE q and k, append k and v: one launch
+                prog.append(_DevCall("sandy_hip_device_decode_qkv", dev.handle, C.c_uint32(self.k_pools[layer]), kid,
+                                     C.c_uint32(self.v_pools[layer]), vid, C.c_int32(B), d(self.qkv),
+                                     C.c_int32(c.heads), d(self.pos), C.c_double(c.theta), C.c_int32(1),
+                                     d(self.qr)))
+            else:  # the reference program's separate ops
+                prog.append(_Call("sandy_hip_rope", d(q_in), d(self.pos), C.c_double(c.theta), C.c_int64(-1),
+                                  C.c_int32(1), d(q_out), stream=s))
+                prog.append(_Call("sandy_hip_rope", d(k_in), d(self.pos), C.c_double(c.theta), C.c_int64(-1),
+                                  C.c_int32(1), d(k_out), stream=s))
+                if B == 1:
+                    v_rows = v_view  # one sequence: the v slice is already contiguous
+                else:  # contiguous [B, kv_heads, 1, D] rows for the batched append
+                    prog.append(_Call("sandy_hip_elementwise", copy_nodes, C.c_int32(1), C.c_uint32(0), v_arr, None,
+                                      C.c_int32(1), d(self.vr), stream=s))
+                    v_rows = self.vr
+                prog.append(_DevCall("sandy_hip_device_paged_append_step", dev.handle,
+                                     C.c_uint32(self.k_pools[layer]), kid, C.c_int32(B), d(self.kr)))
+                prog.append(_DevCall("sandy_hip_device_paged_append_step", dev.handle,
+                                     C.c_uint32(self.v_pools[layer]), vid, C.c_int32(B), d(v_rows)))
             kc, table, _ = dev.paged_views(self.k_pools[layer])
             vc, _, _ = dev.paged_views(self.v_pools[layer])
-            table.contents.dims[0] = 1
+            table.contents.dims[0] = B  # rows 0..B-1: the sequences' slots
             self._keep += [kc, vc, table]
             prog.append(_Call("sandy_hip_paged_attention", d(self.qr), kc, vc, table, d(self.pos), C.c_int64(0),
                               C.c_double(1.0 / (D ** 0.5)), d(self.ctx), stream=s))
@@ -242,17 +278,21 @@ class TinyLlamaDecoder:
         return prog
 
     # ------------------------------------------------------------------ running
-    def prefill_cache(self, k_rows: list, v_rows: list):
-        """Append context K/V ([1, kv_heads, n, head_dim] per layer) as if
-        earlier tokens had been decoded."""
+    def prefill_cache(self, k_rows: list, v_rows: list, seq: int = 0):
+        """Append context K/V ([1, kv_heads, n, head_dim] per layer) of
+        sequence `seq` as if earlier tokens had been decoded."""
         torch.cuda.synchronize()
         for layer in range(self.cfg.layers):
-            self.dev.append_paged(self.k_seq[layer], k_rows[layer])
-            self.dev.append_paged(self.v_seq[layer], v_rows[layer])
+            self.dev.append_paged(self.k_seq[layer][seq], k_rows[layer])
+            self.dev.append_paged(self.v_seq[layer][seq], v_rows[layer])
         self.dev.synchronize()
 
-    def set_token(self, token: int):
-        self.token.fill_(int(token))
+    def set_token(self, token):
+        """Next input token: one id for every sequence, or one per sequence."""
+        if isinstance(token, int):
+            self.token.fill_(token)
+        else:
+            self.token.copy_(torch.as_tensor(token, dtype=torch.int64).view(self.batch, 1))
         torch.cuda.synchronize()
 
     def step(self):
@@ -273,9 +313,9 @@ class TinyLlamaDecoder:
     def replay(self):
         self.dev.graph_launch(self.graph)
 
-    def length(self) -> int:
+    def length(self, seq: int = 0) -> int:
         self.dev.paged_sync(self.k_pools[0])
-        return self.dev.paged_meta(self.k_seq[0]).grow_length
+        return self.dev.paged_meta(self.k_seq[0][seq]).grow_length
 
     def close(self):
         if self.graph is not None:

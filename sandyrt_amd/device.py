@@ -108,6 +108,17 @@ class HipDevice:
         dcall("sandy_hip_device_paged_append_step", self.handle, C.c_uint32(pool), ids, C.c_int32(len(tensors)),
               desc(rows))
 
+    def decode_qkv(self, k_pool: int, k_tensors, v_pool: int, v_tensors, qkv: torch.Tensor, q_heads: int,
+                   positions: torch.Tensor, theta: float, q_out: torch.Tensor, split_half: bool = True):
+        """RoPE q into q_out, RoPE k and append it, append v -- one launch for
+        a decode step's [count, (q_heads + 2 kv_heads) head_dim] q/k/v rows."""
+        kids = (C.c_uint32 * len(k_tensors))(*k_tensors)
+        vids = (C.c_uint32 * len(v_tensors))(*v_tensors)
+        dcall("sandy_hip_device_decode_qkv", self.handle, C.c_uint32(k_pool), kids, C.c_uint32(v_pool), vids,
+              C.c_int32(len(k_tensors)), desc(qkv), C.c_int32(q_heads), desc(positions), C.c_double(theta),
+              C.c_int32(1 if split_half else 0), desc(q_out))
+        return q_out
+
     def positions(self, pool: int, tensors, out: torch.Tensor):
         ids = (C.c_uint32 * len(tensors))(*tensors)
         dcall("sandy_hip_device_paged_positions", self.handle, C.c_uint32(pool), ids, C.c_int32(len(tensors)),

@@ -194,3 +194,74 @@ def test_graph_captured_decode_steps_match_eager(dev):
     dev.paged_sync(a[0])
     assert dev.paged_meta(a[2][2]).grow_length == ctx[2] + steps
     dev.graph_destroy(graph)
+
+
+@pytest.mark.parametrize("split_half", [True, False])
+def test_decode_qkv_matches_rope_and_step_append(split_half):
+    """sandy_hip_device_decode_qkv == sandy_hip_rope (q and k, per-sequence
+    positions) + sandy_hip_device_paged_append_step (k and v), bit for bit."""
+    from sandyrt_amd import ops
+    from sandyrt_amd._lib import BF16
+    from sandyrt_amd.device import HipDevice
+    B, hq, hkv, D, P = 3, 8, 2, 64, 16
+    dev = HipDevice(0)
+    try:
+        pools, seqs = [], []
+        for _ in range(4):  # fused K, fused V, reference K, reference V
+            p = dev.create_paged_pool([1, hkv, -1, D], BF16, 2, P, max_tensors=B, max_blocks=8)
+            ids = [dev.alloc_paged(p) for _ in range(B)]
+            pools.append(p)
+            seqs.append(ids)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(3)
+        for s, n in enumerate([15, 16, 40]):
+            k0 = torch.randn(1, hkv, n, D, generator=g, device="cuda").to(torch.bfloat16)
+            v0 = torch.randn(1, hkv, n, D, generator=g, device="cuda").to(torch.bfloat16)
+            for i, t in ((0, k0), (1, v0), (2, k0), (3, v0)):
+                dev.reserve_paged(seqs[i][s], 8)
+                dev.append_paged(seqs[i][s], t)
+        qkv = torch.randn(B, (hq + 2 * hkv) * D, generator=g, device="cuda").to(torch.bfloat16)
+        pos = torch.tensor([15, 16, 40], dtype=torch.int64, device="cuda")
+        q_out = torch.empty(B, hq, 1, D, dtype=torch.bfloat16, device="cuda")
+        dev.decode_qkv(pools[0], seqs[0], pools[1], seqs[1], qkv, hq, pos, 1e4, q_out, split_half=split_half)
+        # reference path: rope over [1, heads, B, D] views with position_ids[b], then the step appends
+        q_ref = ops.rope(qkv[:, :hq * D].reshape(B, hq, D).permute(1, 0, 2).unsqueeze(0).contiguous(), 1e4,
+                         split_half=split_half, position_ids=pos)
+        k_ref = ops.rope(qkv[:, hq * D:(hq + hkv) * D].reshape(B, hkv, D).permute(1, 0, 2).unsqueeze(0).contiguous(),
+                         1e4, split_half=split_half, position_ids=pos)
+        k_rows = k_ref[0].permute(1, 0, 2).contiguous().view(B, hkv, 1, D)
+        v_rows = qkv[:, (hq + hkv) * D:].contiguous().view(B, hkv, 1, D)
+        dev.append_step(pools[2], seqs[2], k_rows)
+        dev.append_step(pools[3], seqs[3], v_rows)
+        dev.synchronize()
+        ops.check_device_errors()
+        assert torch.equal(q_out.view(B, hq, D), q_ref[0].permute(1, 0, 2))
+        for s in range(B):
+            for fused, ref in ((0, 2), (1, 3)):
+                dev.paged_sync(pools[fused])
+                dev.paged_sync(pools[ref])
+                got = dev.read_paged(seqs[fused][s], np.uint16)
+                assert got.shape[2] == [15, 16, 40][s] + 1
+                assert np.array_equal(got, dev.read_paged(seqs[ref][s], np.uint16))
+    finally:
+        dev.close()
+
+
+def test_decode_qkv_rejects_bad_shapes():
+    from sandyrt_amd._lib import BF16, SandyError
+    from sandyrt_amd.device import HipDevice
+    dev = HipDevice(0)
+    try:
+        kp = dev.create_paged_pool([1, 2, -1, 64], BF16, 2, 16, max_tensors=2, max_blocks=4)
+        vp = dev.create_paged_pool([1, 2, -1, 64], BF16, 2, 16, max_tensors=2, max_blocks=4)
+        k, v = dev.alloc_paged(kp), dev.alloc_paged(vp)
+        pos = torch.zeros(1, dtype=torch.int64, device="cuda")
+        q_out = torch.empty(1, 8, 1, 64, dtype=torch.bfloat16, device="cuda")
+        bad = torch.zeros(1, 100, dtype=torch.bfloat16, device="cuda")
+        with pytest.raises(SandyError, match="decode qkv input must be"):
+            dev.decode_qkv(kp, [k], vp, [v], bad, 8, pos, 1e4, q_out)
+        good = torch.zeros(1, 12 * 64, dtype=torch.bfloat16, device="cuda")
+        with pytest.raises(SandyError, match="attention heads must be divisible by kv_heads"):
+            dev.decode_qkv(kp, [k], vp, [v], good, 7, pos, 1e4, q_out)
+    finally:
+        dev.close()
