@@ -582,23 +582,41 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
         // K: at most 32 chunks (2048 k) per workgroup, split evenly; the
         // per-wave run is rounded up to a built run length
         const int64_t ksplits = (chunks + 31) / 32;
+        // chunks in flight per wave (4 only for RT * CT <= 2, register bound)
+        int qdepth = 2;
         if (variant < 0 || variant > 8) {
             // Measured on decode shapes with the weights streamed from HBM
-            // (few long streams beat many short ones): the widest column tile
-            // that still gives about 120 workgroups, so the activation rows
-            // are re-read by as few workgroups as possible.
-            const int64_t rt = p.M <= 16 ? 1 : 2;
-            const int64_t rows = (p.M + 16 * rt - 1) / (16 * rt) * p.batches;
-            int ct = 1;
-            for (int c : {4, 2}) {
-                if ((p.N + 16 * c - 1) / (16 * c) * rows * ksplits >= 120) {
-                    ct = c;
-                    break;
+            // (rotated over >= 1 GiB of copies):
+            //   <= 16 rows: 16 x 16 tiles, 16 x 32 from N >= 16384 (lm-head);
+            //   <= 32 rows: 16-row tiles (the second row tile re-reads the
+            //     weights from cache), 32 columns from N K >= 5M;
+            //   weights past 64 MB at 32 rows, and 33..64 rows: 32-row tiles,
+            //     the widest column tile giving >= 120 workgroups;
+            //   4 chunks in flight per wave for weights under 8M elements
+            //   (o projection at 32 rows 8.3 -> 6.1 us, q/k/v at one row
+            //   7.4 -> 5.5 us), 2 for the larger ones.
+            const bool big = p.N * p.K * 2 > (int64_t(64) << 20);
+            int64_t rt = 1, ct = 1;
+            if (p.M <= 16 && !big) {
+                ct = p.N >= 16384 ? 2 : 1;
+                qdepth = 4;
+            } else if (p.M <= 32 && !big) {
+                ct = p.N * p.K >= 5 * (int64_t(1) << 20) ? 2 : 1;
+                qdepth = p.N * p.K < 8 * (int64_t(1) << 20) ? 4 : 2;
+            } else {
+                rt = p.M <= 16 ? 1 : 2;
+                const int64_t rows = (p.M + 16 * rt - 1) / (16 * rt) * p.batches;
+                for (int c : {4, 2}) {
+                    if ((p.N + 16 * c - 1) / (16 * c) * rows * ksplits >= 120) {
+                        ct = c;
+                        break;
+                    }
                 }
             }
             static const int kPick[2][3] = {{0, 4, 6}, {1, 3, 5}};  // [RT 1/2][CT 1/2/4]
             variant = kPick[rt == 1 ? 0 : 1][ct == 1 ? 0 : ct == 2 ? 1 : 2];
         }
+        qdepth = env_int("SANDY_GEMM_Q", qdepth);
         const int RT = kRT[variant], CT = kCT[variant];
         const int64_t row_tiles = (p.M + 16 * RT - 1) / (16 * RT);
         const int64_t col_tiles = (p.N + 16 * CT - 1) / (16 * CT);
@@ -631,8 +649,13 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
         }
         const dim3 grid(static_cast<unsigned>(col_tiles * splits), static_cast<unsigned>(row_tiles),
                         static_cast<unsigned>(p.batches));
-#define WAVES_RUN(RT_, CT_, OCC_, R_) \
-    case R_: hipLaunchKernelGGL((gemm_waves_kernel<RT_, CT_, 2, R_, OCC_>), grid, dim3(256), 0, stream, g); break;
+#define WAVES_RUN(RT_, CT_, OCC_, R_)                                                                          \
+    case R_:                                                                                                   \
+        if (qdepth >= 4 && R_ >= 4 && RT_ * CT_ <= 2)                                                          \
+            hipLaunchKernelGGL((gemm_waves_kernel<RT_, CT_, 4, R_, 1>), grid, dim3(256), 0, stream, g);       \
+        else                                                                                                   \
+            hipLaunchKernelGGL((gemm_waves_kernel<RT_, CT_, 2, R_, OCC_>), grid, dim3(256), 0, stream, g);    \
+        break;
 #define WAVES_CPS(RT_, CT_, OCC_)                                                                          \
     switch (cps) {                                                                                         \
         WAVES_RUN(RT_, CT_, OCC_, 2) WAVES_RUN(RT_, CT_, OCC_, 3) WAVES_RUN(RT_, CT_, OCC_, 4)            \
