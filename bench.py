@@ -55,6 +55,8 @@ def parse():
     p.add_argument("--only", default="", help="comma list of kernels to run (profiling)")
     p.add_argument("--no-extras", action="store_true", help="skip the per-kernel table of the other configs")
     p.add_argument("--no-decode-step", action="store_true", help="skip the whole-model decode tok/s measurement")
+    p.add_argument("--decode-step-only", action="store_true",
+                   help="only the whole-model decode step at config 3's batch and contexts (profiling)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a plain 256 MiB device copy (counter calibration for rocprofv3 --pmc)")
     return p.parse_args()
@@ -518,6 +520,13 @@ def main():
 
     _lib.lib()  # fail loudly if the backend is not built
     torch.cuda.set_device(0)
+    if args.decode_step_only:
+        import numpy as np
+        ctx = np.random.default_rng(2).integers(512, 4097, DEC_B)
+        us, tps, by = decode_step_tok_s(DEC_B, ctx, iters=args.steps)
+        print(json.dumps({"metric": "TinyLlama decode step, batch 32, config-3 contexts", "us_per_step": round(us, 1),
+                          "tok_s": round(tps, 1), "gbs": round(by / (us * 1e-6) / 1e9, 1)}), flush=True)
+        return
     kernels, bytes_per, keep, host = build_workload(args.replicas)
     if args.only:
         kernels = {k: v for k, v in kernels.items() if k in args.only.split(",")}
