@@ -410,6 +410,40 @@ def decode_step_tok_s(batch, contexts, iters=10, seed=2):
     return us, batch / (us * 1e-6), wbytes + kv
 
 
+def gpt2_config1():
+    """BASELINE config 1 on the GPU: GPT-2 small (fp32, random weights
+    N(0, 0.02) from numpy default_rng(0)), a 64-token prompt, 32 greedy tokens;
+    tokens compared with the CPU chain's committed sequence.  The CPU side
+    times the same op chain (the oracle restatement, one core) on a bounded
+    sample: an 8-token prompt and 2 single-token steps."""
+    import json as _json
+    from oracle import oracle as O
+    from oracle.gpt2 import GPT2Oracle
+    from sandyrt_amd.gpt2 import GPT2Config, GPT2Runner, prompt_ids, random_weights
+    cfg = GPT2Config()
+    w = random_weights(cfg, seed=0)
+    prompt = prompt_ids(cfg, 64, seed=0)
+    runner = GPT2Runner(cfg, w, max_seq=128)
+    runner.greedy(prompt[:8], 2)  # warm (generated kernels, workspaces)
+    runner = GPT2Runner(cfg, w, max_seq=128)
+    tokens, t_prompt, t_decode = runner.greedy(prompt, 32)
+    golden = os.path.join(ROOT, "tests", "golden", "gpt2_c1_greedy.json")
+    match = None
+    if os.path.exists(golden):
+        match = tokens == _json.load(open(golden))["tokens"]
+    if not os.path.exists(O.LIB_PATH):
+        O.build()
+    cpu = GPT2Oracle(O.Oracle(), cfg, w)
+    cpu.forward(prompt[:8])
+    t0 = time.perf_counter()
+    for t in (11, 12):
+        cpu.forward([t])
+    cpu_tok_s = 2 / (time.perf_counter() - t0)
+    return {"prompt_ms": round(t_prompt * 1e3, 2), "decode_tok_s": round(31 / t_decode, 1),
+            "tokens_match_cpu": match, "cpu_decode_tok_s": round(cpu_tok_s, 2), "cpu_cores": 1,
+            "cpu_kind": "port", "cpu_sample": "oracle op chain, 2 single-token steps after an 8-token prompt"}
+
+
 def time_kernels(kernels, iters, stream, torch):
     """Average launch duration of each kernel: `iters` back-to-back launches
     rotating over its replicas are captured once as a HIP graph and replayed,
@@ -627,6 +661,8 @@ def main():
                               "gbs": round(eb[n] / (eus[n] * 1e-6) / 1e9, 1),
                               "frac": round(eb[n] / (eus[n] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)} for n in eus}
         moe_us = sum(v for n, v in eus.items() if n.startswith("c5_"))
+        if not args.only:
+            line["c1_gpt2_greedy"] = gpt2_config1()
         if not args.only:
             line["extras_summary"] = {
                 "c4_decode_tok_s": round(GEM_B / (eus["c4_paged_decode"] * 1e-6), 1),

@@ -501,6 +501,62 @@ struct Plan {
     BatchMap bm;
 };
 
+// f32 products of a few rows against a weight read as [n, k] (linear, and
+// matmul with transpose_rhs): lane = one output column, which walks k in the
+// reference's order (acc = bias, then acc + x * w rounded at each step, no
+// contraction), so results stay bit-identical to the CPU path.  The weight
+// row of each lane streams in 8-float chunks with Q chunks in flight; the x
+// values are the same for every lane.  One wave per workgroup spreads even a
+// 768-column output over 12 CUs.
+template <int MR, int Q>
+__global__ __launch_bounds__(64) void gemv_seq_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                     const float* __restrict__ bias, float* __restrict__ out,
+                                                     int64_t M, int64_t N, int64_t K, BatchMap bm) {
+    const int64_t n = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+    const int64_t bz = blockIdx.z;
+    int64_t lo, ro;
+    batch_offsets(bm, bz, lo, ro);
+    const bool live = n < N;
+    const float* wr = w + ro + (live ? n : 0) * K;
+    const float* xr = x + lo;
+    float acc[MR];
+    const float b0 = bias && live ? bias[n] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < MR; r++) acc[r] = b0;
+    const int64_t nch = K / 8;
+    float4 buf[Q][2];
+    auto load = [&](int64_t c, int slot) {
+        const float4* p = reinterpret_cast<const float4*>(wr + c * 8);
+        buf[slot][0] = p[0];
+        buf[slot][1] = p[1];
+    };
+    auto step = [&](int64_t k, float wv) {
+#pragma unroll
+        for (int r = 0; r < MR; r++)
+            if (r < M) acc[r] = __fadd_rn(acc[r], __fmul_rn(xr[r * K + k], wv));
+    };
+#pragma unroll
+    for (int q = 0; q < Q; q++)
+        if (q < nch) load(q, q);
+    for (int64_t c0 = 0; c0 < nch; c0 += Q) {
+#pragma unroll
+        for (int q = 0; q < Q; q++) {
+            const int64_t c = c0 + q;
+            if (c >= nch) break;
+            const float wv[8] = {buf[q][0].x, buf[q][0].y, buf[q][0].z, buf[q][0].w,
+                                 buf[q][1].x, buf[q][1].y, buf[q][1].z, buf[q][1].w};
+            if (c + Q < nch) load(c + Q, q);
+#pragma unroll
+            for (int j = 0; j < 8; j++) step(c * 8 + j, wv[j]);
+        }
+    }
+    for (int64_t k = nch * 8; k < K; k++) step(k, wr[k]);
+    if (!live) return;
+#pragma unroll
+    for (int r = 0; r < MR; r++)
+        if (r < M) out[(bz * M + r) * N + n] = acc[r];
+}
+
 // Fills the plan from operand shapes with the reference's rules; returns an
 // error message or null.
 const char* plan_matmul(const SandyTensor& l, const SandyTensor& r, const SandyTensor& o, bool tl, bool tr, Plan& p) {
@@ -562,7 +618,22 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
     const bool lines = l.dtype == SANDY_BF16 && !tl && tr && p.K % 32 == 0 && p.K > 0 && aligned &&
                        p.K <= (int64_t{1} << 21) && env_int("SANDY_GEMM_SIMT", 0) == 0;
     const bool waves = lines && env_int("SANDY_GEMM_WAVES", p.M <= 64 ? 1 : 0) != 0;
-    if (waves) {
+    // f32, few rows, weight rows contiguous: the exact-order GEMV
+    const bool gemv = l.dtype == SANDY_F32 && !tl && tr && p.M <= 8 && p.K % 4 == 0 && aligned &&
+                      p.lrs == p.K && p.rrs == p.K && env_int("SANDY_GEMM_SIMT", 0) == 0;
+    if (gemv) {
+        const int64_t blocks = (p.N + 63) / 64;
+        if (blocks > 0x7fffffff) return fail(e, SANDY_ERR_UNSUPPORTED, "%s shape exceeds the launch grid", what);
+        const dim3 grid(static_cast<unsigned>(blocks), 1, static_cast<unsigned>(p.batches));
+        const float* x = static_cast<const float*>(pl);
+        const float* w = static_cast<const float*>(pr);
+        const float* b = static_cast<const float*>(pb);
+        float* y = static_cast<float*>(po);
+        if (p.M == 1) hipLaunchKernelGGL((gemv_seq_kernel<1, 16>), grid, dim3(64), 0, stream, x, w, b, y, p.M, p.N, p.K, p.bm);
+        else if (p.M <= 2) hipLaunchKernelGGL((gemv_seq_kernel<2, 16>), grid, dim3(64), 0, stream, x, w, b, y, p.M, p.N, p.K, p.bm);
+        else if (p.M <= 4) hipLaunchKernelGGL((gemv_seq_kernel<4, 12>), grid, dim3(64), 0, stream, x, w, b, y, p.M, p.N, p.K, p.bm);
+        else hipLaunchKernelGGL((gemv_seq_kernel<8, 8>), grid, dim3(64), 0, stream, x, w, b, y, p.M, p.N, p.K, p.bm);
+    } else if (waves) {
         GemmArgs g{};
         g.a = static_cast<const uint16_t*>(pl);
         g.w = static_cast<const uint16_t*>(pr);

@@ -171,6 +171,12 @@ def gelu_mul_nodes():
     ], 15
 
 
+def gelu_nodes():
+    """gelu(x) = (0.5 x)(1 + tanh(0.7978845608028654 (x + 0.044715 x^3))); one input."""
+    nodes, _ = gelu_mul_nodes()
+    return nodes[:14], 13
+
+
 def softcap_nodes(cap: float):
     """softcap(x, c) = tanh(x * (1 / c)) * c; one input."""
     return [

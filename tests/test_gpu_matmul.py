@@ -201,3 +201,17 @@ def test_linear_matches_oracle(ops, oracle, dtype, xshape, out_f):
         assert_equal(got, want, "linear exact order")  # acc starts at bias, k in order
     else:
         assert_close(got, want, dtype, "linear")
+
+
+@pytest.mark.parametrize("rows,in_f,out_f", [(1, 772, 3000), (2, 768, 50), (3, 4, 130), (8, 1000, 65), (4, 770, 33)])
+def test_linear_f32_few_rows_bit_exact(ops, oracle, rows, in_f, out_f):
+    """f32 linear of a few rows (the GPT-2 decode shapes): the exact-order
+    GEMV (k tails past the 8-float chunks included) and, for k not a multiple
+    of 4, the general kernel -- both bit-identical to the CPU."""
+    r = rng(rows * 1000 + in_f + out_f)
+    x = from_f32(normal(r, (rows, in_f)), torch.float32)
+    w = from_f32(normal(r, (out_f, in_f), 0.02), torch.float32)
+    b = from_f32(normal(r, (out_f,)), torch.float32)
+    assert_equal(ops.linear(x, w, b), oracle.linear(to_oracle(x), to_oracle(w), to_oracle(b)), "linear")
+    assert_equal(ops.matmul(x, w, transpose_rhs=True),
+                 oracle.matmul(to_oracle(x), to_oracle(w), transpose_rhs=True), "matmul transposed rhs")

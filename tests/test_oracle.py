@@ -341,3 +341,20 @@ def test_oracle_fuzz_against_reference_build(oracle, ref, seed):
         assert bits_equal(oracle.matmul(lm, rm), ref.matmul(lm, rm))
         assert bits_equal(oracle.matmul(lm, np.swapaxes(rm, -1, -2).copy(), transpose_rhs=True),
                           ref.matmul(lm, np.swapaxes(rm, -1, -2).copy(), transpose_rhs=True))
+
+
+@pytest.mark.skipif(not os.path.exists(O.REF_PATH), reason="reference CPU build (oracle/_ref) not built here")
+def test_gpt2_chain_matches_reference_build_bit_for_bit():
+    """The GPT-2 op chain (oracle/gpt2.py) gives the same logits and greedy
+    tokens on the reference's own src/core build as on the restatement."""
+    from oracle.gpt2 import GPT2Oracle
+    from sandyrt_amd.gpt2 import GPT2Config, prompt_ids, random_weights
+    cfg = GPT2Config(layers=2, hidden=128, heads=2, ffn=512, vocab=700, positions=32)
+    w = random_weights(cfg, seed=11)
+    p = prompt_ids(cfg, 6, seed=11)
+    a, b = GPT2Oracle(O.Oracle(), cfg, w), GPT2Oracle(O.Oracle(reference=True), cfg, w)
+    ids = p
+    for _ in range(3):
+        la, lb = a.forward(ids), b.forward(ids)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+        ids = [int(np.argmax(la))]
