@@ -6,11 +6,11 @@ One step = one pass of the hot path over one batch of synthetic input:
   BASELINE config 2 (TinyLlama-1.1B shape, 4096 tokens x 2048 hidden, bf16,
   inputs N(0,1), seed 1):
     1. residual add + RMSNorm        x, h [4096, 2048] -> x + h, rmsnorm(x + h) * w
-    2. RoPE (theta 1e4, split-half)  q [1, 32, 4096, 64]
-    3. RoPE                          k [1, 4, 4096, 64]
-    4. SiLU-gate group               silu(gate) * up, [4096, 2048] (hipRTC-generated)
+    2. RoPE (theta 1e4, split-half)  q [1, 32, 4096, 64] and k [1, 4, 4096, 64]
+                                     in one launch (sandy_hip_rope_pair)
+    3. SiLU-gate group               silu(gate) * up, [4096, 2048] (hipRTC-generated)
   BASELINE config 3 (paged decode, bf16 KV, block 16, seed 2):
-    5. decode attention, 32 sequences, ctx U[512, 4096], 32 q / 4 kv heads,
+    4. decode attention, 32 sequences, ctx U[512, 4096], 32 q / 4 kv heads,
        D 64, block table = random permutation of a 32768-block pool.
 
 Inputs are resident in HBM before timing.  Each kernel rotates over
@@ -96,7 +96,7 @@ def build_workload(replicas):
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     desc = _lib.desc
-    kernels = {k: [] for k in ("add_rms_norm", "rope_q", "rope_k", "silu_gate", "paged_decode")}
+    kernels = {k: [] for k in ("add_rms_norm", "rope_qk", "silu_gate", "paged_decode")}
     keep = []
     nodes, result = ops.silu_mul_nodes()
     cnodes = ops._nodes(nodes)
@@ -107,8 +107,7 @@ def build_workload(replicas):
     host = {}
     bytes_per = {
         "add_rms_norm": 4 * T * HID * 2 + HID * 2,
-        "rope_q": 2 * HQ * T * HD * 2,
-        "rope_k": 2 * HKV * T * HD * 2,
+        "rope_qk": 2 * (HQ + HKV) * T * HD * 2,
         "silu_gate": 3 * T * HID * 2,
         "paged_decode": int(ctx.sum()) * HKV * HD * 2 * 2 + 2 * DEC_B * HQ * HD * 2 + int(nblk.sum()) * 4,
     }
@@ -126,20 +125,14 @@ def build_workload(replicas):
             d.update({n: desc(t) for n, t in dict(x=x, h=h, w=w, s=s_out, y=y).items()})
             kernels["add_rms_norm"].append(Prepared("sandy_hip_add_rms_norm", d["x"], d["h"], d["w"],
                                                     C.c_double(1e-5), d["s"], d["y"]))
-        if rep < reps["rope_q"]:
+        if rep < reps["rope_qk"]:
             q = torch.randn(1, HQ, T, HD, generator=g, device=dev).to(bf)
-            q_out = torch.empty_like(q)
-            keep += [q, q_out]
-            d.update(q=desc(q), qo=desc(q_out))
-            kernels["rope_q"].append(Prepared("sandy_hip_rope", d["q"], None, C.c_double(1e4), C.c_int64(-1),
-                                              C.c_int32(1), d["qo"]))
-        if rep < reps["rope_k"]:
             k = torch.randn(1, HKV, T, HD, generator=g, device=dev).to(bf)
-            k_out = torch.empty_like(k)
-            keep += [k, k_out]
-            d.update(k=desc(k), ko=desc(k_out))
-            kernels["rope_k"].append(Prepared("sandy_hip_rope", d["k"], None, C.c_double(1e4), C.c_int64(-1),
-                                              C.c_int32(1), d["ko"]))
+            q_out, k_out = torch.empty_like(q), torch.empty_like(k)
+            keep += [q, q_out, k, k_out]
+            d.update(q=desc(q), qo=desc(q_out), k=desc(k), ko=desc(k_out))
+            kernels["rope_qk"].append(Prepared("sandy_hip_rope_pair", d["q"], d["k"], None, C.c_double(1e4),
+                                               C.c_int64(-1), C.c_int32(1), d["qo"], d["ko"]))
         if rep < reps["silu_gate"]:
             gate = torch.randn(T, HID, generator=g, device=dev).to(bf)
             up = torch.randn(T, HID, generator=g, device=dev).to(bf)

@@ -158,6 +158,16 @@ int sandy_hip_add_rms_norm(const SandyTensor* x, const SandyTensor* residual,
 int sandy_hip_rope(const SandyTensor* x, const SandyTensor* position_ids, double theta,
                    int64_t rotary_dim, int32_t split_half, const SandyTensor* out,
                    void* stream, char* err, size_t err_cap);
+/* RoPE of two tensors that share position_ids, sequence length and head dim
+ * (the q and k of one attention) in one launch: q_out / k_out are exactly
+ * what two sandy_hip_rope calls produce.  Per-vector position ids (numel ==
+ * vector count) fall back to one launch per tensor.  Fuses the program's two
+ * RoPEKernelOps (src/models/tinyllama/common.sandy.go:24-25, lowered by
+ * launch_cuda_rope, CudaKernels.h:109-159); the reference has no single
+ * counterpart. */
+int sandy_hip_rope_pair(const SandyTensor* q, const SandyTensor* k, const SandyTensor* position_ids, double theta,
+                        int64_t rotary_dim, int32_t split_half, const SandyTensor* q_out, const SandyTensor* k_out,
+                        void* stream, char* err, size_t err_cap);
 
 /* SoftmaxKernelOp (src/ir/KernelIR.h:494-515; replaces launch_cuda_softmax,
  * src/device/cuda/CudaSoftmaxKernels.cu:145-169).  Any axis. */

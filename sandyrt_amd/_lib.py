@@ -128,6 +128,7 @@ SIGNATURES = {
     "sandy_hip_norm": [C.c_int32, T, T, T, C.c_double, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_add_rms_norm": [T, T, T, C.c_double, T, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_rope": [T, T, C.c_double, C.c_int64, C.c_int32, T, C.c_void_p, ERR, C.c_size_t],
+    "sandy_hip_rope_pair": [T, T, T, C.c_double, C.c_int64, C.c_int32, T, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_softmax": [T, C.c_int64, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_reduce_sum": [T, C.c_int64, C.c_int32, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_gather": [T, T, T, C.c_void_p, ERR, C.c_size_t],

@@ -64,9 +64,9 @@ __device__ __forceinline__ int64_t rope_position(int mode, const void* ids, int3
 // branches cost 15% of the kernel's time).
 template <typename T, int U, bool FULL>
 __global__ __launch_bounds__(256) void rope_split_kernel(
-        const void* __restrict__ x, void* __restrict__ out, const void* __restrict__ ids, int32_t ids_dt, int mode,
-        int64_t seq, int64_t outer, int dim, int rot_pairs, int groups, int per_group, RopeArgs args,
-        uint32_t* errw) {
+        const void* __restrict__ x, void* __restrict__ out, const void* __restrict__ x2, void* __restrict__ out2,
+        int64_t outer_first, const void* __restrict__ ids, int32_t ids_dt, int mode, int64_t seq, int64_t outer,
+        int dim, int rot_pairs, int groups, int per_group, RopeArgs args, uint32_t* errw) {
     const int half = dim >> 1;
     const uint32_t chunks = static_cast<uint32_t>(half >> 3);
     // 32-bit index math (the host keeps seq * chunks * groups below 2^31):
@@ -91,9 +91,10 @@ __global__ __launch_bounds__(256) void rope_split_kernel(
 #pragma unroll
         for (int j = 0; j < U; j++) {
             if (FULL || o0 + j < o_end) {
-                const int64_t base = ((o0 + j) * seq + s) * dim;
-                ra_[j] = Vec8<T>::load_raw(x, base + c * 8);
-                rb_[j] = Vec8<T>::load_raw(x, base + half + c * 8);
+                const bool sec = o0 + j >= outer_first;
+                const int64_t base = ((o0 + j - (sec ? outer_first : 0)) * seq + s) * dim;
+                ra_[j] = Vec8<T>::load_raw(sec ? x2 : x, base + c * 8);
+                rb_[j] = Vec8<T>::load_raw(sec ? x2 : x, base + half + c * 8);
             }
         }
         if (fresh) {
@@ -107,7 +108,9 @@ __global__ __launch_bounds__(256) void rope_split_kernel(
 #pragma unroll
         for (int j = 0; j < U; j++) {
             if (!FULL && o0 + j >= o_end) break;
-            const int64_t base = ((o0 + j) * seq + s) * dim;
+            const bool sec = o0 + j >= outer_first;
+            const int64_t base = ((o0 + j - (sec ? outer_first : 0)) * seq + s) * dim;
+            void* dst = sec ? out2 : out;
             float a[8], b[8], ra[8], rb[8];
             Vec8<T>::unpack(ra_[j], a);
             Vec8<T>::unpack(rb_[j], b);
@@ -122,8 +125,8 @@ __global__ __launch_bounds__(256) void rope_split_kernel(
                     rb[i] = b[i];
                 }
             }
-            Vec8<T>::store(out, base + c * 8, ra);
-            Vec8<T>::store(out, base + half + c * 8, rb);
+            Vec8<T>::store(dst, base + c * 8, ra);
+            Vec8<T>::store(dst, base + half + c * 8, rb);
         }
     }
 }
@@ -132,9 +135,9 @@ __global__ __launch_bounds__(256) void rope_split_kernel(
 // FULL as for the split-half kernel.
 template <typename T, int U, bool FULL>
 __global__ __launch_bounds__(256) void rope_interleaved_kernel(
-        const void* __restrict__ x, void* __restrict__ out, const void* __restrict__ ids, int32_t ids_dt, int mode,
-        int64_t seq, int64_t outer, int dim, int rot_pairs, int groups, int per_group, RopeArgs args,
-        uint32_t* errw) {
+        const void* __restrict__ x, void* __restrict__ out, const void* __restrict__ x2, void* __restrict__ out2,
+        int64_t outer_first, const void* __restrict__ ids, int32_t ids_dt, int mode, int64_t seq, int64_t outer,
+        int dim, int rot_pairs, int groups, int per_group, RopeArgs args, uint32_t* errw) {
     const uint32_t chunks = static_cast<uint32_t>(dim >> 3);
     const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= static_cast<uint32_t>(seq) * chunks * static_cast<uint32_t>(groups)) return;
@@ -152,7 +155,10 @@ __global__ __launch_bounds__(256) void rope_interleaved_kernel(
         typename Vec8<T>::raw raw_[U];
 #pragma unroll
         for (int j = 0; j < U; j++)
-            if (FULL || o0 + j < o_end) raw_[j] = Vec8<T>::load_raw(x, ((o0 + j) * seq + s) * dim + c * 8);
+            if (FULL || o0 + j < o_end) {
+                const bool sec = o0 + j >= outer_first;
+                raw_[j] = Vec8<T>::load_raw(sec ? x2 : x, ((o0 + j - (sec ? outer_first : 0)) * seq + s) * dim + c * 8);
+            }
         if (fresh) {
             const float fp = static_cast<float>(pos);
 #pragma unroll
@@ -177,7 +183,8 @@ __global__ __launch_bounds__(256) void rope_interleaved_kernel(
                     r[2 * i + 1] = a[2 * i + 1];
                 }
             }
-            Vec8<T>::store(out, ((o0 + j) * seq + s) * dim + c * 8, r);
+            const bool sec = o0 + j >= outer_first;
+            Vec8<T>::store(sec ? out2 : out, ((o0 + j - (sec ? outer_first : 0)) * seq + s) * dim + c * 8, r);
         }
     }
 }
@@ -235,39 +242,56 @@ __global__ __launch_bounds__(256) void rope_generic_kernel(
 
 using namespace sandy_hip;
 
-extern "C" int sandy_hip_rope(const SandyTensor* x, const SandyTensor* position_ids, double theta,
-                              int64_t rotary_dim, int32_t split_half, const SandyTensor* out,
-                              void* stream_, char* err, size_t err_cap) {
-    Err e{err, err_cap};
-    hipStream_t stream = static_cast<hipStream_t>(stream_);
+namespace sandy_hip {
+namespace {
+
+struct RopeShape {
+    int64_t seq, dim, total, vectors, outer;
+};
+
+// Validation shared by both entry points; fills the shape of x.
+int rope_check(const SandyTensor* x, const SandyTensor* out, RopeShape& sh, Err e) {
     if (!valid_rank(x) || !valid_rank(out)) return fail(e, SANDY_ERR_INVALID, "rope tensor rank out of range");
     if (!is_float(x->dtype)) return fail(e, SANDY_ERR_INVALID, "rope input unsupported dtype");
     if (!same_shape(*x, *out)) return fail(e, SANDY_ERR_INVALID, "rope output shape mismatch");
     if (out->dtype != x->dtype) return fail(e, SANDY_ERR_INVALID, "rope output dtype mismatch");
+    if (x->rank < 2) return fail(e, SANDY_ERR_INVALID, "rope input must have rank >= 2");
+    sh.seq = x->dims[x->rank - 2];
+    sh.dim = x->dims[x->rank - 1];
+    if (sh.dim <= 0 || sh.dim % 2 != 0) return fail(e, SANDY_ERR_INVALID, "rope last dimension must be positive and even");
+    sh.total = numel(*x);
+    sh.vectors = sh.total / sh.dim;
+    sh.outer = sh.seq ? sh.vectors / sh.seq : 0;
+    return SANDY_OK;
+}
+
+// RoPE of n = 1 or 2 tensors sharing the positions, sequence length and head
+// dim (checked by the caller); the fast kernels take both in one launch.
+int rope_run(const SandyTensor* const* xs, const SandyTensor* const* outs, int n, const SandyTensor* position_ids,
+             double theta, int64_t rotary_dim, int32_t split_half, hipStream_t stream, Err e) {
+    RopeShape sh[2];
+    for (int i = 0; i < n; i++) {
+        const int st = rope_check(xs[i], outs[i], sh[i], e);
+        if (st) return st;
+    }
     if (position_ids && !is_index(position_ids->dtype))
         return fail(e, SANDY_ERR_INVALID, "rope position_ids must be i32 or i64");
-    if (x->rank < 2) return fail(e, SANDY_ERR_INVALID, "rope input must have rank >= 2");
     const float th = static_cast<float>(theta);
     if (th <= 0.0f) return fail(e, SANDY_ERR_INVALID, "rope theta must be > 0");
-    const int64_t seq = x->dims[x->rank - 2];
-    const int64_t dim = x->dims[x->rank - 1];
-    if (dim <= 0 || dim % 2 != 0) return fail(e, SANDY_ERR_INVALID, "rope last dimension must be positive and even");
+    const int64_t seq = sh[0].seq, dim = sh[0].dim;
     if (rotary_dim < 0) rotary_dim = dim;
     if (rotary_dim <= 0 || rotary_dim % 2 != 0) return fail(e, SANDY_ERR_INVALID, "rope rotary_dim must be positive and even");
     if (rotary_dim > dim) return fail(e, SANDY_ERR_INVALID, "rope rotary_dim must be <= last dimension");
     if (rotary_dim / 2 > kMaxPairs) return fail(e, SANDY_ERR_UNSUPPORTED, "rope rotary_dim above %d", 2 * kMaxPairs);
-    const int64_t total = numel(*x);
-    if (total == 0) return ok(e);
-    const int64_t vectors = total / dim;
-    const int64_t outer = seq ? vectors / seq : 0;
-    int mode = 0;
-    if (position_ids) {
+    int mode[2] = {0, 0};
+    for (int i = 0; i < n; i++) {
+        if (!position_ids) continue;
         const int64_t cnt = numel(*position_ids);
-        if (cnt != 1 && cnt != seq && cnt != vectors)
+        if (cnt != 1 && cnt != seq && cnt != sh[i].vectors)
             return fail(e, SANDY_ERR_INVALID, "rope position_ids numel must be 1, sequence length, or vector count");
         if (!contiguous(*position_ids)) return fail(e, SANDY_ERR_UNSUPPORTED, "rope position_ids must be contiguous");
-        mode = cnt == 1 ? 1 : (cnt == vectors ? 3 : 2);
-        if (mode == 3 && outer == 1) mode = 2;  // ids[v] == ids[v % seq] when there is one sequence
+        mode[i] = cnt == 1 ? 1 : (cnt == sh[i].vectors && cnt != seq ? 3 : 2);
+        if (mode[i] == 3 && sh[i].outer == 1) mode[i] = 2;  // ids[v] == ids[v % seq] when there is one sequence
     }
     RopeArgs args;
     const int rot_pairs = static_cast<int>(rotary_dim / 2);
@@ -278,18 +302,27 @@ extern "C" int sandy_hip_rope(const SandyTensor* x, const SandyTensor* position_
     if (status) return status;
     const void* ids = position_ids ? base_ptr(*position_ids) : nullptr;
     const int32_t ids_dt = position_ids ? position_ids->dtype : SANDY_I64;
-    const void* px = base_ptr(*x);
-    void* po = base_ptr(*out);
-    const bool bf = x->dtype == SANDY_BF16;
-    const bool aligned = ((reinterpret_cast<uintptr_t>(px) | reinterpret_cast<uintptr_t>(po)) & 15u) == 0;
-    bool fast = contiguous(*x) && contiguous(*out) && aligned && dim <= 2 * kMaxPairs * 2 &&
-                      (split_half ? (dim / 2) % 8 == 0 : dim % 8 == 0);
+    const bool bf = xs[0]->dtype == SANDY_BF16;
+    // one launch over both tensors' heads when both take the fast kernels with
+    // one position rule (per-vector ids differ between the tensors)
+    bool fast = n == 1 || (mode[0] == mode[1] && mode[0] != 3);
+    int64_t total = 0, outer = 0;
+    for (int i = 0; i < n; i++) {
+        const void* px = base_ptr(*xs[i]);
+        const void* po = base_ptr(*outs[i]);
+        const bool aligned = ((reinterpret_cast<uintptr_t>(px) | reinterpret_cast<uintptr_t>(po)) & 15u) == 0;
+        fast = fast && contiguous(*xs[i]) && contiguous(*outs[i]) && aligned &&
+               (split_half ? (dim / 2) % 8 == 0 : dim % 8 == 0);
+        total += sh[i].total;
+        outer += sh[i].outer;
+    }
+    if (total == 0) return ok(e);
     int groups = 1, per = 1;
     int64_t threads = 0;
     if (fast) {
         const int chunks = static_cast<int>(split_half ? dim / 16 : dim / 8);
         const int64_t base_threads = seq * chunks;
-        if (mode == 3) {
+        if (mode[0] == 3) {
             groups = static_cast<int>(outer);
         } else {
             // threads (each reusing its sincos over `per` heads): numel / 32 within
@@ -297,6 +330,12 @@ extern "C" int sandy_hip_rope(const SandyTensor* x, const SandyTensor* position_
             const int64_t want = std::min<int64_t>(131072, std::max<int64_t>(32768, total / 32));
             groups = static_cast<int>(std::min<int64_t>(outer, std::max<int64_t>(1, want / std::max<int64_t>(1, base_threads))));
             per = static_cast<int>((outer + groups - 1) / groups);
+            // prefer a head count per group that divides the heads (unguarded kernel)
+            for (int d = per; d > 1 && d * 2 > per; d--)
+                if (outer % d == 0) {
+                    per = d;
+                    break;
+                }
             groups = static_cast<int>((outer + per - 1) / per);
         }
         threads = base_threads * groups;
@@ -304,12 +343,18 @@ extern "C" int sandy_hip_rope(const SandyTensor* x, const SandyTensor* position_
     }
     if (fast) {
         dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+        const void* px = base_ptr(*xs[0]);
+        void* po = base_ptr(*outs[0]);
+        const void* px2 = n == 2 ? base_ptr(*xs[1]) : px;
+        void* po2 = n == 2 ? base_ptr(*outs[1]) : po;
+        const int64_t outer_first = sh[0].outer;
+        const int md = mode[0];
         // up to four heads' loads in flight per thread (mode 3 has one head per group)
         const int u = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
         const bool full = outer % per == 0 && per % u == 0 && rot_pairs == dim / 2;
 #define SANDY_ROPE_LAUNCH(KERNEL, T, U, F)                                                                        \
-    hipLaunchKernelGGL((KERNEL<T, U, F>), grid, dim3(256), 0, stream, px, po, ids, ids_dt, mode, seq, outer,     \
-                       static_cast<int>(dim), rot_pairs, groups, per, args, errw)
+    hipLaunchKernelGGL((KERNEL<T, U, F>), grid, dim3(256), 0, stream, px, po, px2, po2, outer_first, ids, ids_dt, \
+                       md, seq, outer, static_cast<int>(dim), rot_pairs, groups, per, args, errw)
 #define SANDY_ROPE_F(KERNEL, T, U)                                 \
     do {                                                           \
         if (full) SANDY_ROPE_LAUNCH(KERNEL, T, U, true);           \
@@ -332,18 +377,50 @@ extern "C" int sandy_hip_rope(const SandyTensor* x, const SandyTensor* position_
 #undef SANDY_ROPE_F
 #undef SANDY_ROPE_LAUNCH
     } else {
-        Strided st{};
-        st.rank = x->rank;
-        for (int i = 0; i < x->rank; i++) {
-            st.dims[i] = x->dims[i];
-            st.xs[i] = x->strides[i];
-            st.os[i] = out->strides[i];
+        for (int i = 0; i < n; i++) {
+            if (sh[i].total == 0) continue;
+            const SandyTensor* x = xs[i];
+            const SandyTensor* out = outs[i];
+            Strided st{};
+            st.rank = x->rank;
+            for (int d = 0; d < x->rank; d++) {
+                st.dims[d] = x->dims[d];
+                st.xs[d] = x->strides[d];
+                st.os[d] = out->strides[d];
+            }
+            const int64_t t = sh[i].vectors * (dim / 2);
+            dim3 grid(static_cast<unsigned>((t + 255) / 256));
+            hipLaunchKernelGGL(rope_generic_kernel, grid, dim3(256), 0, stream, base_ptr(*x), x->dtype, base_ptr(*out),
+                               ids, ids_dt, mode[i], seq, sh[i].vectors, static_cast<int>(dim), rot_pairs,
+                               split_half ? 1 : 0, st, args, errw);
         }
-        const int64_t threads = vectors * (dim / 2);
-        dim3 grid(static_cast<unsigned>((threads + 255) / 256));
-        hipLaunchKernelGGL(rope_generic_kernel, grid, dim3(256), 0, stream, px, x->dtype, po, ids, ids_dt, mode, seq,
-                           vectors, static_cast<int>(dim), rot_pairs, split_half ? 1 : 0, st, args, errw);
     }
     SANDY_HIP_TRY(hipGetLastError(), e, "rope launch");
     return ok(e);
+}
+
+} // namespace
+} // namespace sandy_hip
+
+extern "C" int sandy_hip_rope(const SandyTensor* x, const SandyTensor* position_ids, double theta,
+                              int64_t rotary_dim, int32_t split_half, const SandyTensor* out,
+                              void* stream_, char* err, size_t err_cap) {
+    const SandyTensor* xs[1] = {x};
+    const SandyTensor* outs[1] = {out};
+    return rope_run(xs, outs, 1, position_ids, theta, rotary_dim, split_half, static_cast<hipStream_t>(stream_),
+                    Err{err, err_cap});
+}
+
+extern "C" int sandy_hip_rope_pair(const SandyTensor* q, const SandyTensor* k, const SandyTensor* position_ids,
+                                   double theta, int64_t rotary_dim, int32_t split_half, const SandyTensor* q_out,
+                                   const SandyTensor* k_out, void* stream_, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    if (!valid_rank(q) || !valid_rank(k)) return fail(e, SANDY_ERR_INVALID, "rope tensor rank out of range");
+    if (q->dtype != k->dtype) return fail(e, SANDY_ERR_INVALID, "rope pair inputs must have one dtype");
+    if (q->rank < 2 || k->rank < 2 || q->dims[q->rank - 1] != k->dims[k->rank - 1] ||
+        q->dims[q->rank - 2] != k->dims[k->rank - 2])
+        return fail(e, SANDY_ERR_INVALID, "rope pair inputs must share sequence length and last dimension");
+    const SandyTensor* xs[2] = {q, k};
+    const SandyTensor* outs[2] = {q_out, k_out};
+    return rope_run(xs, outs, 2, position_ids, theta, rotary_dim, split_half, static_cast<hipStream_t>(stream_), e);
 }

@@ -72,6 +72,18 @@ def rope(x, theta: float, rotary_dim: int = -1, split_half: bool = False, positi
     return out
 
 
+def rope_pair(q, k, theta: float, rotary_dim: int = -1, split_half: bool = False, position_ids=None, q_out=None,
+              k_out=None):
+    """RoPE of q and k (same positions, sequence length and head dim) in one
+    launch; identical to rope(q) and rope(k)."""
+    _require_gpu(q, k, position_ids)
+    q_out = torch.empty_like(q) if q_out is None else q_out
+    k_out = torch.empty_like(k) if k_out is None else k_out
+    call("sandy_hip_rope_pair", desc(q), desc(k), desc(position_ids), float(theta), int(rotary_dim),
+         int(bool(split_half)), desc(q_out), desc(k_out))
+    return q_out, k_out
+
+
 def softmax(x, axis: int = -1, out=None):
     """SoftmaxKernelOp (src/core/TensorCalc.cpp:1337-1399)."""
     _require_gpu(x)

@@ -188,3 +188,50 @@ def test_embedding_bad_id_sets_device_error(ops):
     ops.embedding(torch.tensor([0, 4], device="cuda"), w)
     with pytest.raises(SandyError, match="embedding id out of range"):
         ops.check_device_errors()
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("ids_kind", [None, "offset", "seq"])
+def test_rope_pair_matches_two_single_calls(ops, dtype, split, ids_kind):
+    """rope_pair(q, k) == rope(q), rope(k) bit for bit: one launch over both
+    tensors' heads (per-vector ids: one launch per tensor)."""
+    r = rng(17)
+    q = from_f32(normal(r, (2, 8, 6, 64)), dtype)
+    k = from_f32(normal(r, (2, 2, 6, 64)), dtype)
+    ids = {None: None, "offset": torch.tensor([40], device="cuda"),
+           "seq": torch.tensor([3, 9, 1, 4000, 7, 0], device="cuda")}[ids_kind]
+    qo, ko = ops.rope_pair(q, k, 1e4, split_half=split, position_ids=ids)
+    assert torch.equal(qo, ops.rope(q, 1e4, split_half=split, position_ids=ids))
+    assert torch.equal(ko, ops.rope(k, 1e4, split_half=split, position_ids=ids))
+
+
+def test_rope_pair_config2_shapes_and_fallback(ops, oracle):
+    """BASELINE config 2's q [1,32,4096,64] and k [1,4,4096,64] in one launch
+    against the oracle; unaligned views take the general kernel per tensor,
+    and so do per-vector position ids (they differ between q and k)."""
+    r = rng(18)
+    q = from_f32(normal(r, (1, 32, 4096, 64)), torch.bfloat16)
+    k = from_f32(normal(r, (1, 4, 4096, 64)), torch.bfloat16)
+    qo, ko = ops.rope_pair(q, k, 1e4, split_half=True)
+    assert_close(qo, oracle.rope(to_oracle(q), 1e4, split_half=True), torch.bfloat16, "q")
+    assert_close(ko, oracle.rope(to_oracle(k), 1e4, split_half=True), torch.bfloat16, "k")
+    qs, ks = q[:, :, 1:], k[:, :, 1:]  # strided views
+    qo2, ko2 = ops.rope_pair(qs, ks, 1e4, split_half=True)
+    assert torch.equal(qo2, ops.rope(qs, 1e4, split_half=True))
+    assert torch.equal(ko2, ops.rope(ks, 1e4, split_half=True))
+    # per-vector ids (q and k with equal vector counts): one launch per tensor
+    qv, kv = q[:, :4, :5].contiguous(), k[:, :, :5].contiguous()
+    ids = torch.arange(20, device="cuda") * 37
+    qo3, ko3 = ops.rope_pair(qv, kv, 1e4, split_half=True, position_ids=ids)
+    assert torch.equal(qo3, ops.rope(qv, 1e4, split_half=True, position_ids=ids))
+    assert torch.equal(ko3, ops.rope(kv, 1e4, split_half=True, position_ids=ids))
+
+
+def test_rope_pair_rejects_mismatched_tensors(ops):
+    from sandyrt_amd._lib import SandyError
+    q = torch.zeros(1, 4, 8, 64, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(SandyError, match="must share sequence length and last dimension"):
+        ops.rope_pair(q, torch.zeros(1, 2, 8, 32, dtype=torch.bfloat16, device="cuda"), 1e4)
+    with pytest.raises(SandyError, match="must have one dtype"):
+        ops.rope_pair(q, torch.zeros(1, 2, 8, 64, dtype=torch.float32, device="cuda"), 1e4)
