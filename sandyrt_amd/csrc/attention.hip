@@ -734,23 +734,32 @@ struct GenArgs {
     uint32_t* errw;
 };
 
-template <typename T>
-__device__ __forceinline__ float kv_load(const GenArgs& a, const void* base, const int64_t* st, int b, int kh,
-                                         int64_t key, int64_t d, bool& ok) {
-    if (!a.paged) return Vec8<T>::load1(base, b * st[0] + kh * st[1] + key * st[2] + d * st[3]);
+// Element offset of row (b, kh, key) of K or V and its head-dim stride;
+// a paged key whose block id is outside the pool clears `ok` (offset 0).
+__device__ __forceinline__ int64_t kv_row(const GenArgs& a, const int64_t* st, int b, int kh, int64_t key, bool& ok) {
+    if (!a.paged) return b * st[0] + kh * st[1] + key * st[2];
     const int64_t page = key / a.page_size;
     const int32_t blk = a.table[b * a.table_stride + page];
     if (blk < 0 || blk >= a.num_pages) {
         ok = false;
-        return 0.0f;
+        return 0;
     }
-    return Vec8<T>::load1(base, static_cast<int64_t>(blk) * a.page_elems + (kh * a.page_size + key % a.page_size) * a.d + d);
+    return static_cast<int64_t>(blk) * a.page_elems + (kh * a.page_size + key % a.page_size) * a.d;
 }
 
+// The reference's algorithm per (query, head, batch), in its operation order:
+// float scores q.k summed over d in order, times scale; masked keys -inf; max;
+// a double sum of exp(s - max); out[d] = sum over unmasked keys in order of
+// (expf(s - max) * (1 / (float)sum)) * v[key][d].  The order is kept, the
+// latency is not: q sits in LDS, each key's row address is computed once,
+// and K / V values are loaded 16 at a time ahead of the in-order sums (a
+// masked key adds an exact +0.0 through a select instead of a branch).
 template <typename T>
 __global__ __launch_bounds__(256) void attention_general_kernel(GenArgs a) {
+    constexpr int kU = 16;
     __shared__ float fred[4];
     __shared__ double dred[4];
+    __shared__ float qv[512];
     const int qi = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
     const int kh = h / (a.hq / a.hkv);
@@ -765,17 +774,29 @@ __global__ __launch_bounds__(256) void attention_general_kernel(GenArgs a) {
     const int64_t qpos = base_pos + qi;
     const int64_t min_key = a.window > 0 ? max<int64_t>(0, qpos + 1 - a.window) : 0;
     const int64_t tk = a.tk;
+    const int64_t D = a.d;
     float* sc = a.scores + ((static_cast<int64_t>(b) * a.hq + h) * a.tq + qi) * tk;
     const int64_t qoff = b * a.qs[0] + h * a.qs[1] + qi * a.qs[2];
+    for (int64_t d = tid; d < D; d += 256) qv[d] = Vec8<T>::load1(a.q, qoff + d * a.qs[3]);
+    __syncthreads();
+    const int64_t kd = a.paged ? 1 : a.ks[3];
+    const int64_t vd = a.paged ? 1 : a.vs[3];
     float lmax = -INFINITY;
     bool ok = true;
     for (int64_t key = tid; key < tk; key += 256) {
         float s = -INFINITY;
         if (key <= qpos && key >= min_key) {
+            const int64_t row = kv_row(a, a.ks, b, kh, key, ok);
             float acc = 0.0f;
-            for (int64_t d = 0; d < a.d; d++)
-                acc = __fadd_rn(acc, __fmul_rn(Vec8<T>::load1(a.q, qoff + d * a.qs[3]),
-                                               kv_load<T>(a, a.k, a.ks, b, kh, key, d, ok)));
+            int64_t d = 0;
+            for (; d + kU <= D; d += kU) {
+                float kv[kU];
+#pragma unroll
+                for (int j = 0; j < kU; j++) kv[j] = Vec8<T>::load1(a.k, row + (d + j) * kd);
+#pragma unroll
+                for (int j = 0; j < kU; j++) acc = __fadd_rn(acc, __fmul_rn(qv[d + j], kv[j]));
+            }
+            for (; d < D; d++) acc = __fadd_rn(acc, __fmul_rn(qv[d], Vec8<T>::load1(a.k, row + d * kd)));
             s = __fmul_rn(acc, a.scale);
         }
         sc[key] = s;
@@ -788,7 +809,7 @@ __global__ __launch_bounds__(256) void attention_general_kernel(GenArgs a) {
     const float mx = fmaxf(fmaxf(fred[0], fred[1]), fmaxf(fred[2], fred[3]));
     const int64_t ooff = b * a.os[0] + h * a.os[1] + qi * a.os[2];
     if (mx == -INFINITY) {
-        for (int64_t d = tid; d < a.d; d += 256) Vec8<T>::store1(a.out, ooff + d * a.os[3], 0.0f);
+        for (int64_t d = tid; d < D; d += 256) Vec8<T>::store1(a.out, ooff + d * a.os[3], 0.0f);
         return;
     }
     double sum = 0.0;
@@ -797,15 +818,26 @@ __global__ __launch_bounds__(256) void attention_general_kernel(GenArgs a) {
     if ((tid & 63) == 0) dred[tid >> 6] = sum;
     __syncthreads();
     const double total = dred[0] + dred[1] + dred[2] + dred[3];
-    for (int64_t d = tid; d < a.d; d += 256) {
+    const float inv = total != 0.0 ? 1.0f / static_cast<float>(total) : 0.0f;
+    // keys past the query's position or below the window are masked for every d
+    const int64_t k_end = min<int64_t>(tk, qpos + 1);
+    for (int64_t d = tid; d < D; d += 256) {
         float acc = 0.0f;
         if (total != 0.0) {
-            const float inv = 1.0f / static_cast<float>(total);
-            for (int64_t key = 0; key < tk; key++) {
-                const float s = sc[key];
-                if (s == -INFINITY) continue;
-                const float prob = __fmul_rn(expf(__fsub_rn(s, mx)), inv);
-                acc = __fadd_rn(acc, __fmul_rn(prob, kv_load<T>(a, a.v, a.vs, b, kh, key, d, ok)));
+            for (int64_t k0 = min_key; k0 < k_end; k0 += kU) {
+                float vv[kU], sv[kU];
+#pragma unroll
+                for (int j = 0; j < kU; j++) {
+                    const int64_t key = k0 + j;
+                    sv[j] = key < k_end ? sc[key] : -INFINITY;
+                    vv[j] = 0.0f;
+                    if (sv[j] != -INFINITY) vv[j] = Vec8<T>::load1(a.v, kv_row(a, a.vs, b, kh, key, ok) + d * vd);
+                }
+#pragma unroll
+                for (int j = 0; j < kU; j++) {
+                    const float prob = __fmul_rn(expf(__fsub_rn(sv[j], mx)), inv);
+                    acc = __fadd_rn(acc, sv[j] == -INFINITY ? 0.0f : __fmul_rn(prob, vv[j]));
+                }
             }
         }
         Vec8<T>::store1(a.out, ooff + d * a.os[3], acc);
@@ -845,6 +877,7 @@ extern "C" int sandy_hip_attention(const SandyTensor* q, const SandyTensor* k, c
     if (k->dims[o + 2] != D || v->dims[o + 2] != D) return fail(e, SANDY_ERR_INVALID, "attention head dimension mismatch");
     if (hq <= 0 || hkv <= 0 || hq % hkv != 0) return fail(e, SANDY_ERR_INVALID, "attention heads must be divisible by kv_heads");
     if (!same_shape(*q, *out) || out->dtype != q->dtype) return fail(e, SANDY_ERR_INVALID, "attention output shape mismatch");
+    if (D > 512) return fail(e, SANDY_ERR_UNSUPPORTED, "attention head dimension above 512");
     if (position_offsets) {
         if (!is_index(position_offsets->dtype)) return fail(e, SANDY_ERR_INVALID, "attention position_offsets must be i32 or i64");
         const int64_t n = numel(*position_offsets);
@@ -1007,6 +1040,7 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         SANDY_HIP_TRY(hipGetLastError(), e, "paged attention launch");
         return ok(e);
     }
+    if (D > 512) return fail(e, SANDY_ERR_UNSUPPORTED, "attention head dimension above 512");
     GenArgs a{};
     a.q = base_ptr(*q);
     for (int i = 0; i < 4; i++) {

@@ -502,55 +502,105 @@ struct Plan {
 };
 
 // f32 products of a few rows against a weight read as [n, k] (linear, and
-// matmul with transpose_rhs): lane = one output column, which walks k in the
-// reference's order (acc = bias, then acc + x * w rounded at each step, no
-// contraction), so results stay bit-identical to the CPU path.  The weight
-// row of each lane streams in 8-float chunks with Q chunks in flight; the x
-// values are the same for every lane.  One wave per workgroup spreads even a
-// 768-column output over 12 CUs.
+// matmul with transpose_rhs).  Each output column walks k in the reference's
+// order (acc = bias, then acc + x * w rounded at each step, no contraction),
+// so results stay bit-identical to the CPU path.  A wave owns 16 output
+// columns: it loads their weight rows 32 k at a time as whole 128-byte lines
+// (8 lanes per line, Q chunks in flight) into an LDS tile, and lanes 0..15
+// then walk their row in order.  Per-lane row streams (64 distinct lines per
+// load instruction) were bound by the CU's outstanding misses (59 us for
+// 768 x 768); 16 columns per wave also spreads a 768-column output over 48
+// CUs.  The activation rows are staged in LDS per block of k.
 template <int MR, int Q>
 __global__ __launch_bounds__(64) void gemv_seq_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                      const float* __restrict__ bias, float* __restrict__ out,
                                                      int64_t M, int64_t N, int64_t K, BatchMap bm) {
-    const int64_t n = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
+    constexpr int kCols = 16;  // output columns per wave
+    constexpr int kXs = 8192;  // activation floats staged in LDS per block of k
+    constexpr int kRow = 33;   // tile row stride in floats (conflict-free column walks)
+    __shared__ float xs[kXs];
+    __shared__ float tile[kCols * kRow];
+    const int lane = threadIdx.x;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kCols;
+    const int64_t n = n0 + lane;
     const int64_t bz = blockIdx.z;
     int64_t lo, ro;
     batch_offsets(bm, bz, lo, ro);
-    const bool live = n < N;
-    const float* wr = w + ro + (live ? n : 0) * K;
+    const bool live = lane < kCols && n < N;
     const float* xr = x + lo;
+    // this lane's two 16-byte pieces of each chunk: rows (lane / 8) and 8 + (lane / 8), piece lane % 8
+    const int prow[2] = {lane >> 3, 8 + (lane >> 3)};
+    const float* wrow[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) wrow[i] = w + ro + min<int64_t>(n0 + prow[i], N - 1) * K + (lane & 7) * 4;
     float acc[MR];
     const float b0 = bias && live ? bias[n] : 0.0f;
 #pragma unroll
     for (int r = 0; r < MR; r++) acc[r] = b0;
-    const int64_t nch = K / 8;
+    const int64_t kb_len = max<int64_t>(32, (kXs / M) & ~int64_t(31));
     float4 buf[Q][2];
-    auto load = [&](int64_t c, int slot) {
-        const float4* p = reinterpret_cast<const float4*>(wr + c * 8);
-        buf[slot][0] = p[0];
-        buf[slot][1] = p[1];
-    };
-    auto step = [&](int64_t k, float wv) {
-#pragma unroll
-        for (int r = 0; r < MR; r++)
-            if (r < M) acc[r] = __fadd_rn(acc[r], __fmul_rn(xr[r * K + k], wv));
-    };
-#pragma unroll
-    for (int q = 0; q < Q; q++)
-        if (q < nch) load(q, q);
-    for (int64_t c0 = 0; c0 < nch; c0 += Q) {
-#pragma unroll
-        for (int q = 0; q < Q; q++) {
-            const int64_t c = c0 + q;
-            if (c >= nch) break;
-            const float wv[8] = {buf[q][0].x, buf[q][0].y, buf[q][0].z, buf[q][0].w,
-                                 buf[q][1].x, buf[q][1].y, buf[q][1].z, buf[q][1].w};
-            if (c + Q < nch) load(c + Q, q);
-#pragma unroll
-            for (int j = 0; j < 8; j++) step(c * 8 + j, wv[j]);
+    for (int64_t kb = 0; kb < K; kb += kb_len) {
+        const int64_t len = min(kb_len, K - kb);
+        __syncthreads();  // the previous block's reads of xs are done
+        for (int64_t j = lane; j < M * len; j += 64) {
+            const int64_t r = j / len, kk = j - r * len;
+            xs[r * len + kk] = xr[r * K + kb + kk];
         }
+        __syncthreads();
+        const int64_t nch = len / 32;
+        auto load = [&](int64_t c, int slot) {
+#pragma unroll
+            for (int i = 0; i < 2; i++) buf[slot][i] = *reinterpret_cast<const float4*>(wrow[i] + kb + c * 32);
+        };
+#pragma unroll
+        for (int q = 0; q < Q; q++)
+            if (q < nch) load(q, q);
+        for (int64_t c0 = 0; c0 < nch; c0 += Q) {
+#pragma unroll
+            for (int q = 0; q < Q; q++) {
+                const int64_t c = c0 + q;
+                if (c >= nch) break;
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    float* t = tile + prow[i] * kRow + (lane & 7) * 4;
+                    t[0] = buf[q][i].x;
+                    t[1] = buf[q][i].y;
+                    t[2] = buf[q][i].z;
+                    t[3] = buf[q][i].w;
+                }
+                if (c + Q < nch) load(c + Q, q);
+                __syncthreads();
+                if (lane < kCols) {
+                    // every LDS read is unconditional (rows past M read row M - 1), so the
+                    // compiler issues them ahead of the in-order chain; only the
+                    // accumulate is selected
+                    const float* trow = tile + lane * kRow;
+                    float wv[32];
+#pragma unroll
+                    for (int j = 0; j < 32; j++) wv[j] = trow[j];
+#pragma unroll
+                    for (int r = 0; r < MR; r++) {
+                        const float* xc = xs + min<int64_t>(r, M - 1) * len + c * 32;
+                        float xv[32];
+#pragma unroll
+                        for (int j = 0; j < 32; j++) xv[j] = xc[j];
+                        float a_r = acc[r];
+#pragma unroll
+                        for (int j = 0; j < 32; j++) a_r = __fadd_rn(a_r, __fmul_rn(xv[j], wv[j]));
+                        acc[r] = r < M ? a_r : acc[r];
+                    }
+                }
+                __syncthreads();  // the tile is rewritten by the next chunk
+            }
+        }
+        if (live)  // k tail past the 32-wide chunks, in order
+            for (int64_t kk = nch * 32; kk < len; kk++) {
+                const float wv = w[ro + n * K + kb + kk];
+#pragma unroll
+                for (int r = 0; r < MR; r++)
+                    if (r < M) acc[r] = __fadd_rn(acc[r], __fmul_rn(xs[r * len + kk], wv));
+            }
     }
-    for (int64_t k = nch * 8; k < K; k++) step(k, wr[k]);
     if (!live) return;
 #pragma unroll
     for (int r = 0; r < MR; r++)
@@ -622,16 +672,16 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
     const bool gemv = l.dtype == SANDY_F32 && !tl && tr && p.M <= 8 && p.K % 4 == 0 && aligned &&
                       p.lrs == p.K && p.rrs == p.K && env_int("SANDY_GEMM_SIMT", 0) == 0;
     if (gemv) {
-        const int64_t blocks = (p.N + 63) / 64;
+        const int64_t blocks = (p.N + 15) / 16;
         if (blocks > 0x7fffffff) return fail(e, SANDY_ERR_UNSUPPORTED, "%s shape exceeds the launch grid", what);
         const dim3 grid(static_cast<unsigned>(blocks), 1, static_cast<unsigned>(p.batches));
         const float* x = static_cast<const float*>(pl);
         const float* w = static_cast<const float*>(pr);
         const float* b = static_cast<const float*>(pb);
         float* y = static_cast<float*>(po);
-        if (p.M == 1) hipLaunchKernelGGL((gemv_seq_kernel<1, 16>), grid, dim3(64), 0, stream, x, w, b, y, p.M, p.N, p.K, p.bm);
-        else if (p.M <= 2) hipLaunchKernelGGL((gemv_seq_kernel<2, 16>), grid, dim3(64), 0, stream, x, w, b, y, p.M, p.N, p.K, p.bm);
-        else if (p.M <= 4) hipLaunchKernelGGL((gemv_seq_kernel<4, 12>), grid, dim3(64), 0, stream, x, w, b, y, p.M, p.N, p.K, p.bm);
+        if (p.M == 1) hipLaunchKernelGGL((gemv_seq_kernel<1, 8>), grid, dim3(64), 0, stream, x, w, b, y, p.M, p.N, p.K, p.bm);
+        else if (p.M <= 2) hipLaunchKernelGGL((gemv_seq_kernel<2, 8>), grid, dim3(64), 0, stream, x, w, b, y, p.M, p.N, p.K, p.bm);
+        else if (p.M <= 4) hipLaunchKernelGGL((gemv_seq_kernel<4, 8>), grid, dim3(64), 0, stream, x, w, b, y, p.M, p.N, p.K, p.bm);
         else hipLaunchKernelGGL((gemv_seq_kernel<8, 8>), grid, dim3(64), 0, stream, x, w, b, y, p.M, p.N, p.K, p.bm);
     } else if (waves) {
         GemmArgs g{};
