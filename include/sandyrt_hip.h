@@ -258,6 +258,19 @@ int sandy_hip_matmul(const SandyTensor* lhs, const SandyTensor* rhs, int32_t tra
  * TensorCalc.cpp:722-773 -- the reference's CUDA device rejects it,
  * src/device/cuda/CudaDevice.cpp:536-537): out[.., o] = bias[o] +
  * sum_i x[.., i] * weight[o, i]. */
+/* Gated MLP input projection in one launch: out[.., m, i] = act(gate) * up
+ * with gate = lhs . W[2i]^T and up = lhs . W[2i + 1]^T, each rounded to the
+ * output dtype as sandy_hip_matmul stores it, then the SiLU (activation 1) or
+ * GELU (2) scalar DAG of the element-wise group, fp32, rounded once.  rhs is
+ * [2 ffn, k] with the gate and up rows interleaved; out is [.., m, ffn].
+ * Bit-identical to sandy_hip_matmul (transpose_rhs) followed by
+ * sandy_hip_elementwise.  bf16, k a multiple of 32, at most 64 rows (the
+ * decode GEMM); otherwise SANDY_ERR_UNSUPPORTED.  Fuses the program's
+ * gate/up __matmul pair and its __mul(__silu(gate), up) group
+ * (src/models/tinyllama/common.sandy.go:3-5); the reference has no single
+ * counterpart. */
+int sandy_hip_matmul_glu(const SandyTensor* lhs, const SandyTensor* rhs, int32_t activation, const SandyTensor* out,
+                         void* stream, char* err, size_t err_cap);
 int sandy_hip_linear(const SandyTensor* x, const SandyTensor* weight, const SandyTensor* bias,
                      const SandyTensor* out, void* stream, char* err, size_t err_cap);
 

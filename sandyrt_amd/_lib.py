@@ -139,6 +139,7 @@ SIGNATURES = {
     "sandy_hip_moe_matmul": [T, T, T, C.c_int32, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_matmul": [T, T, C.c_int32, C.c_int32, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_linear": [T, T, T, T, C.c_void_p, ERR, C.c_size_t],
+    "sandy_hip_matmul_glu": [T, T, C.c_int32, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_moe_scatter_sum": [T, T, T, T, C.c_void_p, ERR, C.c_size_t],
 }
 

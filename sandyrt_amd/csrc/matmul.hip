@@ -77,7 +77,24 @@ struct GemmArgs {
     float* part;           // [tiles, splits, 4 waves, RT * CT * 64 lanes * 4]
     uint32_t* counters;    // [tiles] arrivals (zero between launches)
     BatchMap bm;
+    int32_t glu;           // 0: plain; 1 / 2: gated SiLU / GELU epilogue (weight rows interleaved gate, up)
 };
+
+// Gated activation of one bf16-rounded (gate, up) pair with the scalar DAGs
+// of src/ir/BuiltinLowering.cpp:116-158 in their node order (silu(g) * up,
+// gelu(g) * up), fp32 arithmetic without contraction -- what the generated
+// element-wise group computes from the two GEMM outputs.
+__device__ __forceinline__ float glu_pair(int kind, float gv, float uv) {
+    if (kind == 1) {
+        const float h = __fmul_rn(0.5f, gv);
+        return __fmul_rn(__fmul_rn(h, __fadd_rn(1.0f, tanhf(h))), uv);
+    }
+    const float h = __fmul_rn(0.5f, gv);
+    const float x3 = __fmul_rn(__fmul_rn(gv, gv), gv);
+    const float inner = __fadd_rn(gv, __fmul_rn(0.044715f, x3));
+    const float t = tanhf(__fmul_rn(0.7978845608028654f, inner));
+    return __fmul_rn(__fmul_rn(h, __fadd_rn(1.0f, t)), uv);
+}
 
 // Prefill-sized products: workgroup = 16 * RT rows x 64 * CT columns of one
 // batch; wave w owns columns n0 = (tile * 4 + w) * 16 * CT .. + 16 * CT.  Per
@@ -347,6 +364,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     const int64_t ob = bz * M * N;
     auto emit = [&](int t, int c, const f32x4_t& v) {
         const int64_t nc = n0 + 16 * c + (lane & 15);
+        if (g.glu) {
+            // columns (2i, 2i + 1) = (gate_i, up_i) sit in lanes (l, l ^ 1); both
+            // are rounded to bf16 as the plain GEMM would store them, and the
+            // even lane writes act[row, i] of the [M, N / 2] output (every lane
+            // takes part in the shuffle)
+            const int64_t half = N >> 1;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float gv = bf16_to_f32(f32_to_bf16(v[i]));
+                const float uv = __shfl_xor(gv, 1, 64);
+                const int64_t rr = r0 + 16 * t + 4 * (lane >> 4) + i;
+                if ((lane & 1) == 0 && nc < N && rr < M)
+                    g.out[(bz * M + rr) * half + (nc >> 1)] = f32_to_bf16(glu_pair(g.glu, gv, uv));
+            }
+            return;
+        }
         if (nc >= N) return;
         const float bias = g.bias ? bf16_to_f32(g.bias[nc]) : 0.0f;
 #pragma unroll
@@ -657,7 +690,7 @@ const char* plan_matmul(const SandyTensor& l, const SandyTensor& r, const SandyT
 }
 
 int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const SandyTensor* bias, const SandyTensor& o,
-           bool tl, bool tr, hipStream_t stream, Err e, const char* what) {
+           bool tl, bool tr, hipStream_t stream, Err e, const char* what, int glu = 0) {
     if (p.batches == 0 || p.M == 0 || p.N == 0) return ok(e);
     if (p.batches > 65535) return fail(e, SANDY_ERR_UNSUPPORTED, "%s batch count exceeds 65535", what);
     const void* pl = base_ptr(l);
@@ -668,6 +701,8 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
     const bool lines = l.dtype == SANDY_BF16 && !tl && tr && p.K % 32 == 0 && p.K > 0 && aligned &&
                        p.K <= (int64_t{1} << 21) && env_int("SANDY_GEMM_SIMT", 0) == 0;
     const bool waves = lines && env_int("SANDY_GEMM_WAVES", p.M <= 64 ? 1 : 0) != 0;
+    if (glu && !waves)
+        return fail(e, SANDY_ERR_UNSUPPORTED, "%s needs bf16 operands, k a multiple of 32 and at most 64 rows", what);
     // f32, few rows, weight rows contiguous: the exact-order GEMV
     const bool gemv = l.dtype == SANDY_F32 && !tl && tr && p.M <= 8 && p.K % 4 == 0 && aligned &&
                       p.lrs == p.K && p.rrs == p.K && env_int("SANDY_GEMM_SIMT", 0) == 0;
@@ -693,6 +728,7 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
         g.N = p.N;
         g.K = p.K;
         g.bm = p.bm;
+        g.glu = glu;
         // tile: 16 * RT rows x 16 * CT columns (variants: RT 1 / 2 / 4 with
         // CT 1, then (RT, CT) = (2, 2), (1, 2), (2, 4), (1, 4), (4, 2), (4, 4))
         static const int kRT[] = {1, 2, 4, 2, 1, 2, 1, 4, 4};
@@ -855,6 +891,29 @@ extern "C" int sandy_hip_matmul(const SandyTensor* lhs, const SandyTensor* rhs, 
     if (const char* msg = plan_matmul(*lhs, *rhs, *out, transpose_lhs != 0, transpose_rhs != 0, p))
         return fail(e, SANDY_ERR_INVALID, "%s", msg);
     return launch(p, *lhs, *rhs, nullptr, *out, transpose_lhs != 0, transpose_rhs != 0, stream, e, "matmul");
+}
+
+extern "C" int sandy_hip_matmul_glu(const SandyTensor* lhs, const SandyTensor* rhs, int32_t activation,
+                                    const SandyTensor* out, void* stream_, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    if (!valid_rank(lhs) || !valid_rank(rhs) || !valid_rank(out))
+        return fail(e, SANDY_ERR_INVALID, "matmul requires lhs, rhs and out");
+    if (activation != 1 && activation != 2) return fail(e, SANDY_ERR_INVALID, "gated matmul activation must be 1 (silu) or 2 (gelu)");
+    if (lhs->dtype != rhs->dtype || lhs->dtype != out->dtype)
+        return fail(e, SANDY_ERR_INVALID, "matmul operands must have same dtype");
+    if (!contiguous(*lhs) || !contiguous(*rhs) || !contiguous(*out))
+        return fail(e, SANDY_ERR_UNSUPPORTED, "matmul requires contiguous tensor views");
+    if (rhs->rank != 2 || rhs->dims[0] % 2 != 0)
+        return fail(e, SANDY_ERR_INVALID, "gated matmul weight must be [2 * ffn, k] with gate and up rows interleaved");
+    // plan the product against the full [.., M, 2 ffn] output; the epilogue writes half of it
+    SandyTensor full = *out;
+    if (full.rank < 1 || full.dims[full.rank - 1] * 2 != rhs->dims[0])
+        return fail(e, SANDY_ERR_INVALID, "matmul output shape mismatch");
+    full.dims[full.rank - 1] = rhs->dims[0];
+    Plan p{};
+    if (const char* msg = plan_matmul(*lhs, *rhs, full, false, true, p)) return fail(e, SANDY_ERR_INVALID, "%s", msg);
+    return launch(p, *lhs, *rhs, nullptr, *out, false, true, stream, e, "gated matmul", activation);
 }
 
 extern "C" int sandy_hip_linear(const SandyTensor* x, const SandyTensor* weight, const SandyTensor* bias,

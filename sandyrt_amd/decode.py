@@ -20,6 +20,9 @@ Layout choices (same arithmetic as the reference program):
   * RoPE of q and k and the two paged appends of each block run as one
     launch (sandy_hip_device_decode_qkv); fused_qkv=False issues the
     reference program's separate rope / append ops instead.
+  * the gate/up GEMM applies the SiLU gate in its epilogue
+    (sandy_hip_matmul_glu, gate/up weight rows interleaved once at
+    construction); fused_glu=False runs the GEMM and the SiLU group.
   * q/k/v weights are concatenated into one [q + k + v, hidden] matrix and
     gate/up into one [2 * ffn, hidden] matrix, so each is one GEMM; the
     q/k/v and gate/up outputs are contiguous views of those GEMM outputs.
@@ -135,8 +138,17 @@ class TinyLlamaDecoder:
     Sequence b owns row b of every layer's block table (its pool slot), so
     the attention reads the pools' tables directly."""
 
-    def __init__(self, dev: HipDevice, cfg: DecodeConfig, weights: dict, batch: int = 1, fused_qkv: bool = True):
-        self.dev, self.cfg, self.w, self.batch, self.fused_qkv = dev, cfg, weights, batch, fused_qkv
+    def __init__(self, dev: HipDevice, cfg: DecodeConfig, weights: dict, batch: int = 1, fused_qkv: bool = True,
+                 fused_glu: bool = True):
+        self.dev, self.cfg, self.w, self.batch = dev, cfg, weights, batch
+        self.fused_qkv, self.fused_glu = fused_qkv, fused_glu
+        # row-interleaved gate/up weights for the gated GEMM epilogue (the
+        # caller's weight dict is left as it is)
+        self.w_glu = {}
+        if fused_glu:
+            for layer in range(cfg.layers):
+                gu = weights[f"{layer}.gate_up"]
+                self.w_glu[layer] = ops.interleave_glu_weight(gu[:cfg.ffn], gu[cfg.ffn:])
         c, B = cfg, batch
         bf = torch.bfloat16
         pages = (c.max_context + c.page_size - 1) // c.page_size
@@ -263,10 +275,14 @@ class TinyLlamaDecoder:
                               d(self.o), stream=s))
             prog.append(_Call("sandy_hip_add_rms_norm", d(self.o), d(x_in), d(w[f"{layer}.post_norm"]),
                               C.c_double(c.eps), d(res_b), d(h2d), stream=s))
-            prog.append(_Call("sandy_hip_matmul", d(h2d), d(w[f"{layer}.gate_up"]), C.c_int32(0), C.c_int32(1),
-                              d(self.gu), stream=s))
-            prog.append(_Call("sandy_hip_elementwise", nodes, C.c_int32(len(silu)), C.c_uint32(sres), arr, bc,
-                              C.c_int32(2), d(self.act), stream=s))
+            if self.fused_glu:  # gate/up GEMM with the SiLU gate in its epilogue: one launch
+                prog.append(_Call("sandy_hip_matmul_glu", d(h2d), d(self.w_glu[layer]), C.c_int32(1), d(self.act),
+                                  stream=s))
+            else:
+                prog.append(_Call("sandy_hip_matmul", d(h2d), d(w[f"{layer}.gate_up"]), C.c_int32(0), C.c_int32(1),
+                                  d(self.gu), stream=s))
+                prog.append(_Call("sandy_hip_elementwise", nodes, C.c_int32(len(silu)), C.c_uint32(sres), arr, bc,
+                                  C.c_int32(2), d(self.act), stream=s))
             prog.append(_Call("sandy_hip_matmul", d(self.act), d(w[f"{layer}.down"]), C.c_int32(0), C.c_int32(1),
                               d(self.d), stream=s))
         prog.append(_Call("sandy_hip_add_rms_norm", d(self.d), d(res_b), d(w["norm"]), C.c_double(c.eps), d(res_a),

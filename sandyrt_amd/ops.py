@@ -321,6 +321,23 @@ def matmul(lhs, rhs, transpose_lhs: bool = False, transpose_rhs: bool = False, o
     return out
 
 
+def interleave_glu_weight(gate_w, up_w):
+    """[ffn, k] gate and up weights -> the [2 ffn, k] row-interleaved weight
+    of matmul_glu (row 2i = gate_i, row 2i + 1 = up_i)."""
+    return torch.stack([gate_w, up_w], dim=1).reshape(2 * gate_w.shape[0], gate_w.shape[1]).contiguous()
+
+
+def matmul_glu(x, w_interleaved, activation: str = "silu", out=None):
+    """act(x @ gate^T) * (x @ up^T) in one launch; bit-identical to matmul then
+    the silu_mul / gelu_mul group."""
+    _require_gpu(x, w_interleaved)
+    code = {"silu": 1, "gelu": 2}[activation]
+    shape = list(x.shape[:-1]) + [w_interleaved.shape[0] // 2]
+    out = torch.empty(shape, dtype=x.dtype, device=x.device) if out is None else out
+    call("sandy_hip_matmul_glu", desc(x), desc(w_interleaved), code, desc(out))
+    return out
+
+
 def linear(x, weight, bias, out=None):
     """LinearKernelOp (TensorCalc.cpp:722-773): bias + x @ weight^T."""
     _require_gpu(x, weight, bias)

@@ -192,9 +192,10 @@ def test_batched_decode_matches_oracle_per_sequence(oracle):
 
 
 def test_fused_qkv_step_matches_separate_ops_bit_for_bit():
-    """The fused q/k/v launch (RoPE q and k, both appends) and the reference
-    program's separate rope / append ops give identical logits, tokens and
-    caches, step after step, for a batch with ragged contexts."""
+    """The fused launches (RoPE q and k with both appends; the gate/up GEMM
+    with the SiLU gate in its epilogue) and the reference program's separate
+    ops give identical logits, tokens and caches, step after step, for a
+    batch with ragged contexts."""
     from sandyrt_amd.decode import DecodeConfig, TinyLlamaDecoder, random_weights
     from sandyrt_amd.device import HipDevice
     cfg = DecodeConfig(layers=2, hidden=512, heads=8, kv_heads=2, head_dim=64, ffn=1024, vocab=1500, page_size=16,
@@ -202,8 +203,8 @@ def test_fused_qkv_step_matches_separate_ops_bit_for_bit():
     w = random_weights(cfg, seed=8)
     dev = HipDevice(0)
     try:
-        a = TinyLlamaDecoder(dev, cfg, w, batch=4, fused_qkv=True)
-        b = TinyLlamaDecoder(dev, cfg, w, batch=4, fused_qkv=False)
+        a = TinyLlamaDecoder(dev, cfg, w, batch=4, fused_qkv=True, fused_glu=True)
+        b = TinyLlamaDecoder(dev, cfg, w, batch=4, fused_qkv=False, fused_glu=False)
         r = rng(9)
         for s, n in enumerate([3, 16, 17, 90]):
             ks = [from_f32(normal(r, (1, cfg.kv_heads, n, cfg.head_dim)), torch.bfloat16) for _ in range(cfg.layers)]

@@ -215,3 +215,33 @@ def test_linear_f32_few_rows_bit_exact(ops, oracle, rows, in_f, out_f):
     assert_equal(ops.linear(x, w, b), oracle.linear(to_oracle(x), to_oracle(w), to_oracle(b)), "linear")
     assert_equal(ops.matmul(x, w, transpose_rhs=True),
                  oracle.matmul(to_oracle(x), to_oracle(w), transpose_rhs=True), "matmul transposed rhs")
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu"])
+@pytest.mark.parametrize("m,k,ffn", [(1, 2048, 5632), (5, 64, 80), (32, 2048, 5632), (64, 2560, 1024),
+                                     (32, 5632, 96), (3, 128, 40)])
+def test_matmul_glu_matches_matmul_then_group(ops, act, m, k, ffn):
+    """The gated epilogue equals the GEMM (gate and up outputs rounded to
+    bf16) followed by the element-wise group, bit for bit; K-split shapes
+    (k 5632) and odd row counts included."""
+    r = rng(m + k + ffn)
+    x = from_f32(normal(r, (m, k)), torch.bfloat16)
+    wg = from_f32(normal(r, (ffn, k), 0.05), torch.bfloat16)
+    wu = from_f32(normal(r, (ffn, k), 0.05), torch.bfloat16)
+    got = ops.matmul_glu(x, ops.interleave_glu_weight(wg, wu), act)
+    gate = ops.matmul(x, wg, transpose_rhs=True)
+    up = ops.matmul(x, wu, transpose_rhs=True)
+    nodes, res = ops.silu_mul_nodes() if act == "silu" else ops.gelu_mul_nodes()
+    want = ops.elementwise(nodes, res, [gate, up])
+    assert torch.equal(got, want)
+
+
+def test_matmul_glu_rejects_unsupported(ops):
+    from sandyrt_amd._lib import SandyError
+    x = torch.zeros(2, 40, dtype=torch.bfloat16, device="cuda")  # k not a multiple of 32
+    w = torch.zeros(8, 40, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(SandyError, match="gated matmul needs bf16 operands"):
+        ops.matmul_glu(x, w)
+    with pytest.raises(SandyError, match="with gate and up rows interleaved"):
+        ops.matmul_glu(torch.zeros(2, 64, dtype=torch.bfloat16, device="cuda"),
+                       torch.zeros(7, 64, dtype=torch.bfloat16, device="cuda"))
