@@ -53,6 +53,15 @@ struct EwArgs {
     int32_t orank;
 };
 
+// The vectorised kernel reads only pointers and element counts: a 144-byte
+// argument block instead of the 1.2 KB one the strided kernel needs.
+struct EwVecArgs {
+    const void* in[SANDY_HIP_MAX_INPUTS];
+    int64_t numel[SANDY_HIP_MAX_INPUTS];
+    void* out;
+    int64_t n;
+};
+
 // The generated code declares the same struct layout.
 const char* kPrelude = R"(
 typedef unsigned short u16;
@@ -61,6 +70,7 @@ struct EwArgs {
   const void* in[8]; i64 numel[8]; i64 dims[8][8]; i64 strides[8][8]; int rank[8];
   void* out; i64 n; i64 odims[8]; i64 ostrides[8]; int orank;
 };
+struct EwVecArgs { const void* in[8]; i64 numel[8]; void* out; i64 n; };
 __device__ __forceinline__ float bf2f(u16 b) { return __uint_as_float(((unsigned)b) << 16); }
 __device__ __forceinline__ u16 f2bf(float f) { unsigned u = __float_as_uint(f); return (u16)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16); }
 __device__ __forceinline__ i64 strided_index(const i64* dims, const i64* strides, int rank, i64 lin) {
@@ -142,7 +152,8 @@ std::string generate(const SandyScalarNode* nodes, int count, uint32_t result, c
                      const int* modes, int nin, int32_t out_dt, bool vec) {
     std::ostringstream s;
     s << kPrelude;
-    s << "extern \"C\" __global__ __launch_bounds__(256) void sandy_ew(EwArgs a) {\n";
+    s << "extern \"C\" __global__ __launch_bounds__(256) void sandy_ew(" << (vec ? "EwVecArgs" : "EwArgs")
+      << " a) {\n";
     if (vec) {
         // chunk j of 8 elements; a thread takes chunks c and c + 256 of each
         // 512-chunk stride of the grid
@@ -350,7 +361,16 @@ extern "C" int sandy_hip_elementwise(const SandyScalarNode* nodes, int32_t node_
     int64_t blocks64 = (threads + 255) / 256;
     if (vec) blocks64 = std::min<int64_t>(blocks64, 4096);
     const unsigned blocks = static_cast<unsigned>(blocks64);
-    void* params[] = {&args};
+    EwVecArgs vargs{};
+    if (vec) {
+        for (int i = 0; i < input_count; i++) {
+            vargs.in[i] = args.in[i];
+            vargs.numel[i] = args.numel[i];
+        }
+        vargs.out = args.out;
+        vargs.n = args.n;
+    }
+    void* params[] = {vec ? static_cast<void*>(&vargs) : static_cast<void*>(&args)};
     SANDY_HIP_TRY(hipModuleLaunchKernel(c.fn, blocks, 1, 1, 256, 1, 1, 0, stream, params, nullptr), e,
                   "elementwise launch");
     return ok(e);

@@ -283,6 +283,112 @@ __global__ __launch_bounds__(256) void topk_wide_merge_kernel(const float* __res
     }
 }
 
+// Greedy selection (k == 1) over long rows in one pass.  (value desc, index
+// asc) is the unsigned order of the 64-bit key  ord(value) << 32 | ~index,
+// where ord maps the float's bits to an order-preserving u32 (-0 taken as +0,
+// the reference compares them equal; NaN mapped to 0, below every number).
+// Workgroup (chunk, row) reduces its U * 2048 elements to one key, merges it
+// into the row's slot with a 64-bit atomic max, and the last workgroup of the
+// row to arrive (a counter) takes the slot (resetting it and the
+// counter to zero for the next call), re-reads the winning element so the
+// value is stored bit for bit, and writes value and index.
+__device__ __forceinline__ uint32_t order_key(float v) {
+    uint32_t u = __float_as_uint(v);
+    if ((u << 1) == 0) u = 0;                 // -0 -> +0
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0u;  // NaN: lowest
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// one row's key and counter, alone on a 256-byte span: rows' atomics then
+// land in different memory channels instead of queueing on one line
+constexpr int kArgmaxSlotWords = 32;
+
+__device__ __forceinline__ uint64_t key_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+template <typename T, int U, bool VEC>
+__global__ __launch_bounds__(256) void argmax_wide_kernel(const void* __restrict__ x, int64_t n, int chunks,
+                                                          uint64_t* __restrict__ slots, void* __restrict__ values,
+                                                          void* __restrict__ indices, int32_t idx_dt) {
+    constexpr int kChunk = U * 2048;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t row = blockIdx.y;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kChunk;
+    const int64_t rbase = row * n;
+    uint32_t best_ord = 0, best_idx = 0xffffffffu;
+    bool any = false;
+    if constexpr (VEC) {
+        typename Vec8<T>::raw raw[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t i0 = c0 + 2048 * u + 8 * tid;
+            raw[u] = Vec8<T>::load_raw(x, rbase + (i0 < n ? i0 : 0));  // n % 8 == 0: a vector is all in or all out
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t i0 = c0 + 2048 * u + 8 * tid;
+            if (i0 >= n) break;
+            float v[8];
+            Vec8<T>::unpack(raw[u], v);
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const uint32_t o = order_key(v[q]);
+                if (!any || o > best_ord) {  // indices increase: strict > keeps the first of equals
+                    best_ord = o;
+                    best_idx = static_cast<uint32_t>(i0 + q);
+                    any = true;
+                }
+            }
+        }
+    } else {
+        float v[8 * U];
+#pragma unroll
+        for (int j = 0; j < 8 * U; j++) {
+            const int64_t i = c0 + tid + 256 * j;
+            v[j] = Vec8<T>::load1(x, rbase + (i < n ? i : 0));
+        }
+#pragma unroll
+        for (int j = 0; j < 8 * U; j++) {
+            const int64_t i = c0 + tid + 256 * j;
+            if (i >= n) break;
+            const uint32_t o = order_key(v[j]);
+            if (!any || o > best_ord) {
+                best_ord = o;
+                best_idx = static_cast<uint32_t>(i);
+                any = true;
+            }
+        }
+    }
+    // a thread with no element keeps key 0, which any element's key beats
+    // or equals (ties at 0 are NaN-only rows, where ~index still orders)
+    uint64_t key = any ? (static_cast<uint64_t>(best_ord) << 32) | static_cast<uint32_t>(~best_idx) : 0;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(key), o, 64);
+        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(key >> 32), o, 64);
+        key = key_max(key, (static_cast<uint64_t>(hi) << 32) | lo);
+    }
+    __shared__ uint64_t wk[4];
+    if (lane == 0) wk[wave] = key;
+    __syncthreads();
+    if (tid != 0) return;
+    key = key_max(key_max(wk[0], wk[1]), key_max(wk[2], wk[3]));
+    uint64_t* slot = slots + kArgmaxSlotWords * row;
+    uint64_t* ctr = slot + 1;
+    // device-scope atomics resolve past the XCD's L2; waiting for the max to
+    // return before counting orders the two without an acquire/release pair
+    // (which would write back and invalidate the L2 in every workgroup)
+    const uint64_t before = __hip_atomic_fetch_max(slot, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const uint64_t prev = __hip_atomic_fetch_add(ctr, uint64_t{1} + 0 * before, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev != static_cast<uint64_t>(chunks - 1)) return;
+    __hip_atomic_store(ctr, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t win = __hip_atomic_exchange(slot, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int64_t idx = static_cast<int64_t>(~static_cast<uint32_t>(win));
+    Vec8<T>::store1(values, row, Vec8<T>::load1(x, rbase + idx));
+    store_index(indices, idx_dt, row, idx);
+}
+
 // ---------------------------------------------------------------- moe_gather
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
@@ -903,6 +1009,33 @@ extern "C" int sandy_hip_topk(const SandyTensor* x, int64_t k, int64_t axis, con
         else { TOPK_LAUNCH(16); }
 #undef TOPK_LAUNCH
 #undef TOPK_RANK
+    } else if (inner == 1 && k == 1 && outer <= 65535 && n < (int64_t{1} << 31)) {
+        // workgroup chunk of U * 2048 elements: the largest U in {2, 4, 8}
+        // that still gives at least 2048 workgroups
+        static const int forced = [] {
+            const char* v = std::getenv("SANDY_ARGMAX_U");
+            return v ? std::atoi(v) : 0;
+        }();
+        int u = 8;
+        while (u > 2 && outer * ((n + u * 2048 - 1) / (u * 2048)) < 2048) u >>= 1;
+        if (forced == 2 || forced == 4 || forced == 8) u = forced;
+        const int64_t chunks = (n + u * 2048 - 1) / (u * 2048);
+        int status = 0;
+        uint64_t* slots = static_cast<uint64_t*>(
+            device_counters(2, static_cast<size_t>(outer) * kArgmaxSlotWords * sizeof(uint64_t), stream, e, &status));
+        if (status) return status;
+        dim3 g1(static_cast<unsigned>(chunks), static_cast<unsigned>(outer));
+        const bool vec = n % 8 == 0 && (reinterpret_cast<uintptr_t>(px) & 31) == 0;
+        const int ch = static_cast<int>(chunks);
+        const int32_t idt = indices->dtype;
+#define ARGMAX_LAUNCH(T, UU)                                                                                           \
+    if (vec) hipLaunchKernelGGL((argmax_wide_kernel<T, UU, true>), g1, dim3(256), 0, stream, px, n, ch, slots, pv, pi, idt); \
+    else hipLaunchKernelGGL((argmax_wide_kernel<T, UU, false>), g1, dim3(256), 0, stream, px, n, ch, slots, pv, pi, idt)
+#define ARGMAX_U(T) \
+    if (u == 2) { ARGMAX_LAUNCH(T, 2); } else if (u == 4) { ARGMAX_LAUNCH(T, 4); } else { ARGMAX_LAUNCH(T, 8); }
+        if (bf) { ARGMAX_U(BF16); } else { ARGMAX_U(F32); }
+#undef ARGMAX_U
+#undef ARGMAX_LAUNCH
     } else if (inner == 1 && k <= kWideMaxK && outer <= 65535) {
         const int64_t chunks = (n + kWideChunk - 1) / kWideChunk;
         int status = 0;

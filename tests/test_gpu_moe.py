@@ -53,6 +53,42 @@ def test_greedy_argmax_ties_take_lowest_id(ops, dtype):
     assert v[:, 0].float().cpu().tolist() == [30.0, 31.0, 29.0]
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_greedy_argmax_signed_zero_and_negative_rows(ops, oracle, dtype):
+    """The one-pass argmax orders values through an integer key: -0 and +0
+    must stay equal (index decides, the stored value keeps its sign bit),
+    all-negative and -inf rows must resolve like the CPU."""
+    x = torch.full((4, 20000), -5.0, dtype=dtype, device="cuda")
+    x[0, :] = -1.0
+    x[0, 7] = -0.0
+    x[0, 9000] = 0.0          # equal to -0: lowest index (7) wins, value -0
+    x[1, :] = float("-inf")   # every element equal: index 0
+    x[2, 19999] = -4.0
+    x[3, 123] = 0.0
+    x[3, 50] = -0.0
+    for _ in range(2):  # the second call runs on the slots the first reset
+        v, i = ops.topk(x, 1)
+        wv, wi = oracle.topk(to_oracle(x), 1)
+        assert_equal(i, wi, "argmax indices")
+        assert_equal(v, wv, "argmax values")
+        assert torch.signbit(v.float()).cpu().tolist() == [[True], [True], [True], [True]]
+        assert i[:, 0].cpu().tolist() == [7, 0, 19999, 50]
+
+
+@pytest.mark.parametrize("shape", [(160, 262144), (64, 262144), (9, 100003)])
+@pytest.mark.parametrize("index_dtype", [torch.int64, torch.int32])
+def test_greedy_argmax_many_rows_repeated(ops, oracle, shape, index_dtype):
+    """All three chunk widths of the one-pass argmax (the row count sets it),
+    two calls in a row, int32 and int64 indices."""
+    r = rng(shape[0])
+    x = from_f32(np.round(normal(r, shape) * 4) / 4, torch.bfloat16)
+    wv, wi = oracle.topk(to_oracle(x), 1, index_dtype=np.int64 if index_dtype == torch.int64 else np.int32)
+    for _ in range(2):
+        v, i = ops.topk(x, 1, index_dtype=index_dtype)
+        assert_equal(i, wi, "argmax indices")
+        assert_equal(v, wv, "argmax values")
+
+
 def test_topk_middle_axis_and_i32(ops, oracle):
     r = rng(3)
     x = from_f32(np.round(normal(r, (3, 40, 5)) * 2) / 2, torch.float32)
