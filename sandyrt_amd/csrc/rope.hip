@@ -33,6 +33,7 @@
 #include "common.h"
 
 #include <cmath>
+#include <cstdlib>
 
 namespace sandy_hip {
 namespace {
@@ -127,6 +128,109 @@ __global__ __launch_bounds__(256) void rope_split_kernel(
             }
             Vec8<T>::store(dst, base + c * 8, ra);
             Vec8<T>::store(dst, base + half + c * 8, rb);
+        }
+    }
+}
+
+// Split-half rotation with whole-line accesses: the 2 * chunks lanes of a
+// row (a power of two dividing 64) each load and store one 16- or 32-byte
+// piece, the first chunks lanes from the first half and the rest from the
+// second, so every load and store instruction covers whole rows instead of
+// one half of each.  Partners (lane ^ chunks) swap their raw pieces with a
+// shuffle; each lane computes the sin/cos of four of its eight pairs and takes
+// the other four from its partner.  Same arithmetic as rope_split_kernel.
+template <typename T>
+__device__ __forceinline__ typename Vec8<T>::raw shfl_raw(const typename Vec8<T>::raw& r, int m);
+
+template <>
+__device__ __forceinline__ uint4 shfl_raw<BF16>(const uint4& r, int m) {
+    return uint4{static_cast<uint32_t>(__shfl_xor(static_cast<int>(r.x), m, 64)),
+                 static_cast<uint32_t>(__shfl_xor(static_cast<int>(r.y), m, 64)),
+                 static_cast<uint32_t>(__shfl_xor(static_cast<int>(r.z), m, 64)),
+                 static_cast<uint32_t>(__shfl_xor(static_cast<int>(r.w), m, 64))};
+}
+
+template <>
+__device__ __forceinline__ Vec8<F32>::raw shfl_raw<F32>(const Vec8<F32>::raw& r, int m) {
+    return Vec8<F32>::raw{float4{__shfl_xor(r.a.x, m, 64), __shfl_xor(r.a.y, m, 64), __shfl_xor(r.a.z, m, 64),
+                                 __shfl_xor(r.a.w, m, 64)},
+                          float4{__shfl_xor(r.b.x, m, 64), __shfl_xor(r.b.y, m, 64), __shfl_xor(r.b.z, m, 64),
+                                 __shfl_xor(r.b.w, m, 64)}};
+}
+
+template <typename T, int U, bool FULL>
+__global__ __launch_bounds__(256) void rope_split_lines_kernel(
+        const void* __restrict__ x, void* __restrict__ out, const void* __restrict__ x2, void* __restrict__ out2,
+        int64_t outer_first, const void* __restrict__ ids, int32_t ids_dt, int mode, int64_t seq, int64_t outer,
+        int dim, int rot_pairs, int groups, int per_group, RopeArgs args, uint32_t* errw) {
+    const int half = dim >> 1;
+    const uint32_t chunks = static_cast<uint32_t>(half >> 3);
+    const uint32_t lanes = 2 * chunks;
+    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+    // row-granular exit: a row's lanes leave together, partners stay paired
+    if (t >= static_cast<uint32_t>(seq) * lanes * static_cast<uint32_t>(groups)) return;
+    const uint32_t r = t & (lanes - 1);
+    const bool hi = r >= chunks;
+    const int c = static_cast<int>(r & (chunks - 1));
+    const uint32_t rest = t / lanes;
+    const int64_t s = rest % static_cast<uint32_t>(seq);
+    const int g = static_cast<int>(rest / static_cast<uint32_t>(seq));
+    const int64_t o_begin = static_cast<int64_t>(g) * per_group;
+    const int64_t o_end = min(outer, o_begin + per_group);
+    const int m = static_cast<int>(chunks);
+    float cs[8], sn[8];
+    int64_t pos = -1;
+    for (int64_t o0 = o_begin; o0 < o_end; o0 += U) {
+        const bool fresh = mode == 3 || pos < 0;
+        if (fresh) pos = rope_position(mode, ids, ids_dt, o0 * seq + s, s, errw);
+        typename Vec8<T>::raw mine[U];
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            if (FULL || o0 + j < o_end) {
+                const bool sec = o0 + j >= outer_first;
+                const int64_t base = ((o0 + j - (sec ? outer_first : 0)) * seq + s) * dim;
+                mine[j] = Vec8<T>::load_raw(sec ? x2 : x, base + (hi ? half : 0) + c * 8);
+            }
+        }
+        if (fresh) {
+            const float fp = static_cast<float>(pos);
+            float s4[4], c4[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int p = c * 8 + (hi ? 4 : 0) + i;
+                s4[i] = 0.0f;
+                c4[i] = 1.0f;
+                if (FULL || p < rot_pairs) rope_sincos(fp / args.denom[p], &s4[i], &c4[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float so = __shfl_xor(s4[i], m, 64), co = __shfl_xor(c4[i], m, 64);
+                sn[i] = hi ? so : s4[i];
+                cs[i] = hi ? co : c4[i];
+                sn[4 + i] = hi ? s4[i] : so;
+                cs[4 + i] = hi ? c4[i] : co;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            // every lane of a row takes the same branch here (o_end is per row group)
+            if (!FULL && o0 + j >= o_end) break;
+            const typename Vec8<T>::raw other = shfl_raw<T>(mine[j], m);
+            const bool sec = o0 + j >= outer_first;
+            const int64_t base = ((o0 + j - (sec ? outer_first : 0)) * seq + s) * dim;
+            float a[8], b[8], res[8];
+            Vec8<T>::unpack(hi ? other : mine[j], a);
+            Vec8<T>::unpack(hi ? mine[j] : other, b);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int p = c * 8 + i;
+                if (FULL || p < rot_pairs)
+                    res[i] = hi ? __fadd_rn(__fmul_rn(a[i], sn[i]), __fmul_rn(b[i], cs[i]))
+                                : __fsub_rn(__fmul_rn(a[i], cs[i]), __fmul_rn(b[i], sn[i]));
+                else
+                    res[i] = hi ? b[i] : a[i];
+            }
+            Vec8<T>::store(sec ? out2 : out, base + (hi ? half : 0) + c * 8, res);
         }
     }
 }
@@ -319,16 +423,22 @@ int rope_run(const SandyTensor* const* xs, const SandyTensor* const* outs, int n
     if (total == 0) return ok(e);
     int groups = 1, per = 1;
     int64_t threads = 0;
+    bool lines = false;
     if (fast) {
         const int chunks = static_cast<int>(split_half ? dim / 16 : dim / 8);
-        const int64_t base_threads = seq * chunks;
+        // split-half rows whose two halves fit one shuffle group take the
+        // whole-line kernel (twice the lanes, each with one piece)
+        lines = split_half && chunks <= 32 && (chunks & (chunks - 1)) == 0 && !std::getenv("SANDY_ROPE_HALVES");
+        const int64_t base_threads = seq * chunks * (lines ? 2 : 1);
         if (mode[0] == 3) {
             groups = static_cast<int>(outer);
         } else {
             // threads (each reusing its sincos over `per` heads): numel / 32 within
             // [32K, 128K] -- measured best for C2's q (128K) and k (32K) on gfx950
             const int64_t want = std::min<int64_t>(131072, std::max<int64_t>(32768, total / 32));
-            groups = static_cast<int>(std::min<int64_t>(outer, std::max<int64_t>(1, want / std::max<int64_t>(1, base_threads))));
+            // (counted in pieces of 16 elements per row for either kernel)
+            const int64_t row_threads = seq * chunks;
+            groups = static_cast<int>(std::min<int64_t>(outer, std::max<int64_t>(1, want / std::max<int64_t>(1, row_threads))));
             per = static_cast<int>((outer + groups - 1) / groups);
             // prefer a head count per group that divides the heads (unguarded kernel)
             for (int d = per; d > 1 && d * 2 > per; d--)
@@ -366,7 +476,10 @@ int rope_run(const SandyTensor* const* xs, const SandyTensor* const* outs, int n
         else if (u == 2) SANDY_ROPE_F(KERNEL, T, 2);    \
         else SANDY_ROPE_F(KERNEL, T, 1);                \
     } while (0)
-        if (split_half) {
+        if (lines) {
+            if (bf) SANDY_ROPE_U(rope_split_lines_kernel, BF16);
+            else SANDY_ROPE_U(rope_split_lines_kernel, F32);
+        } else if (split_half) {
             if (bf) SANDY_ROPE_U(rope_split_kernel, BF16);
             else SANDY_ROPE_U(rope_split_kernel, F32);
         } else {

@@ -108,6 +108,9 @@ def test_elementwise_rejects_bad_dag(ops):
     dict(shape=(3, 5, 64), split=False, rot=32),            # interleaved partial
     dict(shape=(2, 7, 10), split=False, rot=-1),            # odd widths -> generic path
     dict(shape=(2, 3, 12), split=True, rot=8),
+    dict(shape=(2, 4, 7, 96), split=True, rot=-1),         # 3 pieces per half: half-row kernel
+    dict(shape=(2, 2, 9, 80), split=True, rot=48),         # 5 pieces, partial rotary
+    dict(shape=(1, 3, 5, 16), split=True, rot=-1),         # one piece per half: 2-lane rows
 ])
 def test_rope(ops, oracle, dtype, case):
     r = rng(hash(tuple(case["shape"])) % 2**32)
@@ -115,6 +118,22 @@ def test_rope(ops, oracle, dtype, case):
     got = ops.rope(x, 10000.0, rotary_dim=case["rot"], split_half=case["split"])
     want = oracle.rope(to_oracle(x), 10000.0, rotary_dim=case["rot"], split_half=case["split"])
     assert_close(got, want, dtype, f"rope {case}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_rope_whole_line_kernel_equals_half_row_kernel(ops, monkeypatch, dtype):
+    """Split-half rows with a power-of-two piece count run the whole-line
+    kernel (partner lanes swap halves); SANDY_ROPE_HALVES forces the half-row
+    kernel: both must agree bit for bit, partial rotary and ids included."""
+    r = rng(23)
+    for shape, rot in [((1, 32, 300, 64), -1), ((2, 4, 33, 128), -1), ((1, 2, 9, 512), 128), ((3, 5, 16), -1)]:
+        x = from_f32(normal(r, shape), dtype)
+        ids = torch.tensor([17], device="cuda")
+        got = ops.rope(x, 1e4, rotary_dim=rot, split_half=True, position_ids=ids)
+        monkeypatch.setenv("SANDY_ROPE_HALVES", "1")
+        want = ops.rope(x, 1e4, rotary_dim=rot, split_half=True, position_ids=ids)
+        monkeypatch.delenv("SANDY_ROPE_HALVES")
+        assert torch.equal(got, want), shape
 
 
 @pytest.mark.parametrize("kind", ["offset", "seq", "vectors"])
