@@ -16,10 +16,11 @@
 // rows with atomics (nondeterministic order within an expert), round-trips
 // counts and offsets through the host with stream syncs, combines with fp32
 // atomics and hands the grouped GEMM to cuBLAS.  Here:
-//   - the permute is a device-side stable counting sort in one workgroup per
-//     batch (wave ballots rank equal experts inside each wave; per-wave
-//     counts are prefix-summed in LDS), so rows come out in exactly the CPU
-//     order and no host round trip is needed;
+//   - the permute is a device-side stable counting sort: one workgroup per
+//     (expert, share of its rows) ranks that expert's routes by ballots and
+//     copies its rows in the same launch (one workgroup per batch ranks
+//     longer route lists), so rows come out in exactly the CPU order and no
+//     host round trip is needed;
 //   - the combine is a gather-reduce: one wave per (token, 512 columns)
 //     finds its rows with ballots in row order and accumulates with the
 //     reference's per-add rounding -- bit-identical to the CPU, no atomics;
@@ -425,23 +426,13 @@ __device__ __forceinline__ void scan_expert_counts(int32_t* cursor, int64_t expe
     if (tid == 0) store_index(offsets, off_dt, static_cast<int64_t>(b) * (experts + 1) + experts, seg_total);
 }
 
-// One workgroup per batch.  dest[r] receives the packed row of route r
-// (token-major route order r = token * top_k + slot); rows of one expert are
-// in route order.
-//
-// BITS (all routes staged in LDS, no token listing an expert twice): a
-// token routes to an expert at most once, so the rank of route (token t,
-// expert e) among e's rows is the number of earlier tokens that chose e --
-// a prefix popcount over a per-expert token bitmask built with LDS atomic
-// ORs.  Every step is O(1) per route.  A repeated (token, expert) pair is
-// detected while the masks are built (the bit is already set) and sends the
-// workgroup to the general ranking below.
-//
-// General ranking: pass 1 counts routes per expert; pass 2 walks the routes
-// in order, 1024 at a time: inside a wave, lanes routed to the same expert
-// are ranked by ballot; waves are ordered through LDS prefix sums; a
-// per-expert cursor carries across chunks.
-template <bool BITS>
+// Routes beyond the fused dispatch's limit: one workgroup per batch.
+// dest[r] receives the packed row of route r (token-major route order
+// r = token * top_k + slot); rows of one expert are in route order.  Pass 1
+// counts routes per expert; pass 2 walks the routes in order, 1024 at a time:
+// inside a wave, lanes routed to the same expert are ranked by ballot; waves
+// are ordered through LDS prefix sums; a per-expert cursor carries across
+// chunks.
 __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         const void* __restrict__ ids, int32_t ids_dt, const void* __restrict__ w, int32_t w_dt, int64_t seq,
         int64_t top_k, int64_t experts, void* __restrict__ packed_w, void* __restrict__ token_ids, int32_t tok_dt,
@@ -469,52 +460,6 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
         }
     }
     __syncthreads();
-    if constexpr (BITS) {
-        // [E][W] token bitmasks (64-bit words) and their exclusive prefix popcounts
-        const int64_t W = (seq + 63) / 64;
-        auto* mask = reinterpret_cast<unsigned long long*>(sw + kRouteStage + ((experts * (1 + kRouteWaves)) & 1));
-        int32_t* pref = reinterpret_cast<int32_t*>(mask + experts * W);
-        __shared__ int dup;
-        if (tid == 0) dup = 0;
-        for (int64_t i = tid; i < experts * W; i += kRouteThreads) mask[i] = 0ull;
-        __syncthreads();
-        for (int64_t r = tid; r < routes; r += kRouteThreads) {
-            const int e = sid[r];
-            if (e < 0) continue;
-            const int64_t t = r / top_k;
-            const unsigned long long bit = 1ull << (t & 63);
-            if (atomicOr(&mask[e * W + (t >> 6)], bit) & bit) dup = 1;
-        }
-        __syncthreads();
-        if (!dup) {
-            for (int64_t x = tid; x < experts; x += kRouteThreads) {
-                int32_t run = 0;
-                for (int64_t q = 0; q < W; q++) {
-                    pref[x * W + q] = run;
-                    run += __popcll(mask[x * W + q]);
-                }
-                cursor[x] = run;
-            }
-            __syncthreads();
-            scan_expert_counts(cursor, experts, offsets, off_dt, b, tid, lane, wave);
-            __syncthreads();
-            for (int64_t r = tid; r < routes; r += kRouteThreads) {
-                const int e = sid[r];
-                if (e < 0) {
-                    dest[rb + r] = -1;
-                    continue;
-                }
-                const int64_t t = r / top_k;
-                const unsigned long long m = mask[e * W + (t >> 6)];
-                const int32_t row = cursor[e] + pref[e * W + (t >> 6)] + __popcll(m & ((1ull << (t & 63)) - 1ull));
-                dest[rb + r] = row;
-                store_any(packed_w, w_dt, rb + row, sw[r]);
-                store_index(token_ids, tok_dt, rb + row, t);
-            }
-            return;
-        }
-        // a token lists an expert twice: the general ranking below
-    }
     for (int64_t r = tid; r < routes; r += kRouteThreads) {
         int64_t e;
         if (staged) e = sid[r];
@@ -596,6 +541,142 @@ __global__ __launch_bounds__(256) void moe_copy_rows_kernel(const char* __restri
     }
 }
 
+// Fused permute for up to kDispatchRoutes routes per batch: workgroup =
+// (expert e, share c of C, batch).  Every workgroup reads all route ids
+// (coalesced, L2-resident after the first) and derives, with no atomics and
+// no other workgroup:
+//   - e's offset: the number of valid routes to lower experts;
+//   - e's routes in route order (= token, then slot: the reference's order
+//     within an expert), ranked by per-(chunk, wave) ballot counts and one
+//     exclusive scan in LDS;
+// then writes token id and weight of, and copies x into, the rows q of e
+// with q % C == c (one wave per row).  Share 0 writes e's offset (the last
+// expert also the total).
+constexpr int kDispatchRoutes = 8192;
+
+// CH chunks of 256 routes per thread in registers (16 up to 4096 routes, 32
+// up to 8192): all their loads are in flight at once, so registers, and with
+// them occupancy, scale with CH
+template <int CH>
+__global__ __launch_bounds__(256) void moe_dispatch_kernel(
+        const void* __restrict__ ids, int32_t ids_dt, const void* __restrict__ w, int32_t w_dt, int64_t seq,
+        int64_t top_k, int64_t experts, int shares, const char* __restrict__ x, char* __restrict__ packed,
+        int64_t row_bytes, int aligned, void* __restrict__ packed_w, void* __restrict__ token_ids, int32_t tok_dt,
+        void* __restrict__ offsets, int32_t off_dt, uint32_t* errw) {
+    __shared__ int32_t list[CH * 256];
+    __shared__ int32_t cnt[CH * 4];
+    __shared__ int32_t below_sum, total;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t e = blockIdx.x / shares;
+    const int c = static_cast<int>(blockIdx.x % shares);
+    const int64_t b = blockIdx.y;
+    const int64_t routes = seq * top_k;
+    const int64_t rb = b * routes;
+    const int J = static_cast<int>((routes + 255) / 256);
+    if (tid == 0) below_sum = 0;
+    // every load issued before any is used (one dtype branch, clamped
+    // indices): a guarded load per route would wait for each in turn
+    int64_t raw[CH];
+    if (ids_dt == SANDY_I64) {
+        const int64_t* p = static_cast<const int64_t*>(ids) + rb;
+#pragma unroll
+        for (int j = 0; j < CH; j++) {
+            const int64_t r = tid + 256 * j;
+            raw[j] = p[r < routes ? r : 0];
+        }
+    } else {
+        const int32_t* p = static_cast<const int32_t*>(ids) + rb;
+#pragma unroll
+        for (int j = 0; j < CH; j++) {
+            const int64_t r = tid + 256 * j;
+            raw[j] = p[r < routes ? r : 0];
+        }
+    }
+    int32_t v[CH];
+#pragma unroll
+    for (int j = 0; j < CH; j++) {
+        const int64_t r = tid + 256 * j;
+        v[j] = r >= routes ? -1 : (raw[j] >= 0 && raw[j] < experts ? static_cast<int32_t>(raw[j]) : -2);
+    }
+    int below = 0;
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < CH; j++) {
+        if (j >= J) break;
+        below += v[j] >= 0 && v[j] < e;
+        bad |= v[j] == -2;
+        const uint64_t m = __ballot(v[j] == e);
+        if (lane == 0) cnt[j * 4 + wave] = __popcll(m);
+    }
+    if (bad && e == 0 && c == 0) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_EXPERT_ID));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) below += __shfl_xor(below, o, 64);
+    __syncthreads();
+    if (lane == 0) atomicAdd(&below_sum, below);
+    if (wave == 0) {  // exclusive scan of the J * 4 (chunk, wave) counts, two per lane
+        const int n = J * 4;
+        const int a0 = 2 * lane < n ? cnt[2 * lane] : 0;
+        const int a1 = 2 * lane + 1 < n ? cnt[2 * lane + 1] : 0;
+        int incl = a0 + a1;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int up = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += up;
+        }
+        const int excl = incl - a0 - a1;
+        if (2 * lane < n) cnt[2 * lane] = excl;
+        if (2 * lane + 1 < n) cnt[2 * lane + 1] = excl + a0;
+        if (lane == 63) total = incl;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < CH; j++) {
+        if (j >= J) break;
+        const uint64_t m = __ballot(v[j] == e);
+        if (v[j] == e) list[cnt[j * 4 + wave] + __popcll(m & ((1ull << lane) - 1ull))] = tid + 256 * j;
+    }
+    __syncthreads();
+    const int n = total;
+    const int64_t base = below_sum;
+    if (c == 0 && tid == 0) {
+        store_index(offsets, off_dt, b * (experts + 1) + e, base);
+        if (e == experts - 1) store_index(offsets, off_dt, b * (experts + 1) + experts, base + n);
+    }
+    // one wave per row of this share
+    for (int q = c + shares * wave; q < n; q += shares * 4) {
+        const int64_t r = list[q];
+        const int64_t row = base + q;
+        const int64_t t = r / top_k;
+        // the weight's load is issued here, its store after the row's loads
+        const float wr = load_any(w, w_dt, rb + r);
+        const char* src = x + (b * seq + t) * row_bytes;
+        char* dst = packed + (rb + row) * row_bytes;
+        if (aligned) {
+            typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));
+            constexpr int kU = 8;  // 8 KiB of the row in flight per wave
+            for (int64_t o0 = lane * 16; o0 < row_bytes; o0 += 64 * 16 * kU) {
+                u32x4_nt tmp[kU];
+#pragma unroll
+                for (int u = 0; u < kU; u++) {
+                    const int64_t o = o0 + u * 64 * 16;
+                    if (o < row_bytes) tmp[u] = *reinterpret_cast<const u32x4_nt*>(src + o);
+                }
+#pragma unroll
+                for (int u = 0; u < kU; u++) {
+                    const int64_t o = o0 + u * 64 * 16;
+                    if (o < row_bytes) __builtin_nontemporal_store(tmp[u], reinterpret_cast<u32x4_nt*>(dst + o));
+                }
+            }
+        } else {
+            for (int64_t o = lane; o < row_bytes; o += 64) dst[o] = src[o];
+        }
+        if (lane == 0) {
+            store_any(packed_w, w_dt, rb + row, wr);
+            store_index(token_ids, tok_dt, rb + row, t);
+        }
+    }
+}
+
 // ---------------------------------------------------------------- moe_scatter_sum
 // Workgroup = (batch, 4 tokens, 512-column chunk); wave = one token.  The
 // batch's token ids are staged in LDS once per workgroup; each wave collects
@@ -603,6 +684,9 @@ __global__ __launch_bounds__(256) void moe_copy_rows_kernel(const char* __restri
 // time: the 8 rows' loads are issued together and accumulated in row order
 // with the reference's two roundings (product, then sum rounded to the output
 // dtype) -- bit-identical to the CPU, no atomics.
+__device__ __forceinline__ float elem_to_f32(uint16_t b) { return bf16_to_f32(b); }
+__device__ __forceinline__ float elem_to_f32(float f) { return f; }
+
 constexpr int kCombineStage = 8192;  // rows staged in LDS (32 KiB)
 constexpr int kCombineHits = 128;    // per-wave hit list
 
@@ -628,10 +712,20 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
         constexpr int kBatch = 16;
         for (int64_t r0 = threadIdx.x; r0 < rows; r0 += 256 * kBatch) {
             int64_t v[kBatch];
+            // one dtype branch around the whole batch: a per-load select made
+            // the compiler wait for every load in turn
+            if (tok_dt == SANDY_I64) {
 #pragma unroll
-            for (int u = 0; u < kBatch; u++) {
-                const int64_t r = r0 + 256 * u;
-                v[u] = load_index(tok, tok_dt, mb + (r < rows ? r : 0));
+                for (int u = 0; u < kBatch; u++) {
+                    const int64_t r = r0 + 256 * u;
+                    v[u] = static_cast<const int64_t*>(tok)[mb + (r < rows ? r : 0)];
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < kBatch; u++) {
+                    const int64_t r = r0 + 256 * u;
+                    v[u] = static_cast<const int32_t*>(tok)[mb + (r < rows ? r : 0)];
+                }
             }
 #pragma unroll
             for (int u = 0; u < kBatch; u++) {
@@ -647,35 +741,60 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
     if (t >= seq) return;
     const int64_t c0 = ch * 512 + lane * 8;
     const bool vec = (hidden & 7) == 0;
-    const int32_t wdt = sizeof(typename Vec8<T>::elem) == 2 ? SANDY_BF16 : SANDY_F32;
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) acc[i] = 0.0f;
     // accumulate the n collected rows of hit[wave], 8 loads in flight at a time
+    // every load of a group of 8 rows is issued before any is used: rows
+    // past n repeat row g and columns past the end repeat column 0 (their
+    // values are not accumulated), so no load sits behind a branch
     auto accumulate = [&](int n) {
+        const int64_t cc = c0 < hidden ? c0 : 0;
         for (int g = 0; g < n; g += 8) {
-            float pv[8][8];
-            float wv[8];
+            using E = typename Vec8<T>::elem;
+            int64_t row[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const bool in = g + u < n;
-                const int64_t row = in ? hit[wave][g + u] : 0;
-                wv[u] = in ? load_any(pw, wdt, mb + row) : 0.0f;
-                const int64_t src = (mb + row) * hidden + c0;
-                if (in && c0 < hidden) {
-                    if (vec) {
-                        Vec8<T>::load(packed, src, pv[u]);
-                    } else {
+            for (int u = 0; u < 8; u++) row[u] = hit[wave][g + u < n ? g + u : g];
+            if (vec) {
+                // raw row pieces first, then the raw weights, converted only
+                // when used (a conversion is a use: it would wait for the load)
+                typename Vec8<T>::raw pr[8];
+                E we[8];
 #pragma unroll
-                        for (int i = 0; i < 8; i++) pv[u][i] = c0 + i < hidden ? Vec8<T>::load1(packed, src + i) : 0.0f;
+                for (int u = 0; u < 8; u++) pr[u] = Vec8<T>::load_raw(packed, (mb + row[u]) * hidden + cc);
+#pragma unroll
+                for (int u = 0; u < 8; u++) we[u] = static_cast<const E*>(pw)[mb + row[u]];
+                // computed for every u and kept by a select: a branch around
+                // the uses lets the compiler sink each load into it
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const bool live = g + u < n && c0 < hidden;
+                    float pv[8];
+                    Vec8<T>::unpack(pr[u], pv);
+                    const float wv = elem_to_f32(we[u]);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        const float nv = Vec8<T>::round(__fadd_rn(acc[i], __fmul_rn(wv, pv[i])));
+                        acc[i] = live ? nv : acc[i];
                     }
                 }
-            }
+            } else {
+                float wv[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++)
-                if (g + u < n)
+                for (int u = 0; u < 8; u++) wv[u] = Vec8<T>::load1(pw, mb + row[u]);
+                float pv[8][8];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+#pragma unroll
+                    for (int i = 0; i < 8; i++)
+                        pv[u][i] = Vec8<T>::load1(packed, (mb + row[u]) * hidden + (c0 + i < hidden ? c0 + i : 0));
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    if (g + u >= n) break;
 #pragma unroll
                     for (int i = 0; i < 8; i++) acc[i] = Vec8<T>::round(__fadd_rn(acc[i], __fmul_rn(wv[u], pv[u][i])));
+                }
+            }
         }
         __builtin_amdgcn_wave_barrier();
     };
@@ -1110,27 +1229,34 @@ extern "C" int sandy_hip_moe_gather(const SandyTensor* x, const SandyTensor* top
     int status = 0;
     uint32_t* errw = device_error_word(e, &status);
     if (status) return status;
+    const int64_t row_bytes = hidden * static_cast<int64_t>(dtype_size(x->dtype));
+    const int aligned = (row_bytes % 16 == 0) &&
+                        ((reinterpret_cast<uintptr_t>(base_ptr(*x)) | reinterpret_cast<uintptr_t>(base_ptr(*packed_x))) & 15) == 0;
+    if (routes <= kDispatchRoutes && batch <= 65535 && env_int("SANDY_MOE_ROUTE_GENERAL", 0) == 0) {
+        // about 512 workgroups, each expert's rows shared by up to 8: every
+        // workgroup re-reads the route ids, so more workgroups cost more
+        // than their extra copy bandwidth gains (config 5: 8 -> 11.6 us,
+        // 4 -> 11.3, 2 -> 14.0, 16 -> 16.7)
+        const int64_t shares = std::max<int64_t>(1, std::min<int64_t>(8, 512 / std::max<int64_t>(1, num_experts * batch)));
+        if (num_experts * shares > 0x7fffffff) return fail(e, SANDY_ERR_UNSUPPORTED, "moe_gather too many experts");
+        dim3 grid(static_cast<unsigned>(num_experts * shares), static_cast<unsigned>(batch));
+        hipLaunchKernelGGL(routes <= 4096 ? moe_dispatch_kernel<16> : moe_dispatch_kernel<32>, grid, dim3(256), 0, stream, base_ptr(*topk_ids), topk_ids->dtype,
+                           base_ptr(*topk_weights), topk_weights->dtype, seq, top_k, num_experts,
+                           static_cast<int>(shares), static_cast<const char*>(base_ptr(*x)),
+                           static_cast<char*>(base_ptr(*packed_x)), row_bytes, aligned, base_ptr(*packed_weights),
+                           base_ptr(*token_ids), token_ids->dtype, base_ptr(*expert_offsets), expert_offsets->dtype,
+                           errw);
+        SANDY_HIP_TRY(hipGetLastError(), e, "moe_gather launch");
+        return ok(e);
+    }
     int32_t* dest = static_cast<int32_t*>(device_workspace(2, static_cast<size_t>(batch * routes) * sizeof(int32_t), stream, e, &status));
     if (status) return status;
-    // token bitmask ranking when every route is staged and the masks fit
-    const int64_t words = (seq + 63) / 64;
-    const size_t lds_bits = lds + 4 + static_cast<size_t>(num_experts * words) * 12;
-    const bool bits = routes <= kRouteStage && lds_bits <= 64 * 1024 && env_int("SANDY_MOE_ROUTE_GENERAL", 0) == 0;
-    if (bits)
-        hipLaunchKernelGGL(moe_route_kernel<true>, dim3(static_cast<unsigned>(batch)), dim3(kRouteThreads), lds_bits,
-                           stream, base_ptr(*topk_ids), topk_ids->dtype, base_ptr(*topk_weights), topk_weights->dtype,
-                           seq, top_k, num_experts, base_ptr(*packed_weights), base_ptr(*token_ids), token_ids->dtype,
-                           base_ptr(*expert_offsets), expert_offsets->dtype, dest, errw);
-    else
-        hipLaunchKernelGGL(moe_route_kernel<false>, dim3(static_cast<unsigned>(batch)), dim3(kRouteThreads), lds,
-                           stream, base_ptr(*topk_ids), topk_ids->dtype, base_ptr(*topk_weights), topk_weights->dtype,
-                           seq, top_k, num_experts, base_ptr(*packed_weights), base_ptr(*token_ids), token_ids->dtype,
-                           base_ptr(*expert_offsets), expert_offsets->dtype, dest, errw);
+    hipLaunchKernelGGL(moe_route_kernel, dim3(static_cast<unsigned>(batch)), dim3(kRouteThreads), lds, stream,
+                       base_ptr(*topk_ids), topk_ids->dtype, base_ptr(*topk_weights), topk_weights->dtype, seq, top_k,
+                       num_experts, base_ptr(*packed_weights), base_ptr(*token_ids), token_ids->dtype,
+                       base_ptr(*expert_offsets), expert_offsets->dtype, dest, errw);
     if (routes > 0 && hidden > 0) {
         const int64_t waves = batch * routes;
-        const int64_t row_bytes = hidden * static_cast<int64_t>(dtype_size(x->dtype));
-        const int aligned = (row_bytes % 16 == 0) &&
-                            ((reinterpret_cast<uintptr_t>(base_ptr(*x)) | reinterpret_cast<uintptr_t>(base_ptr(*packed_x))) & 15) == 0;
         hipLaunchKernelGGL(moe_copy_rows_kernel, dim3(static_cast<unsigned>((waves + 3) / 4)), dim3(256), 0, stream,
                            static_cast<const char*>(base_ptr(*x)), static_cast<char*>(base_ptr(*packed_x)), dest, batch,
                            seq, top_k, row_bytes, aligned);

@@ -127,13 +127,13 @@ def test_router_chain_config5(ops, oracle):
 # ------------------------------------------------------------------ moe_gather
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("T,H,E,K", [(512, 2816, 128, 8), (37, 64, 16, 4), (5, 24, 300, 2), (1, 8, 4, 1),
-                                     (700, 16, 64, 8), (130, 16, 8, 3)])
+                                     (700, 16, 64, 8), (130, 16, 8, 3), (1100, 16, 64, 8), (3, 20, 1, 1)])
 @pytest.mark.parametrize("idx", [np.int64, np.int32])
-@pytest.mark.parametrize("ranking", ["bitmask", "general"])
+@pytest.mark.parametrize("ranking", ["dispatch", "general"])
 def test_moe_gather_bit_exact(ops, oracle, monkeypatch, dtype, T, H, E, K, idx, ranking):
-    """Token bitmask ranking (the default when every route fits in LDS) and
-    the general ballot ranking give the reference's packing bit for bit;
-    700 x 8 routes exceed the staging area and always take the general path."""
+    """The fused per-expert dispatch (the default up to 8192 routes) and the
+    single-workgroup ballot ranking plus row copy give the reference's
+    packing bit for bit; 1100 x 8 routes always take the general path."""
     if ranking == "general":
         monkeypatch.setenv("SANDY_MOE_ROUTE_GENERAL", "1")
     r = rng(T * 7 + E)
