@@ -140,20 +140,59 @@ struct DecodeQkvArgs {
     int32_t v_slots[kMaxFusedStep];
 };
 
+// STAGED (head_dim % 8 == 0, 16-byte aligned rows of at most 16 KiB): the
+// position and lengths are requested first, then the sequence's whole q/k/v
+// row as 16-byte pieces (up to four per thread in flight); the block-table
+// reads that depend on the lengths go out while the row is still arriving.
+// The rotation, the K append and the 16-byte V copy then read the row from
+// LDS.  Otherwise each pair is read from global memory.
+constexpr int kStageRowBytes = 16384;
+
+template <bool STAGED>
 __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t srow[STAGED ? kStageRowBytes / 2 : 8];
+    __shared__ float sden[kMaxFusedPairs];
     const int b = blockIdx.x;
+    const uint16_t* grow = a.qkv + b * a.row_stride;
+    const int n = (a.hq + 2 * a.hkv) * a.d;
+    const int nv = n / 8;  // 16-byte pieces of the row, at most 1024 when staged: four per thread
+    const int t0 = threadIdx.x;
+    const int v0 = t0 < nv ? t0 : nv - 1, v1 = t0 + 256 < nv ? t0 + 256 : nv - 1;
+    const int v2 = t0 + 512 < nv ? t0 + 512 : nv - 1, v3 = t0 + 768 < nv ? t0 + 768 : nv - 1;
+    uint4 p0{}, p1{}, p2{}, p3{};
+    if constexpr (STAGED) {  // the row's loads go out first: they depend on nothing
+        const uint4* g16 = reinterpret_cast<const uint4*>(grow);
+        p0 = g16[v0];
+        p1 = g16[v1];
+        p2 = g16[v2];
+        p3 = g16[v3];
+    }
+    // the angle denominators, indexed per lane, read once into LDS (a
+    // per-lane index into the argument block is a memory load per use)
+    const float den = a.denom[threadIdx.x < kMaxFusedPairs ? threadIdx.x : 0];
+    __builtin_amdgcn_sched_barrier(0);  // keep those loads ahead of the slot -> length -> table chain
     const int32_t ks = a.k_slots[b], vs = a.v_slots[b];
     int64_t pos = load_index(a.pos, a.pos_dt, b);
     const int32_t kl = a.k_len[ks], vl = a.v_len[vs];
-    __syncthreads();  // every thread has read the lengths before they advance
+    const int32_t kblk = kl / a.page_size < a.k_max_blocks ? a.k_table[ks * a.k_max_blocks + kl / a.page_size] : -1;
+    const int32_t vblk = vl / a.page_size < a.v_max_blocks ? a.v_table[vs * a.v_max_blocks + vl / a.page_size] : -1;
+    if (threadIdx.x < kMaxFusedPairs) sden[threadIdx.x] = den;
+    if constexpr (STAGED) {
+        // unconditional stores (a guarded store would pull its load in behind
+        // the guard); clamped pieces rewrite the same bytes
+        uint4* s16 = reinterpret_cast<uint4*>(srow);
+        s16[v0] = p0;
+        s16[v1] = p1;
+        s16[v2] = p2;
+        s16[v3] = p3;
+    }
+    __syncthreads();  // the row is staged, and every thread has read the lengths before they advance
     if (pos < 0) {
         if (threadIdx.x == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_POSITION));
         pos = 0;
     }
-    const int32_t kblk = kl / a.page_size < a.k_max_blocks ? a.k_table[ks * a.k_max_blocks + kl / a.page_size] : -1;
-    const int32_t vblk = vl / a.page_size < a.v_max_blocks ? a.v_table[vs * a.v_max_blocks + vl / a.page_size] : -1;
+    const uint16_t* row = STAGED ? srow : grow;
     const int half = a.d >> 1;
-    const uint16_t* row = a.qkv + b * a.row_stride;
     const float fp = static_cast<float>(pos);
     const int64_t row_bytes = static_cast<int64_t>(a.d) * 2;
     for (int pi = threadIdx.x; pi < (a.hq + a.hkv) * half; pi += 256) {
@@ -161,7 +200,7 @@ __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a) {
         const int i0 = a.split_half ? i : 2 * i, i1 = a.split_half ? i + half : 2 * i + 1;
         const float x0 = bf16_to_f32(row[head * a.d + i0]), x1 = bf16_to_f32(row[head * a.d + i1]);
         float sn, cs;
-        rope_sincos(fp / a.denom[i], &sn, &cs);
+        rope_sincos(fp / sden[i], &sn, &cs);
         const uint16_t r0 = f32_to_bf16(__fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn)));
         const uint16_t r1 = f32_to_bf16(__fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs)));
         if (head < a.hq) {
@@ -177,11 +216,20 @@ __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a) {
     }
     if (vblk >= 0) {
         const uint16_t* v = row + (a.hq + a.hkv) * a.d;
-        for (int e = threadIdx.x; e < a.hkv * a.d; e += 256) {
-            const int kh = e / a.d;
-            uint16_t* vd = reinterpret_cast<uint16_t*>(
-                a.v_pages + vblk * a.page_bytes + (kh * a.page_size + vl % a.page_size) * row_bytes);
-            vd[e - kh * a.d] = v[e];
+        if constexpr (STAGED) {
+            for (int e8 = threadIdx.x; e8 < a.hkv * a.d / 8; e8 += 256) {
+                const int e = e8 * 8, kh = e / a.d;
+                char* vd = a.v_pages + vblk * a.page_bytes + (kh * a.page_size + vl % a.page_size) * row_bytes +
+                           static_cast<int64_t>(e - kh * a.d) * 2;
+                *reinterpret_cast<uint4*>(vd) = *reinterpret_cast<const uint4*>(v + e);
+            }
+        } else {
+            for (int e = threadIdx.x; e < a.hkv * a.d; e += 256) {
+                const int kh = e / a.d;
+                uint16_t* vd = reinterpret_cast<uint16_t*>(
+                    a.v_pages + vblk * a.page_bytes + (kh * a.page_size + vl % a.page_size) * row_bytes);
+                vd[e - kh * a.d] = v[e];
+            }
         }
     }
     __syncthreads();
@@ -670,7 +718,10 @@ int sandy_hip_device_decode_qkv(SandyHipDevice* d, uint32_t k_pool, const uint32
     a.errw = errw;
     // the rope kernel's denominators: theta^(2i/d) in float, as the CPU reference
     for (int i = 0; i < D / 2; i++) a.denom[i] = std::pow(th, static_cast<float>(2 * i) / static_cast<float>(D));
-    hipLaunchKernelGGL(decode_qkv_kernel, dim3(static_cast<unsigned>(count)), dim3(256), 0, d->impl.stream, a);
+    const bool staged = D % 8 == 0 && a.row_stride % 8 == 0 && (reinterpret_cast<uintptr_t>(a.qkv) & 15) == 0 &&
+                        (q_heads + 2 * hkv) * D * 2 <= kStageRowBytes;
+    if (staged) hipLaunchKernelGGL(decode_qkv_kernel<true>, dim3(static_cast<unsigned>(count)), dim3(256), 0, d->impl.stream, a);
+    else hipLaunchKernelGGL(decode_qkv_kernel<false>, dim3(static_cast<unsigned>(count)), dim3(256), 0, d->impl.stream, a);
     SANDY_HIP_TRY(hipGetLastError(), e, "decode qkv launch");
     return ok(e);
 }

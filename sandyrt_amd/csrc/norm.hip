@@ -25,7 +25,13 @@ constexpr int kRowsPerBlock = 4;  // 4 waves, one row each
 // is guarded (guards around the loads cost ~15% here by serialising them).
 // All of a lane's loads are issued before any value is used.  NTL reads the
 // streamed inputs non-temporally.
-template <typename T, int NCH, bool RESID, bool HASW, bool FULL, bool NTL>
+// Loads are issued before any is used, without guards: a chunk past the row
+// end re-reads the row's last chunk (its values are not used), since a
+// guarded load is sunk into its guard and waits there.  WPRE (few rows, a
+// latency-bound launch) also requests the weights with the row; with many
+// rows the weights are L2-resident and are read after the reduction, which
+// keeps the register count down.
+template <typename T, int NCH, bool RESID, bool HASW, bool FULL, bool WPRE>
 __global__ __launch_bounds__(256) void rms_rows_kernel(
         const void* __restrict__ x, const void* __restrict__ resid, const void* __restrict__ w,
         void* __restrict__ sum_out, void* __restrict__ out, int64_t rows, int cols, float eps) {
@@ -34,33 +40,38 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(
     if (row >= rows) return;
     const int chunks = cols >> 3;
     const int64_t base = row * cols;
-    typename Vec8<T>::raw xr[NCH], hr[NCH];
+    typename Vec8<T>::raw xr[NCH], hr[NCH], wr[NCH];
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
         const int c = lane + j * 64;
-        if (FULL || c < chunks) {
-            xr[j] = NTL ? Vec8<T>::load_raw_nt(x, base + c * 8) : Vec8<T>::load_raw(x, base + c * 8);
-            if constexpr (RESID)
-                hr[j] = NTL ? Vec8<T>::load_raw_nt(resid, base + c * 8) : Vec8<T>::load_raw(resid, base + c * 8);
+        const int cc = FULL || c < chunks ? c : chunks - 1;
+        xr[j] = Vec8<T>::load_raw_nt(x, base + cc * 8);
+        if constexpr (RESID) hr[j] = Vec8<T>::load_raw_nt(resid, base + cc * 8);
+    }
+    if constexpr (HASW && WPRE) {
+#pragma unroll
+        for (int j = 0; j < NCH; j++) {
+            const int c = lane + j * 64;
+            wr[j] = Vec8<T>::load_raw(w, (FULL || c < chunks ? c : chunks - 1) * 8);
         }
+        __builtin_amdgcn_sched_barrier(0);  // keep them in flight with the row (not sunk to their use)
     }
     float v[NCH][8];
     double acc = 0.0;
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
         const int c = lane + j * 64;
-        if (FULL || c < chunks) {
-            Vec8<T>::unpack(xr[j], v[j]);
-            if constexpr (RESID) {
-                float h[8];
-                Vec8<T>::unpack(hr[j], h);
+        const bool in = FULL || c < chunks;
+        Vec8<T>::unpack(xr[j], v[j]);
+        if constexpr (RESID) {
+            float h[8];
+            Vec8<T>::unpack(hr[j], h);
 #pragma unroll
-                for (int i = 0; i < 8; i++) v[j][i] = Vec8<T>::round(__fadd_rn(v[j][i], h[i]));
-                Vec8<T>::store(sum_out, base + c * 8, v[j]);
-            }
-#pragma unroll
-            for (int i = 0; i < 8; i++) acc += static_cast<double>(v[j][i]) * static_cast<double>(v[j][i]);
+            for (int i = 0; i < 8; i++) v[j][i] = Vec8<T>::round(__fadd_rn(v[j][i], h[i]));
+            if (in) Vec8<T>::store(sum_out, base + c * 8, v[j]);
         }
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc += in ? static_cast<double>(v[j][i]) * static_cast<double>(v[j][i]) : 0.0;
     }
     acc = wave_sum(acc);
     const float inv = 1.0f / sqrtf(static_cast<float>(acc / static_cast<double>(cols)) + eps);
@@ -70,7 +81,10 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(
         if (FULL || c < chunks) {
             float y[8];
             float wv[8];
-            if constexpr (HASW) Vec8<T>::load(w, c * 8, wv);
+            if constexpr (HASW) {
+                if constexpr (WPRE) Vec8<T>::unpack(wr[j], wv);
+                else Vec8<T>::load(w, c * 8, wv);
+            }
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 y[i] = __fmul_rn(v[j][i], inv);
@@ -194,12 +208,18 @@ __global__ __launch_bounds__(256) void norm_generic_kernel(
 template <typename T, int NCH, bool RESID, bool HASW>
 void launch_rms_n(bool full, dim3 grid, hipStream_t s, const void* x, const void* r, const void* w, void* so,
                   void* out, int64_t rows, int cols, float eps) {
-    if (full)
-        hipLaunchKernelGGL((rms_rows_kernel<T, NCH, RESID, HASW, true, true>), grid, dim3(256), 0, s, x, r, w, so,
-                           out, rows, cols, eps);
-    else
-        hipLaunchKernelGGL((rms_rows_kernel<T, NCH, RESID, HASW, false, true>), grid, dim3(256), 0, s, x, r, w,
-                           so, out, rows, cols, eps);
+    // weights with the row when the launch is a few waves (latency-bound)
+    const bool wpre = rows <= 1024;
+#define RMS_LAUNCH(F, P) \
+    hipLaunchKernelGGL((rms_rows_kernel<T, NCH, RESID, HASW, F, P>), grid, dim3(256), 0, s, x, r, w, so, out, rows, cols, eps)
+    if (full) {
+        if (wpre) RMS_LAUNCH(true, true);
+        else RMS_LAUNCH(true, false);
+    } else {
+        if (wpre) RMS_LAUNCH(false, true);
+        else RMS_LAUNCH(false, false);
+    }
+#undef RMS_LAUNCH
 }
 
 template <typename T, bool RESID, bool HASW>
