@@ -103,25 +103,43 @@ template <typename T, int NV>
 __global__ __launch_bounds__(256) void topk_rank_kernel(const void* __restrict__ x, void* __restrict__ values,
                                                         void* __restrict__ indices, int32_t idx_dt, int64_t rows,
                                                         int axis, int k) {
-    __shared__ float row_v[4][64 * NV];
+    __shared__ __attribute__((aligned(16))) float row_v[4][64 * NV];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wave;
     if (row >= rows) return;
     float v[NV];
+    // unguarded loads (clamped index), so all are in flight at once; slots
+    // past the row hold -inf, which never ranks above an element (a tie
+    // at -inf goes to the lower index, and every pad index is higher)
 #pragma unroll
     for (int j = 0; j < NV; j++) {
         const int c = lane + 64 * j;
-        v[j] = c < axis ? Vec8<T>::load1(x, row * axis + c) : 0.0f;
-        if (c < axis) row_v[wave][c] = v[j];
+        v[j] = Vec8<T>::load1(x, row * axis + (c < axis ? c : axis - 1));
+    }
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int c = lane + 64 * j;
+        row_v[wave][c] = c < axis ? v[j] : -INFINITY;
     }
     __builtin_amdgcn_wave_barrier();
     int rank[NV];
 #pragma unroll
     for (int j = 0; j < NV; j++) rank[j] = 0;
-    for (int a = 0; a < axis; a++) {
-        const float o = row_v[wave][a];
+    // eight elements per step from two 128-bit LDS reads, the next step's
+    // reads issued before this step's compares
+    const float4* rv4 = reinterpret_cast<const float4*>(row_v[wave]);
+    const int steps = (axis + 7) / 8;  // 64 * NV is a multiple of 8: reads stay inside the row
+    float4 c0 = rv4[0], c1 = rv4[1];
+    for (int s8 = 0; s8 < steps; s8++) {
+        const int nx = s8 + 1 < steps ? s8 + 1 : s8;
+        const float4 n0 = rv4[2 * nx], n1 = rv4[2 * nx + 1];
+        const float o[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
 #pragma unroll
-        for (int j = 0; j < NV; j++) rank[j] += better(o, a, v[j], lane + 64 * j) ? 1 : 0;
+        for (int q = 0; q < 8; q++)
+#pragma unroll
+            for (int j = 0; j < NV; j++) rank[j] += better(o[q], 8 * s8 + q, v[j], lane + 64 * j) ? 1 : 0;
+        c0 = n0;
+        c1 = n1;
     }
 #pragma unroll
     for (int j = 0; j < NV; j++) {

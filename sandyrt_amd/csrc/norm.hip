@@ -106,11 +106,22 @@ __global__ __launch_bounds__(256) void layer_rows_kernel(
     const int64_t base = row * cols;
     float v[NCH][8];
     double sum = 0.0;
+    // row, weight and bias loads all issued first, unguarded (clamped chunk:
+    // a guarded load waits behind its guard); used only for c < chunks
+    typename Vec8<T>::raw xr[NCH], wr[NCH], br[NCH];
 #pragma unroll
     for (int j = 0; j < NCH; j++) {
         const int c = lane + j * 64;
+        const int cc = c < chunks ? c : chunks - 1;
+        xr[j] = Vec8<T>::load_raw(x, base + cc * 8);
+        wr[j] = Vec8<T>::load_raw(w, cc * 8);
+        br[j] = Vec8<T>::load_raw(b, cc * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        const int c = lane + j * 64;
+        Vec8<T>::unpack(xr[j], v[j]);
         if (c < chunks) {
-            Vec8<T>::load(x, base + c * 8, v[j]);
 #pragma unroll
             for (int i = 0; i < 8; i++) sum += static_cast<double>(v[j][i]);
         }
@@ -136,8 +147,8 @@ __global__ __launch_bounds__(256) void layer_rows_kernel(
         const int c = lane + j * 64;
         if (c < chunks) {
             float wv[8], bv[8], y[8];
-            Vec8<T>::load(w, c * 8, wv);
-            Vec8<T>::load(b, c * 8, bv);
+            Vec8<T>::unpack(wr[j], wv);
+            Vec8<T>::unpack(br[j], bv);
 #pragma unroll
             for (int i = 0; i < 8; i++)
                 y[i] = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(v[j][i], meanf), inv), wv[i]), bv[i]);

@@ -28,9 +28,15 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const void* __restric
     float v[NCH];
     float m = -INFINITY;
 #pragma unroll
+    // unguarded loads (clamped index) so that all are in flight at once; a
+    // guarded load waits behind its guard
     for (int j = 0; j < NCH; j++) {
         const int c = lane + j * 64;
-        v[j] = c < cols ? Vec8<T>::load1(x, base + c) : -INFINITY;
+        v[j] = Vec8<T>::load1(x, base + (c < cols ? c : cols - 1));
+    }
+#pragma unroll
+    for (int j = 0; j < NCH; j++) {
+        v[j] = lane + j * 64 < cols ? v[j] : -INFINITY;
         m = fmaxf(m, v[j]);
     }
     m = wave_max(m);
