@@ -127,7 +127,8 @@ def test_router_chain_config5(ops, oracle):
 # ------------------------------------------------------------------ moe_gather
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("T,H,E,K", [(512, 2816, 128, 8), (37, 64, 16, 4), (5, 24, 300, 2), (1, 8, 4, 1),
-                                     (700, 16, 64, 8), (130, 16, 8, 3), (1100, 16, 64, 8), (3, 20, 1, 1)])
+                                     (700, 16, 64, 8), (130, 16, 8, 3), (1024, 16, 64, 8), (1100, 16, 64, 8),
+                                     (3, 20, 1, 1)])
 @pytest.mark.parametrize("idx", [np.int64, np.int32])
 @pytest.mark.parametrize("ranking", ["dispatch", "general"])
 def test_moe_gather_bit_exact(ops, oracle, monkeypatch, dtype, T, H, E, K, idx, ranking):
