@@ -844,6 +844,110 @@ __global__ __launch_bounds__(256) void attention_general_kernel(GenArgs a) {
     }
 }
 
+// The same algorithm and operation order for up to kGenStage keys, with the
+// round trips cut: each key's thread looks up its K and V rows once (paged:
+// one block-table read each, issued together) and keeps the V row offset in
+// LDS; the K row is requested 64 values at a time ahead of the in-order dot
+// product; scores and probabilities stay in LDS; P.V reads 32 keys' values
+// per batch, all in flight, from the staged offsets (clamped key, kept by a
+// select).  Results are identical to attention_general_kernel.
+constexpr int kGenStage = 2048;
+
+template <typename T>
+__global__ __launch_bounds__(256) void attention_staged_kernel(GenArgs a) {
+    constexpr int kC = 64;  // K values in flight per key
+    constexpr int kV = 32;  // keys per P.V batch
+    __shared__ float fred[4];
+    __shared__ double dred[4];
+    __shared__ float qv[512];
+    __shared__ float ssc[kGenStage];
+    __shared__ float sprob[kGenStage];
+    __shared__ int64_t svrow[kGenStage];
+    const int qi = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int kh = h / (a.hq / a.hkv);
+    int64_t base_pos = 0;
+    if (a.pos) {
+        base_pos = load_index(a.pos, a.pos_dt, b);
+        if (base_pos < 0) {
+            if (tid == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
+            return;
+        }
+    }
+    const int64_t qpos = base_pos + qi;
+    const int64_t min_key = a.window > 0 ? max<int64_t>(0, qpos + 1 - a.window) : 0;
+    const int64_t tk = a.tk;
+    const int64_t D = a.d;
+    const int64_t qoff = b * a.qs[0] + h * a.qs[1] + qi * a.qs[2];
+    for (int64_t d = tid; d < D; d += 256) qv[d] = Vec8<T>::load1(a.q, qoff + d * a.qs[3]);
+    __syncthreads();
+    const int64_t kd = a.paged ? 1 : a.ks[3];
+    const int64_t vd = a.paged ? 1 : a.vs[3];
+    float lmax = -INFINITY;
+    bool ok = true;
+    for (int64_t key = tid; key < tk; key += 256) {
+        float s = -INFINITY;
+        const bool live = key <= qpos && key >= min_key;
+        const int64_t krow = live ? kv_row(a, a.ks, b, kh, key, ok) : 0;
+        svrow[key] = live ? kv_row(a, a.vs, b, kh, key, ok) : 0;
+        if (live) {
+            float acc = 0.0f;
+            for (int64_t d0 = 0; d0 < D; d0 += kC) {
+                float kv[kC];
+#pragma unroll
+                for (int j = 0; j < kC; j++) kv[j] = Vec8<T>::load1(a.k, krow + (d0 + j < D ? d0 + j : D - 1) * kd);
+#pragma unroll
+                for (int j = 0; j < kC; j++)
+                    if (d0 + j < D) acc = __fadd_rn(acc, __fmul_rn(qv[d0 + j], kv[j]));
+            }
+            s = __fmul_rn(acc, a.scale);
+        }
+        ssc[key] = s;
+        lmax = fmaxf(lmax, s);
+    }
+    if (!ok) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
+    lmax = wave_max(lmax);
+    if ((tid & 63) == 0) fred[tid >> 6] = lmax;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(fred[0], fred[1]), fmaxf(fred[2], fred[3]));
+    const int64_t ooff = b * a.os[0] + h * a.os[1] + qi * a.os[2];
+    if (mx == -INFINITY) {
+        for (int64_t d = tid; d < D; d += 256) Vec8<T>::store1(a.out, ooff + d * a.os[3], 0.0f);
+        return;
+    }
+    double sum = 0.0;
+    for (int64_t key = tid; key < tk; key += 256) sum += exp(static_cast<double>(__fsub_rn(ssc[key], mx)));
+    sum = wave_sum(sum);
+    if ((tid & 63) == 0) dred[tid >> 6] = sum;
+    __syncthreads();
+    const double total = dred[0] + dred[1] + dred[2] + dred[3];
+    const float inv = total != 0.0 ? 1.0f / static_cast<float>(total) : 0.0f;
+    for (int64_t key = tid; key < tk; key += 256) sprob[key] = __fmul_rn(expf(__fsub_rn(ssc[key], mx)), inv);
+    __syncthreads();
+    const int64_t k_end = min<int64_t>(tk, qpos + 1);
+    for (int64_t d = tid; d < D; d += 256) {
+        float acc = 0.0f;
+        if (total != 0.0) {
+            for (int64_t k0 = min_key; k0 < k_end; k0 += kV) {
+                float vv[kV];
+#pragma unroll
+                for (int j = 0; j < kV; j++) {
+                    const int64_t key = k0 + j < k_end ? k0 + j : k_end - 1;
+                    vv[j] = Vec8<T>::load1(a.v, svrow[key] + d * vd);
+                }
+#pragma unroll
+                for (int j = 0; j < kV; j++) {
+                    const int64_t key = k0 + j;
+                    if (key >= k_end) break;
+                    const float sv = ssc[key];
+                    acc = __fadd_rn(acc, sv == -INFINITY ? 0.0f : __fmul_rn(sprob[key], vv[j]));
+                }
+            }
+        }
+        Vec8<T>::store1(a.out, ooff + d * a.os[3], acc);
+    }
+}
+
 int env_int(const char* name, int dflt) {
     const char* v = std::getenv(name);
     return v ? std::atoi(v) : dflt;
@@ -918,8 +1022,14 @@ extern "C" int sandy_hip_attention(const SandyTensor* q, const SandyTensor* k, c
     if (status) return status;
     a.errw = errw;
     dim3 grid(static_cast<unsigned>(tq), static_cast<unsigned>(hq), static_cast<unsigned>(B));
-    if (q->dtype == SANDY_BF16) hipLaunchKernelGGL(attention_general_kernel<BF16>, grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL(attention_general_kernel<F32>, grid, dim3(256), 0, stream, a);
+    if (a.tk <= kGenStage && env_int("SANDY_ATTN_UNSTAGED", 0) == 0) {
+        if (q->dtype == SANDY_BF16) hipLaunchKernelGGL(attention_staged_kernel<BF16>, grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL(attention_staged_kernel<F32>, grid, dim3(256), 0, stream, a);
+    } else if (q->dtype == SANDY_BF16) {
+        hipLaunchKernelGGL(attention_general_kernel<BF16>, grid, dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL(attention_general_kernel<F32>, grid, dim3(256), 0, stream, a);
+    }
     SANDY_HIP_TRY(hipGetLastError(), e, "attention launch");
     return ok(e);
 }
@@ -1072,8 +1182,14 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
     if (status) return status;
     a.errw = errw;
     dim3 grid(1, static_cast<unsigned>(hq), static_cast<unsigned>(B));
-    if (q->dtype == SANDY_BF16) hipLaunchKernelGGL(attention_general_kernel<BF16>, grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL(attention_general_kernel<F32>, grid, dim3(256), 0, stream, a);
+    if (a.tk <= kGenStage && env_int("SANDY_ATTN_UNSTAGED", 0) == 0) {
+        if (q->dtype == SANDY_BF16) hipLaunchKernelGGL(attention_staged_kernel<BF16>, grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL(attention_staged_kernel<F32>, grid, dim3(256), 0, stream, a);
+    } else if (q->dtype == SANDY_BF16) {
+        hipLaunchKernelGGL(attention_general_kernel<BF16>, grid, dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL(attention_general_kernel<F32>, grid, dim3(256), 0, stream, a);
+    }
     SANDY_HIP_TRY(hipGetLastError(), e, "paged attention launch");
     return ok(e);
 }

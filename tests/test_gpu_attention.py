@@ -161,6 +161,47 @@ def test_dense_attention(ops, oracle, dtype, case):
     assert_close(got, want, dtype, f"attention {case}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_general_attention_staged_equals_unstaged(ops, monkeypatch, dtype):
+    """Up to 2048 keys the general attention runs its staged form (row
+    offsets, scores and probabilities in LDS, batched K/V loads);
+    SANDY_ATTN_UNSTAGED forces the per-use form.  Same operation order:
+    the outputs must agree bit for bit (dense and paged, windows, head
+    dimensions that are not a multiple of the 64-value K batch)."""
+    r = rng(77)
+    for B, hq, hkv, tq, tk, D, window, pos in [(2, 8, 2, 1, 300, 64, 0, [299, 17]), (1, 4, 1, 3, 90, 100, 20, [80]),
+                                              (1, 2, 2, 1, 2048, 64, 0, [2047]), (2, 2, 1, 2, 33, 512, 0, None)]:
+        q = from_f32(normal(r, (B, hq, tq, D), 0.35), dtype)
+        k = from_f32(normal(r, (B, hkv, tk, D), 0.35), dtype)
+        v = from_f32(normal(r, (B, hkv, tk, D)), dtype)
+        p_ = torch.tensor(pos, device="cuda") if pos is not None else None
+        got = ops.attention(q, k, v, p_, window, -1.0)
+        monkeypatch.setenv("SANDY_ATTN_UNSTAGED", "1")
+        want = ops.attention(q, k, v, p_, window, -1.0)
+        monkeypatch.delenv("SANDY_ATTN_UNSTAGED")
+        assert torch.equal(got, want), (B, hq, hkv, tq, tk, D)
+    # paged pools with small pages (the general kernel's paged form)
+    q, kpool, vpool, table, pos = make_paged(r, 3, 4, 2, 64, 2, [1, 9, 30], 30, dtype)
+    args = (q, ops.PagedCache(kpool), ops.PagedCache(vpool), torch.from_numpy(table).cuda(), torch.from_numpy(pos).cuda())
+    got = ops.paged_attention(*args, window=5)
+    monkeypatch.setenv("SANDY_ATTN_UNSTAGED", "1")
+    want = ops.paged_attention(*args, window=5)
+    monkeypatch.delenv("SANDY_ATTN_UNSTAGED")
+    assert torch.equal(got, want), "paged"
+
+
+def test_general_attention_long_keys_unstaged(ops, oracle):
+    """More than 2048 keys take the per-use form (scores in the workspace)."""
+    r = rng(78)
+    q = from_f32(normal(r, (1, 2, 1, 64), 0.35), torch.float32)
+    k = from_f32(normal(r, (1, 1, 2500, 64), 0.35), torch.float32)
+    v = from_f32(normal(r, (1, 1, 2500, 64)), torch.float32)
+    pos = torch.tensor([2400], device="cuda")
+    got = ops.attention(q, k, v, pos, 0, -1.0)
+    want = oracle.attention(to_oracle(q), to_oracle(k), to_oracle(v), pos.cpu().numpy(), 0, -1.0)
+    assert_close(got, want, torch.float32, "attention 2500 keys")
+
+
 def test_dense_attention_seeded_fuzz(ops, oracle):
     """The reference's own fuzz recipe (CudaDeviceTest.cpp:3082-3170): seed
     0x5a17d00d, uniform inputs, random windows, offsets and GQA groups."""
