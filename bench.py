@@ -55,6 +55,8 @@ def parse():
     p.add_argument("--only", default="", help="comma list of kernels to run (profiling)")
     p.add_argument("--no-extras", action="store_true", help="skip the per-kernel table of the other configs")
     p.add_argument("--no-decode-step", action="store_true", help="skip the whole-model decode tok/s measurement")
+    p.add_argument("--gpt2-only", action="store_true",
+                   help="only config 1 (GPT-2 greedy decode on the GPU, tokens checked against the CPU chain)")
     p.add_argument("--decode-step-only", action="store_true",
                    help="only the whole-model decode step at config 3's batch and contexts (profiling)")
     p.add_argument("--calibrate-copy", action="store_true",
@@ -547,6 +549,9 @@ def main():
 
     _lib.lib()  # fail loudly if the backend is not built
     torch.cuda.set_device(0)
+    if args.gpt2_only:
+        print(json.dumps({"metric": "GPT-2 small greedy decode (config 1)", **gpt2_config1()}), flush=True)
+        return
     if args.decode_step_only:
         import numpy as np
         ctx = np.random.default_rng(2).integers(512, 4097, DEC_B)
