@@ -126,7 +126,8 @@ def test_rope_whole_line_kernel_equals_half_row_kernel(ops, monkeypatch, dtype):
     kernel (partner lanes swap halves); SANDY_ROPE_HALVES forces the half-row
     kernel: both must agree bit for bit, partial rotary and ids included."""
     r = rng(23)
-    for shape, rot in [((1, 32, 300, 64), -1), ((2, 4, 33, 128), -1), ((1, 2, 9, 512), 128), ((3, 5, 16), -1)]:
+    for shape, rot in [((1, 32, 300, 64), -1), ((2, 4, 33, 128), -1), ((1, 2, 9, 512), 128), ((3, 5, 16), -1),
+                       ((1, 36, 4096, 64), -1)]:  # 36 heads: groups of 6
         x = from_f32(normal(r, shape), dtype)
         ids = torch.tensor([17], device="cuda")
         got = ops.rope(x, 1e4, rotary_dim=rot, split_half=True, position_ids=ids)
