@@ -36,7 +36,9 @@ __global__ __launch_bounds__(256) void rms_rows_kernel(
         const void* __restrict__ x, const void* __restrict__ resid, const void* __restrict__ w,
         void* __restrict__ sum_out, void* __restrict__ out, int64_t rows, int cols, float eps) {
     const int lane = threadIdx.x & 63;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+    // a wave per row: WPRE launches one-wave workgroups, the others four
+    const int64_t row = WPRE ? static_cast<int64_t>(blockIdx.x)
+                             : static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
     if (row >= rows) return;
     const int chunks = cols >> 3;
     const int64_t base = row * cols;
@@ -219,10 +221,13 @@ __global__ __launch_bounds__(256) void norm_generic_kernel(
 template <typename T, int NCH, bool RESID, bool HASW>
 void launch_rms_n(bool full, dim3 grid, hipStream_t s, const void* x, const void* r, const void* w, void* so,
                   void* out, int64_t rows, int cols, float eps) {
-    // weights with the row when the launch is a few waves (latency-bound)
+    // weights with the row when the launch is a few waves (latency-bound);
+    // then also one wave per workgroup, so the rows spread over as many CUs
     const bool wpre = rows <= 1024;
+    const dim3 g = wpre ? dim3(static_cast<unsigned>(rows)) : grid;
+    const dim3 blk = wpre ? dim3(64) : dim3(256);
 #define RMS_LAUNCH(F, P) \
-    hipLaunchKernelGGL((rms_rows_kernel<T, NCH, RESID, HASW, F, P>), grid, dim3(256), 0, s, x, r, w, so, out, rows, cols, eps)
+    hipLaunchKernelGGL((rms_rows_kernel<T, NCH, RESID, HASW, F, P>), g, blk, 0, s, x, r, w, so, out, rows, cols, eps)
     if (full) {
         if (wpre) RMS_LAUNCH(true, true);
         else RMS_LAUNCH(true, false);
