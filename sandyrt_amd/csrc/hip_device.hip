@@ -86,13 +86,40 @@ __global__ __launch_bounds__(256) void paged_append_step_kernel(const char* __re
                                                                 int64_t prefix, int64_t page_size, int64_t row_bytes,
                                                                 int64_t page_bytes, uint32_t* errw, StepArgs args) {
     const int i = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    // rows of up to 1 KiB (16-byte multiples), up to 16 of them: this thread's
+    // pieces (rows wave + 4j, piece lane) are requested before the
+    // slot -> length -> block-table chain they do not depend on
+    const bool pre = (row_bytes & 15) == 0 && row_bytes <= 1024 && prefix <= 16;
+    // (four named registers: an array here was placed in LDS, whose writes
+    // waited for the loads)
+    uint4 p0{}, p1{}, p2{}, p3{};
+    const int w4 = threadIdx.x >> 6;
+    if (pre) {
+        const int64_t np = row_bytes / 16;
+        const int64_t lc = lane < np ? lane : np - 1;
+        const char* rb = rows + static_cast<int64_t>(i) * prefix * row_bytes + lc * 16;
+        auto at = [&](int64_t p) { return reinterpret_cast<const uint4*>(rb + (p < prefix ? p : prefix - 1) * row_bytes); };
+        p0 = *at(w4);
+        p1 = *at(w4 + 4);
+        p2 = *at(w4 + 8);
+        p3 = *at(w4 + 12);
+    }
     const int32_t slot = args.slots[i];
     const int32_t len = lengths[slot];
     __syncthreads();  // every wave has read the length before it advances
     const int32_t page = len / page_size;
     const int32_t blk = page < max_blocks ? table[slot * max_blocks + page] : -1;
-    if (blk >= 0) {
-        const int lane = threadIdx.x & 63;
+    if (blk >= 0 && pre) {
+        char* db = pages + blk * page_bytes + (len % page_size) * row_bytes + lane * 16;
+        const int64_t pstride = page_size * row_bytes;
+        if (lane * 16 < row_bytes) {
+            if (w4 < prefix) *reinterpret_cast<uint4*>(db + w4 * pstride) = p0;
+            if (w4 + 4 < prefix) *reinterpret_cast<uint4*>(db + (w4 + 4) * pstride) = p1;
+            if (w4 + 8 < prefix) *reinterpret_cast<uint4*>(db + (w4 + 8) * pstride) = p2;
+            if (w4 + 12 < prefix) *reinterpret_cast<uint4*>(db + (w4 + 12) * pstride) = p3;
+        }
+    } else if (blk >= 0) {
         for (int64_t p = threadIdx.x >> 6; p < prefix; p += 4) {
             const char* s = rows + (static_cast<int64_t>(i) * prefix + p) * row_bytes;
             char* d = pages + blk * page_bytes + (p * page_size + len % page_size) * row_bytes;
