@@ -244,7 +244,9 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
             blkv = in && ok ? id : -1;
         }
         auto blk_of = [&](int it) -> int32_t { return __builtin_amdgcn_readlane(blkv, it); };
-        auto key0_of = [&](int it) -> int64_t { return sr.key_begin + 16 * (c0 + wave + 4 * it); };
+        // key indices fit 32 bits (the host keeps max_blocks * page_size below 2^31)
+        const int n_keys = static_cast<int>(sr.n_keys), min_key = static_cast<int>(sr.min_key);
+        auto key0_of = [&](int it) -> int { return static_cast<int>(sr.key_begin + 16 * (c0 + wave + 4 * it)); };
 
         // A batch of NB tiles: S^T on MFMA, one online-softmax update for the
         // whole batch (one cross-lane max and sum), V^T through LDS, PV on MFMA.
@@ -261,7 +263,7 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
             float mx = -INFINITY;
 #pragma unroll
             for (int n = 0; n < NB; n++) {
-                const int64_t t0 = key0_of(it0 + n);
+                const int t0 = key0_of(it0 + n);
                 f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int kk = 0; kk < D / 32; kk++)
@@ -269,14 +271,13 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
                                                                  __builtin_bit_cast(bf16x8_t, qv[kk]), sc, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int64_t key = t0 + 4 * j + i;
-                    const bool valid = live_n[n] && key < sr.n_keys && key >= sr.min_key;
+                    const int key = t0 + 4 * j + i;
+                    const bool valid = live_n[n] && key < n_keys && key >= min_key;
                     sv[n][i] = valid ? sc[i] * a.scale_log2 : -INFINITY;
                     mx = fmaxf(mx, sv[n][i]);
                 }
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = max_xor32(max_xor16(mx));
             const float m_new = fmaxf(m, mx);
             float p[NB][4];
             float rs = 0.0f;
@@ -284,13 +285,12 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
             for (int n = 0; n < NB; n++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const float e2 = exp2f(sv[n][i] - m_new);
+                    const float e2 = __builtin_amdgcn_exp2f(sv[n][i] - m_new);
                     p[n][i] = sv[n][i] == -INFINITY ? 0.0f : bf16_to_f32(f32_to_bf16(e2));
                     rs += p[n][i];
                 }
-            rs += __shfl_xor(rs, 16, 64);
-            rs += __shfl_xor(rs, 32, 64);
-            const float alpha = m == -INFINITY ? (m_new == -INFINITY ? 1.0f : 0.0f) : exp2f(m - m_new);
+            rs = sum_xor32(sum_xor16(rs));
+            const float alpha = m == -INFINITY ? (m_new == -INFINITY ? 1.0f : 0.0f) : __builtin_amdgcn_exp2f(m - m_new);
             l = l * alpha + rs;
             m = m_new;
 #pragma unroll
@@ -299,8 +299,8 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
             // V tiles -> LDS (row = key; masked keys zeroed so they cannot inject NaN)
 #pragma unroll
             for (int n = 0; n < NB; n++) {
-                const int64_t vkey = key0_of(it0 + n) + (lane & 15);
-                const bool vvalid = live_n[n] && vkey < sr.n_keys && vkey >= sr.min_key;
+                const int vkey = key0_of(it0 + n) + (lane & 15);
+                const bool vvalid = live_n[n] && vkey < n_keys && vkey >= min_key;
                 unsigned char* row = vl + (n * 16 + (lane & 15)) * kRow + 16 * j;
 #pragma unroll
                 for (int kk = 0; kk < D / 32; kk++) {
@@ -376,7 +376,7 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
             for (int w = 0; w < 4; w++) {
                 const float mw = ml[(w * G + gg) * 2];
                 if (mw == -INFINITY) continue;
-                const float f = exp2f(mw - M);
+                const float f = __builtin_amdgcn_exp2f(mw - M);
                 O0 += red[(w * G + gg) * D + d] * f;
                 O1 += red[(w * G + gg) * D + d + 1] * f;
                 L += ml[(w * G + gg) * 2 + 1] * f;
@@ -516,8 +516,8 @@ __device__ __forceinline__ void fused_merge(const PagedArgs& a, int b, int kh, i
                 const float ms = __uint_as_float(static_cast<uint32_t>(mv[q]));
                 if (s0 + q >= n_splits || ms == -INFINITY) continue;
                 const float mn = fmaxf(M, ms);
-                const float fo = M == -INFINITY ? 0.0f : exp2f(M - mn);
-                const float fs = exp2f(ms - mn);
+                const float fo = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - mn);
+                const float fs = __builtin_amdgcn_exp2f(ms - mn);
                 L = L * fo + __uint_as_float(static_cast<uint32_t>(mv[q] >> 32)) * fs;
                 O0 = O0 * fo + __uint_as_float(static_cast<uint32_t>(ov[q])) * fs;
                 O1 = O1 * fo + __uint_as_float(static_cast<uint32_t>(ov[q] >> 32)) * fs;
@@ -660,8 +660,8 @@ __global__ __launch_bounds__(64) void paged_decode_units_merge_kernel(PagedArgs 
         for (int u = 0; u < R; u++) {
             if (s0 + u >= n_splits || ms[u] == -INFINITY) continue;
             const float mn = fmaxf(M, ms[u]);
-            const float fo = M == -INFINITY ? 0.0f : exp2f(M - mn);
-            const float fs = exp2f(ms[u] - mn);
+            const float fo = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - mn);
+            const float fs = __builtin_amdgcn_exp2f(ms[u] - mn);
             L = L * fo + ls[u] * fs;
 #pragma unroll
             for (int i = 0; i < PER; i++) O[i] = O[i] * fo + os[u][i] * fs;
@@ -1072,7 +1072,7 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
                          q->strides[0] % 8 == 0 && q->strides[1] % 8 == 0 && out->strides[0] % 2 == 0 &&
                          out->strides[1] % 2 == 0 && (reinterpret_cast<uintptr_t>(base_ptr(*out)) & 3u) == 0;
     const bool mfma = q->dtype == SANDY_BF16 && (D == 64 || D == 128 || D == 256) && G <= 16 && P % 16 == 0 &&
-                      table->dims[1] > 0 &&
+                      table->dims[1] > 0 && table->dims[1] * P <= (1LL << 30) &&
                       aligned && env_int("SANDY_PAGED_GENERIC", 0) == 0;
     if (mfma) {
         PagedArgs a{};

@@ -281,6 +281,28 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Lane l combined with lane l ^ 16 (or l ^ 32) through gfx950's
+// v_permlane16_swap / v_permlane32_swap: with both operands v, the pair
+// returned holds v[l & ~16] and v[l | 16] (v[l & 31] and v[l | 32]), so one
+// VALU exchange replaces an LDS-routed ds_bpermute.  The result is the same
+// in both lanes of a pair (max and + are commutative).
+__device__ __forceinline__ float max_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 constexpr int kWave = 64;
 
 } // namespace sandy_hip
