@@ -38,8 +38,8 @@
 //     reading the position alongside the first partials) is kept behind
 //     SANDY_PAGED_FUSED_MERGE=0.  No host round trip and no allocation per
 //     call.
-// The probabilities fed to the PV product are rounded to bf16 and the
-// normaliser sums those rounded values, so O / L stays a convex combination.
+// The probabilities enter the PV product as two bf16 operands (hi + lo), so
+// P keeps about 17 bits and the normaliser is the float sum of the same p.
 #include "common.h"
 
 #include <algorithm>
@@ -85,11 +85,17 @@ struct PagedArgs {
     int32_t fused;       // merge in the last-arriving workgroup of each (sequence, kv head)
 };
 
-__device__ __forceinline__ short4_t pack_p(const float (&p)[4]) {
-    short4_t r;
+// p = hi + lo with hi = bf16(p) and lo = bf16(p - hi): two bf16 MFMA operands
+// that carry p to about 2^-17 relative, so P.V on bf16 MFMA keeps the float
+// probabilities of the reference (TensorCalc.cpp:1167-1314) instead of
+// bf16-rounded ones.
+__device__ __forceinline__ void split_p(const float (&p)[4], short4_t& hi, short4_t& lo) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) r[i] = static_cast<short>(f32_to_bf16(p[i]));
-    return r;
+    for (int i = 0; i < 4; i++) {
+        const uint16_t h = f32_to_bf16(p[i]);
+        hi[i] = static_cast<short>(h);
+        lo[i] = static_cast<short>(f32_to_bf16(p[i] - bf16_to_f32(h)));
+    }
 }
 
 template <int D>
@@ -286,7 +292,7 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const float e2 = __builtin_amdgcn_exp2f(sv[n][i] - m_new);
-                    p[n][i] = sv[n][i] == -INFINITY ? 0.0f : bf16_to_f32(f32_to_bf16(e2));
+                    p[n][i] = sv[n][i] == -INFINITY ? 0.0f : e2;
                     rs += p[n][i];
                 }
             rs = sum_xor32(sum_xor16(rs));
@@ -313,7 +319,8 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int n = 0; n < NB; n++) {
-                const short4_t pb = pack_p(p[n]);
+                short4_t pb, pl;
+                split_p(p[n], pb, pl);
 #pragma unroll
                 for (int t = 0; t < D / 16; t++) {
                     // ds_read_b64_tr_b16: in each 16-lane group, lane i gets element i % 4 of the
@@ -324,6 +331,7 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
                     const short4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                         (short4_t __attribute__((address_space(3)))*)((unsigned char __attribute__((address_space(3)))*)src));
                     acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pl, acc[t], 0, 0, 0);
                 }
             }
             __builtin_amdgcn_wave_barrier();

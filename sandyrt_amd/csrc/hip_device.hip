@@ -84,13 +84,16 @@ __global__ __launch_bounds__(256) void paged_append_step_kernel(const char* __re
                                                                 const int32_t* __restrict__ table,
                                                                 int32_t* __restrict__ lengths, int64_t max_blocks,
                                                                 int64_t prefix, int64_t page_size, int64_t row_bytes,
-                                                                int64_t page_bytes, uint32_t* errw, StepArgs args) {
+                                                                int64_t page_bytes, uint32_t* errw, StepArgs args,
+                                                                int32_t aligned16) {
     const int i = blockIdx.x;
     const int lane = threadIdx.x & 63;
-    // rows of up to 1 KiB (16-byte multiples), up to 16 of them: this thread's
-    // pieces (rows wave + 4j, piece lane) are requested before the
-    // slot -> length -> block-table chain they do not depend on
-    const bool pre = (row_bytes & 15) == 0 && row_bytes <= 1024 && prefix <= 16;
+    // rows of up to 1 KiB (16-byte multiples at 16-byte aligned addresses:
+    // `aligned16` covers the rows view and the page pool), up to 16 of them:
+    // this thread's pieces (rows wave + 4j, piece lane) are requested before
+    // the slot -> length -> block-table chain they do not depend on
+    const bool vec = aligned16 && (row_bytes & 15) == 0;
+    const bool pre = vec && row_bytes <= 1024 && prefix <= 16;
     // (four named registers: an array here was placed in LDS, whose writes
     // waited for the loads)
     uint4 p0{}, p1{}, p2{}, p3{};
@@ -123,7 +126,7 @@ __global__ __launch_bounds__(256) void paged_append_step_kernel(const char* __re
         for (int64_t p = threadIdx.x >> 6; p < prefix; p += 4) {
             const char* s = rows + (static_cast<int64_t>(i) * prefix + p) * row_bytes;
             char* d = pages + blk * page_bytes + (p * page_size + len % page_size) * row_bytes;
-            if ((row_bytes & 15) == 0) {
+            if (vec) {
                 for (int64_t o = lane * 16; o < row_bytes; o += 64 * 16)
                     *reinterpret_cast<uint4*>(d + o) = *reinterpret_cast<const uint4*>(s + o);
             } else {
@@ -657,6 +660,13 @@ int sandy_hip_device_paged_append_step(SandyHipDevice* d, uint32_t pool, const u
         auto it = d->impl.tensors.find(tensors[i]);
         if (it == d->impl.tensors.end() || it->second.pool != pool)
             return fail(e, SANDY_ERR_INVALID, "hip device paged tensor not found");
+        // two rows for one tensor would race on its device length
+        for (int j = 0; j < i; j++)
+            if (tensors[j] == tensors[i])
+                return fail(e, SANDY_ERR_INVALID, "paged append step tensors must be distinct");
+    }
+    for (int i = 0; i < count; i++) {
+        auto it = d->impl.tensors.find(tensors[i]);
         PagedTensor& t = it->second;
         // host bookkeeping advances in step with the device (graph replays: see paged_sync)
         if (t.grow_length + 1 > static_cast<int64_t>(t.pages.size()) * p.desc.page_size && !d->impl.capturing) {
@@ -669,7 +679,9 @@ int sandy_hip_device_paged_append_step(SandyHipDevice* d, uint32_t pool, const u
     hipLaunchKernelGGL(paged_append_step_kernel, dim3(static_cast<unsigned>(count)), dim3(256), 0, d->impl.stream,
                        static_cast<const char*>(base_ptr(*rows)), p.pages, p.table, p.lengths, p.desc.max_blocks,
                        p.prefix, p.desc.page_size, static_cast<int64_t>(p.inner * p.elem),
-                       static_cast<int64_t>(p.page_elems * p.elem), errw, args);
+                       static_cast<int64_t>(p.page_elems * p.elem), errw, args,
+                       static_cast<int32_t>(((reinterpret_cast<uintptr_t>(base_ptr(*rows)) |
+                                              reinterpret_cast<uintptr_t>(p.pages)) & 15u) == 0));
     SANDY_HIP_TRY(hipGetLastError(), e, "paged append step launch");
     return ok(e);
 }

@@ -84,7 +84,7 @@ def test_decode_step_eager_and_graph_match_oracle(oracle):
             got_logits = to_oracle(dec.logits)
             got_token = int(dec.token.item())
             want = oracle_step(oracle, cfg, wn, kc, vc, token, ctx0 + step)
-            assert_close(got_logits, want, torch.bfloat16, f"logits, step {step}")
+            assert_close(got_logits, want, torch.bfloat16, f"logits, step {step}", floor=1.0)  # whole-model chain
             wf = O.to_f32(want).ravel()
             top2 = np.sort(wf)[-2:]
             if top2[1] - top2[0] > 0.05 * float(np.sqrt(np.mean(wf ** 2))):
@@ -96,7 +96,7 @@ def test_decode_step_eager_and_graph_match_oracle(oracle):
             dev.paged_sync(dec.k_pools[layer])
             got_k = dev.read_paged(dec.k_seq[layer][0], np.uint16)
             assert got_k.shape == kc[layer].shape
-            assert_close(got_k, kc[layer], torch.bfloat16, f"K cache layer {layer}")
+            assert_close(got_k, kc[layer], torch.bfloat16, f"K cache layer {layer}", floor=1.0)
         dec.close()
     finally:
         dev.close()
@@ -175,7 +175,8 @@ def test_batched_decode_matches_oracle_per_sequence(oracle):
             got_tokens = dec.token.view(-1).cpu().tolist()
             for b in range(B):
                 want = oracle_step(oracle, cfg, wn, kc[b], vc[b], tokens[b], ctx0[b] + step)
-                assert_close(got_logits[b:b + 1], want, torch.bfloat16, f"logits, sequence {b}, step {step}")
+                assert_close(got_logits[b:b + 1], want, torch.bfloat16, f"logits, sequence {b}, step {step}",
+                             floor=1.0)  # whole-model chain
                 wf = O.to_f32(want).ravel()
                 top2 = np.sort(wf)[-2:]
                 if top2[1] - top2[0] > 0.05 * float(np.sqrt(np.mean(wf ** 2))):
@@ -185,7 +186,7 @@ def test_batched_decode_matches_oracle_per_sequence(oracle):
         for b in range(B):
             dev.paged_sync(dec.k_pools[1])
             got_k = dev.read_paged(dec.k_seq[1][b], np.uint16)
-            assert_close(got_k, kc[b][1], torch.bfloat16, f"K cache layer 1, sequence {b}")
+            assert_close(got_k, kc[b][1], torch.bfloat16, f"K cache layer 1, sequence {b}", floor=1.0)
         dec.close()
     finally:
         dev.close()

@@ -265,3 +265,60 @@ def test_decode_qkv_rejects_bad_shapes():
             dev.decode_qkv(kp, [k], vp, [v], good, 7, pos, 1e4, q_out)
     finally:
         dev.close()
+
+
+# (rows per sequence, row bytes): the pre-requested fast form (<= 16 rows of
+# <= 1 KiB, 16-byte multiples) at its limits, and the loop forms past them
+# (17 rows, 2 KiB rows, 6-byte rows).
+STEP_SHAPES = [(12, 256), (16, 1024), (17, 128), (4, 2048), (3, 6)]
+
+
+@pytest.mark.parametrize("prefix,row_bytes", STEP_SHAPES)
+def test_append_step_row_shapes_bit_exact(dev, prefix, row_bytes):
+    """Several decode steps of append_step, read back as the concatenation of
+    the rows (CpuDevice.cpp:465-554, 611-676), bit for bit."""
+    from sandyrt_amd._lib import BF16
+    inner = row_bytes // 2
+    count = 3
+    torch.cuda.synchronize()
+    pool = dev.create_paged_pool([1, prefix, -1, inner], BF16, 2, 16, max_tensors=count, max_blocks=8)
+    ts = [dev.alloc_paged(pool) for _ in range(count)]
+    r = rng(prefix * 1000 + row_bytes)
+    want = [[] for _ in ts]
+    for step in range(18):  # crosses a page boundary
+        rows = from_f32(normal(r, (count, prefix, 1, inner)), torch.bfloat16)
+        torch.cuda.synchronize()
+        dev.append_step(pool, ts, rows)
+        for i in range(count):
+            want[i].append(bf16_np(rows[i:i + 1]))
+    dev.synchronize()
+    for i, t in enumerate(ts):
+        assert np.array_equal(dev.read_paged(t, np.uint16), np.concatenate(want[i], axis=2))
+
+
+def test_append_step_misaligned_rows_view(dev):
+    """A rows view whose storage offset leaves it 2 bytes off 16-byte
+    alignment takes the element-wise copy and still appends exactly."""
+    from sandyrt_amd._lib import BF16
+    prefix, inner, count = 4, 64, 2
+    torch.cuda.synchronize()
+    pool = dev.create_paged_pool([1, prefix, -1, inner], BF16, 2, 16, max_tensors=count, max_blocks=4)
+    ts = [dev.alloc_paged(pool) for _ in range(count)]
+    r = rng(5)
+    base = from_f32(normal(r, (count * prefix * inner + 1,)), torch.bfloat16)
+    rows = base[1:].view(count, prefix, 1, inner)
+    assert rows.data_ptr() % 16 == 2
+    torch.cuda.synchronize()
+    dev.append_step(pool, ts, rows)
+    dev.synchronize()
+    for i, t in enumerate(ts):
+        assert np.array_equal(dev.read_paged(t, np.uint16), bf16_np(rows[i:i + 1].contiguous()))
+
+
+def test_append_step_rejects_repeated_tensor(dev):
+    from sandyrt_amd._lib import BF16, SandyError
+    pool = dev.create_paged_pool([1, 2, -1, 64], BF16, 2, 16, max_tensors=2, max_blocks=4)
+    t = dev.alloc_paged(pool)
+    rows = torch.zeros(2, 2, 1, 64, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(SandyError, match="tensors must be distinct"):
+        dev.append_step(pool, [t, t], rows)

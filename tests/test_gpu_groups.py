@@ -56,7 +56,9 @@ def test_silu_gate_matches_unfused_reference_chain(ops, oracle, dtype):
     op = oracle.binary("add", one, t)
     s = oracle.binary("mul", hx, op)
     want = oracle.binary("mul", s, uo)
-    assert_close(got, want, dtype, "silu*up vs unfused chain")
+    # the unfused chain rounds to bf16 after each of its five ops: a different
+    # computation, compared on the tensor scale
+    assert_close(got, want, dtype, "silu*up vs unfused chain", floor=1.0)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)

@@ -95,3 +95,43 @@ def test_norm_rejects_bad_shapes(ops):
         ops.rms_norm(x, torch.zeros(7, device="cuda"), 1e-5)
     with pytest.raises(SandyError, match="operands must have same dtype"):
         ops.rms_norm(x, torch.zeros(8, device="cuda", dtype=torch.bfloat16), 1e-5)
+
+
+# Launches of more than 1024 rows take the four-rows-per-workgroup form (the
+# weights read after the reduction); 1024 and 1025 rows pin the switch.
+LARGE = [(4096, 2048), (1500, 2560), (1030, 300), (1024, 512), (1025, 512)]
+
+
+@pytest.mark.parametrize("shape", LARGE)
+@pytest.mark.parametrize("with_weight", [True, False])
+def test_rms_norm_many_rows(ops, oracle, shape, with_weight):
+    r = rng(hash(("many", shape, with_weight)) % 2**32)
+    x = from_f32(normal(r, shape), torch.bfloat16)
+    w = from_f32(normal(r, shape[-1:]), torch.bfloat16) if with_weight else None
+    got = ops.rms_norm(x, w, 1e-5)
+    want = oracle.rms_norm(to_oracle(x), to_oracle(w) if w is not None else None, 1e-5)
+    # bf16 squares are exact in double: the row sums, and so the outputs, are the CPU's bit for bit
+    assert_equal(got, want, f"rms_norm {shape}")
+
+
+@pytest.mark.parametrize("shape", LARGE)
+def test_add_rms_norm_many_rows(ops, oracle, shape):
+    r = rng(hash(("add", shape)) % 2**32)
+    x = from_f32(normal(r, shape), torch.bfloat16)
+    h = from_f32(normal(r, shape), torch.bfloat16)
+    w = from_f32(normal(r, shape[-1:]), torch.bfloat16)
+    s, y = ops.add_rms_norm(x, h, w, 1e-5)
+    want_s = oracle.binary("add", to_oracle(x), to_oracle(h))
+    assert_equal(s, want_s, f"residual sum {shape}")
+    assert_close(y, oracle.rms_norm(want_s, to_oracle(w), 1e-5), torch.bfloat16, f"rms_norm(sum) {shape}")
+
+
+def test_add_rms_norm_many_rows_f32(ops, oracle):
+    r = rng(99)
+    x = from_f32(normal(r, (2048, 1000)), torch.float32)
+    h = from_f32(normal(r, (2048, 1000)), torch.float32)
+    w = from_f32(normal(r, (1000,)), torch.float32)
+    s, y = ops.add_rms_norm(x, h, w, 1e-5)
+    want_s = oracle.binary("add", to_oracle(x), to_oracle(h))
+    assert_equal(s, want_s, "residual sum f32")
+    assert_close(y, oracle.rms_norm(want_s, to_oracle(w), 1e-5), torch.float32, "rms_norm(sum) f32")
