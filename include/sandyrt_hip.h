@@ -210,6 +210,23 @@ int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedCache* k_cac
                               const SandyTensor* position_offsets, int64_t window, double scale,
                               const SandyTensor* out, void* stream, char* err, size_t err_cap);
 
+/*
+ * sandy_hip_paged_attention without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops that forbid hipMalloc).  Same arguments,
+ * semantics and errors as sandy_hip_paged_attention, restricted to the bf16
+ * MFMA decode shapes (head dim 64/128/256, at most 16 q heads per kv head,
+ * page_size a multiple of 16, 16-byte aligned q and pools); the split
+ * partials, B * Hq * ceil(max_blocks * page_size / split) * (D + 2) floats,
+ * must fit the library's fixed 8 MiB per-GPU scratch, else
+ * SANDY_ERR_UNSUPPORTED.  Calls that overlap on one GPU share that scratch
+ * and race.
+ */
+int sandy_hip_paged_attention_noalloc(const SandyTensor* q, const SandyPagedCache* k_cache,
+                                      const SandyPagedCache* v_cache, const SandyTensor* block_table,
+                                      const SandyTensor* position_offsets, int64_t window, double scale,
+                                      const SandyTensor* out, void* stream, char* err, size_t err_cap);
+
 /* ---------------------------------------------------------------- MoE */
 
 /* TopKKernelOp (replaces launch_cuda_topk, src/device/cuda/CudaTopKKernels.cu:

@@ -44,6 +44,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 
 namespace sandy_hip {
 namespace {
@@ -1042,12 +1043,18 @@ extern "C" int sandy_hip_attention(const SandyTensor* q, const SandyTensor* k, c
     return ok(e);
 }
 
-extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedCache* kc, const SandyPagedCache* vc,
-                                         const SandyTensor* table, const SandyTensor* position_offsets,
-                                         int64_t window, double scale, const SandyTensor* out, void* stream_,
-                                         char* err, size_t err_cap) {
-    Err e{err, err_cap};
-    hipStream_t stream = static_cast<hipStream_t>(stream_);
+namespace {
+
+// Shape of a paged decode call, validated (the reference's error wording).
+struct PagedCall {
+    int64_t B, hq, D, hkv, P, G, max_blocks;
+    float sc;
+    bool mfma;  // the bf16 MFMA decode kernel takes it
+};
+
+int check_paged(const SandyTensor* q, const SandyPagedCache* kc, const SandyPagedCache* vc, const SandyTensor* table,
+                const SandyTensor* position_offsets, int64_t window, double scale, const SandyTensor* out, Err e,
+                PagedCall* c) {
     if (!valid_rank(q) || !valid_rank(out) || !valid_rank(table) || !valid_rank(position_offsets) || !kc || !vc)
         return fail(e, SANDY_ERR_INVALID, "paged attention requires q, caches, block table, positions and output");
     if (!is_float(q->dtype)) return fail(e, SANDY_ERR_INVALID, "attention q unsupported dtype");
@@ -1067,97 +1074,138 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
     if (!is_index(position_offsets->dtype) || numel(*position_offsets) != B || !contiguous(*position_offsets))
         return fail(e, SANDY_ERR_INVALID, "attention position_offsets length must match batch");
     if (q->strides[3] != 1 || out->strides[3] != 1) return fail(e, SANDY_ERR_UNSUPPORTED, "paged attention needs unit head-dim stride");
-    if (B == 0) return ok(e);
-    int status = 0;
-    uint32_t* errw = device_error_word(e, &status);
-    if (status) return status;
     const int64_t G = hq / hkv;
-    const int64_t max_blocks = table->dims[1];
-    const float sc = scale <= 0.0 ? 1.0f / sqrtf(static_cast<float>(D)) : static_cast<float>(scale);
-
     const bool aligned = ((reinterpret_cast<uintptr_t>(base_ptr(*q)) | reinterpret_cast<uintptr_t>(kc->pool) |
                            reinterpret_cast<uintptr_t>(vc->pool)) & 15u) == 0 &&
                          q->strides[0] % 8 == 0 && q->strides[1] % 8 == 0 && out->strides[0] % 2 == 0 &&
                          out->strides[1] % 2 == 0 && (reinterpret_cast<uintptr_t>(base_ptr(*out)) & 3u) == 0;
-    const bool mfma = q->dtype == SANDY_BF16 && (D == 64 || D == 128 || D == 256) && G <= 16 && P % 16 == 0 &&
-                      table->dims[1] > 0 && table->dims[1] * P <= (1LL << 30) &&
-                      aligned && env_int("SANDY_PAGED_GENERIC", 0) == 0;
-    if (mfma) {
-        PagedArgs a{};
-        a.q = static_cast<const uint16_t*>(base_ptr(*q));
-        a.q_sb = q->strides[0];
-        a.q_sh = q->strides[1];
-        a.out = static_cast<uint16_t*>(base_ptr(*out));
-        a.o_sb = out->strides[0];
-        a.o_sh = out->strides[1];
-        a.k_pool = static_cast<const uint16_t*>(kc->pool);
-        a.v_pool = static_cast<const uint16_t*>(vc->pool);
-        a.page_elems = hkv * P * D;
-        a.num_pages = kc->num_pages;
-        a.table = static_cast<const int32_t*>(base_ptr(*table));
-        a.table_stride = table->strides[0];
-        a.max_blocks = max_blocks;
-        a.pos = base_ptr(*position_offsets);
-        a.pos_dt = position_offsets->dtype;
-        a.page_size = static_cast<int32_t>(P);
-        int lg = 0;
-        while ((1LL << lg) < P) lg++;
-        a.log2_page = lg;
-        a.hq = static_cast<int32_t>(hq);
-        a.hkv = static_cast<int32_t>(hkv);
-        a.group = static_cast<int32_t>(G);
-        a.window = window;
-        a.scale_log2 = sc * kLog2e;
-        a.batch = static_cast<int32_t>(B);
-        a.errw = errw;
-        a.fused = env_int("SANDY_PAGED_FUSED_MERGE", 1);
+    c->B = B;
+    c->hq = hq;
+    c->D = D;
+    c->hkv = hkv;
+    c->P = P;
+    c->G = G;
+    c->max_blocks = table->dims[1];
+    c->sc = scale <= 0.0 ? 1.0f / sqrtf(static_cast<float>(D)) : static_cast<float>(scale);
+    c->mfma = q->dtype == SANDY_BF16 && (D == 64 || D == 128 || D == 256) && G <= 16 && P % 16 == 0 &&
+              table->dims[1] > 0 && table->dims[1] * P <= (1LL << 30) && aligned &&
+              env_int("SANDY_PAGED_GENERIC", 0) == 0;
+    return SANDY_OK;
+}
+
+// The MFMA decode launch.  `fixed` = nullptr: partials in the grow-only
+// device workspace, split merge fused into the decode kernel (arrival
+// counters); otherwise partials in the caller-free region `fixed` of
+// `fixed_cap` bytes and the two-launch form (decode, then merge), which needs
+// no counters and no memory that must start at zero.
+int launch_paged_mfma(const PagedCall& c, const SandyTensor* q, const SandyPagedCache* kc, const SandyPagedCache* vc,
+                      const SandyTensor* table, const SandyTensor* position_offsets, int64_t window,
+                      const SandyTensor* out, uint32_t* errw, char* fixed, size_t fixed_cap, hipStream_t stream,
+                      Err e) {
+    const int64_t B = c.B, hq = c.hq, D = c.D, hkv = c.hkv, P = c.P, G = c.G, max_blocks = c.max_blocks;
+    int status = 0;
+    PagedArgs a{};
+    a.q = static_cast<const uint16_t*>(base_ptr(*q));
+    a.q_sb = q->strides[0];
+    a.q_sh = q->strides[1];
+    a.out = static_cast<uint16_t*>(base_ptr(*out));
+    a.o_sb = out->strides[0];
+    a.o_sh = out->strides[1];
+    a.k_pool = static_cast<const uint16_t*>(kc->pool);
+    a.v_pool = static_cast<const uint16_t*>(vc->pool);
+    a.page_elems = hkv * P * D;
+    a.num_pages = kc->num_pages;
+    a.table = static_cast<const int32_t*>(base_ptr(*table));
+    a.table_stride = table->strides[0];
+    a.max_blocks = max_blocks;
+    a.pos = base_ptr(*position_offsets);
+    a.pos_dt = position_offsets->dtype;
+    a.page_size = static_cast<int32_t>(P);
+    int lg = 0;
+    while ((1LL << lg) < P) lg++;
+    a.log2_page = lg;
+    a.hq = static_cast<int32_t>(hq);
+    a.hkv = static_cast<int32_t>(hkv);
+    a.group = static_cast<int32_t>(G);
+    a.window = window;
+    a.scale_log2 = c.sc * kLog2e;
+    a.batch = static_cast<int32_t>(B);
+    a.errw = errw;
+    a.fused = fixed ? 0 : env_int("SANDY_PAGED_FUSED_MERGE", 1);
+    const int64_t max_keys = max_blocks * P;
+    const int nb = D == 64 ? 2 : 1;
+    const size_t lds_v = 4 * nb * 16 * (2 * D + 8);
+    const size_t lds_r = (4 * G * D + 4 * G * 2) * sizeof(float);
+    const size_t lds = std::max(lds_v, lds_r);
+    dim3 mgrid(static_cast<unsigned>(hq), static_cast<unsigned>(B));
+    void* args[] = {&a};
+    // split units of 64*NT keys; about 1024 units at the longest context
+    // (measured best with the fused merge: config 3 at 512 keys, config 4 at 1024)
+    // (the nearest size on a log scale: a table slightly longer than 4096
+    // keys keeps 512-key splits)
+    const int64_t forced = env_int("SANDY_PAGED_SPLIT", 0);
+    int64_t split = forced > 0 ? forced : (max_keys * B * hkv) / 1024;
+    const int nt = forced > 0 ? (split <= 128 && D == 64 ? 2 : split <= 256 ? 4 : split <= 512 ? 8 : 16)
+                              : (split <= 362 ? 4 : split <= 724 ? 8 : 16);
+    split = 64 * nt;
+    a.split_keys = static_cast<int32_t>(split);
+    a.max_splits = static_cast<int32_t>((max_keys + split - 1) / split);
+    const int64_t units = static_cast<int64_t>(a.max_splits) * hkv * B;
+    if (units > (1LL << 26)) return fail(e, SANDY_ERR_UNSUPPORTED, "paged attention batch too large");
+    const size_t slots = static_cast<size_t>(B * hq * a.max_splits);
+    const size_t ws_bytes = slots * (D + 2) * sizeof(float);
+    char* ws = fixed;
+    if (fixed) {
+        if (ws_bytes > fixed_cap)
+            return fail(e, SANDY_ERR_UNSUPPORTED,
+                        "paged attention without allocation needs %zu bytes of split partials; its fixed scratch holds %zu",
+                        ws_bytes, fixed_cap);
+    } else {
+        ws = static_cast<char*>(device_workspace(0, ws_bytes, stream, e, &status));
+        if (status) return status;
         if (a.fused) {
             a.counters = static_cast<uint32_t*>(
                 device_counters(0, static_cast<size_t>(B * hkv) * sizeof(uint32_t), stream, e, &status));
             if (status) return status;
         }
-        const int64_t max_keys = max_blocks * P;
-        const int nb = D == 64 ? 2 : 1;
-        const size_t lds_v = 4 * nb * 16 * (2 * D + 8);
-        const size_t lds_r = (4 * G * D + 4 * G * 2) * sizeof(float);
-        const size_t lds = std::max(lds_v, lds_r);
-        dim3 mgrid(static_cast<unsigned>(hq), static_cast<unsigned>(B));
-        void* args[] = {&a};
-        // split units of 64*NT keys; about 1024 units at the longest context
-        // (measured best with the fused merge: config 3 at 512 keys, config 4 at 1024)
-        // (the nearest size on a log scale: a table slightly longer than 4096
-        // keys keeps 512-key splits)
-        const int64_t forced = env_int("SANDY_PAGED_SPLIT", 0);
-        int64_t split = forced > 0 ? forced : (max_keys * B * hkv) / 1024;
-        const int nt = forced > 0 ? (split <= 128 && D == 64 ? 2 : split <= 256 ? 4 : split <= 512 ? 8 : 16)
-                                  : (split <= 362 ? 4 : split <= 724 ? 8 : 16);
-        split = 64 * nt;
-        a.split_keys = static_cast<int32_t>(split);
-        a.max_splits = static_cast<int32_t>((max_keys + split - 1) / split);
-        const size_t slots = static_cast<size_t>(B * hq * a.max_splits);
-        char* ws = static_cast<char*>(device_workspace(0, slots * (D + 2) * sizeof(float), stream, e, &status));
-        if (status) return status;
-        a.ws_o = reinterpret_cast<float*>(ws);
-        a.ws_ml = reinterpret_cast<float*>(ws + slots * D * sizeof(float));
-        const int64_t units = static_cast<int64_t>(a.max_splits) * hkv * B;
-        if (units > (1LL << 26)) return fail(e, SANDY_ERR_UNSUPPORTED, "paged attention batch too large");
-        // schedule: work units numbered over the active splits (default; best
-        // when context lengths vary) or the static
-        // split-major schedule (SANDY_PAGED_STATIC=1; one fewer memory round
-        // trip, best when the batch's contexts are about equal: 22.2 vs
-        // 25.1 us at 32 x 2304 keys, 26.4 vs 24.9 us at U[512, 4096])
-        const bool stat = a.fused && env_int("SANDY_PAGED_STATIC", 0) != 0;
-        SANDY_HIP_TRY(hipLaunchKernel(stat ? static_kernel(static_cast<int>(D), nt) : units_kernel(static_cast<int>(D), nt),
-                                      dim3(static_cast<unsigned>(units)),
-                                      dim3(256), args, lds, stream), e, "paged attention launch");
-        const void* mfn = D == 64 ? reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<64>)
-                        : D == 128 ? reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<128>)
-                                   : reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<256>);
-        if (!a.fused)
-            SANDY_HIP_TRY(hipLaunchKernel(mfn, mgrid, dim3(64), args, 0, stream), e, "paged attention merge launch");
-        SANDY_HIP_TRY(hipGetLastError(), e, "paged attention launch");
-        return ok(e);
     }
+    a.ws_o = reinterpret_cast<float*>(ws);
+    a.ws_ml = reinterpret_cast<float*>(ws + slots * D * sizeof(float));
+    // schedule: work units numbered over the active splits (default; best
+    // when context lengths vary) or the static
+    // split-major schedule (SANDY_PAGED_STATIC=1; one fewer memory round
+    // trip, best when the batch's contexts are about equal: 22.2 vs
+    // 25.1 us at 32 x 2304 keys, 26.4 vs 24.9 us at U[512, 4096])
+    const bool stat = a.fused && env_int("SANDY_PAGED_STATIC", 0) != 0;
+    SANDY_HIP_TRY(hipLaunchKernel(stat ? static_kernel(static_cast<int>(D), nt) : units_kernel(static_cast<int>(D), nt),
+                                  dim3(static_cast<unsigned>(units)), dim3(256), args, lds, stream),
+                  e, "paged attention launch");
+    const void* mfn = D == 64 ? reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<64>)
+                    : D == 128 ? reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<128>)
+                               : reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<256>);
+    if (!a.fused)
+        SANDY_HIP_TRY(hipLaunchKernel(mfn, mgrid, dim3(64), args, 0, stream), e, "paged attention merge launch");
+    SANDY_HIP_TRY(hipGetLastError(), e, "paged attention launch");
+    return ok(e);
+}
+
+} // namespace
+
+extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedCache* kc, const SandyPagedCache* vc,
+                                         const SandyTensor* table, const SandyTensor* position_offsets,
+                                         int64_t window, double scale, const SandyTensor* out, void* stream_,
+                                         char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    PagedCall c{};
+    int status = check_paged(q, kc, vc, table, position_offsets, window, scale, out, e, &c);
+    if (status) return status;
+    if (c.B == 0) return ok(e);
+    uint32_t* errw = device_error_word(e, &status);
+    if (status) return status;
+    if (c.mfma) return launch_paged_mfma(c, q, kc, vc, table, position_offsets, window, out, errw, nullptr, 0, stream, e);
+    const int64_t B = c.B, hq = c.hq, D = c.D, hkv = c.hkv, P = c.P, max_blocks = c.max_blocks;
+    const float sc = c.sc;
     if (D > 512) return fail(e, SANDY_ERR_UNSUPPORTED, "attention head dimension above 512");
     GenArgs a{};
     a.q = base_ptr(*q);
@@ -1200,4 +1248,63 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
     }
     SANDY_HIP_TRY(hipGetLastError(), e, "paged attention launch");
     return ok(e);
+}
+
+namespace {
+
+// Scratch of sandy_hip_paged_attention_noalloc: the (O, max, sum) split
+// partials of its two-launch decode, at most kNoAllocScratch bytes (config 4
+// -- 64 sequences of up to 8192 keys, 8 q heads, D 256 -- needs 4.2 MB;
+// config 3 2.2 MB).  Each GPU the library runs on holds its own copy until
+// the process ends.  Host code never passes the name: it uses the address
+// hipGetSymbolAddress gives for the current device (scratch_address).
+constexpr size_t kNoAllocScratch = 8u << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratch];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kScratchDevices] = {};
+
+int scratch_address(Err e, char** out) {
+    int dev = 0;
+    SANDY_HIP_TRY(hipGetDevice(&dev), e, "hipGetDevice");
+    if (dev < 0 || dev >= kScratchDevices) return fail(e, SANDY_ERR_HIP, "device ordinal %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* p = nullptr;
+        const hipError_t st = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (st != hipSuccess) return fail(e, SANDY_ERR_HIP, "paged attention scratch address: %s", hipGetErrorString(st));
+        g_scratch[dev] = p;
+    }
+    *out = static_cast<char*>(g_scratch[dev]);
+    return SANDY_OK;
+}
+
+} // namespace
+
+// The no-allocation variant of sandy_hip_paged_attention (bf16 MFMA decode
+// shapes only): its split partials live in the file-scope `scratch` above,
+// so it calls no allocator, and the split merge runs as a second launch, so
+// nothing in the scratch has to start at zero.  Calls overlapping on one GPU
+// share the scratch and race.
+extern "C" int sandy_hip_paged_attention_noalloc(const SandyTensor* q, const SandyPagedCache* kc,
+                                                 const SandyPagedCache* vc, const SandyTensor* table,
+                                                 const SandyTensor* position_offsets, int64_t window, double scale,
+                                                 const SandyTensor* out, void* stream_, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    PagedCall c{};
+    int status = check_paged(q, kc, vc, table, position_offsets, window, scale, out, e, &c);
+    if (status) return status;
+    if (!c.mfma)
+        return fail(e, SANDY_ERR_UNSUPPORTED,
+                    "paged attention without allocation takes bf16 q with head dim 64, 128 or 256, at most 16 q heads "
+                    "per kv head, 16-row pages and 16-byte aligned operands");
+    if (c.B == 0) return ok(e);
+    uint32_t* errw = device_error_word(e, &status);
+    if (status) return status;
+    char* ws = nullptr;
+    status = scratch_address(e, &ws);
+    if (status) return status;
+    return launch_paged_mfma(c, q, kc, vc, table, position_offsets, window, out, errw, ws, kNoAllocScratch, stream, e);
 }

@@ -26,6 +26,12 @@ struct DeviceState {
 std::mutex g_mu;
 DeviceState g_dev[kMaxDevices];
 
+// The sticky error word of each device lives in this file-scope device array
+// (zero when the module loads; word 0 is used), so that no entry point has to
+// allocate for it.  Each GPU holds its own copy; host code uses the address
+// hipGetSymbolAddress returns for the current device, never the name.
+static __device__ __align__(256) uint32_t error_words[64];
+
 int current_device(Err e, int* dev) {
     hipError_t st = hipGetDevice(dev);
     if (st != hipSuccess) return fail(e, SANDY_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(st));
@@ -43,9 +49,7 @@ uint32_t* device_error_word(Err e, int* status) {
     DeviceState& s = g_dev[dev];
     if (!s.error_word) {
         void* p = nullptr;
-        hipError_t st = hipMalloc(&p, 256);
-        if (st == hipSuccess) st = hipMemset(p, 0, 256);
-        if (st == hipSuccess) st = hipDeviceSynchronize();
+        hipError_t st = hipGetSymbolAddress(&p, HIP_SYMBOL(error_words));
         if (st != hipSuccess) {
             *status = fail(e, SANDY_ERR_HIP, "device error word: %s", hipGetErrorString(st));
             return nullptr;

@@ -241,6 +241,18 @@ def paged_attention(q, k_cache: PagedCache, v_cache: PagedCache, block_table, po
     return out
 
 
+def paged_attention_noalloc(q, k_cache: PagedCache, v_cache: PagedCache, block_table, position_offsets,
+                            window: int = 0, scale: float = -1.0, out=None):
+    """paged_attention through the entry point that allocates nothing (its
+    split partials sit in the library's fixed per-GPU scratch); `out` must be
+    given by callers that cannot allocate."""
+    _require_gpu(q, block_table, position_offsets, k_cache.pool, v_cache.pool)
+    out = torch.empty_like(q) if out is None else out
+    call("sandy_hip_paged_attention_noalloc", desc(q), k_cache.struct(), v_cache.struct(), desc(block_table),
+         desc(position_offsets), int(window), float(scale), desc(out))
+    return out
+
+
 # ------------------------------------------------------------------ MoE
 def topk(x, k: int, axis: int = -1, index_dtype=torch.int64, values=None, indices=None):
     """TopKKernelOp: value descending, index ascending on ties (TensorCalc.cpp:1447-1518)."""
