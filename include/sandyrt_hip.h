@@ -89,6 +89,27 @@ typedef struct SandyPagedCache {
     int64_t num_pages;        /* pool capacity in pages */
 } SandyPagedCache;
 
+/*
+ * The reference's own paged tensor, as CudaDevice hands it to a kernel
+ * (CudaDeviceBufferView with paged = true, src/device/cuda/CudaKernels.h:
+ * 19-28; pages built by CudaPagedTensorPool, CudaPagedTensor.cpp:187-226):
+ * `pages` is the device array of page_count page start addresses (the
+ * reference's void** page table), `dims` the logical shape -- [B, Hkv, T, D]
+ * or [Hkv, T, D] with the grow dimension T at rank - 2 -- and a page holds
+ * page_size rows of T for every leading element: [prefix, page_size, D] with
+ * prefix = B * Hkv (rank 4) or Hkv.  One page list serves the whole batch,
+ * so T is the batch's padded key length (addressing: CudaKernelUtils.cuh:
+ * 82-108).
+ */
+typedef struct SandyPagedView {
+    const void* pages;        /* device array of uint64 page addresses */
+    int32_t dtype;
+    int32_t rank;             /* 3 or 4 */
+    int64_t dims[4];
+    int64_t page_size;        /* power of two */
+    int64_t page_count;       /* pages in the table (>= ceil(T / page_size)) */
+} SandyPagedView;
+
 /* One node of a fused element-wise scalar DAG (ScalarNode, src/ir/KernelIR.h:346-355). */
 typedef struct SandyScalarNode {
     uint32_t id;
@@ -209,6 +230,20 @@ int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedCache* k_cac
                               const SandyPagedCache* v_cache, const SandyTensor* block_table,
                               const SandyTensor* position_offsets, int64_t window, double scale,
                               const SandyTensor* out, void* stream, char* err, size_t err_cap);
+
+/*
+ * AttentionKernelOp with paged K/V exactly as the reference's engine passes
+ * them (launch_cuda_attention with paged inputs, src/device/cuda/
+ * CudaAttentionKernels.cu:680-766 over CudaPagedTensor pages; batched decode
+ * is rank-4 attention with padded T and position_offsets,
+ * src/core/TensorCalc.cpp:1167-1314).  q [B,Hq,Tq,D] (or rank 3) and out as
+ * in sandy_hip_attention; k and v are reference-layout paged views.  Decode
+ * (Tq = 1, bf16, D 64/128/256) runs the MFMA paged decode kernel reading the
+ * page table directly; other shapes run the general attention kernel.
+ */
+int sandy_hip_attention_paged_view(const SandyTensor* q, const SandyPagedView* k, const SandyPagedView* v,
+                                   const SandyTensor* position_offsets, int64_t window, double scale,
+                                   const SandyTensor* out, void* stream, char* err, size_t err_cap);
 
 /*
  * sandy_hip_paged_attention without any allocation.  No counterpart in the

@@ -62,6 +62,17 @@ class SandyPagedCache(C.Structure):
     ]
 
 
+class SandyPagedView(C.Structure):
+    _fields_ = [
+        ("pages", C.c_void_p),
+        ("dtype", C.c_int32),
+        ("rank", C.c_int32),
+        ("dims", C.c_int64 * 4),
+        ("page_size", C.c_int64),
+        ("page_count", C.c_int64),
+    ]
+
+
 class SandyScalarNode(C.Structure):
     _fields_ = [
         ("id", C.c_uint32),
@@ -117,6 +128,7 @@ class SandyPagedMeta(C.Structure):
 
 T = C.POINTER(SandyTensor)
 P = C.POINTER(SandyPagedCache)
+PV = C.POINTER(SandyPagedView)
 ERR = C.c_char_p
 
 # name -> argtypes (every function returns int; the last three args are
@@ -134,6 +146,7 @@ SIGNATURES = {
     "sandy_hip_gather": [T, T, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_attention": [T, T, T, T, C.c_int64, C.c_double, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_paged_attention": [T, P, P, T, T, C.c_int64, C.c_double, T, C.c_void_p, ERR, C.c_size_t],
+    "sandy_hip_attention_paged_view": [T, PV, PV, T, C.c_int64, C.c_double, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_paged_attention_noalloc": [T, P, P, T, T, C.c_int64, C.c_double, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_topk": [T, C.c_int64, C.c_int64, T, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_moe_gather": [T, T, T, C.c_int64, C.c_int64, T, T, T, T, C.c_void_p, ERR, C.c_size_t],

@@ -84,6 +84,16 @@ struct PagedArgs {
     uint32_t* errw;
     uint32_t* counters;  // [B, Hkv] arrivals for the fused merge (zero between launches)
     int32_t fused;       // merge in the last-arriving workgroup of each (sequence, kv head)
+    // The reference's own paged tensor (CudaPagedTensor.cpp:187-226, addressed as
+    // CudaKernelUtils.cuh:82-108): when k_pages is set, page ordinal p of K
+    // (of V) starts at k_pages[p] (v_pages[p]), one page list for the whole
+    // batch, and sequence b's kv head kh is page row b * kv_rows_b + kh.
+    // Otherwise pages are block ids into k_pool / v_pool, one table row per
+    // sequence, and kv_rows_b is 0.
+    const uint64_t* k_pages;
+    const uint64_t* v_pages;
+    int32_t kv_rows_b;
+    int64_t tk;  // logical length of the grow dimension: keys at or past it never attend
 };
 
 // p = hi + lo with hi = bf16(p) and lo = bf16(p - hi): two bf16 MFMA operands
@@ -114,12 +124,14 @@ constexpr int kBufferWord3 = 0x00020000;  // gfx9 buffer resource word 3: raw dw
 // zeros without touching memory, so tiles past a piece cost no bandwidth and
 // every load can stay unconditional.
 template <int D>
-__device__ __forceinline__ void load_tile(const PagedArgs& a, int32_t blk, int64_t in_page, int kh, int lane,
-                                          TileRegs<D>& r) {
-    const int64_t off = blk < 0 ? 0 : static_cast<int64_t>(blk) * a.page_elems + (static_cast<int64_t>(kh) * a.page_size + in_page) * D;
-    const int bytes = blk < 0 ? 0 : 32 * D;
-    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.k_pool + off), 0, bytes, kBufferWord3);
-    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.v_pool + off), 0, bytes, kBufferWord3);
+__device__ __forceinline__ void load_tile(const PagedArgs& a, uint64_t kpage, uint64_t vpage, int64_t in_page, int row,
+                                          int lane, TileRegs<D>& r) {
+    const int64_t off = (static_cast<int64_t>(row) * a.page_size + in_page) * D;
+    const int bytes = kpage == 0 ? 0 : 32 * D;
+    uint16_t* kp = kpage == 0 ? const_cast<uint16_t*>(a.q) : reinterpret_cast<uint16_t*>(kpage) + off;
+    uint16_t* vp = kpage == 0 ? const_cast<uint16_t*>(a.q) : reinterpret_cast<uint16_t*>(vpage) + off;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(kp, 0, bytes, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(vp, 0, bytes, kBufferWord3);
     const int voff = ((lane & 15) * D + 8 * (lane >> 4)) * 2;
 #pragma unroll
     for (int kk = 0; kk < D / 32; kk++) {
@@ -137,7 +149,7 @@ struct SplitRange {
 
 __device__ __forceinline__ SplitRange seq_range(const PagedArgs& a, int64_t pos) {
     SplitRange r;
-    r.n_keys = min(pos + 1, a.max_blocks * static_cast<int64_t>(a.page_size));
+    r.n_keys = min(min(pos + 1, a.max_blocks * static_cast<int64_t>(a.page_size)), a.tk);
     r.min_key = a.window > 0 ? max<int64_t>(0, pos + 1 - a.window) : 0;
     r.key_begin = (r.min_key >> 4) << 4;
     const int64_t span = max<int64_t>(0, r.n_keys - r.key_begin);
@@ -235,22 +247,34 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
 
     {
         const int64_t c0 = tile_a;  // tile_b - tile_a <= 4 * NT: one pass of the ring
-        // lane i: block id of this wave's tile i (-1: none / invalid)
-        int32_t blkv;
+        // lane i: start addresses of the K and V pages of this wave's tile i (0: none / invalid)
+        uint64_t kpv, vpv;
         {
             const int64_t tile = c0 + wave + 4 * lane;
             const int64_t page = (sr.key_begin + 16 * tile) >> a.log2_page;
             // a tile wholly below a sliding window's first key needs no data
             const bool in = lane < NT && tile < tile_b && page < a.max_blocks &&
                             sr.key_begin + 16 * tile + 15 >= sr.min_key;
-            int32_t id;
-            if constexpr (PRE) id = pre->id;
-            else id = a.table[b * a.table_stride + (in ? page : 0)];  // max_blocks >= 1
-            const bool ok = id >= 0 && id < a.num_pages;
+            bool ok;
+            if (a.k_pages) {
+                kpv = a.k_pages[in ? page : 0];  // max_blocks >= 1
+                vpv = a.v_pages[in ? page : 0];
+                ok = kpv != 0 && vpv != 0;
+            } else {
+                int32_t id;
+                if constexpr (PRE) id = pre->id;
+                else id = a.table[b * a.table_stride + (in ? page : 0)];
+                ok = id >= 0 && id < a.num_pages;
+                kpv = reinterpret_cast<uint64_t>(a.k_pool + static_cast<int64_t>(ok ? id : 0) * a.page_elems);
+                vpv = reinterpret_cast<uint64_t>(a.v_pool + static_cast<int64_t>(ok ? id : 0) * a.page_elems);
+            }
             if (in && !ok) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
-            blkv = in && ok ? id : -1;
+            if (!(in && ok)) kpv = vpv = 0;
         }
-        auto blk_of = [&](int it) -> int32_t { return __builtin_amdgcn_readlane(blkv, it); };
+        const int row = b * a.kv_rows_b + kh;  // page row of (sequence b, kv head kh)
+        auto kpage_of = [&](int it) -> uint64_t { return static_cast<uint64_t>(lane_read64(static_cast<int64_t>(kpv), it)); };
+        auto vpage_of = [&](int it) -> uint64_t { return static_cast<uint64_t>(lane_read64(static_cast<int64_t>(vpv), it)); };
+        auto blk_of = [&](int it) -> int32_t { return kpage_of(it) != 0 ? 0 : -1; };
         // key indices fit 32 bits (the host keeps max_blocks * page_size below 2^31)
         const int n_keys = static_cast<int>(sr.n_keys), min_key = static_cast<int>(sr.min_key);
         auto key0_of = [&](int it) -> int { return static_cast<int>(sr.key_begin + 16 * (c0 + wave + 4 * it)); };
@@ -342,7 +366,8 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
         auto load_batch = [&](TileRegs<D> (&buf)[NB], int it0) {
 #pragma unroll
             for (int n = 0; n < NB; n++)
-                load_tile<D>(a, blk_of(it0 + n), key0_of(it0 + n) & (a.page_size - 1), kh, lane, buf[n]);
+                load_tile<D>(a, kpage_of(it0 + n), vpage_of(it0 + n), key0_of(it0 + n) & (a.page_size - 1), row, lane,
+                             buf[n]);
         };
         // NT tiles per wave, fully unrolled: every load is unconditional (empty
         // ranges past the piece), so the wait counts stay exact and the later
@@ -741,12 +766,29 @@ struct GenArgs {
     float scale;
     float* scores;  // [B, Hq, Tq, tk]
     uint32_t* errw;
+    // the reference's paged tensor: page p of K (V) at k_pages[p] (v_pages[p]),
+    // one page list for the batch, (b, kh) on page row b * kv_rows_b + kh;
+    // k and v are then null and offsets are absolute element addresses
+    const uint64_t* k_pages;
+    const uint64_t* v_pages;
+    int64_t kv_rows_b;
 };
 
 // Element offset of row (b, kh, key) of K or V and its head-dim stride;
-// a paged key whose block id is outside the pool clears `ok` (offset 0).
-__device__ __forceinline__ int64_t kv_row(const GenArgs& a, const int64_t* st, int b, int kh, int64_t key, bool& ok) {
+// a paged key whose block id is outside the pool (or whose page address is
+// null) clears `ok` (offset 0).
+__device__ __forceinline__ int64_t kv_row(const GenArgs& a, const int64_t* st, const uint64_t* pages, int b, int kh,
+                                          int64_t key, bool& ok) {
     if (!a.paged) return b * st[0] + kh * st[1] + key * st[2];
+    if (pages) {
+        const uint64_t at = pages[key / a.page_size];
+        if (at == 0) {
+            ok = false;
+            return 0;
+        }
+        const int64_t esz = a.dt == SANDY_F32 ? 4 : 2;
+        return static_cast<int64_t>(at) / esz + ((b * a.kv_rows_b + kh) * a.page_size + key % a.page_size) * a.d;
+    }
     const int64_t page = key / a.page_size;
     const int32_t blk = a.table[b * a.table_stride + page];
     if (blk < 0 || blk >= a.num_pages) {
@@ -795,7 +837,7 @@ __global__ __launch_bounds__(256) void attention_general_kernel(GenArgs a) {
     for (int64_t key = tid; key < tk; key += 256) {
         float s = -INFINITY;
         if (key <= qpos && key >= min_key) {
-            const int64_t row = kv_row(a, a.ks, b, kh, key, ok);
+            const int64_t row = kv_row(a, a.ks, a.k_pages, b, kh, key, ok);
             float acc = 0.0f;
             int64_t d = 0;
             for (; d + kU <= D; d += kU) {
@@ -840,7 +882,7 @@ __global__ __launch_bounds__(256) void attention_general_kernel(GenArgs a) {
                     const int64_t key = k0 + j;
                     sv[j] = key < k_end ? sc[key] : -INFINITY;
                     vv[j] = 0.0f;
-                    if (sv[j] != -INFINITY) vv[j] = Vec8<T>::load1(a.v, kv_row(a, a.vs, b, kh, key, ok) + d * vd);
+                    if (sv[j] != -INFINITY) vv[j] = Vec8<T>::load1(a.v, kv_row(a, a.vs, a.v_pages, b, kh, key, ok) + d * vd);
                 }
 #pragma unroll
                 for (int j = 0; j < kU; j++) {
@@ -897,8 +939,8 @@ __global__ __launch_bounds__(256) void attention_staged_kernel(GenArgs a) {
     for (int64_t key = tid; key < tk; key += 256) {
         float s = -INFINITY;
         const bool live = key <= qpos && key >= min_key;
-        const int64_t krow = live ? kv_row(a, a.ks, b, kh, key, ok) : 0;
-        svrow[key] = live ? kv_row(a, a.vs, b, kh, key, ok) : 0;
+        const int64_t krow = live ? kv_row(a, a.ks, a.k_pages, b, kh, key, ok) : 0;
+        svrow[key] = live ? kv_row(a, a.vs, a.v_pages, b, kh, key, ok) : 0;
         if (live) {
             float acc = 0.0f;
             for (int64_t d0 = 0; d0 < D; d0 += kC) {
@@ -1050,6 +1092,18 @@ struct PagedCall {
     int64_t B, hq, D, hkv, P, G, max_blocks;
     float sc;
     bool mfma;  // the bf16 MFMA decode kernel takes it
+    int64_t q_sb, q_sh, o_sb, o_sh;  // element strides of q / out over batch and head
+    // where the pages are: pool mode (block ids through `table` into k_pool /
+    // v_pool) or the reference's page tables (k_pages / v_pages)
+    const void* k_pool;
+    const void* v_pool;
+    int64_t num_pages;
+    const int32_t* table;
+    int64_t table_stride;
+    const uint64_t* k_pages;
+    const uint64_t* v_pages;
+    int64_t kv_rows_b;
+    int64_t tk;  // logical key count (pool mode: max_blocks * P)
 };
 
 int check_paged(const SandyTensor* q, const SandyPagedCache* kc, const SandyPagedCache* vc, const SandyTensor* table,
@@ -1090,6 +1144,18 @@ int check_paged(const SandyTensor* q, const SandyPagedCache* kc, const SandyPage
     c->mfma = q->dtype == SANDY_BF16 && (D == 64 || D == 128 || D == 256) && G <= 16 && P % 16 == 0 &&
               table->dims[1] > 0 && table->dims[1] * P <= (1LL << 30) && aligned &&
               env_int("SANDY_PAGED_GENERIC", 0) == 0;
+    c->q_sb = q->strides[0];
+    c->q_sh = q->strides[1];
+    c->o_sb = out->strides[0];
+    c->o_sh = out->strides[1];
+    c->k_pool = kc->pool;
+    c->v_pool = vc->pool;
+    c->num_pages = kc->num_pages;
+    c->table = static_cast<const int32_t*>(base_ptr(*table));
+    c->table_stride = table->strides[0];
+    c->k_pages = c->v_pages = nullptr;
+    c->kv_rows_b = 0;
+    c->tk = table->dims[1] * P;
     return SANDY_OK;
 }
 
@@ -1098,25 +1164,28 @@ int check_paged(const SandyTensor* q, const SandyPagedCache* kc, const SandyPage
 // counters); otherwise partials in the caller-free region `fixed` of
 // `fixed_cap` bytes and the two-launch form (decode, then merge), which needs
 // no counters and no memory that must start at zero.
-int launch_paged_mfma(const PagedCall& c, const SandyTensor* q, const SandyPagedCache* kc, const SandyPagedCache* vc,
-                      const SandyTensor* table, const SandyTensor* position_offsets, int64_t window,
+int launch_paged_mfma(const PagedCall& c, const SandyTensor* q, const SandyTensor* position_offsets, int64_t window,
                       const SandyTensor* out, uint32_t* errw, char* fixed, size_t fixed_cap, hipStream_t stream,
                       Err e) {
     const int64_t B = c.B, hq = c.hq, D = c.D, hkv = c.hkv, P = c.P, G = c.G, max_blocks = c.max_blocks;
     int status = 0;
     PagedArgs a{};
     a.q = static_cast<const uint16_t*>(base_ptr(*q));
-    a.q_sb = q->strides[0];
-    a.q_sh = q->strides[1];
+    a.q_sb = c.q_sb;
+    a.q_sh = c.q_sh;
     a.out = static_cast<uint16_t*>(base_ptr(*out));
-    a.o_sb = out->strides[0];
-    a.o_sh = out->strides[1];
-    a.k_pool = static_cast<const uint16_t*>(kc->pool);
-    a.v_pool = static_cast<const uint16_t*>(vc->pool);
+    a.o_sb = c.o_sb;
+    a.o_sh = c.o_sh;
+    a.k_pool = static_cast<const uint16_t*>(c.k_pool);
+    a.v_pool = static_cast<const uint16_t*>(c.v_pool);
     a.page_elems = hkv * P * D;
-    a.num_pages = kc->num_pages;
-    a.table = static_cast<const int32_t*>(base_ptr(*table));
-    a.table_stride = table->strides[0];
+    a.num_pages = c.num_pages;
+    a.table = c.table;
+    a.table_stride = c.table_stride;
+    a.k_pages = c.k_pages;
+    a.v_pages = c.v_pages;
+    a.kv_rows_b = static_cast<int32_t>(c.kv_rows_b);
+    a.tk = c.tk;
     a.max_blocks = max_blocks;
     a.pos = base_ptr(*position_offsets);
     a.pos_dt = position_offsets->dtype;
@@ -1132,7 +1201,7 @@ int launch_paged_mfma(const PagedCall& c, const SandyTensor* q, const SandyPaged
     a.batch = static_cast<int32_t>(B);
     a.errw = errw;
     a.fused = fixed ? 0 : env_int("SANDY_PAGED_FUSED_MERGE", 1);
-    const int64_t max_keys = max_blocks * P;
+    const int64_t max_keys = std::min(max_blocks * P, c.tk);
     const int nb = D == 64 ? 2 : 1;
     const size_t lds_v = 4 * nb * 16 * (2 * D + 8);
     const size_t lds_r = (4 * G * D + 4 * G * 2) * sizeof(float);
@@ -1176,7 +1245,7 @@ int launch_paged_mfma(const PagedCall& c, const SandyTensor* q, const SandyPaged
     // split-major schedule (SANDY_PAGED_STATIC=1; one fewer memory round
     // trip, best when the batch's contexts are about equal: 22.2 vs
     // 25.1 us at 32 x 2304 keys, 26.4 vs 24.9 us at U[512, 4096])
-    const bool stat = a.fused && env_int("SANDY_PAGED_STATIC", 0) != 0;
+    const bool stat = a.fused && !c.k_pages && env_int("SANDY_PAGED_STATIC", 0) != 0;
     SANDY_HIP_TRY(hipLaunchKernel(stat ? static_kernel(static_cast<int>(D), nt) : units_kernel(static_cast<int>(D), nt),
                                   dim3(static_cast<unsigned>(units)), dim3(256), args, lds, stream),
                   e, "paged attention launch");
@@ -1203,7 +1272,7 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
     if (c.B == 0) return ok(e);
     uint32_t* errw = device_error_word(e, &status);
     if (status) return status;
-    if (c.mfma) return launch_paged_mfma(c, q, kc, vc, table, position_offsets, window, out, errw, nullptr, 0, stream, e);
+    if (c.mfma) return launch_paged_mfma(c, q, position_offsets, window, out, errw, nullptr, 0, stream, e);
     const int64_t B = c.B, hq = c.hq, D = c.D, hkv = c.hkv, P = c.P, max_blocks = c.max_blocks;
     const float sc = c.sc;
     if (D > 512) return fail(e, SANDY_ERR_UNSUPPORTED, "attention head dimension above 512");
@@ -1247,6 +1316,126 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
         hipLaunchKernelGGL(attention_general_kernel<F32>, grid, dim3(256), 0, stream, a);
     }
     SANDY_HIP_TRY(hipGetLastError(), e, "paged attention launch");
+    return ok(e);
+}
+
+// AttentionKernelOp with the reference's own paged K/V (a CudaDeviceBufferView
+// with paged = true: page table, logical shape, page size and count).  Same
+// validation and semantics as sandy_hip_attention on the dense tensors the
+// pages hold; decode steps (Tq = 1) of the bf16 MFMA shapes take the paged
+// decode kernel in page-table mode, everything else the general kernel.
+extern "C" int sandy_hip_attention_paged_view(const SandyTensor* q, const SandyPagedView* k, const SandyPagedView* v,
+                                              const SandyTensor* position_offsets, int64_t window, double scale,
+                                              const SandyTensor* out, void* stream_, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    if (!valid_rank(q) || !valid_rank(out) || !k || !v) return fail(e, SANDY_ERR_INVALID, "attention tensor rank out of range");
+    if (!k->pages || !v->pages) return fail(e, SANDY_ERR_INVALID, "attention paged view requires a page table");
+    if (!is_float(q->dtype) || !is_float(k->dtype) || !is_float(v->dtype))
+        return fail(e, SANDY_ERR_INVALID, "attention q unsupported dtype");
+    if (q->dtype != k->dtype || q->dtype != v->dtype) return fail(e, SANDY_ERR_INVALID, "attention operands must have same dtype");
+    const int rank = q->rank;
+    if ((rank != 3 && rank != 4) || k->rank != rank || v->rank != rank)
+        return fail(e, SANDY_ERR_INVALID, "attention q, k, and v must all have rank 3 or rank 4");
+    if (window < 0) return fail(e, SANDY_ERR_INVALID, "attention window must be >= 0");
+    const int o = rank == 4 ? 1 : 0;
+    const int64_t B = rank == 4 ? q->dims[0] : 1;
+    if (rank == 4 && (k->dims[0] != B || v->dims[0] != B)) return fail(e, SANDY_ERR_INVALID, "attention batch dimension mismatch");
+    const int64_t hq = q->dims[o], hkv = k->dims[o], tq = q->dims[o + 1], tk = k->dims[o + 1], D = q->dims[o + 2];
+    if (v->dims[o] != hkv) return fail(e, SANDY_ERR_INVALID, "attention k and v head count mismatch");
+    if (v->dims[o + 1] != tk) return fail(e, SANDY_ERR_INVALID, "attention k and v sequence dimension mismatch");
+    if (k->dims[o + 2] != D || v->dims[o + 2] != D) return fail(e, SANDY_ERR_INVALID, "attention head dimension mismatch");
+    if (hq <= 0 || hkv <= 0 || hq % hkv != 0) return fail(e, SANDY_ERR_INVALID, "attention heads must be divisible by kv_heads");
+    if (!same_shape(*q, *out) || out->dtype != q->dtype) return fail(e, SANDY_ERR_INVALID, "attention output shape mismatch");
+    if (D > 512) return fail(e, SANDY_ERR_UNSUPPORTED, "attention head dimension above 512");
+    const int64_t P = k->page_size;
+    if (P <= 0 || (P & (P - 1)) != 0 || v->page_size != P)
+        return fail(e, SANDY_ERR_INVALID, "paged tensor pool page_size must be a power of two");
+    if (tk < 0 || k->page_count < (tk + P - 1) / P || v->page_count < (tk + P - 1) / P)
+        return fail(e, SANDY_ERR_INVALID, "paged tensor page count does not cover its logical shape");
+    if (position_offsets) {
+        if (!is_index(position_offsets->dtype)) return fail(e, SANDY_ERR_INVALID, "attention position_offsets must be i32 or i64");
+        const int64_t n = numel(*position_offsets);
+        if (rank == 4 && n != B) return fail(e, SANDY_ERR_INVALID, "attention position_offsets length must match batch");
+        if (rank == 3 && n != 1) return fail(e, SANDY_ERR_INVALID, "attention unbatched position_offsets must have one element");
+        if (!contiguous(*position_offsets)) return fail(e, SANDY_ERR_UNSUPPORTED, "attention position_offsets must be contiguous");
+    }
+    if (numel(*q) == 0) return ok(e);
+    int status = 0;
+    uint32_t* errw = device_error_word(e, &status);
+    if (status) return status;
+    const float sc = scale <= 0.0 ? 1.0f / sqrtf(static_cast<float>(D)) : static_cast<float>(scale);
+    const int64_t q_sb = rank == 4 ? q->strides[0] : 0, q_sh = q->strides[o];
+    const int64_t o_sb = rank == 4 ? out->strides[0] : 0, o_sh = out->strides[o];
+    const int64_t G = hq / hkv;
+    const bool aligned = (reinterpret_cast<uintptr_t>(base_ptr(*q)) & 15u) == 0 && q_sb % 8 == 0 && q_sh % 8 == 0 &&
+                         o_sb % 2 == 0 && o_sh % 2 == 0 && (reinterpret_cast<uintptr_t>(base_ptr(*out)) & 3u) == 0 &&
+                         q->strides[rank - 1] == 1 && out->strides[rank - 1] == 1;
+    const bool mfma = tq == 1 && position_offsets && q->dtype == SANDY_BF16 && (D == 64 || D == 128 || D == 256) &&
+                      G <= 16 && P % 16 == 0 && tk > 0 && tk <= (1LL << 30) && aligned &&
+                      env_int("SANDY_PAGED_GENERIC", 0) == 0;
+    if (mfma) {
+        PagedCall c{};
+        c.B = B;
+        c.hq = hq;
+        c.D = D;
+        c.hkv = hkv;
+        c.P = P;
+        c.G = G;
+        c.max_blocks = (tk + P - 1) / P;
+        c.sc = sc;
+        c.mfma = true;
+        c.q_sb = q_sb;
+        c.q_sh = q_sh;
+        c.o_sb = o_sb;
+        c.o_sh = o_sh;
+        c.k_pages = static_cast<const uint64_t*>(k->pages);
+        c.v_pages = static_cast<const uint64_t*>(v->pages);
+        c.kv_rows_b = rank == 4 ? hkv : 0;
+        c.tk = tk;
+        return launch_paged_mfma(c, q, position_offsets, window, out, errw, nullptr, 0, stream, e);
+    }
+    GenArgs a{};
+    auto fill4 = [&](const SandyTensor* t, int64_t* st) {
+        if (rank == 4) for (int i = 0; i < 4; i++) st[i] = t->strides[i];
+        else { st[0] = 0; for (int i = 0; i < 3; i++) st[i + 1] = t->strides[i]; }
+    };
+    a.q = base_ptr(*q);
+    fill4(q, a.qs);
+    a.out = base_ptr(*out);
+    fill4(out, a.os);
+    a.k = nullptr;  // page-table mode: offsets are absolute element addresses
+    a.v = nullptr;
+    a.dt = q->dtype;
+    a.paged = 1;
+    a.page_size = P;
+    a.k_pages = static_cast<const uint64_t*>(k->pages);
+    a.v_pages = static_cast<const uint64_t*>(v->pages);
+    a.kv_rows_b = rank == 4 ? hkv : 0;
+    a.max_blocks = (tk + P - 1) / P;
+    a.pos = position_offsets ? base_ptr(*position_offsets) : nullptr;
+    a.pos_dt = position_offsets ? position_offsets->dtype : SANDY_I64;
+    a.hq = static_cast<int32_t>(hq);
+    a.hkv = static_cast<int32_t>(hkv);
+    a.tq = static_cast<int32_t>(tq);
+    a.tk = tk;
+    a.d = D;
+    a.window = window;
+    a.scale = sc;
+    const size_t sbytes = static_cast<size_t>(B * hq * tq * std::max<int64_t>(tk, 1)) * sizeof(float);
+    a.scores = static_cast<float*>(device_workspace(1, sbytes, stream, e, &status));
+    if (status) return status;
+    a.errw = errw;
+    dim3 grid(static_cast<unsigned>(tq), static_cast<unsigned>(hq), static_cast<unsigned>(B));
+    if (a.tk <= kGenStage && env_int("SANDY_ATTN_UNSTAGED", 0) == 0) {
+        if (q->dtype == SANDY_BF16) hipLaunchKernelGGL(attention_staged_kernel<BF16>, grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL(attention_staged_kernel<F32>, grid, dim3(256), 0, stream, a);
+    } else if (q->dtype == SANDY_BF16) {
+        hipLaunchKernelGGL(attention_general_kernel<BF16>, grid, dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL(attention_general_kernel<F32>, grid, dim3(256), 0, stream, a);
+    }
+    SANDY_HIP_TRY(hipGetLastError(), e, "attention launch");
     return ok(e);
 }
 
@@ -1306,5 +1495,5 @@ extern "C" int sandy_hip_paged_attention_noalloc(const SandyTensor* q, const San
     char* ws = nullptr;
     status = scratch_address(e, &ws);
     if (status) return status;
-    return launch_paged_mfma(c, q, kc, vc, table, position_offsets, window, out, errw, ws, kNoAllocScratch, stream, e);
+    return launch_paged_mfma(c, q, position_offsets, window, out, errw, ws, kNoAllocScratch, stream, e);
 }

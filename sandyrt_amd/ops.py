@@ -241,6 +241,39 @@ def paged_attention(q, k_cache: PagedCache, v_cache: PagedCache, block_table, po
     return out
 
 
+class PagedView:
+    """The reference's own paged tensor (CudaPagedTensor): a logical shape
+    [B, Hkv, T, D] (or [Hkv, T, D]) whose grow dimension T lives in pages of
+    [prefix, page_size, D] (prefix = B * Hkv or Hkv), one page list for the
+    batch.  `pages` is a device uint64 tensor of page start addresses."""
+
+    def __init__(self, pages: torch.Tensor, dims, page_size: int, dtype: torch.dtype):
+        assert pages.is_cuda and pages.dtype in (torch.int64, torch.uint64) and pages.dim() == 1
+        self.pages, self.dims, self.page_size, self.dtype = pages, list(dims), page_size, dtype
+
+    def struct(self):
+        s = _lib.SandyPagedView()
+        s.pages = self.pages.data_ptr()
+        s.dtype = _lib._TORCH_TO_CODE[self.dtype]
+        s.rank = len(self.dims)
+        for i, d in enumerate(self.dims):
+            s.dims[i] = d
+        s.page_size = self.page_size
+        s.page_count = self.pages.numel()
+        return C.pointer(s)
+
+
+def attention_paged_view(q, k: PagedView, v: PagedView, position_offsets=None, window: int = 0,
+                         scale: float = -1.0, out=None):
+    """AttentionKernelOp over the reference's paged K/V (batched decode: rank 4,
+    padded T, position_offsets [B])."""
+    _require_gpu(q, k.pages, v.pages)
+    out = torch.empty_like(q) if out is None else out
+    call("sandy_hip_attention_paged_view", desc(q), k.struct(), v.struct(), desc(position_offsets), int(window),
+         float(scale), desc(out))
+    return out
+
+
 def paged_attention_noalloc(q, k_cache: PagedCache, v_cache: PagedCache, block_table, position_offsets,
                             window: int = 0, scale: float = -1.0, out=None):
     """paged_attention through the entry point that allocates nothing (its
