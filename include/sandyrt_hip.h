@@ -262,6 +262,29 @@ int sandy_hip_paged_attention_noalloc(const SandyTensor* q, const SandyPagedCach
                                       const SandyTensor* position_offsets, int64_t window, double scale,
                                       const SandyTensor* out, void* stream, char* err, size_t err_cap);
 
+/* ---------------------------------------------------------------- layout */
+
+/* LayoutTransformKind, in the reference's order (src/ir/KernelIR.h:268-274). */
+enum SandyLayoutKind {
+    SANDY_LAYOUT_RESHAPE = 0,
+    SANDY_LAYOUT_TRANSPOSE = 1,
+    SANDY_LAYOUT_PERMUTE = 2,
+    SANDY_LAYOUT_SLICE = 3,
+    SANDY_LAYOUT_CONTIGUOUS = 4
+};
+
+/*
+ * LayoutTransformKernelOp (replaces launch_cuda_layout_transform,
+ * src/device/cuda/CudaLayoutTransformKernels.cu:25-78, dispatched at
+ * CudaDevice.cpp:527-530): copies the logical elements of the strided view
+ * `in` into `out` in row-major order -- the element count and dtype must
+ * match, the shapes may differ (reshape).  The engine passes the input view
+ * that a transpose or permute produced (Engine.cpp:606-754), so `kind` only
+ * rejects SANDY_LAYOUT_SLICE, which is always an alias.  Any dtype.
+ */
+int sandy_hip_layout_transform(const SandyTensor* in, const SandyTensor* out, int32_t kind, void* stream,
+                               char* err, size_t err_cap);
+
 /* ---------------------------------------------------------------- MoE */
 
 /* TopKKernelOp (replaces launch_cuda_topk, src/device/cuda/CudaTopKKernels.cu:

@@ -241,6 +241,19 @@ def paged_attention(q, k_cache: PagedCache, v_cache: PagedCache, block_table, po
     return out
 
 
+# LayoutTransformKind (src/ir/KernelIR.h:268-274)
+RESHAPE, TRANSPOSE, PERMUTE, SLICE, CONTIGUOUS = range(5)
+
+
+def layout_transform(x: torch.Tensor, out: torch.Tensor | None = None, kind: int = CONTIGUOUS):
+    """LayoutTransformKernelOp: the logical elements of the (strided) view x,
+    in row-major order, into out (default: a contiguous tensor of x's shape)."""
+    _require_gpu(x, out)
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device) if out is None else out
+    call("sandy_hip_layout_transform", desc(x), desc(out), int(kind))
+    return out
+
+
 class PagedView:
     """The reference's own paged tensor (CudaPagedTensor): a logical shape
     [B, Hkv, T, D] (or [Hkv, T, D]) whose grow dimension T lives in pages of
