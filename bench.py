@@ -309,6 +309,45 @@ def build_extras(replicas):
         kernels["c2_silu_gate_ffn"].append(Prepared("sandy_hip_elementwise", csn, C.c_int32(len(snodes)),
                                                     C.c_uint32(sres), arr, bc2, C.c_int32(2), dd["a"]))
     bytes_per["c2_silu_gate_ffn"] = 3 * T * FFN * 2
+    # ---- config 2 RoPE from a cos/sin cache (built once per forward pass and
+    # shared by q, k and the 22 layers; its build is timed on its own)
+    kernels["c2_rope_cache"], kernels["c2_rope_qk_cached"] = [], []
+    for rep in range(replicas_for(2 * (HQ + HKV) * T * HD * 2, replicas)):
+        g.manual_seed(13 + 100 * rep)
+        qq = torch.randn(1, HQ, T, HD, generator=g, device=dev).to(bf)
+        kk_ = torch.randn(1, HKV, T, HD, generator=g, device=dev).to(bf)
+        qo_, ko_ = torch.empty_like(qq), torch.empty_like(kk_)
+        cache = torch.empty(T, HD // 2, 2, dtype=torch.float32, device=dev)
+        dd = {kk: desc(v) for kk, v in dict(q=qq, k=kk_, qo=qo_, ko=ko_, c=cache).items()}
+        keep += [qq, kk_, qo_, ko_, cache, dd]
+        kernels["c2_rope_cache"].append(Prepared("sandy_hip_rope_cache", None, C.c_int64(T), C.c_double(1e4),
+                                                 C.c_int64(-1), C.c_int64(HD), C.c_int32(1), dd["c"]))
+        kernels["c2_rope_cache"][-1](torch.cuda.current_stream().cuda_stream)
+        kernels["c2_rope_qk_cached"].append(Prepared("sandy_hip_rope_pair_cached", dd["q"], dd["k"], dd["c"],
+                                                     dd["qo"], dd["ko"]))
+    bytes_per["c2_rope_cache"] = T * (HD // 2) * 8
+    bytes_per["c2_rope_qk_cached"] = 2 * (HQ + HKV) * T * HD * 2 + T * (HD // 2) * 8
+    # ---- plain streams of the config-2 groups' byte counts: the practical
+    # ceiling at these sizes (a 1-read/1-write copy of RoPE q+k's bytes, and a
+    # 2-read/1-write residual add of SiLU-gate's)
+    kernels["c2_copy_rope_bytes"], kernels["c2_add_silu_bytes"] = [], []
+    anodes, ares = ops.residual_add_nodes()
+    can = ops._nodes(anodes)
+    keep += [can]
+    for rep in range(replicas_for(2 * (HQ + HKV) * T * HD * 2, replicas)):
+        src = torch.empty((HQ + HKV) * T * HD, dtype=bf, device=dev).normal_(generator=g)
+        dst = torch.empty_like(src)
+        a_ = torch.randn(T, HID, generator=g, device=dev).to(bf)
+        b_ = torch.randn(T, HID, generator=g, device=dev).to(bf)
+        o_ = torch.empty_like(a_)
+        dd = {kk: desc(v) for kk, v in dict(s=src, d=dst, a=a_, b=b_, o=o_).items()}
+        arr = (_lib.SandyTensor * 2)(dd["a"].contents, dd["b"].contents)
+        keep += [src, dst, a_, b_, o_, dd, arr]
+        kernels["c2_copy_rope_bytes"].append(Prepared("sandy_hip_layout_transform", dd["s"], dd["d"], C.c_int32(4)))
+        kernels["c2_add_silu_bytes"].append(Prepared("sandy_hip_elementwise", can, C.c_int32(len(anodes)),
+                                                     C.c_uint32(ares), arr, bc2, C.c_int32(2), dd["o"]))
+    bytes_per["c2_copy_rope_bytes"] = 2 * (HQ + HKV) * T * HD * 2
+    bytes_per["c2_add_silu_bytes"] = 3 * T * HID * 2
     # ---- config 5 (one copy: the 1.5 GB of expert weights exceed the cache)
     g.manual_seed(4)
     logits = torch.randn(MOE_T, MOE_E, generator=g, device=dev)

@@ -190,6 +190,29 @@ int sandy_hip_rope_pair(const SandyTensor* q, const SandyTensor* k, const SandyT
                         int64_t rotary_dim, int32_t split_half, const SandyTensor* q_out, const SandyTensor* k_out,
                         void* stream, char* err, size_t err_cap);
 
+/*
+ * The cos/sin of a forward pass's RoPE positions, computed once and shared by
+ * q, k and every layer.  No counterpart in the reference, which evaluates
+ * powf/cosf/sinf per pair inside every RoPE launch (CudaRoPEKernels.cu:
+ * 130-247); the values are those sandy_hip_rope uses (same angle, same
+ * sin/cos).  cache [seq, rotary_dim / 2, 2] f32 = (cos, sin) of position(s) /
+ * theta^(2i / d), d = dim (split_half) or rotary_dim; position_ids NULL
+ * (position s), numel 1 (ids[0] + s) or numel seq (ids[s]).
+ */
+int sandy_hip_rope_cache(const SandyTensor* position_ids, int64_t seq, double theta, int64_t rotary_dim,
+                         int64_t dim, int32_t split_half, const SandyTensor* cache, void* stream, char* err,
+                         size_t err_cap);
+
+/*
+ * Split-half RoPE of q and k (k may be NULL) from a cache made by
+ * sandy_hip_rope_cache for the same sequence length: bit-identical to
+ * sandy_hip_rope_pair with that cache's positions, theta and rotary_dim.
+ * Contiguous, 16-byte aligned rows whose half is 8, 16, ..., 256 elements.
+ */
+int sandy_hip_rope_pair_cached(const SandyTensor* q, const SandyTensor* k, const SandyTensor* cache,
+                               const SandyTensor* q_out, const SandyTensor* k_out, void* stream, char* err,
+                               size_t err_cap);
+
 /* SoftmaxKernelOp (src/ir/KernelIR.h:494-515; replaces launch_cuda_softmax,
  * src/device/cuda/CudaSoftmaxKernels.cu:145-169).  Any axis. */
 int sandy_hip_softmax(const SandyTensor* x, int64_t axis, const SandyTensor* out,

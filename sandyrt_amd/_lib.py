@@ -146,6 +146,9 @@ SIGNATURES = {
     "sandy_hip_gather": [T, T, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_attention": [T, T, T, T, C.c_int64, C.c_double, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_paged_attention": [T, P, P, T, T, C.c_int64, C.c_double, T, C.c_void_p, ERR, C.c_size_t],
+    "sandy_hip_rope_cache": [T, C.c_int64, C.c_double, C.c_int64, C.c_int64, C.c_int32, T, C.c_void_p, ERR,
+                             C.c_size_t],
+    "sandy_hip_rope_pair_cached": [T, T, T, T, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_layout_transform": [T, T, C.c_int32, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_attention_paged_view": [T, PV, PV, T, C.c_int64, C.c_double, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_paged_attention_noalloc": [T, P, P, T, T, C.c_int64, C.c_double, T, C.c_void_p, ERR, C.c_size_t],

@@ -87,12 +87,12 @@ struct GemmArgs {
 __device__ __forceinline__ float glu_pair(int kind, float gv, float uv) {
     if (kind == 1) {
         const float h = __fmul_rn(0.5f, gv);
-        return __fmul_rn(__fmul_rn(h, __fadd_rn(1.0f, tanhf(h))), uv);
+        return __fmul_rn(__fmul_rn(h, __fadd_rn(1.0f, sandy_tanh(h))), uv);
     }
     const float h = __fmul_rn(0.5f, gv);
     const float x3 = __fmul_rn(__fmul_rn(gv, gv), gv);
     const float inner = __fadd_rn(gv, __fmul_rn(0.044715f, x3));
-    const float t = tanhf(__fmul_rn(0.7978845608028654f, inner));
+    const float t = sandy_tanh(__fmul_rn(0.7978845608028654f, inner));
     return __fmul_rn(__fmul_rn(h, __fadd_rn(1.0f, t)), uv);
 }
 

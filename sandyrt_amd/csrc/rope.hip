@@ -158,11 +158,15 @@ __device__ __forceinline__ Vec8<F32>::raw shfl_raw<F32>(const Vec8<F32>::raw& r,
                                  __shfl_xor(r.b.w, m, 64)}};
 }
 
-template <typename T, int U, bool FULL>
+// TAB: the cos/sin of every (sequence index, pair) come from a table built
+// by rope_cache_kernel (one [seq, rot_pairs] float2 table shared by q, k and
+// every layer of a forward pass) instead of being evaluated here.
+template <typename T, int U, bool FULL, bool TAB = false>
 __global__ __launch_bounds__(256) void rope_split_lines_kernel(
         const void* __restrict__ x, void* __restrict__ out, const void* __restrict__ x2, void* __restrict__ out2,
         int64_t outer_first, const void* __restrict__ ids, int32_t ids_dt, int mode, int64_t seq, int64_t outer,
-        int dim, int rot_pairs, int groups, int per_group, RopeArgs args, uint32_t* errw) {
+        int dim, int rot_pairs, int groups, int per_group, RopeArgs args, uint32_t* errw,
+        const float2* __restrict__ tab = nullptr) {
     const int half = dim >> 1;
     const uint32_t chunks = static_cast<uint32_t>(half >> 3);
     const uint32_t lanes = 2 * chunks;
@@ -182,7 +186,15 @@ __global__ __launch_bounds__(256) void rope_split_lines_kernel(
     int64_t pos = -1;
     for (int64_t o0 = o_begin; o0 < o_end; o0 += U) {
         const bool fresh = mode == 3 || pos < 0;
-        if (fresh) pos = rope_position(mode, ids, ids_dt, o0 * seq + s, s, errw);
+        if (fresh) pos = TAB ? 0 : rope_position(mode, ids, ids_dt, o0 * seq + s, s, errw);
+        float2 tv[4];
+        if (TAB && fresh) {  // requested with the row's loads
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int p = c * 8 + (hi ? 4 : 0) + i;
+                tv[i] = tab[s * rot_pairs + (FULL || p < rot_pairs ? p : 0)];
+            }
+        }
         typename Vec8<T>::raw mine[U];
 #pragma unroll
         for (int j = 0; j < U; j++) {
@@ -200,7 +212,14 @@ __global__ __launch_bounds__(256) void rope_split_lines_kernel(
                 const int p = c * 8 + (hi ? 4 : 0) + i;
                 s4[i] = 0.0f;
                 c4[i] = 1.0f;
-                if (FULL || p < rot_pairs) rope_sincos(fp / args.denom[p], &s4[i], &c4[i]);
+                if (TAB) {
+                    if (FULL || p < rot_pairs) {
+                        c4[i] = tv[i].x;
+                        s4[i] = tv[i].y;
+                    }
+                } else if (FULL || p < rot_pairs) {
+                    rope_sincos(fp / args.denom[p], &s4[i], &c4[i]);
+                }
             }
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -339,6 +358,21 @@ __global__ __launch_bounds__(256) void rope_generic_kernel(
     rope_sincos(static_cast<float>(pos) / args.denom[p], &sn, &cs);
     store_any(out, dt, o0, __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn)));
     store_any(out, dt, o1, __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, cs)));
+}
+
+// The cos/sin table: entry (s, p) = (cos, sin) of position(s) / denom[p],
+// the same float angle and rope_sincos as the kernels above.
+__global__ __launch_bounds__(256) void rope_cache_kernel(const void* __restrict__ ids, int32_t ids_dt, int mode,
+                                                         int64_t seq, int rot_pairs, RopeArgs args, uint32_t* errw,
+                                                         float2* __restrict__ tab) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= seq * rot_pairs) return;
+    const int64_t s = t / rot_pairs;
+    const int p = static_cast<int>(t - s * rot_pairs);
+    const int64_t pos = rope_position(mode, ids, ids_dt, s, s, errw);
+    float sn, cs;
+    rope_sincos(static_cast<float>(pos) / args.denom[p], &sn, &cs);
+    tab[t] = make_float2(cs, sn);
 }
 
 } // namespace
@@ -547,4 +581,129 @@ extern "C" int sandy_hip_rope_pair(const SandyTensor* q, const SandyTensor* k, c
     const SandyTensor* xs[2] = {q, k};
     const SandyTensor* outs[2] = {q_out, k_out};
     return rope_run(xs, outs, 2, position_ids, theta, rotary_dim, split_half, static_cast<hipStream_t>(stream_), e);
+}
+
+// The cos/sin cache of a forward pass's positions: cache [seq, rotary_dim / 2,
+// 2] f32 holds (cos, sin) of position(s) / theta^(2i / d) -- d = dim for
+// split-half, rotary_dim for interleaved -- for sequence index s, with the
+// positions of sandy_hip_rope (position_ids NULL: s; numel 1: ids[0] + s;
+// numel seq: ids[s]).
+extern "C" int sandy_hip_rope_cache(const SandyTensor* position_ids, int64_t seq, double theta, int64_t rotary_dim,
+                                    int64_t dim, int32_t split_half, const SandyTensor* cache, void* stream_, char* err,
+                                    size_t err_cap) {
+    Err e{err, err_cap};
+    if (!valid_rank(cache)) return fail(e, SANDY_ERR_INVALID, "rope cache tensor rank out of range");
+    const float th = static_cast<float>(theta);
+    if (th <= 0.0f) return fail(e, SANDY_ERR_INVALID, "rope theta must be > 0");
+    if (dim <= 0 || dim % 2 != 0) return fail(e, SANDY_ERR_INVALID, "rope last dimension must be positive and even");
+    if (rotary_dim < 0) rotary_dim = dim;
+    if (rotary_dim <= 0 || rotary_dim % 2 != 0) return fail(e, SANDY_ERR_INVALID, "rope rotary_dim must be positive and even");
+    if (rotary_dim > dim) return fail(e, SANDY_ERR_INVALID, "rope rotary_dim must be <= last dimension");
+    if (rotary_dim / 2 > kMaxPairs) return fail(e, SANDY_ERR_UNSUPPORTED, "rope rotary_dim above %d", 2 * kMaxPairs);
+    const int rot_pairs = static_cast<int>(rotary_dim / 2);
+    if (cache->dtype != SANDY_F32 || cache->rank != 3 || cache->dims[0] != seq || cache->dims[1] != rot_pairs ||
+        cache->dims[2] != 2 || !contiguous(*cache))
+        return fail(e, SANDY_ERR_INVALID, "rope cache must be a contiguous [seq, rotary_dim / 2, 2] f32 tensor");
+    if ((reinterpret_cast<uintptr_t>(base_ptr(*cache)) & 7u) != 0) return fail(e, SANDY_ERR_UNSUPPORTED, "rope cache must be 8-byte aligned");
+    int mode = 0;
+    if (position_ids) {
+        if (!is_index(position_ids->dtype)) return fail(e, SANDY_ERR_INVALID, "rope position_ids must be i32 or i64");
+        const int64_t cnt = numel(*position_ids);
+        if (cnt != 1 && cnt != seq) return fail(e, SANDY_ERR_INVALID, "rope cache position_ids numel must be 1 or the sequence length");
+        if (!contiguous(*position_ids)) return fail(e, SANDY_ERR_UNSUPPORTED, "rope position_ids must be contiguous");
+        mode = cnt == 1 && seq != 1 ? 1 : 2;
+    }
+    if (seq == 0) return ok(e);
+    RopeArgs args;
+    const float div = static_cast<float>(split_half ? dim : rotary_dim);
+    for (int p = 0; p < rot_pairs; p++) args.denom[p] = std::pow(th, static_cast<float>(2 * p) / div);
+    int status = 0;
+    uint32_t* errw = device_error_word(e, &status);
+    if (status) return status;
+    const int64_t n = seq * rot_pairs;
+    hipLaunchKernelGGL(rope_cache_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream_), position_ids ? base_ptr(*position_ids) : nullptr,
+                       position_ids ? position_ids->dtype : SANDY_I64, mode, seq, rot_pairs, args, errw,
+                       static_cast<float2*>(base_ptr(*cache)));
+    SANDY_HIP_TRY(hipGetLastError(), e, "rope cache launch");
+    return ok(e);
+}
+
+// Split-half RoPE of q (and k, or NULL) from a cos/sin cache built by
+// sandy_hip_rope_cache for the same sequence length and head dim: the same
+// outputs as sandy_hip_rope_pair with the cache's positions and theta.
+extern "C" int sandy_hip_rope_pair_cached(const SandyTensor* q, const SandyTensor* k, const SandyTensor* cache,
+                                          const SandyTensor* q_out, const SandyTensor* k_out, void* stream_,
+                                          char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    const int n = k ? 2 : 1;
+    const SandyTensor* xs[2] = {q, k};
+    const SandyTensor* outs[2] = {q_out, k_out};
+    RopeShape sh[2];
+    for (int i = 0; i < n; i++) {
+        const int st = rope_check(xs[i], outs[i], sh[i], e);
+        if (st) return st;
+    }
+    if (n == 2 && (q->dtype != k->dtype || sh[0].seq != sh[1].seq || sh[0].dim != sh[1].dim))
+        return fail(e, SANDY_ERR_INVALID, "rope pair inputs must share sequence length and last dimension");
+    if (!valid_rank(cache) || cache->dtype != SANDY_F32 || cache->rank != 3 || cache->dims[0] != sh[0].seq ||
+        cache->dims[2] != 2 || !contiguous(*cache) || cache->dims[1] <= 0 || 2 * cache->dims[1] > sh[0].dim)
+        return fail(e, SANDY_ERR_INVALID, "rope cache must be a contiguous [seq, rotary_dim / 2, 2] f32 tensor");
+    const int64_t seq = sh[0].seq, dim = sh[0].dim;
+    const int rot_pairs = static_cast<int>(cache->dims[1]);
+    const int chunks = static_cast<int>(dim / 16);
+    bool ok_shape = dim % 16 == 0 && chunks <= 32 && (chunks & (chunks - 1)) == 0 &&
+                    (reinterpret_cast<uintptr_t>(base_ptr(*cache)) & 7u) == 0;
+    int64_t outer = 0;
+    for (int i = 0; i < n; i++) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(base_ptr(*xs[i])) | reinterpret_cast<uintptr_t>(base_ptr(*outs[i]));
+        ok_shape = ok_shape && contiguous(*xs[i]) && contiguous(*outs[i]) && (a & 15u) == 0;
+        outer += sh[i].outer;
+    }
+    if (!ok_shape)
+        return fail(e, SANDY_ERR_UNSUPPORTED,
+                    "rope from a cache takes contiguous 16-byte aligned split-half rows whose half is a power-of-two "
+                    "multiple of 8 elements (up to 256)");
+    if (outer == 0 || seq == 0) return ok(e);
+    int status = 0;
+    uint32_t* errw = device_error_word(e, &status);
+    if (status) return status;
+    // head groups as the direct kernel: 6 heads when they divide by 6, else
+    // the largest of 4 / 2 / 1 that divides the heads
+    const int per = outer % 6 == 0 ? 6 : outer % 4 == 0 ? 4 : outer % 2 == 0 ? 2 : 1;
+    const int groups = static_cast<int>(outer / per);
+    const int64_t threads = seq * 2 * chunks * groups;
+    if (threads + 255 >= (int64_t(1) << 31)) return fail(e, SANDY_ERR_UNSUPPORTED, "rope from a cache: tensor too large");
+    const bool full = rot_pairs == dim / 2;
+    RopeArgs args{};
+    const void* px = base_ptr(*q);
+    void* po = base_ptr(*q_out);
+    const void* px2 = n == 2 ? base_ptr(*k) : px;
+    void* po2 = n == 2 ? base_ptr(*k_out) : po;
+    const float2* tab = static_cast<const float2*>(base_ptr(*cache));
+    dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+#define SANDY_ROPE_TAB(T, U, F)                                                                                     \
+    hipLaunchKernelGGL((rope_split_lines_kernel<T, U, F, true>), grid, dim3(256), 0, stream, px, po, px2, po2,     \
+                       sh[0].outer, nullptr, SANDY_I64, 0, seq, outer, static_cast<int>(dim), rot_pairs, groups, per, \
+                       args, errw, tab)
+#define SANDY_ROPE_TAB_F(T, U)                 \
+    do {                                       \
+        if (full) SANDY_ROPE_TAB(T, U, true);  \
+        else SANDY_ROPE_TAB(T, U, false);      \
+    } while (0)
+#define SANDY_ROPE_TAB_T(T)                      \
+    do {                                         \
+        if (per == 6) SANDY_ROPE_TAB_F(T, 6);    \
+        else if (per == 4) SANDY_ROPE_TAB_F(T, 4); \
+        else if (per == 2) SANDY_ROPE_TAB_F(T, 2); \
+        else SANDY_ROPE_TAB_F(T, 1);             \
+    } while (0)
+    if (q->dtype == SANDY_BF16) SANDY_ROPE_TAB_T(BF16);
+    else SANDY_ROPE_TAB_T(F32);
+#undef SANDY_ROPE_TAB_T
+#undef SANDY_ROPE_TAB_F
+#undef SANDY_ROPE_TAB
+    SANDY_HIP_TRY(hipGetLastError(), e, "rope launch");
+    return ok(e);
 }

@@ -84,6 +84,27 @@ def rope_pair(q, k, theta: float, rotary_dim: int = -1, split_half: bool = False
     return q_out, k_out
 
 
+def rope_cache(seq: int, dim: int, theta: float, rotary_dim: int = -1, split_half: bool = True, position_ids=None,
+               out=None, device="cuda"):
+    """The cos/sin of a forward pass's positions, [seq, rotary_dim / 2, 2] f32,
+    built once and shared by q, k and every layer (rope_pair_cached)."""
+    _require_gpu(position_ids)
+    rd = dim if rotary_dim < 0 else rotary_dim
+    out = torch.empty(seq, rd // 2, 2, dtype=torch.float32, device=device) if out is None else out
+    call("sandy_hip_rope_cache", desc(position_ids), int(seq), float(theta), int(rotary_dim), int(dim),
+         int(bool(split_half)), desc(out))
+    return out
+
+
+def rope_pair_cached(q, k, cache, q_out=None, k_out=None):
+    """Split-half RoPE of q and k (or q alone, k None) from a rope_cache."""
+    _require_gpu(q, k, cache)
+    q_out = torch.empty_like(q) if q_out is None else q_out
+    k_out = (torch.empty_like(k) if k_out is None else k_out) if k is not None else None
+    call("sandy_hip_rope_pair_cached", desc(q), desc(k), desc(cache), desc(q_out), desc(k_out))
+    return q_out, k_out
+
+
 def softmax(x, axis: int = -1, out=None):
     """SoftmaxKernelOp (src/core/TensorCalc.cpp:1337-1399)."""
     _require_gpu(x)

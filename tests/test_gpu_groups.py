@@ -257,3 +257,48 @@ def test_rope_pair_rejects_mismatched_tensors(ops):
         ops.rope_pair(q, torch.zeros(1, 2, 8, 32, dtype=torch.bfloat16, device="cuda"), 1e4)
     with pytest.raises(SandyError, match="must have one dtype"):
         ops.rope_pair(q, torch.zeros(1, 2, 8, 64, dtype=torch.float32, device="cuda"), 1e4)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("ids_kind", [None, "offset", "seq"])
+@pytest.mark.parametrize("rotary", [-1, 32])
+def test_rope_from_cache_equals_direct(ops, dtype, ids_kind, rotary):
+    """A cos/sin cache built once, applied to q and k: bit-identical to the
+    direct rope_pair (same angle, same sin/cos), full and partial rotary."""
+    r = rng(19)
+    q = from_f32(normal(r, (1, 12, 40, 64)), dtype)
+    k = from_f32(normal(r, (1, 2, 40, 64)), dtype)
+    ids = {None: None, "offset": torch.tensor([4000], device="cuda"),
+           "seq": torch.from_numpy(r.integers(0, 100000, 40)).cuda()}[ids_kind]
+    cache = ops.rope_cache(40, 64, 1e4, rotary_dim=rotary, split_half=True, position_ids=ids)
+    qc, kc = ops.rope_pair_cached(q, k, cache)
+    qd, kd = ops.rope_pair(q, k, 1e4, rotary_dim=rotary, split_half=True, position_ids=ids)
+    assert torch.equal(qc, qd) and torch.equal(kc, kd)
+    q1, none = ops.rope_pair_cached(q, None, cache)
+    assert none is None and torch.equal(q1, qd)
+
+
+def test_rope_from_cache_config2_against_oracle(ops, oracle):
+    r = rng(20)
+    q = from_f32(normal(r, (1, 32, 4096, 64)), torch.bfloat16)
+    k = from_f32(normal(r, (1, 4, 4096, 64)), torch.bfloat16)
+    cache = ops.rope_cache(4096, 64, 1e4, split_half=True)
+    qo, ko = ops.rope_pair_cached(q, k, cache)
+    assert_close(qo, oracle.rope(to_oracle(q), 1e4, split_half=True), torch.bfloat16, "q from cache")
+    assert_close(ko, oracle.rope(to_oracle(k), 1e4, split_half=True), torch.bfloat16, "k from cache")
+    # cache angles: (cos, sin) of pos / 10000^(2i/64), against the oracle's rotation of a unit pair
+    x = torch.zeros(1, 1, 4096, 64, device="cuda")
+    x[..., 0] = 1.0
+    want = oracle.rope(to_oracle(x), 1e4, split_half=True)
+    np.testing.assert_allclose(cache[:, 0, 0].cpu().numpy(), want[0, 0, :, 0], atol=2e-7)
+    np.testing.assert_allclose(cache[:, 0, 1].cpu().numpy(), want[0, 0, :, 32], atol=2e-7)
+
+
+def test_rope_cache_rejects(ops):
+    from sandyrt_amd._lib import SandyError
+    with pytest.raises(SandyError, match="rope cache must be"):
+        ops.rope_cache(8, 64, 1e4, out=torch.empty(8, 31, 2, device="cuda"))
+    cache = ops.rope_cache(8, 48, 1e4)
+    q = torch.zeros(1, 2, 8, 48, dtype=torch.bfloat16, device="cuda")  # half 24: not a power-of-two multiple of 8
+    with pytest.raises(SandyError, match="rope from a cache takes"):
+        ops.rope_pair_cached(q, None, cache)
