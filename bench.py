@@ -543,11 +543,14 @@ def cpu_baseline(host, bytes_per, n_tokens, n_seqs):
     qd = to_oracle(host["qd"])
     t_dec = 0.0
     sample_ctx = 0
+    mat = O.Oracle()  # CpuDevice.cpp:611-676 restated (the reference build compiles only src/core)
     for b in range(n_seqs):
         c = int(ctx[b])
-        kd = O.Oracle().paged_to_dense(kpool, table[b], HKV, c, DEC_PAGE, HD)[None]
-        vd = O.Oracle().paged_to_dense(vpool, table[b], HKV, c, DEC_PAGE, HD)[None]
+        # the reference CPU device materialises the paged K/V as dense tensors
+        # before every attention (CpuDevice.cpp:611-676): timed with it
         t0 = time.perf_counter()
+        kd = mat.paged_to_dense(kpool, table[b], HKV, c, DEC_PAGE, HD)[None]
+        vd = mat.paged_to_dense(vpool, table[b], HKV, c, DEC_PAGE, HD)[None]
         cpu.attention(qd[b:b + 1], kd, vd, np.array([c - 1], np.int64), 0, 0.125)
         t_dec += time.perf_counter() - t0
         sample_ctx += c
@@ -559,21 +562,27 @@ def cpu_baseline(host, bytes_per, n_tokens, n_seqs):
         "cores": 1,
         "kind": kind,
         "sample": (f"config-2 groups on {n_tokens} of {T} tokens and decode attention for {n_seqs} of {DEC_B} "
-                   f"sequences, single thread, scaled linearly to one full step; paged->dense K/V copy not timed"),
+                   f"sequences (paged->dense K/V materialisation of CpuDevice.cpp:611-676 included, as the reference "
+                   f"CPU device runs it before each attention), "
+                   f"single thread, scaled linearly to one full step"),
         "step_seconds": round(t_c2 + t_dec, 3),
     }
 
 
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
-    summary (FETCH_SIZE / WRITE_SIZE scaled by an identity copy), or None."""
+    summary (FETCH_SIZE / WRITE_SIZE scaled by an identity copy), or None --
+    also when the summary's source stamp is not the stamp of the kernels
+    being run (the measurement would describe other code)."""
+    from sandyrt_amd.profile_summary import source_stamp, stamp_of
     path = os.path.join(ROOT, "profiles", "hbm_traffic_bench_kernels.md")
-    if not os.path.exists(path):
+    if stamp_of(path) != source_stamp():
         return None
+    prefix = {"paged_decode": "paged_decode_units_kernel<64,"}.get(kernel)
     for row in open(path):
-        cells = [c.strip() for c in row.strip().strip("|").split("|")]
-        if len(cells) == 7 and cells[0] == kernel:
-            return int(cells[4])
+        cells = [c.strip().strip("`") for c in row.strip().strip("|").split("|")]
+        if prefix and len(cells) == 5 and cells[0].startswith(prefix):
+            return int(float(cells[4]))
     return None
 
 
