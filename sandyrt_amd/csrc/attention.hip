@@ -342,21 +342,45 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
                 }
             }
             __builtin_amdgcn_wave_barrier();
+            // ds_read_b64_tr_b16: in each 16-lane group, lane i gets element i % 4 of the
+            // 8-byte pieces addressed by lanes 4m + i / 4 (m = 0..3), so pointing lane i at
+            // key 4j + i / 4, dims 16t + 4(i % 4) .. + 3 of tile n yields V[4j + m][16t + i], m = 0..3
+            auto v_t = [&](int n, int t) -> short4_t {
+                const int i = lane & 15;
+                const unsigned char* src = vl + (n * 16 + 4 * j + (i >> 2)) * kRow + 2 * (16 * t + 4 * (i & 3));
+                return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (short4_t __attribute__((address_space(3)))*)((unsigned char __attribute__((address_space(3)))*)src));
+            };
+            if constexpr (NB % 2 == 0) {
+                // two tiles per v_mfma_f32_16x16x32_bf16 (twice the work of the 16x16x16 form in
+                // the same passes on gfx950): contraction slot 8j + m holds key 4j + m of tile n
+                // (m < 4) and of tile n + 1 (m >= 4), in V^T and P^T alike
 #pragma unroll
-            for (int n = 0; n < NB; n++) {
-                short4_t pb, pl;
-                split_p(p[n], pb, pl);
+                for (int n = 0; n < NB; n += 2) {
+                    short4_t pb0, pl0, pb1, pl1;
+                    split_p(p[n], pb0, pl0);
+                    split_p(p[n + 1], pb1, pl1);
+                    const bf16x8_t pb = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(pb0, pb1, 0, 1, 2, 3, 4, 5, 6, 7));
+                    const bf16x8_t pl = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(pl0, pl1, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-                for (int t = 0; t < D / 16; t++) {
-                    // ds_read_b64_tr_b16: in each 16-lane group, lane i gets element i % 4 of the
-                    // 8-byte pieces addressed by lanes 4m + i / 4 (m = 0..3), so pointing lane i at
-                    // key 4j + i / 4, dims 16t + 4(i % 4) .. + 3 yields V[4j + m][16t + i], m = 0..3
-                    const int i = lane & 15;
-                    const unsigned char* src = vl + (n * 16 + 4 * j + (i >> 2)) * kRow + 2 * (16 * t + 4 * (i & 3));
-                    const short4_t va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (short4_t __attribute__((address_space(3)))*)((unsigned char __attribute__((address_space(3)))*)src));
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, acc[t], 0, 0, 0);
-                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pl, acc[t], 0, 0, 0);
+                    for (int t = 0; t < D / 16; t++) {
+                        const bf16x8_t va =
+                            __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(v_t(n, t), v_t(n + 1, t), 0, 1, 2, 3, 4, 5, 6, 7));
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, acc[t], 0, 0, 0);
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl, acc[t], 0, 0, 0);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int n = 0; n < NB; n++) {
+                    short4_t pb, pl;
+                    split_p(p[n], pb, pl);
+#pragma unroll
+                    for (int t = 0; t < D / 16; t++) {
+                        const short4_t va = v_t(n, t);
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, acc[t], 0, 0, 0);
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pl, acc[t], 0, 0, 0);
+                    }
                 }
             }
             __builtin_amdgcn_wave_barrier();
