@@ -400,7 +400,7 @@ def build_extras(replicas):
     return kernels, bytes_per, keep
 
 
-def decode_step_tok_s(batch, contexts, iters=10, seed=2):
+def decode_step_tok_s(batch, contexts, iters=10, seed=2, **decoder_opts):
     """Whole TinyLlama-1.1B greedy decode step (22 layers: projections, RoPE,
     paged append, paged decode attention, SiLU-gated MLP, lm-head, greedy
     token; random bf16 weights, synthetic K/V history of the given context
@@ -412,7 +412,7 @@ def decode_step_tok_s(batch, contexts, iters=10, seed=2):
     cfg = DecodeConfig(page_size=DEC_PAGE, max_context=int(max(contexts)) + iters + 64)
     w = random_weights(cfg, seed=seed)
     dev = HipDevice(0)
-    dec = TinyLlamaDecoder(dev, cfg, w, batch=batch)
+    dec = TinyLlamaDecoder(dev, cfg, w, batch=batch, **decoder_opts)
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     for b, n in enumerate(contexts):

@@ -369,6 +369,44 @@ int sandy_hip_matmul(const SandyTensor* lhs, const SandyTensor* rhs, int32_t tra
  * counterpart. */
 int sandy_hip_matmul_glu(const SandyTensor* lhs, const SandyTensor* rhs, int32_t activation, const SandyTensor* out,
                          void* stream, char* err, size_t err_cap);
+
+/*
+ * Row statistics passed between the fused decode GEMMs below: sumsq points to
+ * rows x parts float64 values, row-major, parts = ceil(cols / 16); value
+ * [r, p] is the sum of the squares of row r's columns 16 p .. 16 p + 15 of
+ * the matrix they describe (each square exact in float64, so their sum is the
+ * RMSNorm's sum of squares, src/core/TensorCalc.cpp:1953-2000).
+ */
+typedef struct SandyRowStats {
+    double* sumsq;
+    int64_t rows;
+    int64_t parts;
+} SandyRowStats;
+
+/* Decode projection with the residual add in its epilogue: out[m, n] =
+ * bf16(residual[m, n] + bf16(sum_k lhs[m, k] * rhs[n, k])) -- bit-identical to
+ * sandy_hip_matmul (transpose_rhs) followed by the residual add the program
+ * writes next (__add(x, h), src/models/tinyllama/common.sandy.go:1-9) -- and,
+ * when out_stats is given, out's row statistics for sandy_hip_matmul_rms.
+ * bf16, lhs [m, k], rhs [n, k], k a multiple of 32, m <= 64; residual may be
+ * out itself.  The reference runs the two ops separately; this fused form
+ * has no single counterpart there. */
+int sandy_hip_matmul_residual(const SandyTensor* lhs, const SandyTensor* rhs, const SandyTensor* residual,
+                              const SandyTensor* out, const SandyRowStats* out_stats, void* stream, char* err,
+                              size_t err_cap);
+
+/* Decode projection of RMSNorm(lhs) * norm_weight: the normalised row is
+ * formed in the GEMM's operand registers from lhs and its row statistics
+ * (from sandy_hip_matmul_residual), with sandy_hip_norm's arithmetic (float64
+ * sum of squares, float inverse 1 / sqrt(float(sum / k) + eps), y = x * inv *
+ * w rounded once to bf16), so the result is bit-identical to sandy_hip_norm
+ * followed by sandy_hip_matmul (activation 0) or sandy_hip_matmul_glu
+ * (activation 1 / 2, rhs rows interleaved as there).  The reference's
+ * __rms_norm + __matmul pair (src/models/tinyllama/common.sandy.go:1-9); no
+ * single counterpart there. */
+int sandy_hip_matmul_rms(const SandyTensor* lhs, const SandyRowStats* lhs_stats, const SandyTensor* norm_weight,
+                         double eps, const SandyTensor* rhs, int32_t activation, const SandyTensor* out, void* stream,
+                         char* err, size_t err_cap);
 int sandy_hip_linear(const SandyTensor* x, const SandyTensor* weight, const SandyTensor* bias,
                      const SandyTensor* out, void* stream, char* err, size_t err_cap);
 

@@ -73,6 +73,14 @@ class SandyPagedView(C.Structure):
     ]
 
 
+class SandyRowStats(C.Structure):
+    _fields_ = [
+        ("sumsq", C.c_void_p),
+        ("rows", C.c_int64),
+        ("parts", C.c_int64),
+    ]
+
+
 class SandyScalarNode(C.Structure):
     _fields_ = [
         ("id", C.c_uint32),
@@ -129,6 +137,7 @@ class SandyPagedMeta(C.Structure):
 T = C.POINTER(SandyTensor)
 P = C.POINTER(SandyPagedCache)
 PV = C.POINTER(SandyPagedView)
+RS = C.POINTER(SandyRowStats)
 ERR = C.c_char_p
 
 # name -> argtypes (every function returns int; the last three args are
@@ -158,6 +167,8 @@ SIGNATURES = {
     "sandy_hip_matmul": [T, T, C.c_int32, C.c_int32, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_linear": [T, T, T, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_matmul_glu": [T, T, C.c_int32, T, C.c_void_p, ERR, C.c_size_t],
+    "sandy_hip_matmul_residual": [T, T, T, T, RS, C.c_void_p, ERR, C.c_size_t],
+    "sandy_hip_matmul_rms": [T, RS, T, C.c_double, T, C.c_int32, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_moe_scatter_sum": [T, T, T, T, C.c_void_p, ERR, C.c_size_t],
 }
 

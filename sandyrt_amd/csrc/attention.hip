@@ -1023,11 +1023,6 @@ __global__ __launch_bounds__(256) void attention_staged_kernel(GenArgs a) {
     }
 }
 
-int env_int(const char* name, int dflt) {
-    const char* v = std::getenv(name);
-    return v ? std::atoi(v) : dflt;
-}
-
 } // namespace
 } // namespace sandy_hip
 

@@ -10,6 +10,7 @@
 
 #include <cstdarg>
 #include <cstdint>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -69,6 +70,13 @@ inline bool same_shape(const SandyTensor& a, const SandyTensor& b) {
     for (int i = 0; i < a.rank; i++)
         if (a.dims[i] != b.dims[i]) return false;
     return true;
+}
+
+// Integer value of an environment switch (measurement and test selection of
+// kernel forms), or dflt when unset or empty.
+inline int env_int(const char* name, int dflt) {
+    const char* v = std::getenv(name);
+    return v && *v ? std::atoi(v) : dflt;
 }
 
 inline bool is_float(int32_t dt) { return dt == SANDY_F32 || dt == SANDY_BF16; }
@@ -285,6 +293,29 @@ __device__ __forceinline__ float sandy_tanh(float y) {
     }
     const float e = __builtin_amdgcn_exp2f(2.8853900817779268f * a);
     return copysignf(fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f), y);
+}
+
+// Sum over aligned groups of G lanes (G = 2, 4, 8 or 16) with DPP lane moves
+// (quad swaps, then the half-row and row mirrors): every lane of a group ends
+// with the group's total.  ALU-latency moves, unlike __shfl_xor's LDS
+// crossbar; doubles move as two 32-bit halves.
+template <int CTRL>
+__device__ __forceinline__ double dpp_move(double v) {
+    const uint64_t u = static_cast<uint64_t>(__double_as_longlong(v));
+    const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u)), CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u >> 32)), CTRL, 0xf, 0xf, false);
+    return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                                       static_cast<uint32_t>(lo)));
+}
+
+template <int G>
+__device__ __forceinline__ double group_sum(double v) {
+    static_assert(G == 2 || G == 4 || G == 8 || G == 16, "group of 2, 4, 8 or 16 lanes");
+    v += dpp_move<0xB1>(v);                     // quad_perm [1, 0, 3, 2]: lane ^ 1
+    if constexpr (G >= 4) v += dpp_move<0x4E>(v);   // quad_perm [2, 3, 0, 1]: lane ^ 2
+    if constexpr (G >= 8) v += dpp_move<0x141>(v);  // row_half_mirror: quad 0 <-> quad 1
+    if constexpr (G >= 16) v += dpp_move<0x140>(v); // row_mirror: half row 0 <-> 1
+    return v;
 }
 
 // wave64 butterfly reductions (every lane ends with the full result)

@@ -127,6 +127,14 @@ __device__ __forceinline__ void st8_bf16(void* p, i64 i, const float* v) {
   typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
   __builtin_nontemporal_store(u32x4{r.x, r.y, r.z, r.w}, (u32x4*)((u16*)p + i));
 }
+__device__ __forceinline__ void stc8_bf16(void* p, i64 i, const float* v) {
+  uint4 r;
+  r.x = (unsigned)f2bf(v[0]) | ((unsigned)f2bf(v[1]) << 16);
+  r.y = (unsigned)f2bf(v[2]) | ((unsigned)f2bf(v[3]) << 16);
+  r.z = (unsigned)f2bf(v[4]) | ((unsigned)f2bf(v[5]) << 16);
+  r.w = (unsigned)f2bf(v[6]) | ((unsigned)f2bf(v[7]) << 16);
+  *(uint4*)((u16*)p + i) = r;
+}
 __device__ __forceinline__ void st8_f32(void* p, i64 i, const float* v) {
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   f32x4* q = (f32x4*)((float*)p + i);
@@ -167,6 +175,12 @@ std::string node_expr(const SandyScalarNode& n) {
     return "0.0f";
 }
 
+// chunks of 8 elements per thread per grid stride of the vectorised kernel
+int vec_chunks() {
+    const int u = static_cast<int>(env_int("SANDY_EW_CHUNKS", 2));
+    return u == 1 || u == 4 || u == 8 ? u : 2;
+}
+
 std::string generate(const SandyScalarNode* nodes, int count, uint32_t result, const int32_t* in_dt,
                      const int* modes, int nin, int32_t out_dt, bool vec) {
     std::ostringstream s;
@@ -174,15 +188,17 @@ std::string generate(const SandyScalarNode* nodes, int count, uint32_t result, c
     s << "extern \"C\" __global__ __launch_bounds__(256) void sandy_ew(" << (vec ? "EwVecArgs" : "EwArgs")
       << " a) {\n";
     if (vec) {
-        // chunk j of 8 elements; a thread takes chunks c and c + 256 of each
-        // 512-chunk stride of the grid
+        // chunk j of 8 elements; a thread takes chunks c, c + 256, ... of each
+        // (256 U)-chunk stride of the grid, all U chunks' loads issued first
+        const int U = vec_chunks();
+        const bool plain_st = env_int("SANDY_EW_PLAIN_STORE", 0) != 0;
         s << "  const i64 chunks = a.n >> 3;\n";
-        s << "  for (i64 c0 = (i64)blockIdx.x * 512 + threadIdx.x; c0 < chunks; c0 += (i64)gridDim.x * 512) {\n";
-        s << "    const bool two = c0 + 256 < chunks;\n";
-        for (int u = 0; u < 2; u++) {
-            const std::string cidx = u == 0 ? "c0" : "(c0 + 256)";
+        s << "  for (i64 c0 = (i64)blockIdx.x * " << 256 * U << " + threadIdx.x; c0 < chunks; c0 += (i64)gridDim.x * "
+          << 256 * U << ") {\n";
+        for (int u = 0; u < U; u++) {
+            const std::string cidx = "(c0 + " + std::to_string(256 * u) + ")";
             for (int i = 0; i < nin; i++) s << "    float in" << i << "_" << u << "[8];\n";
-            if (u == 1) s << "    if (two) {\n";
+            if (u > 0) s << "    if (" << cidx << " < chunks) {\n";
             for (int i = 0; i < nin; i++) {
                 const std::string nm = "in" + std::to_string(i) + "_" + std::to_string(u);
                 if (modes[i] == kContig)
@@ -195,12 +211,12 @@ std::string generate(const SandyScalarNode* nodes, int count, uint32_t result, c
                     s << "    { float v = " << (in_dt[i] == SANDY_BF16 ? "bf2f(((const u16*)a.in[" : "(((const float*)a.in[")
                       << i << "])[0]); for (int k = 0; k < 8; k++) " << nm << "[k] = v; }\n";
             }
-            if (u == 1) s << "    }\n";
+            if (u > 0) s << "    }\n";
         }
-        for (int u = 0; u < 2; u++) {
-            const std::string cidx = u == 0 ? "c0" : "(c0 + 256)";
+        for (int u = 0; u < U; u++) {
+            const std::string cidx = "(c0 + " + std::to_string(256 * u) + ")";
             const std::string suf = "_" + std::to_string(u);
-            if (u == 1) s << "    if (!two) break;\n";
+            if (u > 0) s << "    if (" << cidx << " >= chunks) break;\n";
             s << "    {\n    float r[8];\n#pragma unroll\n    for (int k = 0; k < 8; k++) {\n";
             for (int j = 0; j < count; j++) {
                 const auto& n = nodes[j];
@@ -209,7 +225,8 @@ std::string generate(const SandyScalarNode* nodes, int count, uint32_t result, c
                 else s << node_expr(n) << ";\n";
             }
             s << "      r[k] = s" << result << ";\n    }\n";
-            s << "    " << (out_dt == SANDY_BF16 ? "st8_bf16" : "st8_f32") << "(a.out, " << cidx << " * 8, r);\n    }\n";
+            s << "    " << (out_dt == SANDY_BF16 ? (plain_st ? "stc8_bf16" : "st8_bf16") : "st8_f32") << "(a.out, " << cidx
+              << " * 8, r);\n    }\n";
         }
         s << "  }\n}\n";
     } else {
@@ -376,9 +393,10 @@ extern "C" int sandy_hip_elementwise(const SandyScalarNode* nodes, int32_t node_
     }
     // vectorised: 512 chunks of 8 per workgroup per grid stride, at most 4096
     // workgroups (16 per CU); scalar: one element per thread
-    const int64_t threads = vec ? (n / 8 + 1) / 2 : n;
+    const int U = vec_chunks();
+    const int64_t threads = vec ? (n / 8 + U - 1) / U : n;
     int64_t blocks64 = (threads + 255) / 256;
-    if (vec) blocks64 = std::min<int64_t>(blocks64, 4096);
+    if (vec) blocks64 = std::min<int64_t>(blocks64, env_int("SANDY_EW_MAX_BLOCKS", 4096));
     const unsigned blocks = static_cast<unsigned>(blocks64);
     EwVecArgs vargs{};
     if (vec) {

@@ -29,72 +29,13 @@
 //     unaligned shapes).  Register-tiled FMA-free float loops that keep the
 //     reference's k order per output, so f32 results are bit-identical to the
 //     CPU path.
-#include "common.h"
+#include "gemm.h"
 
 #include <algorithm>
 #include <cstdlib>
 
 namespace sandy_hip {
 namespace {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-int env_int(const char* name, int dflt) {
-    const char* v = std::getenv(name);
-    return v && *v ? std::atoi(v) : dflt;
-}
-
-// Element offsets of batch index b in each operand.  For each output batch
-// dim d (innermost first): coordinate c = b mod dims[d]; an operand adds
-// (c / div[d]) * stride[d] (stride 0 where it broadcasts a size-1 or absent
-// dim; div = out dim / operand dim for a grouped dim).
-struct BatchMap {
-    int32_t rank;
-    int64_t dims[SANDY_HIP_MAX_RANK];
-    int64_t l_stride[SANDY_HIP_MAX_RANK], l_div[SANDY_HIP_MAX_RANK];
-    int64_t r_stride[SANDY_HIP_MAX_RANK], r_div[SANDY_HIP_MAX_RANK];
-};
-
-__device__ __forceinline__ void batch_offsets(const BatchMap& m, int64_t b, int64_t& lo, int64_t& ro) {
-    lo = 0;
-    ro = 0;
-    for (int d = m.rank - 1; d >= 0; d--) {
-        const int64_t c = b % m.dims[d];
-        b /= m.dims[d];
-        lo += (c / m.l_div[d]) * m.l_stride[d];
-        ro += (c / m.r_div[d]) * m.r_stride[d];
-    }
-}
-
-struct GemmArgs {
-    const uint16_t* a;     // [.., M, K]
-    const uint16_t* w;     // [.., N, K]
-    const uint16_t* bias;  // [N] or null
-    uint16_t* out;         // [batch, M, N]
-    int64_t M, N, K;
-    int32_t col_tiles, row_tiles, splits, split_chunks;
-    float* part;           // [tiles, splits, 4 waves, RT * CT * 64 lanes * 4]
-    uint32_t* counters;    // [tiles] arrivals (zero between launches)
-    BatchMap bm;
-    int32_t glu;           // 0: plain; 1 / 2: gated SiLU / GELU epilogue (weight rows interleaved gate, up)
-};
-
-// Gated activation of one bf16-rounded (gate, up) pair with the scalar DAGs
-// of src/ir/BuiltinLowering.cpp:116-158 in their node order (silu(g) * up,
-// gelu(g) * up), fp32 arithmetic without contraction -- what the generated
-// element-wise group computes from the two GEMM outputs.
-__device__ __forceinline__ float glu_pair(int kind, float gv, float uv) {
-    if (kind == 1) {
-        const float h = __fmul_rn(0.5f, gv);
-        return __fmul_rn(__fmul_rn(h, __fadd_rn(1.0f, sandy_tanh(h))), uv);
-    }
-    const float h = __fmul_rn(0.5f, gv);
-    const float x3 = __fmul_rn(__fmul_rn(gv, gv), gv);
-    const float inner = __fadd_rn(gv, __fmul_rn(0.044715f, x3));
-    const float t = sandy_tanh(__fmul_rn(0.7978845608028654f, inner));
-    return __fmul_rn(__fmul_rn(h, __fadd_rn(1.0f, t)), uv);
-}
 
 // Prefill-sized products: workgroup = 16 * RT rows x 64 * CT columns of one
 // batch; wave w owns columns n0 = (tile * 4 + w) * 16 * CT .. + 16 * CT.  Per
@@ -230,228 +171,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
                 if (rr < M) g.out[ob + rr * N + nc] = f32_to_bf16(acc[t][c][i] + bias);  // 2-byte: L2 combines them
             }
     }
-}
-
-// Decode-shaped products (a few dozen rows against megabytes of weights):
-// workgroup = 16 * CT output columns x 16 * RT rows; its four waves take
-// consecutive quarters of the workgroup's K range and run independently --
-// no workgroup barrier inside the K loop -- so each wave keeps Q chunks of
-// its weight rows in flight on its own.  A wave loads its 16 * CT weight rows
-// as whole 128-byte lines into a private, swizzled, double-buffered LDS tile
-// (read back in MFMA layout) and its activation rows straight into MFMA
-// A-operand registers (they are L2-resident; every workgroup reads them).
-// The K loop is straight-line over CPS chunks so every register slot is
-// statically named and each LDS write waits only for its own chunk.  The
-// four partial accumulators are summed in wave order through LDS; when the
-// grid also splits K across workgroups, the last-arriving workgroup of each
-// tile sums the splits' fp32 partials in split order (deterministic).
-template <int RT, int CT, int Q, int CPS, int OCC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void gemm_waves_kernel(GemmArgs g) {
-    constexpr int kWTile = 16 * CT * 128;
-    constexpr int kAcc = RT * CT * 64 * 16;  // one wave's accumulators, bytes
-    constexpr int kLds = 4 * 2 * kWTile > 3 * kAcc ? 4 * 2 * kWTile : 3 * kAcc;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[kLds];
-    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int ct = static_cast<int>(blockIdx.x) / g.splits;
-    const int split = static_cast<int>(blockIdx.x) % g.splits;
-    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 16 * RT;
-    const int64_t bz = blockIdx.z;
-    int64_t lo, ro;
-    batch_offsets(g.bm, bz, lo, ro);
-    const int64_t M = g.M, N = g.N, K = g.K;
-    const int64_t n0 = static_cast<int64_t>(ct) * 16 * CT;
-    unsigned char* wt = lds + wave * 2 * kWTile;
-    auto swz = [](int row, int piece) { return row * 128 + ((piece ^ ((row >> 1) & 7)) << 4); };
-    const int ksteps = static_cast<int>(K / 32);
-    const int chunks = (ksteps + 1) / 2;
-    const int wg_begin = split * g.split_chunks;
-    const int wg_end = min(chunks, wg_begin + g.split_chunks);
-    const int c_begin = min(wg_end, wg_begin + wave * CPS);
-    const int c_end = min(wg_end, c_begin + CPS);
-
-    const int64_t wrows = min<int64_t>(16 * CT, N - n0);
-    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(g.w + ro + n0 * K), 0, static_cast<int>(wrows * K * 2), 0x00020000);
-    const int64_t xrows = min<int64_t>(16 * RT, M - r0);
-    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(g.a + lo + r0 * K), 0, static_cast<int>(xrows * K * 2), 0x00020000);
-    const int wlane = static_cast<int>((lane >> 3) * K * 2 + (lane & 7) * 16);
-    const int wstep = static_cast<int>(8 * K * 2);
-    const int wbase[2] = {swz(lane >> 3, lane & 7), swz(8 + (lane >> 3), lane & 7) - 1024};
-    // A operand of tile t, k-step u: row 16 t + lane % 16, 16-byte piece 4 u + lane / 16
-    int xoff[RT][2];
-#pragma unroll
-    for (int t = 0; t < RT; t++)
-#pragma unroll
-        for (int u = 0; u < 2; u++)
-            xoff[t][u] = static_cast<int>((16 * t + (lane & 15)) * K * 2 + (4 * u + (lane >> 4)) * 16);
-    int raddr[2][CT];
-#pragma unroll
-    for (int u = 0; u < 2; u++)
-#pragma unroll
-        for (int c = 0; c < CT; c++) raddr[u][c] = swz(16 * c + (lane & 15), 4 * u + (lane >> 4));
-
-    f32x4_t acc[RT][CT];
-#pragma unroll
-    for (int t = 0; t < RT; t++)
-#pragma unroll
-        for (int c = 0; c < CT; c++) acc[t][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    uint4 wv[Q][2 * CT], xv[Q][RT][2];
-    // clamped re-reads past this wave's range: L2 hits, never multiplied
-    auto load = [&](int ch, int slot) {
-        const int kb = max(0, min(ch, c_end - 1)) * 128;
-#pragma unroll
-        for (int i = 0; i < 2 * CT; i++)
-            wv[slot][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wlane + i * wstep + kb, 0, 0));
-#pragma unroll
-        for (int t = 0; t < RT; t++)
-#pragma unroll
-            for (int u = 0; u < 2; u++)
-                xv[slot][t][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[t][u] + kb, 0, 0));
-    };
-    auto store = [&](int slot, int buf) {
-#pragma unroll
-        for (int i = 0; i < 2 * CT; i++) *reinterpret_cast<uint4*>(wt + buf * kWTile + wbase[i & 1] + i * 1024) = wv[slot][i];
-    };
-    // the second k-step of a half chunk (odd K / 32) is skipped, so the
-    // registers past K never reach an MFMA
-    auto mma = [&](int slot, int buf, int ch) {
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            if (u == 1 && 2 * ch + 1 >= ksteps) break;
-#pragma unroll
-            for (int c = 0; c < CT; c++) {
-                const uint4 bv = *reinterpret_cast<const uint4*>(wt + buf * kWTile + raddr[u][c]);
-#pragma unroll
-                for (int t = 0; t < RT; t++)
-                    acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xv[slot][t][u]),
-                                                                        __builtin_bit_cast(bf16x8_t, bv), acc[t][c],
-                                                                        0, 0, 0);
-            }
-        }
-    };
-#pragma unroll
-    for (int s = 0; s < Q; s++) load(c_begin + s, s);
-    store(0, 0);
-#pragma unroll
-    for (int u = 0; u < CPS; u++) {
-        const int c = c_begin + u;
-        if (c < c_end) mma(u % Q, u & 1, c);
-        if (c + 1 < c_end) store((u + 1) % Q, (u + 1) & 1);
-        load(c + Q, u % Q);
-    }
-
-    // sum the four waves' partials in wave order (LDS reused after a barrier)
-    __syncthreads();
-    if (wave > 0) {
-#pragma unroll
-        for (int t = 0; t < RT; t++)
-#pragma unroll
-            for (int c = 0; c < CT; c++)
-                *reinterpret_cast<f32x4_t*>(lds + (wave - 1) * kAcc + ((t * CT + c) * 64 + lane) * 16) = acc[t][c];
-    }
-    __syncthreads();
-    if (wave == 0) {
-#pragma unroll
-        for (int w = 0; w < 3; w++)
-#pragma unroll
-            for (int t = 0; t < RT; t++)
-#pragma unroll
-                for (int c = 0; c < CT; c++)
-                    acc[t][c] += *reinterpret_cast<const f32x4_t*>(lds + w * kAcc + ((t * CT + c) * 64 + lane) * 16);
-    }
-
-    const int64_t ob = bz * M * N;
-    auto emit = [&](int t, int c, const f32x4_t& v) {
-        const int64_t nc = n0 + 16 * c + (lane & 15);
-        if (g.glu) {
-            // columns (2i, 2i + 1) = (gate_i, up_i) sit in lanes (l, l ^ 1); both
-            // are rounded to bf16 as the plain GEMM would store them, and the
-            // even lane writes act[row, i] of the [M, N / 2] output (every lane
-            // takes part in the shuffle)
-            const int64_t half = N >> 1;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float gv = bf16_to_f32(f32_to_bf16(v[i]));
-                const float uv = __shfl_xor(gv, 1, 64);
-                const int64_t rr = r0 + 16 * t + 4 * (lane >> 4) + i;
-                if ((lane & 1) == 0 && nc < N && rr < M)
-                    g.out[(bz * M + rr) * half + (nc >> 1)] = f32_to_bf16(glu_pair(g.glu, gv, uv));
-            }
-            return;
-        }
-        if (nc >= N) return;
-        const float bias = g.bias ? bf16_to_f32(g.bias[nc]) : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int64_t rr = r0 + 16 * t + 4 * (lane >> 4) + i;
-            if (rr < M) g.out[ob + rr * N + nc] = f32_to_bf16(v[i] + bias);
-        }
-    };
-    if (g.splits == 1) {
-        if (wave == 0)
-#pragma unroll
-            for (int t = 0; t < RT; t++)
-#pragma unroll
-                for (int c = 0; c < CT; c++) emit(t, c, acc[t][c]);
-        return;
-    }
-    // split-K across workgroups: partials written through to the agent's coherence
-    // point, then the last-arriving workgroup of the tile sums them (wave 0 holds the tile)
-    const int64_t tile = (bz * g.row_tiles + blockIdx.y) * g.col_tiles + ct;
-    constexpr int kTileFloats = RT * CT * 64 * 4;
-    float* pbase = g.part + tile * g.splits * kTileFloats;
-    if (wave == 0) {
-#pragma unroll
-        for (int t = 0; t < RT; t++)
-#pragma unroll
-            for (int c = 0; c < CT; c++) {
-                uint64_t* p = reinterpret_cast<uint64_t*>(pbase + split * kTileFloats + ((t * CT + c) * 64 + lane) * 4);
-                __hip_atomic_store(p, static_cast<uint64_t>(__float_as_uint(acc[t][c][0])) |
-                                          (static_cast<uint64_t>(__float_as_uint(acc[t][c][1])) << 32),
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(p + 1, static_cast<uint64_t>(__float_as_uint(acc[t][c][2])) |
-                                              (static_cast<uint64_t>(__float_as_uint(acc[t][c][3])) << 32),
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-    }
-    __shared__ int is_last;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t* ctr = g.counters + tile;
-        const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        is_last = prev == static_cast<uint32_t>(g.splits - 1);
-        if (is_last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!is_last || wave != 0) return;
-#pragma unroll
-    for (int t = 0; t < RT; t++)
-#pragma unroll
-        for (int c = 0; c < CT; c++) {
-            f32x4_t sum = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            const int64_t off = ((t * CT + c) * 64 + lane) * 4;
-            for (int s0 = 0; s0 < g.splits; s0 += 8) {
-                uint64_t w0[8], w1[8];
-#pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    const int s = s0 + q < g.splits ? s0 + q : s0;
-                    uint64_t* p = reinterpret_cast<uint64_t*>(pbase + s * kTileFloats + off);
-                    w0[q] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    w1[q] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-#pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    if (s0 + q >= g.splits) break;
-                    sum[0] += __uint_as_float(static_cast<uint32_t>(w0[q]));
-                    sum[1] += __uint_as_float(static_cast<uint32_t>(w0[q] >> 32));
-                    sum[2] += __uint_as_float(static_cast<uint32_t>(w1[q]));
-                    sum[3] += __uint_as_float(static_cast<uint32_t>(w1[q] >> 32));
-                }
-            }
-            emit(t, c, sum);
-        }
 }
 
 // Any dtype, either operand transposed: 64 x 64 output tile per workgroup,
@@ -689,8 +408,20 @@ const char* plan_matmul(const SandyTensor& l, const SandyTensor& r, const SandyT
     return nullptr;
 }
 
+// The decode GEMM's fused forms: a residual-add epilogue with row sums of
+// squares, and an RMSNorm prologue from such sums.
+struct Fusion {
+    const uint16_t* resid = nullptr;
+    double* rsq_out = nullptr;
+    int64_t rsq_parts = 0;
+    const double* rsq_in = nullptr;
+    int64_t rsq_in_parts = 0;
+    const uint16_t* norm_w = nullptr;
+    float eps = 0.0f;
+};
+
 int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const SandyTensor* bias, const SandyTensor& o,
-           bool tl, bool tr, hipStream_t stream, Err e, const char* what, int glu = 0) {
+           bool tl, bool tr, hipStream_t stream, Err e, const char* what, int glu = 0, const Fusion* fz = nullptr) {
     if (p.batches == 0 || p.M == 0 || p.N == 0) return ok(e);
     if (p.batches > 65535) return fail(e, SANDY_ERR_UNSUPPORTED, "%s batch count exceeds 65535", what);
     const void* pl = base_ptr(l);
@@ -701,8 +432,10 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
     const bool lines = l.dtype == SANDY_BF16 && !tl && tr && p.K % 32 == 0 && p.K > 0 && aligned &&
                        p.K <= (int64_t{1} << 21) && env_int("SANDY_GEMM_SIMT", 0) == 0;
     const bool waves = lines && env_int("SANDY_GEMM_WAVES", p.M <= 64 ? 1 : 0) != 0;
-    if (glu && !waves)
+    if ((glu || fz) && !waves)
         return fail(e, SANDY_ERR_UNSUPPORTED, "%s needs bf16 operands, k a multiple of 32 and at most 64 rows", what);
+    if (fz && p.batches != 1) return fail(e, SANDY_ERR_UNSUPPORTED, "%s takes one [m, k] matrix", what);
+    const bool norm = fz && fz->norm_w;
     // f32, few rows, weight rows contiguous: the exact-order GEMV
     const bool gemv = l.dtype == SANDY_F32 && !tl && tr && p.M <= 8 && p.K % 4 == 0 && aligned &&
                       p.lrs == p.K && p.rrs == p.K && env_int("SANDY_GEMM_SIMT", 0) == 0;
@@ -729,6 +462,15 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
         g.K = p.K;
         g.bm = p.bm;
         g.glu = glu;
+        if (fz) {
+            g.resid = fz->resid;
+            g.rsq_out = fz->rsq_out;
+            g.rsq_parts = fz->rsq_parts;
+            g.rsq_in = fz->rsq_in;
+            g.rsq_in_parts = fz->rsq_in_parts;
+            g.norm_w = fz->norm_w;
+            g.eps = fz->eps;
+        }
         // tile: 16 * RT rows x 16 * CT columns (variants: RT 1 / 2 / 4 with
         // CT 1, then (RT, CT) = (2, 2), (1, 2), (2, 4), (1, 4), (4, 2), (4, 4))
         static const int kRT[] = {1, 2, 4, 2, 1, 2, 1, 4, 4};
@@ -774,6 +516,8 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
             variant = kPick[rt == 1 ? 0 : 1][ct == 1 ? 0 : ct == 2 ? 1 : 2];
         }
         qdepth = env_int("SANDY_GEMM_Q", qdepth);
+        // the RMSNorm-prologue kernels are built for 16- and 32-row tiles only
+        if (norm && kRT[variant] == 4) variant = kCT[variant] == 1 ? 1 : kCT[variant] == 2 ? 3 : 5;
         const int RT = kRT[variant], CT = kCT[variant];
         const int64_t row_tiles = (p.M + 16 * RT - 1) / (16 * RT);
         const int64_t col_tiles = (p.N + 16 * CT - 1) / (16 * CT);
@@ -819,6 +563,11 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
         WAVES_RUN(RT_, CT_, OCC_, 5) WAVES_RUN(RT_, CT_, OCC_, 6) WAVES_RUN(RT_, CT_, OCC_, 8)            \
         WAVES_RUN(RT_, CT_, OCC_, 10) WAVES_RUN(RT_, CT_, OCC_, 12) WAVES_RUN(RT_, CT_, OCC_, 16)         \
     }
+        if (norm) {
+            launch_waves_norm(variant, cps, qdepth, grid, stream, g);
+            SANDY_HIP_TRY(hipGetLastError(), e, what);
+            return ok(e);
+        }
         switch (variant) {
             case 0: WAVES_CPS(1, 1, 4); break;
             case 1: WAVES_CPS(2, 1, 4); break;
@@ -914,6 +663,77 @@ extern "C" int sandy_hip_matmul_glu(const SandyTensor* lhs, const SandyTensor* r
     Plan p{};
     if (const char* msg = plan_matmul(*lhs, *rhs, full, false, true, p)) return fail(e, SANDY_ERR_INVALID, "%s", msg);
     return launch(p, *lhs, *rhs, nullptr, *out, false, true, stream, e, "gated matmul", activation);
+}
+
+// Shared checks of the fused decode GEMMs: bf16, lhs [m, k], rhs [n, k]
+// (transposed weight), row statistics of ceil(cols / 16) float64 partials.
+static int check_fused(const SandyTensor* lhs, const SandyTensor* rhs, const SandyTensor* out, Err e, const char* what) {
+    if (!valid_rank(lhs) || !valid_rank(rhs) || !valid_rank(out))
+        return fail(e, SANDY_ERR_INVALID, "%s requires lhs, rhs and out", what);
+    if (lhs->dtype != SANDY_BF16 || rhs->dtype != SANDY_BF16 || out->dtype != SANDY_BF16)
+        return fail(e, SANDY_ERR_UNSUPPORTED, "%s takes bf16 operands", what);
+    if (lhs->rank != 2 || rhs->rank != 2 || out->rank != 2)
+        return fail(e, SANDY_ERR_INVALID, "%s expects lhs [m, k], rhs [n, k] and out [m, n]", what);
+    if (!contiguous(*lhs) || !contiguous(*rhs) || !contiguous(*out))
+        return fail(e, SANDY_ERR_UNSUPPORTED, "%s requires contiguous tensor views", what);
+    return SANDY_OK;
+}
+
+static bool stats_ok(const SandyRowStats* st, int64_t rows, int64_t cols) {
+    return st && st->sumsq && st->rows == rows && st->parts == (cols + 15) / 16 &&
+           (reinterpret_cast<uintptr_t>(st->sumsq) & 7u) == 0;
+}
+
+extern "C" int sandy_hip_matmul_residual(const SandyTensor* lhs, const SandyTensor* rhs, const SandyTensor* residual,
+                                         const SandyTensor* out, const SandyRowStats* out_stats, void* stream_,
+                                         char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    const char* what = "residual matmul";
+    if (int st = check_fused(lhs, rhs, out, e, what)) return st;
+    if (!valid_rank(residual) || residual->dtype != SANDY_BF16 || !same_shape(*residual, *out) || !contiguous(*residual))
+        return fail(e, SANDY_ERR_INVALID, "%s residual must be a contiguous bf16 tensor shaped like out", what);
+    if (base_ptr(*out) == base_ptr(*lhs)) return fail(e, SANDY_ERR_INVALID, "%s out must not alias lhs", what);
+    Plan p{};
+    if (const char* msg = plan_matmul(*lhs, *rhs, *out, false, true, p)) return fail(e, SANDY_ERR_INVALID, "%s", msg);
+    if (out_stats && !stats_ok(out_stats, p.M, p.N))
+        return fail(e, SANDY_ERR_INVALID, "%s row statistics must be [m, ceil(n / 16)] float64", what);
+    Fusion fz;
+    fz.resid = static_cast<const uint16_t*>(base_ptr(*residual));
+    fz.rsq_out = out_stats ? out_stats->sumsq : nullptr;
+    fz.rsq_parts = out_stats ? out_stats->parts : 0;
+    return launch(p, *lhs, *rhs, nullptr, *out, false, true, stream, e, what, 0, &fz);
+}
+
+extern "C" int sandy_hip_matmul_rms(const SandyTensor* lhs, const SandyRowStats* lhs_stats,
+                                    const SandyTensor* norm_weight, double eps, const SandyTensor* rhs,
+                                    int32_t activation, const SandyTensor* out, void* stream_, char* err,
+                                    size_t err_cap) {
+    Err e{err, err_cap};
+    hipStream_t stream = static_cast<hipStream_t>(stream_);
+    const char* what = "rms matmul";
+    if (int st = check_fused(lhs, rhs, out, e, what)) return st;
+    if (activation < 0 || activation > 2) return fail(e, SANDY_ERR_INVALID, "gated matmul activation must be 1 (silu) or 2 (gelu)");
+    const int64_t K = lhs->dims[1];
+    if (!valid_rank(norm_weight) || norm_weight->dtype != SANDY_BF16 || numel(*norm_weight) != K ||
+        !contiguous(*norm_weight) || (reinterpret_cast<uintptr_t>(base_ptr(*norm_weight)) & 15u) != 0)
+        return fail(e, SANDY_ERR_INVALID, "%s norm weight must be a 16-byte aligned bf16 [k] vector", what);
+    if (!stats_ok(lhs_stats, lhs->dims[0], K))
+        return fail(e, SANDY_ERR_INVALID, "%s row statistics must be [m, ceil(k / 16)] float64", what);
+    SandyTensor full = *out;
+    if (activation) {
+        if (rhs->dims[0] % 2 != 0 || out->dims[1] * 2 != rhs->dims[0])
+            return fail(e, SANDY_ERR_INVALID, "gated matmul weight must be [2 * ffn, k] with gate and up rows interleaved");
+        full.dims[1] = rhs->dims[0];
+    }
+    Plan p{};
+    if (const char* msg = plan_matmul(*lhs, *rhs, full, false, true, p)) return fail(e, SANDY_ERR_INVALID, "%s", msg);
+    Fusion fz;
+    fz.rsq_in = lhs_stats->sumsq;
+    fz.rsq_in_parts = lhs_stats->parts;
+    fz.norm_w = static_cast<const uint16_t*>(base_ptr(*norm_weight));
+    fz.eps = static_cast<float>(eps);
+    return launch(p, *lhs, *rhs, nullptr, *out, false, true, stream, e, what, activation, &fz);
 }
 
 extern "C" int sandy_hip_linear(const SandyTensor* x, const SandyTensor* weight, const SandyTensor* bias,

@@ -1090,11 +1090,6 @@ __global__ void validate_offsets_kernel(const void* __restrict__ offs, int32_t o
     if (lo < 0 || hi < lo || hi > rows) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_OFFSETS));
 }
 
-int env_int(const char* name, int dflt) {
-    const char* v = std::getenv(name);
-    return v ? std::atoi(v) : dflt;
-}
-
 } // namespace
 } // namespace sandy_hip
 

@@ -26,7 +26,13 @@ Layout choices (same arithmetic as the reference program):
   * q/k/v weights are concatenated into one [q + k + v, hidden] matrix and
     gate/up into one [2 * ffn, hidden] matrix, so each is one GEMM; the
     q/k/v and gate/up outputs are contiguous views of those GEMM outputs.
-  * the residual add is fused into the next RMSNorm (sandy_hip_add_rms_norm).
+  * fused_norm (default): the residual adds run in the o and down GEMMs'
+    epilogues (sandy_hip_matmul_residual), which also leave the new residual
+    stream's row sums of squares, and the RMSNorms run in the q/k/v, gate/up
+    and lm-head GEMMs' prologues from those sums (sandy_hip_matmul_rms): no
+    norm launch after block 0's input norm, bit-identical to the unfused
+    program.  fused_norm=False runs each residual add with the next RMSNorm
+    (sandy_hip_add_rms_norm) between plain GEMMs.
 """
 from __future__ import annotations
 
@@ -139,9 +145,9 @@ class TinyLlamaDecoder:
     the attention reads the pools' tables directly."""
 
     def __init__(self, dev: HipDevice, cfg: DecodeConfig, weights: dict, batch: int = 1, fused_qkv: bool = True,
-                 fused_glu: bool = True):
+                 fused_glu: bool = True, fused_norm: bool = True):
         self.dev, self.cfg, self.w, self.batch = dev, cfg, weights, batch
-        self.fused_qkv, self.fused_glu = fused_qkv, fused_glu
+        self.fused_qkv, self.fused_glu, self.fused_norm = fused_qkv, fused_glu, fused_norm
         # row-interleaved gate/up weights for the gated GEMM epilogue (the
         # caller's weight dict is left as it is)
         self.w_glu = {}
@@ -185,6 +191,8 @@ class TinyLlamaDecoder:
         self.d = torch.empty(B, c.hidden, dtype=bf, device=dv)
         self.logits = torch.empty(B, c.vocab, dtype=bf, device=dv)
         self.top_v = torch.empty(B, 1, dtype=bf, device=dv)
+        # row statistics of the two residual-stream buffers (fused_norm)
+        self.stats = [ops.row_stats_buffer(B, c.hidden) for _ in range(2)]
         self._keep = []
         self.program = self._build()
         self.graph = None
@@ -229,6 +237,11 @@ class TinyLlamaDecoder:
         # residual stream: block input x_l in buffer A (x0 for block 0), the
         # residual after attention in buffer B
         res_a, res_b = self.res
+        st_a, st_b = (ops.row_stats(t) for t in self.stats)
+        self._keep += [st_a, st_b]
+        if self.fused_norm:
+            self._build_fused_blocks(prog, x0, nodes, sres, silu, arr, bc, st_a, st_b)
+            return prog
         for layer in range(c.layers):
             if layer == 0:
                 prog.append(_Call("sandy_hip_norm", C.c_int32(0), d(x0), d(w["0.in_norm"]), None, C.c_double(c.eps),
@@ -292,6 +305,62 @@ class TinyLlamaDecoder:
         prog.append(_Call("sandy_hip_topk", d(self.logits), C.c_int64(1), C.c_int64(-1), d(self.top_v),
                           d(self.token), stream=s))
         return prog
+
+    def _attention_calls(self, prog, layer):
+        """q/k/v RoPE, the paged appends and the paged decode attention of one
+        block, from self.qkv to self.ctx (the fused q/k/v launch)."""
+        c, dev, s, B, d = self.cfg, self.dev, self.dev.stream, self.batch, self._d
+        kid = (C.c_uint32 * B)(*self.k_seq[layer])
+        vid = (C.c_uint32 * B)(*self.v_seq[layer])
+        self._keep += [kid, vid]
+        prog.append(_DevCall("sandy_hip_device_decode_qkv", dev.handle, C.c_uint32(self.k_pools[layer]), kid,
+                             C.c_uint32(self.v_pools[layer]), vid, C.c_int32(B), d(self.qkv), C.c_int32(c.heads),
+                             d(self.pos), C.c_double(c.theta), C.c_int32(1), d(self.qr)))
+        kc, table, _ = dev.paged_views(self.k_pools[layer])
+        vc, _, _ = dev.paged_views(self.v_pools[layer])
+        table.contents.dims[0] = B  # rows 0..B-1: the sequences' slots
+        self._keep += [kc, vc, table]
+        prog.append(_Call("sandy_hip_paged_attention", d(self.qr), kc, vc, table, d(self.pos), C.c_int64(0),
+                          C.c_double(1.0 / (c.head_dim ** 0.5)), d(self.ctx), stream=s))
+
+    def _build_fused_blocks(self, prog, x0, nodes, sres, silu, arr, bc, st_a, st_b):
+        """The blocks with the residual adds in the o / down GEMM epilogues and
+        the RMSNorms in the q/k/v, gate/up and lm-head GEMM prologues."""
+        c, w, s, B, d = self.cfg, self.w, self.dev.stream, self.batch, self._d
+        res_a, res_b = self.res
+        ctx2d = self.ctx.view(B, c.heads * c.head_dim)
+        for layer in range(c.layers):
+            if layer == 0:  # the embedding has no statistics: one norm launch
+                prog.append(_Call("sandy_hip_norm", C.c_int32(0), d(x0), d(w["0.in_norm"]), None, C.c_double(c.eps),
+                                  d(self.h), stream=s))
+                prog.append(_Call("sandy_hip_matmul", d(self.h), d(w["0.qkv"]), C.c_int32(0), C.c_int32(1),
+                                  d(self.qkv), stream=s))
+                x_in = x0
+            else:  # x_l in res_a with its statistics
+                prog.append(_Call("sandy_hip_matmul_rms", d(res_a), C.byref(st_a), d(w[f"{layer}.in_norm"]),
+                                  C.c_double(c.eps), d(w[f"{layer}.qkv"]), C.c_int32(0), d(self.qkv), stream=s))
+                x_in = res_a
+            if not self.fused_qkv:
+                raise ValueError("fused_norm takes the fused q/k/v launch")
+            self._attention_calls(prog, layer)
+            # residual after attention: res_b = x_l + o-projection, with statistics
+            prog.append(_Call("sandy_hip_matmul_residual", d(ctx2d), d(w[f"{layer}.o"]), d(x_in), d(res_b),
+                              C.byref(st_b), stream=s))
+            if self.fused_glu:
+                prog.append(_Call("sandy_hip_matmul_rms", d(res_b), C.byref(st_b), d(w[f"{layer}.post_norm"]),
+                                  C.c_double(c.eps), d(self.w_glu[layer]), C.c_int32(1), d(self.act), stream=s))
+            else:
+                prog.append(_Call("sandy_hip_matmul_rms", d(res_b), C.byref(st_b), d(w[f"{layer}.post_norm"]),
+                                  C.c_double(c.eps), d(w[f"{layer}.gate_up"]), C.c_int32(0), d(self.gu), stream=s))
+                prog.append(_Call("sandy_hip_elementwise", nodes, C.c_int32(len(silu)), C.c_uint32(sres), arr, bc,
+                                  C.c_int32(2), d(self.act), stream=s))
+            # x_{l+1} = res_b + down-projection, into res_a with statistics
+            prog.append(_Call("sandy_hip_matmul_residual", d(self.act), d(w[f"{layer}.down"]), d(res_b), d(res_a),
+                              C.byref(st_a), stream=s))
+        prog.append(_Call("sandy_hip_matmul_rms", d(res_a), C.byref(st_a), d(w["norm"]), C.c_double(c.eps),
+                          d(w["lm_head"]), C.c_int32(0), d(self.logits), stream=s))
+        prog.append(_Call("sandy_hip_topk", d(self.logits), C.c_int64(1), C.c_int64(-1), d(self.top_v),
+                          d(self.token), stream=s))
 
     # ------------------------------------------------------------------ running
     def prefill_cache(self, k_rows: list, v_rows: list, seq: int = 0):

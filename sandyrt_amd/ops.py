@@ -417,6 +417,41 @@ def matmul_glu(x, w_interleaved, activation: str = "silu", out=None):
     return out
 
 
+def row_stats_buffer(rows: int, cols: int, device="cuda"):
+    """Float64 [rows, ceil(cols / 16)] buffer for the row statistics the fused
+    decode GEMMs pass along (sums of squares per 16-column group)."""
+    return torch.empty(rows, (cols + 15) // 16, dtype=torch.float64, device=device)
+
+
+def row_stats(buf):
+    """SandyRowStats describing a row_stats_buffer (keep `buf` alive)."""
+    return _lib.SandyRowStats(buf.data_ptr(), buf.shape[0], buf.shape[1])
+
+
+def matmul_residual(x, weight, residual, stats=None, out=None):
+    """bf16(residual + bf16(x @ weight^T)) in one launch (the residual add in
+    the decode GEMM's epilogue); fills `stats` (row_stats_buffer of out's
+    shape) with out's row sums of squares when given."""
+    _require_gpu(x, weight, residual)
+    out = torch.empty(list(x.shape[:-1]) + [weight.shape[0]], dtype=x.dtype, device=x.device) if out is None else out
+    st = C.byref(row_stats(stats)) if stats is not None else None
+    call("sandy_hip_matmul_residual", desc(x), desc(weight), desc(residual), desc(out), st)
+    return out
+
+
+def matmul_rms(x, stats, norm_weight, epsilon: float, weight, activation: str | None = None, out=None):
+    """rms_norm(x, norm_weight) @ weight^T with the normalisation in the GEMM's
+    operand registers, from x's row statistics; activation "silu"/"gelu"
+    takes the row-interleaved gate/up weight as matmul_glu does."""
+    _require_gpu(x, norm_weight, weight)
+    code = {None: 0, "silu": 1, "gelu": 2}[activation]
+    n = weight.shape[0] // (2 if code else 1)
+    out = torch.empty(list(x.shape[:-1]) + [n], dtype=x.dtype, device=x.device) if out is None else out
+    call("sandy_hip_matmul_rms", desc(x), C.byref(row_stats(stats)), desc(norm_weight), float(epsilon), desc(weight),
+         code, desc(out))
+    return out
+
+
 def linear(x, weight, bias, out=None):
     """LinearKernelOp (TensorCalc.cpp:722-773): bias + x @ weight^T."""
     _require_gpu(x, weight, bias)

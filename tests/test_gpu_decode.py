@@ -194,7 +194,9 @@ def test_batched_decode_matches_oracle_per_sequence(oracle):
 
 def test_fused_qkv_step_matches_separate_ops_bit_for_bit():
     """The fused launches (RoPE q and k with both appends; the gate/up GEMM
-    with the SiLU gate in its epilogue) and the reference program's separate
+    with the SiLU gate in its epilogue; the residual adds in the o / down GEMM
+    epilogues and the RMSNorms in the q/k/v, gate/up and lm-head GEMM
+    prologues) and the reference program's separate
     ops give identical logits, tokens and caches, step after step, for a
     batch with ragged contexts."""
     from sandyrt_amd.decode import DecodeConfig, TinyLlamaDecoder, random_weights
@@ -205,7 +207,7 @@ def test_fused_qkv_step_matches_separate_ops_bit_for_bit():
     dev = HipDevice(0)
     try:
         a = TinyLlamaDecoder(dev, cfg, w, batch=4, fused_qkv=True, fused_glu=True)
-        b = TinyLlamaDecoder(dev, cfg, w, batch=4, fused_qkv=False, fused_glu=False)
+        b = TinyLlamaDecoder(dev, cfg, w, batch=4, fused_qkv=False, fused_glu=False, fused_norm=False)
         r = rng(9)
         for s, n in enumerate([3, 16, 17, 90]):
             ks = [from_f32(normal(r, (1, cfg.kv_heads, n, cfg.head_dim)), torch.bfloat16) for _ in range(cfg.layers)]

@@ -245,3 +245,91 @@ def test_matmul_glu_rejects_unsupported(ops):
     with pytest.raises(SandyError, match="with gate and up rows interleaved"):
         ops.matmul_glu(torch.zeros(2, 64, dtype=torch.bfloat16, device="cuda"),
                        torch.zeros(7, 64, dtype=torch.bfloat16, device="cuda"))
+
+
+# ---------------------------------------------------------------- fused decode GEMMs
+def _row_sumsq_groups(t):
+    """Exact float64 sums of squares per (row, 16-column group) of a bf16 matrix."""
+    v = t.float().double().cpu().numpy()
+    m, n = v.shape
+    g = (n + 15) // 16
+    pad = np.zeros((m, g * 16))
+    pad[:, :n] = v * v
+    return pad.reshape(m, g, 16).sum(axis=2)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 2048, 2048), (5, 2048, 2048), (32, 2048, 2048), (32, 5632, 2048),
+                                   (33, 256, 200), (64, 1024, 2560), (3, 96, 40)])
+def test_matmul_residual_matches_matmul_then_add(ops, m, k, n):
+    """Residual epilogue: bit-identical to the GEMM's stored output followed by
+    the residual add (K-split shapes at k 5632, odd widths and row counts);
+    the row statistics equal the exact float64 sums of squares of the sum."""
+    r = rng(m * 7 + k + n)
+    x = from_f32(normal(r, (m, k)), torch.bfloat16)
+    w = from_f32(normal(r, (n, k), 0.05), torch.bfloat16)
+    res = from_f32(normal(r, (m, n)), torch.bfloat16)
+    stats = ops.row_stats_buffer(m, n)
+    got = ops.matmul_residual(x, w, res, stats)
+    prod = ops.matmul(x, w, transpose_rhs=True)
+    nodes, rid = ops.residual_add_nodes()
+    want = ops.elementwise(nodes, rid, [prod, res])
+    assert torch.equal(got, want)
+    np.testing.assert_array_equal(stats.cpu().numpy(), _row_sumsq_groups(want))
+    # in place: out is the residual
+    res2 = res.clone()
+    ops.matmul_residual(x, w, res2, None, out=res2)
+    assert torch.equal(res2, want)
+
+
+@pytest.mark.parametrize("act", [None, "silu", "gelu"])
+@pytest.mark.parametrize("m,k,n", [(1, 2048, 2560), (32, 2048, 2560), (32, 2048, 11264), (16, 2048, 32000),
+                                   (32, 2048, 32000), (48, 2560, 512), (64, 512, 96), (7, 160, 64)])
+def test_matmul_rms_matches_norm_then_matmul(ops, act, m, k, n):
+    """RMSNorm prologue from row statistics: bit-identical to sandy_hip_norm
+    followed by the plain or gated GEMM (tile shapes of every decode
+    projection, the lm-head's 32000 columns, 33..64-row tiles)."""
+    if act and n % 2:
+        pytest.skip("gated weights have an even row count")
+    r = rng(m * 11 + k + n + (0 if act is None else len(act)))
+    x = from_f32(normal(r, (m, k)), torch.bfloat16)
+    nw = from_f32(1.0 + normal(r, (k,), 0.1), torch.bfloat16)
+    w = from_f32(normal(r, (n, k), 0.05), torch.bfloat16)
+    stats = torch.from_numpy(_row_sumsq_groups(x)).cuda()
+    got = ops.matmul_rms(x, stats, nw, 1e-5, w, act)
+    h = ops.rms_norm(x, nw, 1e-5)
+    want = ops.matmul(h, w, transpose_rhs=True) if act is None else ops.matmul_glu(h, w, act)
+    assert torch.equal(got, want)
+
+
+def test_fused_chain_matches_unfused_block(ops):
+    """o projection + residual -> gate/up with the post-attention norm, as the
+    decode step chains them, against add_rms_norm between plain GEMMs."""
+    r = rng(77)
+    m, d, f = 32, 2048, 5632
+    ctx = from_f32(normal(r, (m, d)), torch.bfloat16)
+    x = from_f32(normal(r, (m, d)), torch.bfloat16)
+    wo = from_f32(normal(r, (d, d), 0.02), torch.bfloat16)
+    wgu = ops.interleave_glu_weight(from_f32(normal(r, (f, d), 0.02), torch.bfloat16),
+                                    from_f32(normal(r, (f, d), 0.02), torch.bfloat16))
+    nw = from_f32(1.0 + normal(r, (d,), 0.02), torch.bfloat16)
+    stats = ops.row_stats_buffer(m, d)
+    s = ops.matmul_residual(ctx, wo, x, stats)
+    act = ops.matmul_rms(s, stats, nw, 1e-5, wgu, "silu")
+    o = ops.matmul(ctx, wo, transpose_rhs=True)
+    s2, h = ops.add_rms_norm(o, x, nw, 1e-5)
+    assert torch.equal(s, s2)
+    assert torch.equal(act, ops.matmul_glu(h, wgu, "silu"))
+
+
+def test_fused_gemms_reject_bad_stats(ops):
+    from sandyrt_amd._lib import SandyError
+    x = torch.zeros(4, 64, dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(32, 64, dtype=torch.bfloat16, device="cuda")
+    nw = torch.ones(64, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(SandyError, match=r"row statistics must be \[m, ceil\(k / 16\)\]"):
+        ops.matmul_rms(x, ops.row_stats_buffer(4, 32), nw, 1e-5, w)
+    with pytest.raises(SandyError, match=r"row statistics must be \[m, ceil\(n / 16\)\]"):
+        ops.matmul_residual(x, w, torch.zeros(4, 32, dtype=torch.bfloat16, device="cuda"), ops.row_stats_buffer(4, 64))
+    with pytest.raises(SandyError, match="out must not alias lhs"):
+        sq = torch.zeros(4, 64, dtype=torch.bfloat16, device="cuda")
+        ops.matmul_residual(sq, torch.zeros(64, 64, dtype=torch.bfloat16, device="cuda"), sq, None, out=sq)
