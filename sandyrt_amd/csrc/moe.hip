@@ -695,6 +695,142 @@ __global__ __launch_bounds__(256) void moe_dispatch_kernel(
     }
 }
 
+// Token-major form of the same permute (the default up to 8192 routes):
+// workgroup = (TPW consecutive tokens, batch).  Every workgroup reads the
+// batch's route ids once and builds in LDS the per-expert count of all valid
+// routes and of those before its first route; an exclusive scan of the
+// counts gives the expert offsets.  Its own routes (TPW * k <= 64) are ranked
+// by one wave against the earlier ones of the same expert, so route r lands
+// on row offset[e] + (routes of e before r) -- the reference's expert-major,
+// then token, then slot order.  Each token's row is then read once and
+// written to the rows of its k routes: x is read from HBM once, where the
+// expert-major form reads each row from every XCD that holds one of its
+// experts (1.5x the algorithmic bytes at config 5).
+template <int CH>
+__global__ __launch_bounds__(256) void moe_dispatch_tokens_kernel(
+        const void* __restrict__ ids, int32_t ids_dt, const void* __restrict__ w, int32_t w_dt, int64_t seq,
+        int64_t top_k, int64_t experts, int tpw, const char* __restrict__ x, char* __restrict__ packed,
+        int64_t row_bytes, void* __restrict__ packed_w, void* __restrict__ token_ids, int32_t tok_dt,
+        void* __restrict__ offsets, int32_t off_dt, uint32_t* errw) {
+    extern __shared__ int32_t sh[];
+    int32_t* total = sh;                 // [experts]
+    int32_t* before = sh + experts;      // [experts]
+    int32_t* dest = sh + 2 * experts;    // [64] rows of this workgroup's routes (-1: invalid id)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int64_t b = blockIdx.y;
+    const int64_t routes = seq * top_k;
+    const int64_t rb = b * routes;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * tpw;
+    const int64_t t1 = min<int64_t>(seq, t0 + tpw);
+    const int64_t r0 = t0 * top_k, r1 = t1 * top_k;
+    for (int64_t i = tid; i < 2 * experts; i += 256) sh[i] = 0;
+    int64_t raw[CH];  // every id requested before any is used (clamped)
+    if (ids_dt == SANDY_I64) {
+        const int64_t* p = static_cast<const int64_t*>(ids) + rb;
+#pragma unroll
+        for (int j = 0; j < CH; j++) {
+            const int64_t r = tid + 256 * j;
+            raw[j] = p[r < routes ? r : 0];
+        }
+    } else {
+        const int32_t* p = static_cast<const int32_t*>(ids) + rb;
+#pragma unroll
+        for (int j = 0; j < CH; j++) {
+            const int64_t r = tid + 256 * j;
+            raw[j] = p[r < routes ? r : 0];
+        }
+    }
+    __syncthreads();
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < CH; j++) {
+        const int64_t r = tid + 256 * j;
+        if (r >= routes) break;
+        if (raw[j] < 0 || raw[j] >= experts) {
+            bad = true;
+            continue;
+        }
+        atomicAdd(&total[raw[j]], 1);
+        if (r < r0) atomicAdd(&before[raw[j]], 1);
+    }
+
+    if (bad && blockIdx.x == 0) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_EXPERT_ID));
+    __syncthreads();
+    if (tid < 64) {
+        // exclusive scan of the expert totals into `before` (+= offset), 64 lanes x (experts / 64) each
+        const int per = static_cast<int>((experts + 63) / 64);
+        int run = 0;
+        for (int q = 0; q < per; q++) {
+            const int64_t ex = lane * per + q;
+            run += ex < experts ? total[ex] : 0;
+        }
+        int incl = run;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int up = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += up;
+        }
+        int acc = incl - run;
+        for (int q = 0; q < per; q++) {
+            const int64_t ex = lane * per + q;
+            if (ex < experts) {
+                const int tc = total[ex];
+                if (blockIdx.x == 0) store_index(offsets, off_dt, b * (experts + 1) + ex, acc);
+                before[ex] += acc;
+                acc += tc;
+            }
+        }
+        if (blockIdx.x == 0 && lane == 63) store_index(offsets, off_dt, b * (experts + 1) + experts, incl);
+        // rank this workgroup's routes (lane i: route r0 + i) against the earlier ones of their expert
+        const int64_t r = r0 + lane;
+        int er = -1;
+        if (r < r1) {
+            const int64_t v = ids_dt == SANDY_I64 ? static_cast<const int64_t*>(ids)[rb + r]
+                                                  : static_cast<const int32_t*>(ids)[rb + r];
+            er = v >= 0 && v < experts ? static_cast<int>(v) : -1;
+        }
+        int earlier = 0;
+        for (int j = 0; j < 64; j++) {
+            const int ej = __builtin_amdgcn_readlane(er, j);
+            earlier += j < lane && ej == er;
+        }
+        if (r < r1) {
+            const int row = er >= 0 ? before[er] + earlier : -1;
+            dest[lane] = row;
+            if (row >= 0) {
+                store_any(packed_w, w_dt, rb + row, load_any(w, w_dt, rb + r));
+                store_index(token_ids, tok_dt, rb + row, r / top_k);
+            }
+        }
+    }
+    __syncthreads();
+    // copy: each token's row read once (16-byte pieces), written to its k rows
+    typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));
+    const int P = static_cast<int>(row_bytes >> 4);
+    const int items = static_cast<int>(t1 - t0) * P;
+    constexpr int kU = 8;
+    for (int i0 = 0; i0 < items; i0 += 256 * kU) {
+        u32x4_nt tmp[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const int it = min(i0 + tid + 256 * u, items - 1);
+            const int tl = it / P, pc = it - tl * P;
+            tmp[u] = *reinterpret_cast<const u32x4_nt*>(x + (b * seq + t0 + tl) * row_bytes + pc * 16);
+        }
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const int it = i0 + tid + 256 * u;
+            if (it >= items) break;
+            const int tl = it / P, pc = it - tl * P;
+            for (int s = 0; s < top_k; s++) {
+                const int row = dest[tl * top_k + s];
+                if (row >= 0)
+                    __builtin_nontemporal_store(tmp[u], reinterpret_cast<u32x4_nt*>(packed + (rb + row) * row_bytes + pc * 16));
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- moe_scatter_sum
 // Workgroup = (batch, 4 tokens, 512-column chunk); wave = one token.  The
 // batch's token ids are staged in LDS once per workgroup; each wave collects
@@ -1245,6 +1381,24 @@ extern "C" int sandy_hip_moe_gather(const SandyTensor* x, const SandyTensor* top
     const int64_t row_bytes = hidden * static_cast<int64_t>(dtype_size(x->dtype));
     const int aligned = (row_bytes % 16 == 0) &&
                         ((reinterpret_cast<uintptr_t>(base_ptr(*x)) | reinterpret_cast<uintptr_t>(base_ptr(*packed_x))) & 15) == 0;
+    if (routes <= kDispatchRoutes && batch <= 65535 && aligned && top_k <= 64 && 2 * num_experts + 64 <= 16384 &&
+        env_int("SANDY_MOE_ROUTE_GENERAL", 0) == 0 &&
+        env_int("SANDY_MOE_DISPATCH_EXPERTS", 0) == 0) {
+        // token-major: about 256 workgroups of ceil(seq / 256) tokens (at most 64 routes each)
+        const int64_t tpw = std::max<int64_t>(1, std::min<int64_t>(64 / top_k, (seq + 255) / 256));
+        const int64_t wgs = (seq + tpw - 1) / tpw;
+        if (wgs > 0x7fffffff) return fail(e, SANDY_ERR_UNSUPPORTED, "moe_gather too many tokens");
+        const size_t shb = static_cast<size_t>(2 * num_experts + 64) * sizeof(int32_t);
+        dim3 grid(static_cast<unsigned>(wgs), static_cast<unsigned>(batch));
+        hipLaunchKernelGGL(routes <= 4096 ? moe_dispatch_tokens_kernel<16> : moe_dispatch_tokens_kernel<32>, grid, dim3(256),
+                           shb, stream, base_ptr(*topk_ids), topk_ids->dtype, base_ptr(*topk_weights),
+                           topk_weights->dtype, seq, top_k, num_experts, static_cast<int>(tpw),
+                           static_cast<const char*>(base_ptr(*x)), static_cast<char*>(base_ptr(*packed_x)), row_bytes,
+                           base_ptr(*packed_weights), base_ptr(*token_ids), token_ids->dtype,
+                           base_ptr(*expert_offsets), expert_offsets->dtype, errw);
+        SANDY_HIP_TRY(hipGetLastError(), e, "moe_gather launch");
+        return ok(e);
+    }
     if (routes <= kDispatchRoutes && batch <= 65535 && env_int("SANDY_MOE_ROUTE_GENERAL", 0) == 0) {
         // about 512 workgroups, each expert's rows shared by up to 8: every
         // workgroup re-reads the route ids, so more workgroups cost more
