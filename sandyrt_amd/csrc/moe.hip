@@ -724,6 +724,16 @@ __global__ __launch_bounds__(256) void moe_dispatch_tokens_kernel(
     const int64_t t1 = min<int64_t>(seq, t0 + tpw);
     const int64_t r0 = t0 * top_k, r1 = t1 * top_k;
     for (int64_t i = tid; i < 2 * experts; i += 256) sh[i] = 0;
+    // lane i of wave 0: the id and routing weight of route r0 + i, requested
+    // with the rest (their addresses do not depend on the ranking)
+    const int64_t rmine = min<int64_t>(r0 + lane, max<int64_t>(r1, r0 + 1) - 1);
+    int64_t mine_id = 0;
+    float mine_w = 0.0f;
+    if (tid < 64) {
+        mine_id = ids_dt == SANDY_I64 ? static_cast<const int64_t*>(ids)[rb + rmine]
+                                      : static_cast<const int32_t*>(ids)[rb + rmine];
+        mine_w = load_any(w, w_dt, rb + rmine);
+    }
     int64_t raw[CH];  // every id requested before any is used (clamped)
     if (ids_dt == SANDY_I64) {
         const int64_t* p = static_cast<const int64_t*>(ids) + rb;
@@ -783,12 +793,7 @@ __global__ __launch_bounds__(256) void moe_dispatch_tokens_kernel(
         if (blockIdx.x == 0 && lane == 63) store_index(offsets, off_dt, b * (experts + 1) + experts, incl);
         // rank this workgroup's routes (lane i: route r0 + i) against the earlier ones of their expert
         const int64_t r = r0 + lane;
-        int er = -1;
-        if (r < r1) {
-            const int64_t v = ids_dt == SANDY_I64 ? static_cast<const int64_t*>(ids)[rb + r]
-                                                  : static_cast<const int32_t*>(ids)[rb + r];
-            er = v >= 0 && v < experts ? static_cast<int>(v) : -1;
-        }
+        const int er = r < r1 && mine_id >= 0 && mine_id < experts ? static_cast<int>(mine_id) : -1;
         int earlier = 0;
         for (int j = 0; j < 64; j++) {
             const int ej = __builtin_amdgcn_readlane(er, j);
@@ -798,7 +803,7 @@ __global__ __launch_bounds__(256) void moe_dispatch_tokens_kernel(
             const int row = er >= 0 ? before[er] + earlier : -1;
             dest[lane] = row;
             if (row >= 0) {
-                store_any(packed_w, w_dt, rb + row, load_any(w, w_dt, rb + r));
+                store_any(packed_w, w_dt, rb + row, mine_w);
                 store_index(token_ids, tok_dt, rb + row, r / top_k);
             }
         }
