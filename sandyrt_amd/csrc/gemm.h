@@ -92,8 +92,17 @@ __device__ __forceinline__ float glu_pair(int kind, float gv, float uv) {
 template <int RT, int CT, int Q, int CPS, int OCC, bool NORM = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void gemm_waves_kernel(GemmArgs g) {
     constexpr int kWTile = 16 * CT * 128;
+    // activation rows staged through LDS as whole lines (XL) for tiles of up to
+    // 32 columns, where they are half the bytes a wave loads; the 64-column
+    // tiles load them straight into A registers (measured: o projection
+    // 6.6 -> 5.8 us, q/k/v 7.9 -> 7.3, down 13.6 -> 12.7; lm-head 29.4 -> 33.3)
+    constexpr bool XL = CT <= 2;
+    constexpr int kXTile = XL ? 16 * RT * 128 : 0;  // one chunk of the activation rows
     constexpr int kAcc = RT * CT * 64 * 16;  // one wave's accumulators, bytes
-    constexpr int kLds = 4 * 2 * kWTile > 3 * kAcc ? 4 * 2 * kWTile : 3 * kAcc;
+    // per wave: double-buffered weight tile, one activation tile (a wave's LDS
+    // reads of chunk c are issued before its writes of chunk c + 1, and one
+    // wave's LDS operations complete in order)
+    constexpr int kLds = 4 * (2 * kWTile + kXTile) > 3 * kAcc ? 4 * (2 * kWTile + kXTile) : 3 * kAcc;
     __shared__ __attribute__((aligned(16))) unsigned char lds[kLds];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ct = static_cast<int>(blockIdx.x) / g.splits;
@@ -104,7 +113,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     batch_offsets(g.bm, bz, lo, ro);
     const int64_t M = g.M, N = g.N, K = g.K;
     const int64_t n0 = static_cast<int64_t>(ct) * 16 * CT;
-    unsigned char* wt = lds + wave * 2 * kWTile;
+    unsigned char* wt = lds + wave * (2 * kWTile + kXTile);
+    unsigned char* xt = wt + 2 * kWTile;
     auto swz = [](int row, int piece) { return row * 128 + ((piece ^ ((row >> 1) & 7)) << 4); };
     const int ksteps = static_cast<int>(K / 32);
     const int chunks = (ksteps + 1) / 2;
@@ -122,18 +132,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     const int wlane = static_cast<int>((lane >> 3) * K * 2 + (lane & 7) * 16);
     const int wstep = static_cast<int>(8 * K * 2);
     const int wbase[2] = {swz(lane >> 3, lane & 7), swz(8 + (lane >> 3), lane & 7) - 1024};
-    // A operand of tile t, k-step u: row 16 t + lane % 16, 16-byte piece 4 u + lane / 16
-    int xoff[RT][2];
-#pragma unroll
-    for (int t = 0; t < RT; t++)
-#pragma unroll
-        for (int u = 0; u < 2; u++)
-            xoff[t][u] = static_cast<int>((16 * t + (lane & 15)) * K * 2 + (4 * u + (lane >> 4)) * 16);
     int raddr[2][CT];
 #pragma unroll
     for (int u = 0; u < 2; u++)
 #pragma unroll
         for (int c = 0; c < CT; c++) raddr[u][c] = swz(16 * c + (lane & 15), 4 * u + (lane >> 4));
+    // A operand of tile t, k-step u: row 16 t + lane % 16, 16-byte piece 4 u + lane / 16 -- in the
+    // activation tile (XL) or in global memory
+    int aaddr[2][RT];
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+            aaddr[u][t] = XL ? swz(16 * t + (lane & 15), 4 * u + (lane >> 4))
+                             : static_cast<int>((16 * t + (lane & 15)) * K * 2 + (4 * u + (lane >> 4)) * 16);
 
     f32x4_t acc[RT][CT];
 #pragma unroll
@@ -177,7 +189,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
                 rres[t][c][1] = h[2] | (h[3] << 16);
             }
     }
-    uint4 wv[Q][2 * CT], xv[Q][RT][2], nv[NORM ? Q : 1][2];
+    uint4 wv[Q][2 * CT], xv[Q][2 * RT], nv[NORM ? Q : 1][2];
     const __amdgpu_buffer_rsrc_t nres = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(NORM ? g.norm_w : g.w), 0, NORM ? static_cast<int>(K * 2) : 0, 0x00020000);
     // clamped re-reads past this wave's range: L2 hits, never multiplied
@@ -186,11 +198,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
         for (int i = 0; i < 2 * CT; i++)
             wv[slot][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wlane + i * wstep + kb, 0, 0));
+        // XL: the activation rows as whole lines too (8 rows x 128 bytes per
+        // instruction), staged through LDS like the weights; otherwise the
+        // A operands themselves (half of 16 lines per instruction)
 #pragma unroll
-        for (int t = 0; t < RT; t++)
-#pragma unroll
-            for (int u = 0; u < 2; u++)
-                xv[slot][t][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xres, xoff[t][u] + kb, 0, 0));
+        for (int i = 0; i < 2 * RT; i++)
+            xv[slot][i] = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                           xres, XL ? wlane + i * wstep + kb : aaddr[i & 1][i >> 1] + kb, 0, 0));
         if constexpr (NORM)
 #pragma unroll
             for (int u = 0; u < 2; u++)
@@ -215,6 +230,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     auto store = [&](int slot, int buf) {
 #pragma unroll
         for (int i = 0; i < 2 * CT; i++) *reinterpret_cast<uint4*>(wt + buf * kWTile + wbase[i & 1] + i * 1024) = wv[slot][i];
+        if constexpr (XL)
+#pragma unroll
+            for (int i = 0; i < 2 * RT; i++) *reinterpret_cast<uint4*>(xt + wbase[i & 1] + i * 1024) = xv[slot][i];
     };
     // the second k-step of a half chunk (odd K / 32) is skipped, so the
     // registers past K never reach an MFMA
@@ -225,8 +243,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
             uint4 av[RT];
 #pragma unroll
             for (int t = 0; t < RT; t++) {
-                if constexpr (NORM) av[t] = normed(xv[slot][t][u], nv[slot][u], inv[t]);
-                else av[t] = xv[slot][t][u];
+                const uint4 xa = XL ? *reinterpret_cast<const uint4*>(xt + aaddr[u][t]) : xv[slot][2 * t + u];
+                if constexpr (NORM) av[t] = normed(xa, nv[slot][u], inv[t]);
+                else av[t] = xa;
             }
 #pragma unroll
             for (int c = 0; c < CT; c++) {
