@@ -739,6 +739,15 @@ __global__ __launch_bounds__(64) void paged_decode_units_merge_kernel(PagedArgs 
 template <int D, int NB>
 const void* units_for(int nt) {
     constexpr int kOcc4 = D == 64 ? 5 : 1;  // spill-free only for D = 64, four tiles per wave
+    if constexpr (D == 256) {
+        // held to 2 waves per SIMD: 248 VGPRs and no spills, where the unbounded
+        // allocation (246 VGPRs + 64 AGPRs) leaves one wave per SIMD -- twice the
+        // resident units (config 4: 132.0 -> 122.9 us with 512-key splits)
+        return nt == 2   ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 2, 2, 2>)
+               : nt == 4 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 4, 2, 2>)
+               : nt == 8 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 8, 2, 2>)
+                         : reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 16, 2, 2>);
+    }
     return nt == 2   ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 2, 2, kOcc4>)
            : nt == 4 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 4, 2, kOcc4>)
            : nt == 8 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 8, 2, 1>)
@@ -1232,7 +1241,8 @@ int launch_paged_mfma(const PagedCall& c, const SandyTensor* q, const SandyTenso
     // (the nearest size on a log scale: a table slightly longer than 4096
     // keys keeps 512-key splits)
     const int64_t forced = env_int("SANDY_PAGED_SPLIT", 0);
-    int64_t split = forced > 0 ? forced : (max_keys * B * hkv) / 1024;
+    // (D 256: half of it -- 4x the bytes per key; config 4: 512 keys, 122.9 vs 130.4 us at 1024)
+    int64_t split = forced > 0 ? forced : (max_keys * B * hkv) / (D == 256 ? 2048 : 1024);
     const int nt = forced > 0 ? (split <= 128 && D == 64 ? 2 : split <= 256 ? 4 : split <= 512 ? 8 : 16)
                               : (split <= 362 ? 4 : split <= 724 ? 8 : 16);
     split = 64 * nt;
