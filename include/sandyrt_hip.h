@@ -536,6 +536,28 @@ int sandy_hip_device_decode_qkv(SandyHipDevice* dev, uint32_t k_pool, const uint
                                 const uint32_t* v_tensors, int32_t count, const SandyTensor* qkv, int32_t q_heads,
                                 const SandyTensor* positions, double theta, int32_t split_half,
                                 const SandyTensor* q_out, char* err, size_t err_cap);
+/* The q/k/v projection of one decode step with sandy_hip_device_decode_qkv
+ * in its epilogue: one launch for the GEMM, both RoPEs and both appends.
+ * lhs [count, k] bf16 (count <= 64) is the block input; with lhs_stats and
+ * norm_weight (both or neither) it is RMS-normalised first, as in
+ * sandy_hip_matmul_rms.  rhs [(q_heads + 2 kv_heads) head_dim, k] is the
+ * fused q/k/v weight; for split_half RoPE its q and k rows must be
+ * pair-ordered within each head (row i of a head, then row i + head_dim / 2,
+ * for i < head_dim / 2; v rows as they are).  Sequence i's row is appended at
+ * row positions[i] of k_tensors[i] and v_tensors[i], whose device lengths must
+ * equal positions[i] (as sandy_hip_device_paged_lengths returns them; a
+ * mismatch sets SANDY_DEVERR_POSITION) and become positions[i] + 1.  Results
+ * are bit-identical to sandy_hip_matmul_rms / sandy_hip_matmul into a qkv
+ * buffer followed by sandy_hip_device_decode_qkv.  Fuses the q/k/v
+ * MatMulKernelOp (src/ir/KernelIR.h), its two RoPEKernelOps (KernelIR.h:575-610)
+ * and two Engine::paged_append_op calls (src/engine/Engine.cpp:548-596) of
+ * the TinyLlama eval_token program (src/models/tinyllama/common.sandy.go:
+ * 11-28); the reference has no single counterpart. */
+int sandy_hip_device_matmul_qkv(SandyHipDevice* dev, const SandyTensor* lhs, const SandyRowStats* lhs_stats,
+                                const SandyTensor* norm_weight, double eps, const SandyTensor* rhs, uint32_t k_pool,
+                                const uint32_t* k_tensors, uint32_t v_pool, const uint32_t* v_tensors, int32_t count,
+                                int32_t q_heads, const SandyTensor* positions, double theta, int32_t split_half,
+                                const SandyTensor* q_out, char* err, size_t err_cap);
 /* positions[i] = device length of tensors[i] - 1 (int32 or int64 output), for
  * the position_offsets of decode attention inside a captured step. */
 int sandy_hip_device_paged_positions(SandyHipDevice* dev, uint32_t pool, const uint32_t* tensors, int32_t count,

@@ -196,6 +196,8 @@ DEVICE_SIGNATURES = {
     "sandy_hip_device_paged_lengths": ([DEV, C.c_uint32, U32P, C.c_int32, T], C.c_int),
     "sandy_hip_device_decode_qkv": ([DEV, C.c_uint32, U32P, C.c_uint32, U32P, C.c_int32, T, C.c_int32, T, C.c_double,
                                      C.c_int32, T], C.c_int),
+    "sandy_hip_device_matmul_qkv": ([DEV, T, C.POINTER(SandyRowStats), T, C.c_double, T, C.c_uint32, U32P, C.c_uint32,
+                                     U32P, C.c_int32, C.c_int32, T, C.c_double, C.c_int32, T], C.c_int),
     "sandy_hip_device_paged_meta": ([DEV, C.c_uint32, C.POINTER(SandyPagedMeta)], C.c_int),
     "sandy_hip_device_paged_read": ([DEV, C.c_uint32, C.c_void_p, C.c_uint64], C.c_int),
     "sandy_hip_device_paged_views": ([DEV, C.c_uint32, P, T, T], C.c_int),

@@ -308,6 +308,11 @@ __device__ __forceinline__ double dpp_move(double v) {
                                                        static_cast<uint32_t>(lo)));
 }
 
+// the value of lane ^ 1 (quad_perm [1, 0, 3, 2]), a VALU move
+__device__ __forceinline__ float lane_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
+}
+
 template <int G>
 __device__ __forceinline__ double group_sum(double v) {
     static_assert(G == 2 || G == 4 || G == 8 || G == 16, "group of 2, 4, 8 or 16 lanes");

@@ -33,6 +33,32 @@ __device__ __forceinline__ void batch_offsets(const BatchMap& m, int64_t b, int6
     }
 }
 
+// q/k/v epilogue of the decode GEMM (sandy_hip_device_matmul_qkv): row r of
+// the product is sequence r's q/k/v row.  Its q and k columns are RoPE-rotated
+// (q into q_out [M, hq, d], k appended to the sequence's K pages) and its v
+// columns appended to the V pages, at row pos[r] of the sequence, whose K and
+// V lengths become pos[r] + 1.  With split-half RoPE the weight's q and k rows
+// come pair-ordered within each head (rows i and i + d / 2 adjacent), so both
+// values of a rotation pair sit in lanes l and l ^ 1 of an MFMA tile.
+constexpr int kQkvMaxPairs = 128;
+constexpr int kQkvMaxRows = 64;
+struct QkvRope {
+    uint16_t* q_out;
+    char* k_pages;
+    char* v_pages;
+    const int32_t* k_table;
+    const int32_t* v_table;
+    int32_t* k_len;
+    int32_t* v_len;
+    int64_t page_bytes;
+    int32_t k_max_blocks, v_max_blocks, page_shift, hq, hkv, d, split_half, pos_dt;
+    const void* pos;
+    uint32_t* errw;
+    float denom[kQkvMaxPairs];  // theta^(2i / d), host float powf
+    int32_t k_slots[kQkvMaxRows];
+    int32_t v_slots[kQkvMaxRows];
+};
+
 struct GemmArgs {
     const uint16_t* a;     // [.., M, K]
     const uint16_t* w;     // [.., N, K]
@@ -57,6 +83,7 @@ struct GemmArgs {
     int64_t rsq_in_parts;
     const uint16_t* norm_w;
     float eps;
+    QkvRope qr;
 };
 
 // Gated activation of one bf16-rounded (gate, up) pair with the scalar DAGs
@@ -89,7 +116,7 @@ __device__ __forceinline__ float glu_pair(int kind, float gv, float uv) {
 // four partial accumulators are summed in wave order through LDS; when the
 // grid also splits K across workgroups, the last-arriving workgroup of each
 // tile sums the splits' fp32 partials in split order (deterministic).
-template <int RT, int CT, int Q, int CPS, int OCC, bool NORM = false>
+template <int RT, int CT, int Q, int CPS, int OCC, bool NORM = false, bool ROPE = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void gemm_waves_kernel(GemmArgs g) {
     constexpr int kWTile = 16 * CT * 128;
     // activation rows staged through LDS as whole lines (XL) for tiles of up to
@@ -189,6 +216,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
                 rres[t][c][1] = h[2] | (h[3] << 16);
             }
     }
+    // q/k/v epilogue (wave 0 emits the tile): each lane's rows' positions and
+    // slots, and its columns' angle denominators, requested now; the block ids
+    // and lengths that depend on them go out once the first weight chunks are
+    // in flight.  32-bit index math (a 64-bit division is a long software loop)
+    int32_t qpos[RT][4], qks[RT][4], qvs[RT][4], qkb[RT][4], qvb[RT][4], qkl[RT][4], qvl[RT][4];
+    float qden[CT], qsn[RT][4][CT], qcs[RT][4][CT];
+    if constexpr (ROPE) {
+        // every wave requests them (a wave-0-only branch makes the compiler
+        // copy the results at the join, waiting for each load there)
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int rr = min(static_cast<int>(r0) + 16 * t + 4 * (lane >> 4) + i, static_cast<int>(M) - 1);
+                qpos[t][i] = static_cast<int32_t>(load_index(g.qr.pos, g.qr.pos_dt, rr));
+                qks[t][i] = g.qr.k_slots[rr];
+                qvs[t][i] = g.qr.v_slots[rr];
+            }
+#pragma unroll
+        for (int c = 0; c < CT; c++) {
+            const uint32_t nc = static_cast<uint32_t>(min<int64_t>(n0 + 16 * c + (lane & 15), N - 1));
+            qden[c] = g.qr.denom[(nc % static_cast<uint32_t>(g.qr.d)) >> 1];
+        }
+    }
     uint4 wv[Q][2 * CT], xv[Q][2 * RT], nv[NORM ? Q : 1][2];
     const __amdgpu_buffer_rsrc_t nres = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(NORM ? g.norm_w : g.w), 0, NORM ? static_cast<int>(K * 2) : 0, 0x00020000);
@@ -258,6 +309,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
             }
         }
     };
+    auto rope_ids = [&]() {
+        // slot -> block id of the row's page and the slot's lengths, requested
+        // unconditionally (clamped indices; a block index past the table is
+        // flagged in the epilogue, the loaded id ignored)
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int32_t bi = max(qpos[t][i], 0) >> g.qr.page_shift;
+                const int32_t ks = qks[t][i], vs = qvs[t][i];
+                qkb[t][i] = g.qr.k_table[ks * g.qr.k_max_blocks + min(bi, g.qr.k_max_blocks - 1)];
+                qvb[t][i] = g.qr.v_table[vs * g.qr.v_max_blocks + min(bi, g.qr.v_max_blocks - 1)];
+                qkl[t][i] = g.qr.k_len[ks];
+                qvl[t][i] = g.qr.v_len[vs];
+            }
+        // the rotation angles of this lane's (row, column) pairs, while the
+        // first chunks are in flight (the epilogue only multiplies)
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int c = 0; c < CT; c++)
+                    rope_sincos(static_cast<float>(max(qpos[t][i], 0)) / qden[c], &qsn[t][i][c], &qcs[t][i][c]);
+    };
 #pragma unroll
     for (int s = 0; s < Q; s++) load(c_begin + s, s);
     if constexpr (NORM) {
@@ -283,6 +359,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         if (c < c_end) mma(u % Q, u & 1, c);
         if (c + 1 < c_end) store((u + 1) % Q, (u + 1) & 1);
         load(c + Q, u % Q);
+        // q/k/v epilogue ids after the first chunk: the positions they index by
+        // arrived with it, so nothing waits and every first chunk went out first
+        if constexpr (ROPE)
+            if (u == 0) rope_ids();
     }
 
     // sum the four waves' partials in wave order (LDS reused after a barrier)
@@ -306,8 +386,98 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     }
 
     const int64_t ob = bz * M * N;
+    // q/k/v epilogue: each element's destination (null: none) and value,
+    // stored together once every element is computed -- stores count in the
+    // same counter as loads here, so a wait the compiler places between
+    // address computations would otherwise wait for the earlier stores
+    uint16_t* rp[ROPE ? RT : 1][ROPE ? CT : 1][4];
+    uint16_t rv[ROPE ? RT : 1][ROPE ? CT : 1][4];
+    auto rope_stores = [&]() {
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int c = 0; c < CT; c++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (rp[t][c][i]) *rp[t][c][i] = rv[t][c][i];
+    };
     auto emit = [&](int t, int c, const f32x4_t& v) {
         const int64_t nc = n0 + 16 * c + (lane & 15);
+        if constexpr (ROPE) {
+            // the stored bf16 value of this lane's column and of its pair partner
+            // (lane ^ 1), then the RoPE kernel's arithmetic: angle float(pos) /
+            // denominator, rope_sincos, products and sum rounded separately,
+            // bf16 round to nearest even
+            // the argument fields read once per tile (inside the element loop the
+            // compiler re-reads them with a scalar load and a wait per use)
+            const int d = g.qr.d, hq = g.qr.hq, hkv = g.qr.hkv, shift = g.qr.page_shift;
+            const int split_half = g.qr.split_half;
+            const int32_t kmax = g.qr.k_max_blocks, vmax = g.qr.v_max_blocks;
+            const int64_t page_bytes = g.qr.page_bytes;
+            uint16_t* const q_out = g.qr.q_out;
+            char* const k_pages = g.qr.k_pages;
+            char* const v_pages = g.qr.v_pages;
+            int32_t* const k_len = g.qr.k_len;
+            int32_t* const v_len = g.qr.v_len;
+            uint32_t* const errw = g.qr.errw;
+            const int ncl = static_cast<int>(min<int64_t>(nc, N - 1));
+            const int qk_cols = (hq + hkv) * d;
+            const int head = static_cast<int>(static_cast<uint32_t>(ncl) / static_cast<uint32_t>(d));
+            const int cp = ncl - head * d, pair = cp >> 1, second = ncl & 1;
+            const int dst = split_half ? (second ? pair + (d >> 1) : pair) : cp;
+            const int psz = 1 << shift;
+            const float bias = g.bias ? bf16_to_f32(g.bias[ncl]) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                asm volatile("" : "+v"(qpos[t][i]), "+v"(qkb[t][i]), "+v"(qvb[t][i]), "+v"(qkl[t][i]), "+v"(qvl[t][i]),
+                             "+v"(qks[t][i]), "+v"(qvs[t][i]));
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int rr = static_cast<int>(r0) + 16 * t + 4 * (lane >> 4) + i;
+                const float x = bf16_to_f32(f32_to_bf16(v[i] + bias));
+                const float xp = lane_xor1(x);
+                rp[t][c][i] = nullptr;
+                if (rr >= M || nc >= N) continue;
+                const int32_t pos = qpos[t][i];
+                if (pos < 0) {
+                    atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_POSITION));
+                    continue;
+                }
+                const int32_t bi = pos >> shift;
+                const int32_t kb = bi < kmax ? qkb[t][i] : -1;
+                const int32_t vb = bi < vmax ? qvb[t][i] : -1;
+                const int row_in_page = pos & (psz - 1);
+                if (ncl < qk_cols) {
+                    const float x0 = second ? xp : x, x1 = second ? x : xp;
+                    const float sn = qsn[t][i][c], cs = qcs[t][i][c];
+                    rv[t][c][i] = second ? f32_to_bf16(__fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs)))
+                                         : f32_to_bf16(__fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn)));
+                    if (head < hq)
+                        rp[t][c][i] = q_out + (rr * hq + head) * d + dst;
+                    else if (kb >= 0)
+                        rp[t][c][i] = reinterpret_cast<uint16_t*>(k_pages + kb * page_bytes) +
+                                      ((head - hq) * psz + row_in_page) * d + dst;
+                } else {
+                    rv[t][c][i] = f32_to_bf16(x);
+                    if (vb >= 0)
+                        rp[t][c][i] = reinterpret_cast<uint16_t*>(v_pages + vb * page_bytes) +
+                                      ((head - hq - hkv) * psz + row_in_page) * d + cp;
+                }
+                // column tile 0, first column: the row's lengths advance to pos + 1
+                // (they must equal pos: the row is appended there)
+                if (ct == 0 && c == 0 && (lane & 15) == 0) {
+                    const bool fits = kb >= 0 && vb >= 0;
+                    if (!fits) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
+                    if (qkl[t][i] != pos || qvl[t][i] != pos)
+                        atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_POSITION));
+                    else if (fits) {
+                        k_len[qks[t][i]] = pos + 1;
+                        v_len[qvs[t][i]] = pos + 1;
+                    }
+                }
+            }
+            return;
+        }
         if (g.resid) {
             // out = bf16(resid + bf16(v)) (the GEMM's stored value, then the residual
             // add); the 16 lanes of a row reduce the squares of their 16 columns
@@ -334,7 +504,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const float gv = bf16_to_f32(f32_to_bf16(v[i]));
-                const float uv = __shfl_xor(gv, 1, 64);
+                const float uv = lane_xor1(gv);
                 const int64_t rr = r0 + 16 * t + 4 * (lane >> 4) + i;
                 if ((lane & 1) == 0 && nc < N && rr < M)
                     g.out[(bz * M + rr) * half + (nc >> 1)] = f32_to_bf16(glu_pair(g.glu, gv, uv));
@@ -355,6 +525,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
             for (int t = 0; t < RT; t++)
 #pragma unroll
                 for (int c = 0; c < CT; c++) emit(t, c, acc[t][c]);
+        if constexpr (ROPE)
+            if (wave == 0) rope_stores();
         return;
     }
     // split-K across workgroups: partials written through to the agent's coherence
@@ -413,6 +585,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
             }
             emit(t, c, sum);
         }
+    if constexpr (ROPE) rope_stores();
 }
 
 
@@ -420,5 +593,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 // tile variant as in the host heuristic (RT 1 or 2), run length cps, chunks
 // in flight qdepth.
 void launch_waves_norm(int variant, int cps, int qdepth, dim3 grid, hipStream_t stream, const GemmArgs& g);
+
+// Launches gemm_waves_kernel with the q/k/v epilogue (matmul_qkv.hip): RT 1,
+// CT 1 or 2 (variant 0 or 4), run length cps, four chunks in flight.
+void launch_waves_qkv(int variant, int cps, int qdepth, bool norm, dim3 grid, hipStream_t stream, const GemmArgs& g);
+
+// The q/k/v decode GEMM with the RoPE + paged-append epilogue (QkvRope
+// filled in by the caller except its pointers' validation): lhs [m, k] bf16,
+// rhs [n, k] bf16 with n = (hq + 2 hkv) d; with lhs_stats and norm_weight the
+// RMSNorm prologue of sandy_hip_matmul_rms.  Defined in matmul.hip.
+int matmul_qkv(const SandyTensor* lhs, const SandyRowStats* lhs_stats, const SandyTensor* norm_weight, double eps,
+               const SandyTensor* rhs, const QkvRope& qr, hipStream_t stream, Err e);
 
 } // namespace sandy_hip

@@ -16,6 +16,7 @@
 // Error wording follows the reference (CpuDevice.cpp:444-554,
 // CudaPagedTensor.cpp:30-55,232-258, Device.cpp:13-19).
 #include "common.h"
+#include "gemm.h"
 
 #include <algorithm>
 #include <cmath>
@@ -686,14 +687,22 @@ int sandy_hip_device_paged_append_step(SandyHipDevice* d, uint32_t pool, const u
     return ok(e);
 }
 
-int sandy_hip_device_decode_qkv(SandyHipDevice* d, uint32_t k_pool, const uint32_t* k_tensors, uint32_t v_pool,
-                                const uint32_t* v_tensors, int32_t count, const SandyTensor* qkv, int32_t q_heads,
-                                const SandyTensor* positions, double theta, int32_t split_half,
-                                const SandyTensor* q_out, char* err, size_t err_cap) {
-    Err e{err, err_cap};
-    int st = set_device(d, e);
-    if (st) return st;
-    std::lock_guard<std::mutex> lock(d->impl.mu);
+namespace {
+// Shared set-up of the fused decode q/k/v entry points: the pools' geometry
+// and the head counts checked, each sequence's K and V slot looked up, and
+// the host bookkeeping advanced by one row (pages reserved outside capture),
+// as for the step append.
+struct QkvStep {
+    PagedPool* kp = nullptr;
+    PagedPool* vp = nullptr;
+    int64_t hkv = 0, D = 0;
+    int32_t k_slots[kMaxFusedStep];
+    int32_t v_slots[kMaxFusedStep];
+};
+
+int qkv_step(SandyHipDevice* d, uint32_t k_pool, const uint32_t* k_tensors, uint32_t v_pool,
+             const uint32_t* v_tensors, int32_t count, int32_t q_heads, const SandyTensor* positions, double theta,
+             const SandyTensor* q_out, QkvStep& q, Err e) {
     auto kit = d->impl.pools.find(k_pool), vit = d->impl.pools.find(v_pool);
     if (kit == d->impl.pools.end() || vit == d->impl.pools.end())
         return fail(e, SANDY_ERR_INVALID, "hip device paged pool not found");
@@ -706,35 +715,68 @@ int sandy_hip_device_decode_qkv(SandyHipDevice* d, uint32_t k_pool, const uint32
     const int64_t hkv = kp.prefix, D = kp.inner;
     if (D % 2 != 0 || D / 2 > kMaxFusedPairs) return fail(e, SANDY_ERR_UNSUPPORTED, "decode qkv head dimension unsupported");
     if (q_heads <= 0 || q_heads % hkv != 0) return fail(e, SANDY_ERR_INVALID, "attention heads must be divisible by kv_heads");
-    if (!qkv || qkv->dtype != SANDY_BF16 || qkv->rank != 2 || qkv->dims[0] != count ||
-        qkv->dims[1] != (q_heads + 2 * hkv) * D || qkv->strides[1] != 1)
-        return fail(e, SANDY_ERR_INVALID, "decode qkv input must be [count, (q_heads + 2 kv_heads) head_dim] bf16");
     if (!q_out || q_out->dtype != SANDY_BF16 || numel(*q_out) != count * q_heads * D || !contiguous(*q_out))
         return fail(e, SANDY_ERR_INVALID, "decode qkv q output must be contiguous [count, q_heads, 1, head_dim] bf16");
     if (!positions || !is_index(positions->dtype) || numel(*positions) != count || !contiguous(*positions))
         return fail(e, SANDY_ERR_INVALID, "rope position_ids numel must match the sequence count");
-    const float th = static_cast<float>(theta);
-    if (th <= 0.0f) return fail(e, SANDY_ERR_INVALID, "rope theta must be > 0");
-    uint32_t* errw = device_error_word(e, &st);
-    if (st) return st;
-    DecodeQkvArgs a{};
-    for (int i = 0; i < count; i++) {
+    if (static_cast<float>(theta) <= 0.0f) return fail(e, SANDY_ERR_INVALID, "rope theta must be > 0");
+    // every id checked before any bookkeeping moves
+    for (int i = 0; i < count; i++)
         for (int which = 0; which < 2; which++) {
-            const uint32_t id = which ? v_tensors[i] : k_tensors[i];
-            auto it = d->impl.tensors.find(id);
+            auto it = d->impl.tensors.find(which ? v_tensors[i] : k_tensors[i]);
             if (it == d->impl.tensors.end() || it->second.pool != (which ? v_pool : k_pool))
                 return fail(e, SANDY_ERR_INVALID, "hip device paged tensor not found");
-            PagedTensor& t = it->second;
+        }
+    for (int i = 0; i < count; i++) {
+        for (int which = 0; which < 2; which++) {
+            PagedTensor& t = d->impl.tensors.find(which ? v_tensors[i] : k_tensors[i])->second;
             PagedPool& p = which ? vp : kp;
             // host bookkeeping advances in step with the device, as for the step append
             if (t.grow_length + 1 > static_cast<int64_t>(t.pages.size()) * p.desc.page_size && !d->impl.capturing) {
-                st = reserve(d->impl, t, (t.grow_length + p.desc.page_size) / p.desc.page_size, e);
+                const int st = reserve(d->impl, t, (t.grow_length + p.desc.page_size) / p.desc.page_size, e);
                 if (st) return st;
             }
             t.grow_length += 1;
-            (which ? a.v_slots : a.k_slots)[i] = t.slot;
+            (which ? q.v_slots : q.k_slots)[i] = t.slot;
         }
     }
+    q.kp = &kp;
+    q.vp = &vp;
+    q.hkv = hkv;
+    q.D = D;
+    return SANDY_OK;
+}
+} // namespace
+
+int sandy_hip_device_decode_qkv(SandyHipDevice* d, uint32_t k_pool, const uint32_t* k_tensors, uint32_t v_pool,
+                                const uint32_t* v_tensors, int32_t count, const SandyTensor* qkv, int32_t q_heads,
+                                const SandyTensor* positions, double theta, int32_t split_half,
+                                const SandyTensor* q_out, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    auto kit = d->impl.pools.find(k_pool);
+    if (kit != d->impl.pools.end() && kit->second->prefix > 0) {
+        const int64_t hkv = kit->second->prefix, D = kit->second->inner;
+        if (q_heads <= 0 || q_heads % hkv != 0)
+            return fail(e, SANDY_ERR_INVALID, "attention heads must be divisible by kv_heads");
+        if (!qkv || qkv->dtype != SANDY_BF16 || qkv->rank != 2 || qkv->dims[0] != count ||
+            qkv->dims[1] != (q_heads + 2 * hkv) * D || qkv->strides[1] != 1)
+            return fail(e, SANDY_ERR_INVALID, "decode qkv input must be [count, (q_heads + 2 kv_heads) head_dim] bf16");
+    }
+    uint32_t* errw = device_error_word(e, &st);
+    if (st) return st;
+    QkvStep q;
+    st = qkv_step(d, k_pool, k_tensors, v_pool, v_tensors, count, q_heads, positions, theta, q_out, q, e);
+    if (st) return st;
+    PagedPool& kp = *q.kp;
+    PagedPool& vp = *q.vp;
+    const int64_t hkv = q.hkv, D = q.D;
+    const float th = static_cast<float>(theta);
+    DecodeQkvArgs a{};
+    std::copy(q.k_slots, q.k_slots + count, a.k_slots);
+    std::copy(q.v_slots, q.v_slots + count, a.v_slots);
     a.qkv = static_cast<const uint16_t*>(base_ptr(*qkv));
     a.row_stride = qkv->strides[0];
     a.hq = q_heads;
@@ -763,6 +805,73 @@ int sandy_hip_device_decode_qkv(SandyHipDevice* d, uint32_t k_pool, const uint32
     else hipLaunchKernelGGL(decode_qkv_kernel<false>, dim3(static_cast<unsigned>(count)), dim3(256), 0, d->impl.stream, a);
     SANDY_HIP_TRY(hipGetLastError(), e, "decode qkv launch");
     return ok(e);
+}
+
+int sandy_hip_device_matmul_qkv(SandyHipDevice* d, const SandyTensor* lhs, const SandyRowStats* lhs_stats,
+                                const SandyTensor* norm_weight, double eps, const SandyTensor* rhs, uint32_t k_pool,
+                                const uint32_t* k_tensors, uint32_t v_pool, const uint32_t* v_tensors, int32_t count,
+                                int32_t q_heads, const SandyTensor* positions, double theta, int32_t split_half,
+                                const SandyTensor* q_out, char* err, size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    if (count > kQkvMaxRows) return fail(e, SANDY_ERR_UNSUPPORTED, "qkv matmul takes at most %d sequences", kQkvMaxRows);
+    if (!valid_rank(lhs) || lhs->rank != 2 || lhs->dims[0] != count)
+        return fail(e, SANDY_ERR_INVALID, "qkv matmul lhs must be [count, k]");
+    // the kernel appends 2-byte elements at 16-bit page offsets; the page size
+    // is a power of two (checked when the pool was made)
+    uint32_t* errw = device_error_word(e, &st);
+    if (st) return st;
+    // checks that do not move bookkeeping first: the weight shape is checked
+    // again by the GEMM, but a failure there must not leave lengths advanced
+    auto kit = d->impl.pools.find(k_pool);
+    if (kit != d->impl.pools.end()) {
+        if (q_heads <= 0 || q_heads % kit->second->prefix != 0)
+            return fail(e, SANDY_ERR_INVALID, "attention heads must be divisible by kv_heads");
+        const int64_t n = (q_heads + 2 * kit->second->prefix) * kit->second->inner;
+        if (!valid_rank(rhs) || rhs->rank != 2 || rhs->dims[0] != n || rhs->dims[1] != lhs->dims[1])
+            return fail(e, SANDY_ERR_INVALID, "qkv matmul weight must be [(q_heads + 2 kv_heads) head_dim, k]");
+        if (lhs->dtype != SANDY_BF16 || rhs->dtype != SANDY_BF16 || lhs->dims[1] % 32 != 0 || !contiguous(*lhs) ||
+            !contiguous(*rhs) || ((reinterpret_cast<uintptr_t>(base_ptr(*lhs)) | reinterpret_cast<uintptr_t>(base_ptr(*rhs))) & 15u))
+            return fail(e, SANDY_ERR_UNSUPPORTED, "qkv matmul needs contiguous 16-byte aligned bf16 operands, k a multiple of 32");
+    }
+    for (uint32_t id : {k_pool, v_pool}) {
+        auto it = d->impl.pools.find(id);
+        if (it != d->impl.pools.end() &&
+            static_cast<int64_t>(it->second->desc.max_tensors) * it->second->desc.max_blocks > 0x7fffffff)
+            return fail(e, SANDY_ERR_UNSUPPORTED, "qkv matmul block tables exceed 32-bit indexing");
+    }
+    QkvStep q;
+    st = qkv_step(d, k_pool, k_tensors, v_pool, v_tensors, count, q_heads, positions, theta, q_out, q, e);
+    if (st) return st;
+    QkvRope r{};
+    PagedPool& kp = *q.kp;
+    PagedPool& vp = *q.vp;
+    r.q_out = static_cast<uint16_t*>(base_ptr(*q_out));
+    r.k_pages = kp.pages;
+    r.v_pages = vp.pages;
+    r.k_table = kp.table;
+    r.v_table = vp.table;
+    r.k_len = kp.lengths;
+    r.v_len = vp.lengths;
+    r.k_max_blocks = static_cast<int32_t>(kp.desc.max_blocks);
+    r.v_max_blocks = static_cast<int32_t>(vp.desc.max_blocks);
+    r.page_bytes = static_cast<int64_t>(kp.page_elems * kp.elem);
+    r.page_shift = 0;
+    while ((int64_t{1} << r.page_shift) < kp.desc.page_size) r.page_shift++;
+    r.hq = q_heads;
+    r.hkv = static_cast<int32_t>(q.hkv);
+    r.d = static_cast<int32_t>(q.D);
+    r.split_half = split_half ? 1 : 0;
+    r.pos = base_ptr(*positions);
+    r.pos_dt = positions->dtype;
+    r.errw = errw;
+    const float th = static_cast<float>(theta);
+    for (int i = 0; i < q.D / 2; i++) r.denom[i] = std::pow(th, static_cast<float>(2 * i) / static_cast<float>(q.D));
+    std::copy(q.k_slots, q.k_slots + count, r.k_slots);
+    std::copy(q.v_slots, q.v_slots + count, r.v_slots);
+    return matmul_qkv(lhs, lhs_stats, norm_weight, eps, rhs, r, d->impl.stream, e);
 }
 
 namespace {

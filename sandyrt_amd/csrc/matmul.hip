@@ -418,6 +418,7 @@ struct Fusion {
     int64_t rsq_in_parts = 0;
     const uint16_t* norm_w = nullptr;
     float eps = 0.0f;
+    const QkvRope* qr = nullptr;  // q/k/v RoPE + paged-append epilogue
 };
 
 int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const SandyTensor* bias, const SandyTensor& o,
@@ -470,6 +471,7 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
             g.rsq_in_parts = fz->rsq_in_parts;
             g.norm_w = fz->norm_w;
             g.eps = fz->eps;
+            if (fz->qr) g.qr = *fz->qr;
         }
         // tile: 16 * RT rows x 16 * CT columns (variants: RT 1 / 2 / 4 with
         // CT 1, then (RT, CT) = (2, 2), (1, 2), (2, 4), (1, 4), (4, 2), (4, 4))
@@ -518,6 +520,9 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
         qdepth = env_int("SANDY_GEMM_Q", qdepth);
         // the RMSNorm-prologue kernels are built for 16- and 32-row tiles only
         if (norm && kRT[variant] == 4) variant = kCT[variant] == 1 ? 1 : kCT[variant] == 2 ? 3 : 5;
+        // the q/k/v epilogue kernels: 16-row tiles of 16 or 32 columns
+        const bool qkv = fz && fz->qr;
+        if (qkv) variant = kCT[variant] == 1 ? 0 : 4;
         const int RT = kRT[variant], CT = kCT[variant];
         const int64_t row_tiles = (p.M + 16 * RT - 1) / (16 * RT);
         const int64_t col_tiles = (p.N + 16 * CT - 1) / (16 * CT);
@@ -563,6 +568,11 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
         WAVES_RUN(RT_, CT_, OCC_, 5) WAVES_RUN(RT_, CT_, OCC_, 6) WAVES_RUN(RT_, CT_, OCC_, 8)            \
         WAVES_RUN(RT_, CT_, OCC_, 10) WAVES_RUN(RT_, CT_, OCC_, 12) WAVES_RUN(RT_, CT_, OCC_, 16)         \
     }
+        if (qkv) {
+            launch_waves_qkv(variant, cps, qdepth, norm, grid, stream, g);
+            SANDY_HIP_TRY(hipGetLastError(), e, what);
+            return ok(e);
+        }
         if (norm) {
             launch_waves_norm(variant, cps, qdepth, grid, stream, g);
             SANDY_HIP_TRY(hipGetLastError(), e, what);
@@ -735,6 +745,48 @@ extern "C" int sandy_hip_matmul_rms(const SandyTensor* lhs, const SandyRowStats*
     fz.eps = static_cast<float>(eps);
     return launch(p, *lhs, *rhs, nullptr, *out, false, true, stream, e, what, activation, &fz);
 }
+
+namespace sandy_hip {
+int matmul_qkv(const SandyTensor* lhs, const SandyRowStats* lhs_stats, const SandyTensor* norm_weight, double eps,
+               const SandyTensor* rhs, const QkvRope& qr, hipStream_t stream, Err e) {
+    const char* what = "qkv matmul";
+    if (!valid_rank(lhs) || !valid_rank(rhs)) return fail(e, SANDY_ERR_INVALID, "%s requires lhs and rhs", what);
+    if (lhs->dtype != SANDY_BF16 || rhs->dtype != SANDY_BF16) return fail(e, SANDY_ERR_UNSUPPORTED, "%s takes bf16 operands", what);
+    if (lhs->rank != 2 || rhs->rank != 2 || !contiguous(*lhs) || !contiguous(*rhs))
+        return fail(e, SANDY_ERR_INVALID, "%s expects contiguous lhs [m, k] and rhs [n, k]", what);
+    const int64_t M = lhs->dims[0], K = lhs->dims[1];
+    if (M > kQkvMaxRows) return fail(e, SANDY_ERR_UNSUPPORTED, "%s takes at most %d rows", what, kQkvMaxRows);
+    if (rhs->dims[0] != static_cast<int64_t>(qr.hq + 2 * qr.hkv) * qr.d || rhs->dims[1] != K)
+        return fail(e, SANDY_ERR_INVALID, "%s weight must be [(q_heads + 2 kv_heads) head_dim, k]", what);
+    const bool norm = lhs_stats || norm_weight;
+    if (norm) {
+        if (!valid_rank(norm_weight) || norm_weight->dtype != SANDY_BF16 || numel(*norm_weight) != K ||
+            !contiguous(*norm_weight) || (reinterpret_cast<uintptr_t>(base_ptr(*norm_weight)) & 15u) != 0)
+            return fail(e, SANDY_ERR_INVALID, "%s norm weight must be a 16-byte aligned bf16 [k] vector", what);
+        if (!stats_ok(lhs_stats, M, K))
+            return fail(e, SANDY_ERR_INVALID, "%s row statistics must be [m, ceil(k / 16)] float64", what);
+    }
+    // the product is planned against an [m, n] output the epilogue never writes
+    SandyTensor full{};
+    full.dtype = SANDY_BF16;
+    full.rank = 2;
+    full.dims[0] = M;
+    full.dims[1] = rhs->dims[0];
+    full.strides[0] = rhs->dims[0];
+    full.strides[1] = 1;
+    Plan p{};
+    if (const char* msg = plan_matmul(*lhs, *rhs, full, false, true, p)) return fail(e, SANDY_ERR_INVALID, "%s", msg);
+    Fusion fz;
+    if (norm) {
+        fz.rsq_in = lhs_stats->sumsq;
+        fz.rsq_in_parts = lhs_stats->parts;
+        fz.norm_w = static_cast<const uint16_t*>(base_ptr(*norm_weight));
+        fz.eps = static_cast<float>(eps);
+    }
+    fz.qr = &qr;
+    return launch(p, *lhs, *rhs, nullptr, full, false, true, stream, e, what, 0, &fz);
+}
+} // namespace sandy_hip
 
 extern "C" int sandy_hip_linear(const SandyTensor* x, const SandyTensor* weight, const SandyTensor* bias,
                                 const SandyTensor* out, void* stream_, char* err, size_t err_cap) {

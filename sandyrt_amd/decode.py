@@ -31,7 +31,10 @@ Layout choices (same arithmetic as the reference program):
     stream's row sums of squares, and the RMSNorms run in the q/k/v, gate/up
     and lm-head GEMMs' prologues from those sums (sandy_hip_matmul_rms): no
     norm launch after block 0's input norm, bit-identical to the unfused
-    program.  fused_norm=False runs each residual add with the next RMSNorm
+    program.  With it, fused_rope_gemm (default, up to 64 sequences) also
+    moves the RoPE of q and k and both paged appends into the q/k/v GEMM's
+    epilogue (sandy_hip_device_matmul_qkv, q/k weight rows pair-ordered once
+    at construction).  fused_norm=False runs each residual add with the next RMSNorm
     (sandy_hip_add_rms_norm) between plain GEMMs.
 """
 from __future__ import annotations
@@ -145,9 +148,17 @@ class TinyLlamaDecoder:
     the attention reads the pools' tables directly."""
 
     def __init__(self, dev: HipDevice, cfg: DecodeConfig, weights: dict, batch: int = 1, fused_qkv: bool = True,
-                 fused_glu: bool = True, fused_norm: bool = True):
+                 fused_glu: bool = True, fused_norm: bool = True, fused_rope_gemm: bool = True):
         self.dev, self.cfg, self.w, self.batch = dev, cfg, weights, batch
         self.fused_qkv, self.fused_glu, self.fused_norm = fused_qkv, fused_glu, fused_norm
+        # the RoPE and paged appends in the q/k/v GEMM's epilogue (fused_norm
+        # programs of at most 64 sequences): q/k rows pair-ordered once here
+        self.fused_rope_gemm = fused_rope_gemm and fused_norm and fused_qkv and batch <= 64
+        self.w_qkv = {}
+        if self.fused_rope_gemm:
+            for layer in range(cfg.layers):
+                self.w_qkv[layer] = ops.pair_rope_weight(weights[f"{layer}.qkv"], cfg.heads, cfg.kv_heads,
+                                                         cfg.head_dim)
         # row-interleaved gate/up weights for the gated GEMM epilogue (the
         # caller's weight dict is left as it is)
         self.w_glu = {}
@@ -316,6 +327,11 @@ class TinyLlamaDecoder:
         prog.append(_DevCall("sandy_hip_device_decode_qkv", dev.handle, C.c_uint32(self.k_pools[layer]), kid,
                              C.c_uint32(self.v_pools[layer]), vid, C.c_int32(B), d(self.qkv), C.c_int32(c.heads),
                              d(self.pos), C.c_double(c.theta), C.c_int32(1), d(self.qr)))
+        self._paged_attention_call(prog, layer)
+
+    def _paged_attention_call(self, prog, layer):
+        """Paged decode attention of one block, self.qr -> self.ctx."""
+        c, dev, s, B, d = self.cfg, self.dev, self.dev.stream, self.batch, self._d
         kc, table, _ = dev.paged_views(self.k_pools[layer])
         vc, _, _ = dev.paged_views(self.v_pools[layer])
         table.contents.dims[0] = B  # rows 0..B-1: the sequences' slots
@@ -333,16 +349,31 @@ class TinyLlamaDecoder:
             if layer == 0:  # the embedding has no statistics: one norm launch
                 prog.append(_Call("sandy_hip_norm", C.c_int32(0), d(x0), d(w["0.in_norm"]), None, C.c_double(c.eps),
                                   d(self.h), stream=s))
-                prog.append(_Call("sandy_hip_matmul", d(self.h), d(w["0.qkv"]), C.c_int32(0), C.c_int32(1),
-                                  d(self.qkv), stream=s))
                 x_in = x0
-            else:  # x_l in res_a with its statistics
-                prog.append(_Call("sandy_hip_matmul_rms", d(res_a), C.byref(st_a), d(w[f"{layer}.in_norm"]),
-                                  C.c_double(c.eps), d(w[f"{layer}.qkv"]), C.c_int32(0), d(self.qkv), stream=s))
-                x_in = res_a
+            else:
+                x_in = res_a  # x_l with its statistics
             if not self.fused_qkv:
                 raise ValueError("fused_norm takes the fused q/k/v launch")
-            self._attention_calls(prog, layer)
+            if self.fused_rope_gemm:
+                # q/k/v GEMM (RMSNorm prologue past block 0) with RoPE and both appends in its epilogue
+                kid = (C.c_uint32 * B)(*self.k_seq[layer])
+                vid = (C.c_uint32 * B)(*self.v_seq[layer])
+                self._keep += [kid, vid]
+                lhs, st, nw = (d(self.h), None, None) if layer == 0 else (d(res_a), C.byref(st_a),
+                                                                           d(w[f"{layer}.in_norm"]))
+                prog.append(_DevCall("sandy_hip_device_matmul_qkv", self.dev.handle, lhs, st, nw, C.c_double(c.eps),
+                                     d(self.w_qkv[layer]), C.c_uint32(self.k_pools[layer]), kid,
+                                     C.c_uint32(self.v_pools[layer]), vid, C.c_int32(B), C.c_int32(c.heads),
+                                     d(self.pos), C.c_double(c.theta), C.c_int32(1), d(self.qr)))
+                self._paged_attention_call(prog, layer)
+            else:
+                if layer == 0:
+                    prog.append(_Call("sandy_hip_matmul", d(self.h), d(w["0.qkv"]), C.c_int32(0), C.c_int32(1),
+                                      d(self.qkv), stream=s))
+                else:
+                    prog.append(_Call("sandy_hip_matmul_rms", d(res_a), C.byref(st_a), d(w[f"{layer}.in_norm"]),
+                                      C.c_double(c.eps), d(w[f"{layer}.qkv"]), C.c_int32(0), d(self.qkv), stream=s))
+                self._attention_calls(prog, layer)
             # residual after attention: res_b = x_l + o-projection, with statistics
             prog.append(_Call("sandy_hip_matmul_residual", d(ctx2d), d(w[f"{layer}.o"]), d(x_in), d(res_b),
                               C.byref(st_b), stream=s))

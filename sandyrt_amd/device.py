@@ -119,6 +119,23 @@ class HipDevice:
               C.c_int32(1 if split_half else 0), desc(q_out))
         return q_out
 
+    def matmul_qkv(self, x: torch.Tensor, w_paired: torch.Tensor, k_pool: int, k_tensors, v_pool: int, v_tensors,
+                   q_heads: int, positions: torch.Tensor, theta: float, q_out: torch.Tensor, split_half: bool = True,
+                   stats=None, norm_weight: torch.Tensor = None, eps: float = 0.0):
+        """The q/k/v projection with decode_qkv in its epilogue (one launch):
+        x [count, k] (RMS-normalised first with the row statistics `stats` of
+        ops.row_stats and `norm_weight`), w_paired from ops.pair_rope_weight,
+        rows appended at positions[i], which must equal the tensors' lengths."""
+        if (stats is None) != (norm_weight is None):
+            raise ValueError("matmul_qkv takes both stats and norm_weight or neither")
+        kids = (C.c_uint32 * len(k_tensors))(*k_tensors)
+        vids = (C.c_uint32 * len(v_tensors))(*v_tensors)
+        st = C.byref(_lib.SandyRowStats(stats.data_ptr(), stats.shape[0], stats.shape[1])) if stats is not None else None
+        dcall("sandy_hip_device_matmul_qkv", self.handle, desc(x), st, desc(norm_weight), C.c_double(eps), desc(w_paired), C.c_uint32(k_pool), kids, C.c_uint32(v_pool), vids,
+              C.c_int32(len(k_tensors)), C.c_int32(q_heads), desc(positions), C.c_double(theta),
+              C.c_int32(1 if split_half else 0), desc(q_out))
+        return q_out
+
     def positions(self, pool: int, tensors, out: torch.Tensor):
         ids = (C.c_uint32 * len(tensors))(*tensors)
         dcall("sandy_hip_device_paged_positions", self.handle, C.c_uint32(pool), ids, C.c_int32(len(tensors)),

@@ -406,6 +406,20 @@ def interleave_glu_weight(gate_w, up_w):
     return torch.stack([gate_w, up_w], dim=1).reshape(2 * gate_w.shape[0], gate_w.shape[1]).contiguous()
 
 
+def pair_rope_weight(w_qkv, q_heads: int, kv_heads: int, head_dim: int, split_half: bool = True):
+    """[(q_heads + 2 kv_heads) head_dim, k] fused q/k/v weight -> the row order
+    of sandy_hip_device_matmul_qkv: within each q and k head, row i then row
+    i + head_dim / 2 for i < head_dim / 2 (split-half RoPE pairs adjacent);
+    v rows and interleaved-RoPE weights unchanged."""
+    if not split_half:
+        return w_qkv.contiguous()
+    qk = (q_heads + kv_heads) * head_dim
+    half = head_dim // 2
+    heads = w_qkv[:qk].reshape(q_heads + kv_heads, 2, half, w_qkv.shape[1])
+    paired = heads.permute(0, 2, 1, 3).reshape(qk, w_qkv.shape[1])
+    return torch.cat([paired, w_qkv[qk:]], dim=0).contiguous()
+
+
 def matmul_glu(x, w_interleaved, activation: str = "silu", out=None):
     """act(x @ gate^T) * (x @ up^T) in one launch; bit-identical to matmul then
     the silu_mul / gelu_mul group."""

@@ -247,6 +247,110 @@ def test_decode_qkv_matches_rope_and_step_append(split_half):
         dev.close()
 
 
+# (sequences, q heads, kv heads, head dim, k): TinyLlama's 32/4 x 64 at 1,
+# 3 and 33 rows (16-column tiles at one row, 32-column tiles and three row
+# tiles beyond), Gemma-like 8/2 x 256 with k 2560 (K split over two
+# workgroups, last-arriving sum before the epilogue)
+QKV_SHAPES = [(1, 32, 4, 64, 2048), (3, 32, 4, 64, 2048), (33, 8, 2, 64, 512), (4, 8, 2, 256, 2560)]
+
+
+@pytest.mark.parametrize("norm", [True, False])
+@pytest.mark.parametrize("split_half", [True, False])
+@pytest.mark.parametrize("shape", QKV_SHAPES)
+def test_matmul_qkv_matches_gemm_then_decode_qkv(shape, split_half, norm):
+    """sandy_hip_device_matmul_qkv (q/k weight rows pair-ordered) == the q/k/v
+    GEMM (sandy_hip_matmul_rms / sandy_hip_matmul) into a buffer followed by
+    sandy_hip_device_decode_qkv: q rows, K/V pages and lengths bit for bit."""
+    from sandyrt_amd import ops
+    from sandyrt_amd._lib import BF16
+    from sandyrt_amd.device import HipDevice
+    B, hq, hkv, D, K = shape
+    P = 16
+    dev = HipDevice(0)
+    try:
+        pools, seqs = [], []
+        for _ in range(4):  # fused K, fused V, reference K, reference V
+            p = dev.create_paged_pool([1, hkv, -1, D], BF16, 2, P, max_tensors=B, max_blocks=8)
+            pools.append(p)
+            seqs.append([dev.alloc_paged(p) for _ in range(B)])
+        g = torch.Generator(device="cuda")
+        g.manual_seed(5)
+        ctx = [(7 * s + 15) % 97 for s in range(B)]  # ragged, some on page boundaries
+        ctx[0] = 16
+        for s, n in enumerate(ctx):
+            k0 = torch.randn(1, hkv, n, D, generator=g, device="cuda").to(torch.bfloat16)
+            v0 = torch.randn(1, hkv, n, D, generator=g, device="cuda").to(torch.bfloat16)
+            for i, t in ((0, k0), (1, v0), (2, k0), (3, v0)):
+                dev.reserve_paged(seqs[i][s], 8)
+                dev.append_paged(seqs[i][s], t)
+        n = (hq + 2 * hkv) * D
+        x = torch.randn(B, K, generator=g, device="cuda").to(torch.bfloat16)
+        w = (torch.randn(n, K, generator=g, device="cuda") * K ** -0.5).to(torch.bfloat16)
+        nw = (1 + 0.1 * torch.randn(K, generator=g, device="cuda")).to(torch.bfloat16)
+        pos = torch.tensor(ctx, dtype=torch.int64, device="cuda")
+        q_got = torch.empty(B, hq, 1, D, dtype=torch.bfloat16, device="cuda")
+        q_ref = torch.empty_like(q_got)
+        stats = None
+        if norm:  # exact float64 sums of squares per (row, 16-column group), as the residual epilogue leaves them
+            v = x.double().cpu().numpy()
+            stats = torch.from_numpy((v * v).reshape(B, K // 16, 16).sum(axis=2)).cuda()
+            qkv = ops.matmul_rms(x, stats, nw, 1e-5, w)
+        else:
+            qkv = ops.matmul(x, w, transpose_rhs=True)
+        wp = ops.pair_rope_weight(w, hq, hkv, D, split_half)
+        dev.matmul_qkv(x, wp, pools[0], seqs[0], pools[1], seqs[1], hq, pos, 1e4, q_got, split_half=split_half,
+                       stats=stats, norm_weight=nw if norm else None, eps=1e-5)
+        dev.decode_qkv(pools[2], seqs[2], pools[3], seqs[3], qkv, hq, pos, 1e4, q_ref, split_half=split_half)
+        dev.synchronize()
+        ops.check_device_errors()
+        assert torch.equal(q_got, q_ref)
+        for s in range(B):
+            for fused, ref in ((0, 2), (1, 3)):
+                dev.paged_sync(pools[fused])
+                dev.paged_sync(pools[ref])
+                got = dev.read_paged(seqs[fused][s], np.uint16)
+                assert got.shape[2] == ctx[s] + 1
+                assert np.array_equal(got, dev.read_paged(seqs[ref][s], np.uint16)), (s, fused)
+        # device lengths advanced: the next positions are ctx + 1
+        nxt = torch.empty(B, dtype=torch.int64, device="cuda")
+        dev.lengths(pools[0], seqs[0], nxt)
+        dev.lengths(pools[1], seqs[1], pos)
+        dev.synchronize()
+        assert nxt.tolist() == [c + 1 for c in ctx] and pos.tolist() == nxt.tolist()
+    finally:
+        dev.close()
+
+
+def test_matmul_qkv_position_must_equal_length():
+    """A position that is not the sequence's length is reported as a device
+    position error (SANDY_DEVERR_POSITION) and leaves the length as it was."""
+    from sandyrt_amd import ops
+    from sandyrt_amd._lib import BF16, SandyError
+    from sandyrt_amd.device import HipDevice
+    dev = HipDevice(0)
+    try:
+        kp = dev.create_paged_pool([1, 2, -1, 64], BF16, 2, 16, max_tensors=1, max_blocks=4)
+        vp = dev.create_paged_pool([1, 2, -1, 64], BF16, 2, 16, max_tensors=1, max_blocks=4)
+        k, v = dev.alloc_paged(kp), dev.alloc_paged(vp)
+        dev.reserve_paged(k, 4)
+        dev.reserve_paged(v, 4)
+        x = torch.ones(1, 64, dtype=torch.bfloat16, device="cuda")
+        w = torch.zeros(12 * 64, 64, dtype=torch.bfloat16, device="cuda")
+        q = torch.empty(1, 8, 1, 64, dtype=torch.bfloat16, device="cuda")
+        pos = torch.tensor([3], dtype=torch.int64, device="cuda")
+        dev.matmul_qkv(x, w, kp, [k], vp, [v], 8, pos, 1e4, q)
+        with pytest.raises(SandyError, match="position"):
+            ops.check_device_errors()
+        nxt = torch.empty(1, dtype=torch.int64, device="cuda")
+        dev.lengths(kp, [k], nxt)
+        dev.synchronize()
+        assert nxt.tolist() == [0]
+        with pytest.raises(SandyError, match="weight must be"):
+            dev.matmul_qkv(x, w[:700], kp, [k], vp, [v], 8, pos, 1e4, q)
+    finally:
+        dev.close()
+
+
 def test_decode_qkv_rejects_bad_shapes():
     from sandyrt_amd._lib import BF16, SandyError
     from sandyrt_amd.device import HipDevice
