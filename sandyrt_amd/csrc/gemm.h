@@ -186,7 +186,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     __shared__ float inv_s[kRows];
     // the first 16 partials of this thread, all requested before the weight
     // stream (clamped addresses; unused values dropped by a select when summed)
-    constexpr int kPq = NORM ? 16 : 1;
+    // as many as a 2048-wide row's 128 partials need (longer rows sum the rest
+    // in a loop)
+    constexpr int kPq = NORM ? kRows / 2 : 1;
     double pv[kPq];
     const int64_t prow = NORM ? min<int64_t>(r0 + tid / kTpr, M - 1) : 0;
     if constexpr (NORM) {
@@ -240,7 +242,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
             qden[c] = g.qr.denom[(nc % static_cast<uint32_t>(g.qr.d)) >> 1];
         }
     }
-    uint4 wv[Q][2 * CT], xv[Q][2 * RT], nv[NORM ? Q : 1][2];
+    // norm weights per chunk: XL normalises the activation pieces it stages
+    // (one 16-byte piece per lane), otherwise the A operands (two)
+    uint4 wv[Q][2 * CT], xv[Q][2 * RT], nv[NORM ? Q : 1][XL ? 1 : 2];
     const __amdgpu_buffer_rsrc_t nres = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(NORM ? g.norm_w : g.w), 0, NORM ? static_cast<int>(K * 2) : 0, 0x00020000);
     // clamped re-reads past this wave's range: L2 hits, never multiplied
@@ -257,13 +261,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
             xv[slot][i] = __builtin_bit_cast(
                 uint4, __builtin_amdgcn_raw_buffer_load_b128(
                            xres, XL ? wlane + i * wstep + kb : aaddr[i & 1][i >> 1] + kb, 0, 0));
-        if constexpr (NORM)
+        if constexpr (NORM && XL)
+            nv[slot][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(nres, (lane & 7) * 16 + kb, 0, 0));
+        else if constexpr (NORM)
 #pragma unroll
             for (int u = 0; u < 2; u++)
                 nv[slot][u] = __builtin_bit_cast(uint4,
                                                  __builtin_amdgcn_raw_buffer_load_b128(nres, (4 * u + (lane >> 4)) * 16 + kb, 0, 0));
     };
     float inv[RT];  // RMSNorm prologue: 1 / rms of this lane's A-operand rows
+    float invx[2 * RT];  // (XL) 1 / rms of the rows whose pieces this lane stages
     // y = bf16(x * inv * w): the RMSNorm kernel's operation order, rounded once
     // to nearest even by gfx950's v_cvt_pk_bf16_f32 (f32_to_bf16's rounding)
     auto normed = [&](const uint4& xr, const uint4& wr, float iv) -> uint4 {
@@ -281,9 +288,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     auto store = [&](int slot, int buf) {
 #pragma unroll
         for (int i = 0; i < 2 * CT; i++) *reinterpret_cast<uint4*>(wt + buf * kWTile + wbase[i & 1] + i * 1024) = wv[slot][i];
+        // (NORM) normalised as they are staged: this VALU work overlaps the
+        // previous chunk's MFMAs instead of sitting in front of the next ones
         if constexpr (XL)
 #pragma unroll
-            for (int i = 0; i < 2 * RT; i++) *reinterpret_cast<uint4*>(xt + wbase[i & 1] + i * 1024) = xv[slot][i];
+            for (int i = 0; i < 2 * RT; i++)
+                *reinterpret_cast<uint4*>(xt + wbase[i & 1] + i * 1024) =
+                    NORM ? normed(xv[slot][i], nv[slot][0], invx[i]) : xv[slot][i];
     };
     // the second k-step of a half chunk (odd K / 32) is skipped, so the
     // registers past K never reach an MFMA
@@ -295,7 +306,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
             for (int t = 0; t < RT; t++) {
                 const uint4 xa = XL ? *reinterpret_cast<const uint4*>(xt + aaddr[u][t]) : xv[slot][2 * t + u];
-                if constexpr (NORM) av[t] = normed(xa, nv[slot][u], inv[t]);
+                if constexpr (NORM && !XL) av[t] = normed(xa, nv[slot][u], inv[t]);
                 else av[t] = xa;
             }
 #pragma unroll
@@ -351,6 +362,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         __syncthreads();
 #pragma unroll
         for (int t = 0; t < RT; t++) inv[t] = inv_s[16 * t + (lane & 15)];
+#pragma unroll
+        for (int i = 0; i < 2 * RT; i++) invx[i] = inv_s[(lane >> 3) + 8 * i];
     }
     store(0, 0);
 #pragma unroll
