@@ -750,6 +750,19 @@ __global__ __launch_bounds__(256) void moe_dispatch_tokens_kernel(
             raw[j] = p[r < routes ? r : 0];
         }
     }
+    // the first batch of this workgroup's row pieces, requested with the ids
+    // (they do not depend on the ranking); used after it
+    typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));
+    const int P = static_cast<int>(row_bytes >> 4);
+    const int items = static_cast<int>(t1 - t0) * P;
+    constexpr int kU = 8;
+    u32x4_nt tmp[kU];
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+        const int it = min(tid + 256 * u, items - 1);
+        const int tl = it / P, pc = it - tl * P;
+        tmp[u] = *reinterpret_cast<const u32x4_nt*>(x + (b * seq + t0 + tl) * row_bytes + pc * 16);
+    }
     __syncthreads();
     bool bad = false;
 #pragma unroll
@@ -794,8 +807,10 @@ __global__ __launch_bounds__(256) void moe_dispatch_tokens_kernel(
         // rank this workgroup's routes (lane i: route r0 + i) against the earlier ones of their expert
         const int64_t r = r0 + lane;
         const int er = r < r1 && mine_id >= 0 && mine_id < experts ? static_cast<int>(mine_id) : -1;
+        // over this workgroup's routes only (TPW * k of them, uniform)
+        const int nr = static_cast<int>(r1 - r0);
         int earlier = 0;
-        for (int j = 0; j < 64; j++) {
+        for (int j = 0; j < nr; j++) {
             const int ej = __builtin_amdgcn_readlane(er, j);
             earlier += j < lane && ej == er;
         }
@@ -810,17 +825,14 @@ __global__ __launch_bounds__(256) void moe_dispatch_tokens_kernel(
     }
     __syncthreads();
     // copy: each token's row read once (16-byte pieces), written to its k rows
-    typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));
-    const int P = static_cast<int>(row_bytes >> 4);
-    const int items = static_cast<int>(t1 - t0) * P;
-    constexpr int kU = 8;
     for (int i0 = 0; i0 < items; i0 += 256 * kU) {
-        u32x4_nt tmp[kU];
+        if (i0 > 0) {
 #pragma unroll
-        for (int u = 0; u < kU; u++) {
-            const int it = min(i0 + tid + 256 * u, items - 1);
-            const int tl = it / P, pc = it - tl * P;
-            tmp[u] = *reinterpret_cast<const u32x4_nt*>(x + (b * seq + t0 + tl) * row_bytes + pc * 16);
+            for (int u = 0; u < kU; u++) {
+                const int it = min(i0 + tid + 256 * u, items - 1);
+                const int tl = it / P, pc = it - tl * P;
+                tmp[u] = *reinterpret_cast<const u32x4_nt*>(x + (b * seq + t0 + tl) * row_bytes + pc * 16);
+            }
         }
 #pragma unroll
         for (int u = 0; u < kU; u++) {
