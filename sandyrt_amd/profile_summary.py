@@ -4,6 +4,7 @@
     python -m sandyrt_amd.profile_summary traffic <fetch counter_collection.csv> <write counter_collection.csv>
     python -m sandyrt_amd.profile_summary traffic_bench <fetch csv> <write csv> <bench.py output of the fetch run>
     python -m sandyrt_amd.profile_summary mfma <counter_collection.csv>
+    python -m sandyrt_amd.profile_summary bench_rows <saved traffic table> <bench.py output of the fetch run>
 
 Every table is stamped with the source stamp of the kernels it measured
 (`source_stamp()`: a hash of sandyrt_amd/csrc and include/), so bench.py can
@@ -122,21 +123,21 @@ BENCH_DISPATCH = {
     "rope_qk": ("rope_split_lines_kernel<sandy_hip::BF16, 6, true, false>", "196608"),
     "silu_gate": ("sandy_ew", "524288"),
     "paged_decode": ("paged_decode_units_kernel<64, 2, 8, 2, 1>", "262144"),
-    "c4_paged_decode": ("paged_decode_units_kernel<256, 1, 16, 2, 1>", "262144"),
+    "c4_paged_decode": ("paged_decode_units_kernel<256, 1, 8, 2, 2>", "524288"),
     "c4_rms_norm": ("rms_rows_kernel<sandy_hip::BF16, 8, false, true, false, true>", "4096"),
     "c4_geglu": ("sandy_ew", "40960"),
     "c4_greedy_argmax": ("argmax_wide_kernel<sandy_hip::BF16, 4, true>", "524288"),
     "c1_greedy_argmax": ("argmax_wide_kernel<sandy_hip::F32, 2, false>", "3328"),
-    "c3_qkv_proj": ("sandy_hip::gemm_waves_kernel<1, 2, 4, 8, 1, false>", "40960"),
-    "c3_o_proj": ("sandy_hip::gemm_waves_kernel<1, 1, 4, 8, 1, false>", "65536"),
-    "c3_gate_up_proj": ("sandy_hip::gemm_waves_kernel<1, 2, 2, 8, 4, false>", "180224"),
-    "c3_down_proj": ("sandy_hip::gemm_waves_kernel<1, 2, 2, 8, 4, false>", "98304"),
-    "c3_lm_head": ("sandy_hip::gemm_waves_kernel<2, 4, 2, 8, 2, false>", "128000"),
+    "c3_qkv_proj": ("sandy_hip::gemm_waves_kernel<1, 2, 4, 8, 1, false, false>", "40960"),
+    "c3_o_proj": ("sandy_hip::gemm_waves_kernel<1, 1, 4, 8, 1, false, false>", "65536"),
+    "c3_gate_up_proj": ("sandy_hip::gemm_waves_kernel<1, 2, 2, 8, 4, false, false>", "180224"),
+    "c3_down_proj": ("sandy_hip::gemm_waves_kernel<1, 2, 2, 8, 4, false, false>", "98304"),
+    "c3_lm_head": ("sandy_hip::gemm_waves_kernel<2, 4, 2, 8, 2, false, false>", "128000"),
     "c2_rope_qk_cached": ("rope_split_lines_kernel<sandy_hip::BF16, 6, true, true>", "196608"),
     "c2_rope_cache": ("rope_cache_kernel", "131072"),
     "c2_copy_rope_bytes": ("layout_copy16_kernel", "1179648"),
-    "c5_topk": ("topk_rank_kernel<sandy_hip::F32, 2>", "32768"),
-    "c5_moe_gather": ("moe_dispatch_kernel<16>", "131072"),
+    "c5_topk": ("topk_rank4_kernel<sandy_hip::F32, 2>", "131072"),
+    "c5_moe_gather": ("moe_dispatch_tokens_kernel<16>", "65536"),
     "c5_moe_matmul_gate": ("moe_gemm_lines_kernel<4, 4>", "98304"),
     "c5_swiglu": ("sandy_ew", "180224"),
     "c5_moe_matmul_down": ("moe_gemm_lines_kernel<4, 4>", "360448"),
@@ -147,8 +148,13 @@ BENCH_DISPATCH = {
 def traffic_bench(fetch_path, write_path, bench_log):
     """The traffic table (traffic()) followed by its rows for the bench
     kernels against their algorithmic bytes (the JSON line of `bench_log`)."""
+    return bench_rows(traffic(fetch_path, write_path), bench_log)
+
+
+def bench_rows(table, bench_log):
+    """A traffic() table followed by its rows for the bench kernels (also
+    usable on a table saved earlier: `bench_rows <table.md> <bench log>`)."""
     import json
-    table = traffic(fetch_path, write_path)
     rows = {}
     for line in table.splitlines():
         cells = [c.strip().strip("`") for c in line.strip().strip("|").split("|")]
@@ -186,6 +192,19 @@ def mfma(path, simds=1024):
     return "\n".join(out)
 
 
+def _table_of(path):
+    """The first markdown table (and the line above it) of a saved traffic table."""
+    lines = open(path).read().splitlines()
+    out, seen = [], False
+    for line in lines:
+        if line.startswith("|"):
+            seen = True
+            out.append(line)
+        elif seen:
+            break
+    return "\n".join(out)
+
+
 def main(argv):
     if len(argv) < 2:
         print(__doc__)
@@ -193,7 +212,8 @@ def main(argv):
     kind, args = argv[0], argv[1:]
     print(f"source stamp: `{source_stamp()}`\n")
     print({"trace": lambda: trace(args), "traffic": lambda: traffic(*args[:2]),
-           "traffic_bench": lambda: traffic_bench(*args[:3]), "mfma": lambda: mfma(args[0])}[kind]())
+           "traffic_bench": lambda: traffic_bench(*args[:3]), "mfma": lambda: mfma(args[0]),
+           "bench_rows": lambda: bench_rows(_table_of(args[0]), args[1])}[kind]())
     return 0
 
 
