@@ -720,12 +720,16 @@ int qkv_step(SandyHipDevice* d, uint32_t k_pool, const uint32_t* k_tensors, uint
     if (!positions || !is_index(positions->dtype) || numel(*positions) != count || !contiguous(*positions))
         return fail(e, SANDY_ERR_INVALID, "rope position_ids numel must match the sequence count");
     if (static_cast<float>(theta) <= 0.0f) return fail(e, SANDY_ERR_INVALID, "rope theta must be > 0");
-    // every id checked before any bookkeeping moves
+    // every id checked before any bookkeeping moves; two sequences naming one
+    // tensor would write one row and advance its host length twice
     for (int i = 0; i < count; i++)
         for (int which = 0; which < 2; which++) {
-            auto it = d->impl.tensors.find(which ? v_tensors[i] : k_tensors[i]);
+            const uint32_t* ids = which ? v_tensors : k_tensors;
+            auto it = d->impl.tensors.find(ids[i]);
             if (it == d->impl.tensors.end() || it->second.pool != (which ? v_pool : k_pool))
                 return fail(e, SANDY_ERR_INVALID, "hip device paged tensor not found");
+            for (int j = 0; j < i; j++)
+                if (ids[j] == ids[i]) return fail(e, SANDY_ERR_INVALID, "decode qkv tensors must be distinct");
         }
     for (int i = 0; i < count; i++) {
         for (int which = 0; which < 2; which++) {

@@ -347,6 +347,16 @@ def test_matmul_qkv_position_must_equal_length():
         assert nxt.tolist() == [0]
         with pytest.raises(SandyError, match="weight must be"):
             dev.matmul_qkv(x, w[:700], kp, [k], vp, [v], 8, pos, 1e4, q)
+        # one tensor named by two sequences: rejected before any length moves
+        x2 = torch.ones(2, 64, dtype=torch.bfloat16, device="cuda")
+        q2 = torch.empty(2, 8, 1, 64, dtype=torch.bfloat16, device="cuda")
+        pos2 = torch.zeros(2, dtype=torch.int64, device="cuda")
+        with pytest.raises(SandyError, match="tensors must be distinct"):
+            dev.matmul_qkv(x2, w, kp, [k, k], vp, [v, v], 8, pos2, 1e4, q2)
+        with pytest.raises(SandyError, match="tensors must be distinct"):
+            dev.decode_qkv(kp, [k, k], vp, [v, v], torch.zeros(2, 12 * 64, dtype=torch.bfloat16, device="cuda"), 8,
+                           pos2, 1e4, q2)
+        assert dev.paged_meta(k).grow_length == 1  # only the one call above that launched
     finally:
         dev.close()
 
