@@ -258,6 +258,17 @@ QKV_SHAPES = [(1, 32, 4, 64, 2048), (3, 32, 4, 64, 2048), (33, 8, 2, 64, 512), (
 @pytest.mark.parametrize("split_half", [True, False])
 @pytest.mark.parametrize("shape", QKV_SHAPES)
 def test_matmul_qkv_matches_gemm_then_decode_qkv(shape, split_half, norm):
+    _check_matmul_qkv(shape, split_half, norm, 16, torch.int64)
+
+
+@pytest.mark.parametrize("page,pos_dtype", [(32, torch.int32), (8, torch.int64), (64, torch.int32)])
+def test_matmul_qkv_page_sizes_and_int32_positions(page, pos_dtype):
+    """Other page sizes (row within the page and block index from the page
+    shift) and int32 positions, bit for bit against the two-launch path."""
+    _check_matmul_qkv((5, 16, 4, 128, 1024), True, True, page, pos_dtype)
+
+
+def _check_matmul_qkv(shape, split_half, norm, P, pos_dtype):
     """sandy_hip_device_matmul_qkv (q/k weight rows pair-ordered) == the q/k/v
     GEMM (sandy_hip_matmul_rms / sandy_hip_matmul) into a buffer followed by
     sandy_hip_device_decode_qkv: q rows, K/V pages and lengths bit for bit."""
@@ -265,12 +276,11 @@ def test_matmul_qkv_matches_gemm_then_decode_qkv(shape, split_half, norm):
     from sandyrt_amd._lib import BF16
     from sandyrt_amd.device import HipDevice
     B, hq, hkv, D, K = shape
-    P = 16
     dev = HipDevice(0)
     try:
         pools, seqs = [], []
         for _ in range(4):  # fused K, fused V, reference K, reference V
-            p = dev.create_paged_pool([1, hkv, -1, D], BF16, 2, P, max_tensors=B, max_blocks=8)
+            p = dev.create_paged_pool([1, hkv, -1, D], BF16, 2, P, max_tensors=B, max_blocks=128 // P + 1)
             pools.append(p)
             seqs.append([dev.alloc_paged(p) for _ in range(B)])
         g = torch.Generator(device="cuda")
@@ -281,13 +291,13 @@ def test_matmul_qkv_matches_gemm_then_decode_qkv(shape, split_half, norm):
             k0 = torch.randn(1, hkv, n, D, generator=g, device="cuda").to(torch.bfloat16)
             v0 = torch.randn(1, hkv, n, D, generator=g, device="cuda").to(torch.bfloat16)
             for i, t in ((0, k0), (1, v0), (2, k0), (3, v0)):
-                dev.reserve_paged(seqs[i][s], 8)
+                dev.reserve_paged(seqs[i][s], 128 // P + 1)
                 dev.append_paged(seqs[i][s], t)
         n = (hq + 2 * hkv) * D
         x = torch.randn(B, K, generator=g, device="cuda").to(torch.bfloat16)
         w = (torch.randn(n, K, generator=g, device="cuda") * K ** -0.5).to(torch.bfloat16)
         nw = (1 + 0.1 * torch.randn(K, generator=g, device="cuda")).to(torch.bfloat16)
-        pos = torch.tensor(ctx, dtype=torch.int64, device="cuda")
+        pos = torch.tensor(ctx, dtype=pos_dtype, device="cuda")
         q_got = torch.empty(B, hq, 1, D, dtype=torch.bfloat16, device="cuda")
         q_ref = torch.empty_like(q_got)
         stats = None
