@@ -59,6 +59,33 @@ __device__ __forceinline__ int64_t rope_position(int mode, const void* ids, int3
     return p;
 }
 
+// The position of mode/vec/s in two steps: rope_position_words requests the
+// raw words from a branch-free address (a valid dummy word when the mode needs
+// none) and rope_position_join assembles and range-checks them at the first
+// use, so the loads issued in between are not waited for behind it (a branch
+// on the loaded value, or the sign extension of an int32 id, is a use).
+struct RopeWords {
+    uint32_t lo, hi;
+};
+
+__device__ __forceinline__ RopeWords rope_position_words(int mode, const void* ids, int32_t ids_dt, int64_t vec,
+                                                         int64_t s, const uint32_t* dummy) {
+    const bool i32 = ids_dt == SANDY_I32;
+    const int64_t idx = mode == 2 ? s : mode == 3 ? vec : 0;
+    const uint32_t* p = mode == 0 ? dummy : static_cast<const uint32_t*>(ids) + (i32 ? idx : 2 * idx);
+    RopeWords w;
+    w.lo = p[0];
+    w.hi = p[i32 || mode == 0 ? 0 : 1];
+    return w;
+}
+
+__device__ __forceinline__ int64_t rope_position_join(int mode, int32_t ids_dt, RopeWords w, int64_t s) {
+    if (mode == 0) return s;
+    const int64_t v = ids_dt == SANDY_I32 ? static_cast<int64_t>(static_cast<int32_t>(w.lo))
+                                          : static_cast<int64_t>((static_cast<uint64_t>(w.hi) << 32) | w.lo);
+    return mode == 1 ? v + s : v;
+}
+
 // Split-half, 8 pairs per thread, loads of U heads issued before the sin/cos.
 // grid: (seq * chunks * groups) threads.  FULL: every group holds a multiple
 // of U heads and every pair rotates, so no guards (the per-load and per-pair
@@ -183,10 +210,22 @@ __global__ __launch_bounds__(256) void rope_split_lines_kernel(
     const int64_t o_end = min(outer, o_begin + per_group);
     const int m = static_cast<int>(chunks);
     float cs[8], sn[8];
-    int64_t pos = -1;
+    bool have = false;
     for (int64_t o0 = o_begin; o0 < o_end; o0 += U) {
-        const bool fresh = mode == 3 || pos < 0;
-        if (fresh) pos = TAB ? 0 : rope_position(mode, ids, ids_dt, o0 * seq + s, s, errw);
+        const bool fresh = mode == 3 || !have;
+        // issue order: the position and this lane's angle denominators (their
+        // waits then leave the rows in flight), the cos/sin table entries, the
+        // rows; the position is range-checked once the rows are requested
+        RopeWords pw{0, 0};
+        float den4[4];
+        if (!TAB && fresh) {
+            pw = rope_position_words(mode, ids, ids_dt, o0 * seq + s, s, errw);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int p = c * 8 + (hi ? 4 : 0) + i;
+                den4[i] = args.denom[FULL || p < rot_pairs ? p : 0];
+            }
+        }
         float2 tv[4];
         if (TAB && fresh) {  // requested with the row's loads
 #pragma unroll
@@ -205,6 +244,12 @@ __global__ __launch_bounds__(256) void rope_split_lines_kernel(
             }
         }
         if (fresh) {
+            int64_t pos = TAB ? 0 : rope_position_join(mode, ids_dt, pw, s);
+            if (pos < 0) {
+                atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_POSITION));
+                pos = 0;
+            }
+            have = true;
             const float fp = static_cast<float>(pos);
             float s4[4], c4[4];
 #pragma unroll
@@ -218,7 +263,7 @@ __global__ __launch_bounds__(256) void rope_split_lines_kernel(
                         s4[i] = tv[i].y;
                     }
                 } else if (FULL || p < rot_pairs) {
-                    rope_sincos(fp / args.denom[p], &s4[i], &c4[i]);
+                    rope_sincos(fp / den4[i], &s4[i], &c4[i]);
                 }
             }
 #pragma unroll
