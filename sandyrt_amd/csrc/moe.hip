@@ -30,6 +30,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <cstdlib>
 
 namespace sandy_hip {
@@ -703,87 +704,94 @@ __global__ __launch_bounds__(256) void moe_dispatch_kernel(
 // written to the rows of its k routes: x is read from HBM once, where the
 // expert-major form reads each row from every XCD that holds one of its
 // experts (1.5x the algorithmic bytes at config 5).
-template <int CH>
+//
+// Nothing loaded is consumed before every load is issued: ids are compiled
+// for their width (I64), the routing weight is copied as raw bits (packed
+// weights share its dtype), and the copy is compiled for the route count
+// per token (TK; 0 = any, destination rows read 8 at a time), so each
+// piece's stores issue back to back instead of one LDS round trip apart.
+template <int CH, int TK, bool I64>
 __global__ __launch_bounds__(256) void moe_dispatch_tokens_kernel(
-        const void* __restrict__ ids, int32_t ids_dt, const void* __restrict__ w, int32_t w_dt, int64_t seq,
-        int64_t top_k, int64_t experts, int tpw, const char* __restrict__ x, char* __restrict__ packed,
+        const void* __restrict__ ids, const void* __restrict__ w, int32_t w_dt, int64_t seq,
+        int64_t top_k_arg, int64_t experts, int tpw, const char* __restrict__ x, char* __restrict__ packed,
         int64_t row_bytes, void* __restrict__ packed_w, void* __restrict__ token_ids, int32_t tok_dt,
         void* __restrict__ offsets, int32_t off_dt, uint32_t* errw) {
+    // 32-bit route and expert arithmetic: the launch keeps routes <= 8192
+    // and 2 * experts + 64 <= 16384
+    const int top_k = TK > 0 ? TK : static_cast<int>(top_k_arg);
+    const int E = static_cast<int>(experts);
     extern __shared__ int32_t sh[];
-    int32_t* total = sh;                 // [experts]
-    int32_t* before = sh + experts;      // [experts]
-    int32_t* dest = sh + 2 * experts;    // [64] rows of this workgroup's routes (-1: invalid id)
+    int32_t* total = sh;           // [experts] valid routes (low 16 bits) and those before r0 (high 16 bits)
+    int32_t* before = sh + E;      // [experts] first row of the expert's routes from r0 on
+    int32_t* dest = sh + 2 * E;    // [64] rows of this workgroup's routes (-1: invalid id)
     const int tid = threadIdx.x, lane = tid & 63;
     const int64_t b = blockIdx.y;
-    const int64_t routes = seq * top_k;
+    const int routes = static_cast<int>(seq) * top_k;
     const int64_t rb = b * routes;
-    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * tpw;
-    const int64_t t1 = min<int64_t>(seq, t0 + tpw);
-    const int64_t r0 = t0 * top_k, r1 = t1 * top_k;
-    for (int64_t i = tid; i < 2 * experts; i += 256) sh[i] = 0;
+    const int t0 = static_cast<int>(blockIdx.x) * tpw;
+    const int t1 = min(static_cast<int>(seq), t0 + tpw);
+    const int r0 = t0 * top_k, r1 = t1 * top_k;
+    for (int i = tid; i < E; i += 256) total[i] = 0;
     // lane i of wave 0: the id and routing weight of route r0 + i, requested
     // with the rest (their addresses do not depend on the ranking)
-    const int64_t rmine = min<int64_t>(r0 + lane, max<int64_t>(r1, r0 + 1) - 1);
-    int64_t mine_id = 0;
-    float mine_w = 0.0f;
+    const int rmine = min(r0 + lane, max(r1, r0 + 1) - 1);
+    typedef typename std::conditional<I64, uint64_t, uint32_t>::type id_t;  // unsigned: one range test
+    const id_t* idp = static_cast<const id_t*>(ids) + rb;
+    const bool wbf = w_dt == SANDY_BF16;
+    id_t mine_id = 0;
+    uint32_t mine_w = 0;  // raw bits of the routing weight
     if (tid < 64) {
-        mine_id = ids_dt == SANDY_I64 ? static_cast<const int64_t*>(ids)[rb + rmine]
-                                      : static_cast<const int32_t*>(ids)[rb + rmine];
-        mine_w = load_any(w, w_dt, rb + rmine);
+        mine_id = idp[rmine];
+        mine_w = wbf ? static_cast<uint32_t>(static_cast<const uint16_t*>(w)[rb + rmine])
+                     : static_cast<const uint32_t*>(w)[rb + rmine];
     }
-    int64_t raw[CH];  // every id requested before any is used (clamped)
-    if (ids_dt == SANDY_I64) {
-        const int64_t* p = static_cast<const int64_t*>(ids) + rb;
+    id_t raw[CH];  // every id requested before any is used (clamped)
 #pragma unroll
-        for (int j = 0; j < CH; j++) {
-            const int64_t r = tid + 256 * j;
-            raw[j] = p[r < routes ? r : 0];
-        }
-    } else {
-        const int32_t* p = static_cast<const int32_t*>(ids) + rb;
-#pragma unroll
-        for (int j = 0; j < CH; j++) {
-            const int64_t r = tid + 256 * j;
-            raw[j] = p[r < routes ? r : 0];
-        }
+    for (int j = 0; j < CH; j++) {
+        const int r = tid + 256 * j;
+        raw[j] = idp[r < routes ? r : 0];
     }
     // the first batch of this workgroup's row pieces, requested with the ids
     // (they do not depend on the ranking); used after it
     typedef unsigned u32x4_nt __attribute__((ext_vector_type(4)));
     const int P = static_cast<int>(row_bytes >> 4);
-    const int items = static_cast<int>(t1 - t0) * P;
+    const int items = (t1 - t0) * P;
+    const char* xw = x + (b * seq + t0) * row_bytes;  // this workgroup's first token row
     constexpr int kU = 8;
     u32x4_nt tmp[kU];
 #pragma unroll
     for (int u = 0; u < kU; u++) {
         const int it = min(tid + 256 * u, items - 1);
         const int tl = it / P, pc = it - tl * P;
-        tmp[u] = *reinterpret_cast<const u32x4_nt*>(x + (b * seq + t0 + tl) * row_bytes + pc * 16);
+        tmp[u] = *reinterpret_cast<const u32x4_nt*>(xw + tl * row_bytes + pc * 16);
     }
+    // the ids are first used here, after every load above is issued (the
+    // compiler would otherwise hoist their range tests up to their loads and
+    // wait there, ahead of the row pieces)
+#pragma unroll
+    for (int j = 0; j < CH; j++) asm volatile("" : "+v"(raw[j]));
     __syncthreads();
     bool bad = false;
+    // every id is tested whatever its route (no early exit): a use only past
+    // a branch would let the compiler move that id's load behind the barrier
 #pragma unroll
     for (int j = 0; j < CH; j++) {
-        const int64_t r = tid + 256 * j;
-        if (r >= routes) break;
-        if (raw[j] < 0 || raw[j] >= experts) {
-            bad = true;
-            continue;
-        }
-        atomicAdd(&total[raw[j]], 1);
-        if (r < r0) atomicAdd(&before[raw[j]], 1);
+        const int r = tid + 256 * j;
+        const bool in = r < routes;
+        const bool ok = raw[j] < static_cast<id_t>(E);  // negative ids wrap past E
+        const int e = static_cast<int>(raw[j]);
+        bad = bad || (in && !ok);
+        if (in && ok) atomicAdd(&total[e], r < r0 ? 0x10001 : 1);  // both counts in one atomic (routes < 2^16)
     }
 
     if (bad && blockIdx.x == 0) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_EXPERT_ID));
     __syncthreads();
     if (tid < 64) {
         // exclusive scan of the expert totals into `before` (+= offset), 64 lanes x (experts / 64) each
-        const int per = static_cast<int>((experts + 63) / 64);
+        const int per = (E + 63) >> 6;
+        const int ex0 = lane * per;
         int run = 0;
-        for (int q = 0; q < per; q++) {
-            const int64_t ex = lane * per + q;
-            run += ex < experts ? total[ex] : 0;
-        }
+        for (int q = 0; q < per; q++) run += ex0 + q < E ? total[ex0 + q] & 0xffff : 0;
         int incl = run;
 #pragma unroll
         for (int d = 1; d < 64; d <<= 1) {
@@ -791,21 +799,22 @@ __global__ __launch_bounds__(256) void moe_dispatch_tokens_kernel(
             if (lane >= d) incl += up;
         }
         int acc = incl - run;
+        const int64_t ob = b * (experts + 1);
         for (int q = 0; q < per; q++) {
-            const int64_t ex = lane * per + q;
-            if (ex < experts) {
+            const int ex = ex0 + q;
+            if (ex < E) {
                 const int tc = total[ex];
-                if (blockIdx.x == 0) store_index(offsets, off_dt, b * (experts + 1) + ex, acc);
-                before[ex] += acc;
-                acc += tc;
+                if (blockIdx.x == 0) store_index(offsets, off_dt, ob + ex, acc);
+                before[ex] = acc + (tc >> 16);
+                acc += tc & 0xffff;
             }
         }
-        if (blockIdx.x == 0 && lane == 63) store_index(offsets, off_dt, b * (experts + 1) + experts, incl);
+        if (blockIdx.x == 0 && lane == 63) store_index(offsets, off_dt, ob + E, incl);
         // rank this workgroup's routes (lane i: route r0 + i) against the earlier ones of their expert
-        const int64_t r = r0 + lane;
-        const int er = r < r1 && mine_id >= 0 && mine_id < experts ? static_cast<int>(mine_id) : -1;
+        const int r = r0 + lane;
+        const int er = r < r1 && mine_id < static_cast<id_t>(E) ? static_cast<int>(mine_id) : -1;
         // over this workgroup's routes only (TPW * k of them, uniform)
-        const int nr = static_cast<int>(r1 - r0);
+        const int nr = r1 - r0;
         int earlier = 0;
         for (int j = 0; j < nr; j++) {
             const int ej = __builtin_amdgcn_readlane(er, j);
@@ -815,7 +824,10 @@ __global__ __launch_bounds__(256) void moe_dispatch_tokens_kernel(
             const int row = er >= 0 ? before[er] + earlier : -1;
             dest[lane] = row;
             if (row >= 0) {
-                store_any(packed_w, w_dt, rb + row, mine_w);
+                if (wbf)
+                    static_cast<uint16_t*>(packed_w)[rb + row] = static_cast<uint16_t>(mine_w);
+                else
+                    static_cast<uint32_t*>(packed_w)[rb + row] = mine_w;
                 store_index(token_ids, tok_dt, rb + row, r / top_k);
             }
         }
@@ -828,7 +840,7 @@ __global__ __launch_bounds__(256) void moe_dispatch_tokens_kernel(
             for (int u = 0; u < kU; u++) {
                 const int it = min(i0 + tid + 256 * u, items - 1);
                 const int tl = it / P, pc = it - tl * P;
-                tmp[u] = *reinterpret_cast<const u32x4_nt*>(x + (b * seq + t0 + tl) * row_bytes + pc * 16);
+                tmp[u] = *reinterpret_cast<const u32x4_nt*>(xw + tl * row_bytes + pc * 16);
             }
         }
 #pragma unroll
@@ -836,13 +848,33 @@ __global__ __launch_bounds__(256) void moe_dispatch_tokens_kernel(
             const int it = i0 + tid + 256 * u;
             if (it >= items) break;
             const int tl = it / P, pc = it - tl * P;
-            for (int s = 0; s < top_k; s++) {
-                const int row = dest[tl * top_k + s];
-                if (row >= 0)
-                    __builtin_nontemporal_store(tmp[u], reinterpret_cast<u32x4_nt*>(packed + (rb + row) * row_bytes + pc * 16));
+            constexpr int kS = TK > 0 ? TK : 8;  // destination rows read per group
+            for (int s0 = 0; s0 < top_k; s0 += kS) {
+                int rows[kS];
+#pragma unroll
+                for (int s = 0; s < kS; s++) rows[s] = TK > 0 || s0 + s < top_k ? dest[tl * top_k + s0 + s] : -1;
+#pragma unroll
+                for (int s = 0; s < kS; s++)
+                    if (rows[s] >= 0)
+                        __builtin_nontemporal_store(tmp[u],
+                                                    reinterpret_cast<u32x4_nt*>(packed + (rb + rows[s]) * row_bytes + pc * 16));
             }
         }
     }
+}
+
+template <int CH, int TK>
+const void* dispatch_tokens_for(bool i64) {
+    return i64 ? reinterpret_cast<const void*>(&moe_dispatch_tokens_kernel<CH, TK, true>)
+               : reinterpret_cast<const void*>(&moe_dispatch_tokens_kernel<CH, TK, false>);
+}
+
+template <int CH>
+const void* dispatch_tokens_ch(int64_t top_k, bool i64) {
+    return top_k == 8   ? dispatch_tokens_for<CH, 8>(i64)
+           : top_k == 4 ? dispatch_tokens_for<CH, 4>(i64)
+           : top_k == 2 ? dispatch_tokens_for<CH, 2>(i64)
+                        : dispatch_tokens_for<CH, 0>(i64);
 }
 
 // ---------------------------------------------------------------- moe_scatter_sum
@@ -1404,13 +1436,22 @@ extern "C" int sandy_hip_moe_gather(const SandyTensor* x, const SandyTensor* top
         if (wgs > 0x7fffffff) return fail(e, SANDY_ERR_UNSUPPORTED, "moe_gather too many tokens");
         const size_t shb = static_cast<size_t>(2 * num_experts + 64) * sizeof(int32_t);
         dim3 grid(static_cast<unsigned>(wgs), static_cast<unsigned>(batch));
-        hipLaunchKernelGGL(routes <= 4096 ? moe_dispatch_tokens_kernel<16> : moe_dispatch_tokens_kernel<32>, grid, dim3(256),
-                           shb, stream, base_ptr(*topk_ids), topk_ids->dtype, base_ptr(*topk_weights),
-                           topk_weights->dtype, seq, top_k, num_experts, static_cast<int>(tpw),
-                           static_cast<const char*>(base_ptr(*x)), static_cast<char*>(base_ptr(*packed_x)), row_bytes,
-                           base_ptr(*packed_weights), base_ptr(*token_ids), token_ids->dtype,
-                           base_ptr(*expert_offsets), expert_offsets->dtype, errw);
-        SANDY_HIP_TRY(hipGetLastError(), e, "moe_gather launch");
+        const bool i64 = topk_ids->dtype == SANDY_I64;
+        const void* kern = routes <= 4096 ? dispatch_tokens_ch<16>(top_k, i64) : dispatch_tokens_ch<32>(top_k, i64);
+        const void* ids_p = base_ptr(*topk_ids);
+        const void* w_p = base_ptr(*topk_weights);
+        int32_t w_dt = topk_weights->dtype, tok_dt = token_ids->dtype, off_dt = expert_offsets->dtype;
+        int64_t seq_a = seq, topk_a = top_k, experts_a = num_experts;
+        int tpw_a = static_cast<int>(tpw);
+        const char* x_p = static_cast<const char*>(base_ptr(*x));
+        char* px_p = static_cast<char*>(base_ptr(*packed_x));
+        int64_t rb_a = row_bytes;
+        void* pw_p = base_ptr(*packed_weights);
+        void* tok_p = base_ptr(*token_ids);
+        void* off_p = base_ptr(*expert_offsets);
+        void* args[] = {&ids_p, &w_p, &w_dt, &seq_a, &topk_a, &experts_a, &tpw_a, &x_p, &px_p,
+                        &rb_a, &pw_p, &tok_p, &tok_dt, &off_p, &off_dt, &errw};
+        SANDY_HIP_TRY(hipLaunchKernel(kern, grid, dim3(256), args, shb, stream), e, "moe_gather launch");
         return ok(e);
     }
     if (routes <= kDispatchRoutes && batch <= 65535 && env_int("SANDY_MOE_ROUTE_GENERAL", 0) == 0) {

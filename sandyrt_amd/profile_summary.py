@@ -137,7 +137,7 @@ BENCH_DISPATCH = {
     "c2_rope_cache": ("rope_cache_kernel", "131072"),
     "c2_copy_rope_bytes": ("layout_copy16_kernel", "1179648"),
     "c5_topk": ("topk_rank4_kernel<sandy_hip::F32, 2>", "131072"),
-    "c5_moe_gather": ("moe_dispatch_tokens_kernel<16>", "65536"),
+    "c5_moe_gather": ("moe_dispatch_tokens_kernel<16, 8, true>", "65536"),
     "c5_moe_matmul_gate": ("moe_gemm_lines_kernel<4, 4>", "98304"),
     "c5_swiglu": ("sandy_ew", "180224"),
     "c5_moe_matmul_down": ("moe_gemm_lines_kernel<4, 4>", "360448"),

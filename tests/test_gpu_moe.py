@@ -179,6 +179,35 @@ def test_moe_gather_bad_expert_sets_device_error(ops):
         ops.check_device_errors()
 
 
+@pytest.mark.parametrize("bad,tdt", [(-1, torch.int32), (-1, torch.int64), (1 << 33, torch.int64)])
+def test_moe_gather_bad_expert_top8(ops, oracle, bad, tdt):
+    """Top-8 routes (the dispatch compiled for 8 routes per token) with one
+    invalid id: a negative one, or an int64 id whose high word is set.  The
+    flag is raised and every valid route is still packed as the reference
+    packs it (the invalid route is skipped)."""
+    from sandyrt_amd._lib import SandyError
+    r = rng(33)
+    T, H, E, K = 40, 64, 16, 8
+    ids = np.stack([r.permutation(E)[:K] for _ in range(T)]).astype(np.int64)
+    ids[17, 3] = bad
+    x = from_f32(normal(r, (T, H)), torch.bfloat16)
+    w = from_f32(np.abs(normal(r, (T, K))), torch.bfloat16)
+    px, pw, tok, off = ops.moe_gather(x, torch.from_numpy(ids).to(tdt).cuda(), w, E)
+    with pytest.raises(SandyError, match="moe_gather topk expert id out of range"):
+        ops.check_device_errors()
+    valid = (ids >= 0) & (ids < E)
+    keep = np.where(valid, ids, 0)
+    # the reference's packing of the valid routes: expert-major, then token, then slot
+    order = sorted((int(keep[t, k]), t, k) for t in range(T) for k in range(K) if valid[t, k])
+    xs, ws = to_oracle(x), to_oracle(w)
+    n = len(order)
+    assert_equal(px[:n], np.stack([xs[t] for _, t, _ in order]), "packed_x")
+    assert_equal(pw[:n], np.array([ws[t, k] for _, t, k in order]), "packed_weights")
+    assert_equal(tok[:n], np.array([t for _, t, _ in order]), "token_ids")
+    counts = np.bincount([e for e, _, _ in order], minlength=E)
+    assert_equal(off, np.concatenate([[0], np.cumsum(counts)]), "expert_offsets")
+
+
 # ------------------------------------------------------------------ moe_matmul
 def oracle_matmul_experts(oracle, x, off, w, experts, transpose_rhs=True):
     """Oracle on selected experts only (each expert's rows are independent)."""
