@@ -879,16 +879,19 @@ const void* dispatch_tokens_ch(int64_t top_k, bool i64) {
 
 // ---------------------------------------------------------------- moe_scatter_sum
 // Workgroup = (batch, 4 tokens, 512-column chunk); wave = one token.  The
-// batch's token ids are staged in LDS once per workgroup; each wave collects
-// the rows of its token in row order with ballots, then processes them 8 at a
-// time: the 8 rows' loads are issued together and accumulated in row order
-// with the reference's two roundings (product, then sum rounded to the output
-// dtype) -- bit-identical to the CPU, no atomics.
+// workgroup reads the batch's token ids once (16 loads per thread in flight)
+// and each thread tests its own ids against the workgroup's 4 tokens: a hit
+// is appended to its token's list with an LDS atomic, and each wave then puts
+// its list (the token's k rows) back in row order by ranking.  No wave scans
+// the whole id list.  The rows are processed 8 at a time: the 8 rows' loads
+// are issued together and accumulated in row order with the reference's two
+// roundings (product, then sum rounded to the output dtype) -- bit-identical
+// to the CPU, no atomics on the output.  A token with more than kCombineHits
+// rows falls back to collecting them in row order with ballots.
 __device__ __forceinline__ float elem_to_f32(uint16_t b) { return bf16_to_f32(b); }
 __device__ __forceinline__ float elem_to_f32(float f) { return f; }
 
-constexpr int kCombineStage = 8192;  // rows staged in LDS (32 KiB)
-constexpr int kCombineHits = 128;    // per-wave hit list
+constexpr int kCombineHits = 128;  // per-wave hit list
 
 template <typename T>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict__ packed,
@@ -896,8 +899,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
                                                           const void* __restrict__ tok, int32_t tok_dt,
                                                           void* __restrict__ out, int64_t batch, int64_t rows,
                                                           int64_t hidden, int64_t seq, uint32_t* errw) {
-    __shared__ __attribute__((aligned(16))) int32_t ids[kCombineStage];
     __shared__ int32_t hit[4][kCombineHits];
+    __shared__ int32_t hits_n[4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t chunks = (hidden + 511) / 512;
     const int64_t tgroups = (seq + 3) / 4;
@@ -906,10 +909,13 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
     const int64_t b = blockIdx.x / (chunks * tgroups);
     const int64_t t = tg * 4 + wave;
     const int64_t mb = b * rows;
-    const bool staged = rows <= kCombineStage;
-    if (staged) {
-        // 16 loads per thread in flight at once, then the LDS stores
+    if (threadIdx.x < 4) hits_n[threadIdx.x] = 0;
+    __syncthreads();
+    {
+        // 16 loads per thread in flight at once, then the tests
         constexpr int kBatch = 16;
+        const int64_t tbase = tg * 4;
+        const bool flag = blockIdx.x % (chunks * tgroups) == 0;  // one workgroup per batch raises the flag
         for (int64_t r0 = threadIdx.x; r0 < rows; r0 += 256 * kBatch) {
             int64_t v[kBatch];
             // one dtype branch around the whole batch: a per-load select made
@@ -931,9 +937,13 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
             for (int u = 0; u < kBatch; u++) {
                 const int64_t r = r0 + 256 * u;
                 if (r >= rows) break;
-                if ((v[u] < 0 || v[u] >= seq) && blockIdx.x % (chunks * tgroups) == 0)
-                    atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_TOKEN_ID));
-                ids[r] = static_cast<int32_t>(v[u]);
+                const bool valid = v[u] >= 0 && v[u] < seq;
+                if (!valid && flag) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_TOKEN_ID));
+                const uint64_t d = static_cast<uint64_t>(v[u] - tbase);
+                if (valid && d < 4) {
+                    const int slot = atomicAdd(&hits_n[d], 1);
+                    if (slot < kCombineHits) hit[d][slot] = static_cast<int32_t>(r);
+                }
             }
         }
     }
@@ -999,47 +1009,24 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
         __builtin_amdgcn_wave_barrier();
     };
     int64_t r0 = 0;
-    if (staged && rows <= 64 * 256) {
-        // each lane scans its own run of `seg` consecutive rows (128-bit LDS
-        // reads) into a bit mask; a wave prefix sum of the hit counts places
-        // the hits in row order
-        const int64_t seg = ((rows + 255) / 256) * 4;  // multiple of 4, at most 256
-        const int64_t s0 = lane * seg;
-        int cnt = 0;
-        uint64_t mk[4] = {0, 0, 0, 0};
-        for (int64_t q = 0; q < seg; q += 4) {
-            const int64_t r = s0 + q;
-            if (r >= rows) break;
-            const int4 v = *reinterpret_cast<const int4*>(&ids[r]);  // rows past the end hold stale ids: masked
-            const int vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                if (r + i < rows && vv[i] == t) {
-                    mk[(q + i) >> 6] |= 1ull << ((q + i) & 63);
-                    cnt++;
-                }
+    const int n_hits = hits_n[wave];
+    if (n_hits <= kCombineHits) {
+        // the list holds the token's rows in arrival order: rank each (rows
+        // are distinct) and write it back at its rank
+        const int e0 = lane < n_hits ? hit[wave][lane] : 0;
+        const int e1 = lane + 64 < n_hits ? hit[wave][lane + 64] : 0;
+        int k0 = 0, k1 = 0;
+        for (int j = 0; j < n_hits; j++) {
+            const int ej = hit[wave][j];  // same address in every lane: one broadcast read
+            k0 += ej < e0;
+            k1 += ej < e1;
         }
-        int excl = cnt;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int up = __shfl_up(excl, d, 64);
-            if (lane >= d) excl += up;
-        }
-        const int n_all = __shfl(excl, 63, 64);
-        excl -= cnt;
-        if (n_all <= kCombineHits) {  // else: the chunked collection below
-#pragma unroll
-            for (int w4 = 0; w4 < 4; w4++) {
-                uint64_t m = mk[w4];
-                while (m) {
-                    hit[wave][excl++] = static_cast<int32_t>(s0 + 64 * w4 + __builtin_ctzll(m));
-                    m &= m - 1;
-                }
-            }
-            __builtin_amdgcn_wave_barrier();
-            accumulate(n_all);
-            r0 = rows;
-        }
+        __builtin_amdgcn_wave_barrier();
+        if (lane < n_hits) hit[wave][k0] = e0;
+        if (lane + 64 < n_hits) hit[wave][k1] = e1;
+        __builtin_amdgcn_wave_barrier();
+        accumulate(n_hits);
+        r0 = rows;
     }
     while (r0 < rows) {
         // collect up to kCombineHits rows of token t, in row order
@@ -1047,14 +1034,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
         for (; r0 < rows && n + 64 <= kCombineHits; r0 += 64) {
             const int64_t r = r0 + lane;
             int64_t tr = -1;
-            if (r < rows) {
-                if (staged) tr = ids[r];
-                else {
-                    tr = load_index(tok, tok_dt, mb + r);
-                    if ((tr < 0 || tr >= seq) && t == 0 && ch == 0)
-                        atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_TOKEN_ID));
-                }
-            }
+            if (r < rows) tr = load_index(tok, tok_dt, mb + r);  // invalid ids were flagged above
             const uint64_t hits = __ballot(tr == t);
             if (tr == t) hit[wave][n + __popcll(hits & ((1ull << lane) - 1ull))] = static_cast<int32_t>(r);
             n += __popcll(hits);

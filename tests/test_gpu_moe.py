@@ -286,10 +286,13 @@ def test_moe_matmul_bad_offsets_sets_device_error(ops):
 
 # ------------------------------------------------------------------ moe_scatter_sum
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("T,H,K", [(512, 2816, 8), (9, 24, 3), (4, 100, 2), (1100, 16, 8), (3, 16, 90)])
+@pytest.mark.parametrize("T,H,K", [(512, 2816, 8), (9, 24, 3), (4, 100, 2), (1100, 16, 8), (3, 16, 90), (2, 16, 150),
+                                   (1, 8, 300)])
 def test_moe_scatter_sum_bit_exact(ops, oracle, dtype, T, H, K):
-    """Rows staged in LDS (segment scan) and not (8800 rows), and tokens with
-    more rows than one collection pass holds (3 tokens x 90 rows)."""
+    """Token row lists built by LDS appends and put back in row order (up to
+    128 rows per token, 8800 rows in all at 1100 x 8), and tokens with more
+    rows than a list holds (about 150 and 300 rows), which are collected in
+    row order by ballots instead."""
     r = rng(T + H)
     tok = np.sort(r.integers(0, T, T * K)).astype(np.int64)
     r.shuffle(tok)
