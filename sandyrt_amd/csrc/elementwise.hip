@@ -20,10 +20,10 @@
 // (element index = linear % numel, CudaElementwiseKernels.cu:171-174), scalar
 // (numel 1) or strided (dims/strides passed at launch).  When the output and
 // every input allow it, threads walk the tensor in 8-element chunks with
-// 128-bit loads and stores, two chunks in flight per thread over a grid of at
-// most 4096 workgroups; contiguous inputs are read non-temporally (streamed
-// once; broadcast inputs are re-read and stay cached).  Otherwise one element
-// per thread.
+// 128-bit loads and stores, two chunks in flight per thread (one below 2^20
+// elements) over a grid of at most 4096 workgroups; contiguous inputs are
+// read non-temporally (streamed once; broadcast inputs are re-read and stay
+// cached).  Otherwise one element per thread.
 #include "common.h"
 
 #include <hip/hiprtc.h>
@@ -175,14 +175,18 @@ std::string node_expr(const SandyScalarNode& n) {
     return "0.0f";
 }
 
-// chunks of 8 elements per thread per grid stride of the vectorised kernel
-int vec_chunks() {
-    const int u = static_cast<int>(env_int("SANDY_EW_CHUNKS", 2));
-    return u == 1 || u == 4 || u == 8 ? u : 2;
+// chunks of 8 elements per thread per grid stride of the vectorised kernel:
+// one below 2^20 elements, where twice the workgroups beat two chunks in
+// flight per thread (GeGLU [64, 10240]: 3.55 -> 3.04 us), two above
+// (SwiGLU [4096, 704]: 4.8 vs 5.4 us with one; four is slower everywhere)
+int vec_chunks(int64_t n) {
+    const int u = static_cast<int>(env_int("SANDY_EW_CHUNKS", 0));
+    if (u == 1 || u == 2 || u == 4 || u == 8) return u;
+    return n < (int64_t{1} << 20) ? 1 : 2;
 }
 
 std::string generate(const SandyScalarNode* nodes, int count, uint32_t result, const int32_t* in_dt,
-                     const int* modes, int nin, int32_t out_dt, bool vec) {
+                     const int* modes, int nin, int32_t out_dt, bool vec, int U) {
     std::ostringstream s;
     s << kPrelude;
     s << "extern \"C\" __global__ __launch_bounds__(256) void sandy_ew(" << (vec ? "EwVecArgs" : "EwArgs")
@@ -190,7 +194,6 @@ std::string generate(const SandyScalarNode* nodes, int count, uint32_t result, c
     if (vec) {
         // chunk j of 8 elements; a thread takes chunks c, c + 256, ... of each
         // (256 U)-chunk stride of the grid, all U chunks' loads issued first
-        const int U = vec_chunks();
         const bool plain_st = env_int("SANDY_EW_PLAIN_STORE", 0) != 0;
         s << "  const i64 chunks = a.n >> 3;\n";
         s << "  for (i64 c0 = (i64)blockIdx.x * " << 256 * U << " + threadIdx.x; c0 < chunks; c0 += (i64)gridDim.x * "
@@ -294,8 +297,8 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 // exposed for the code-generation test entry below
 std::string elementwise_source(const SandyScalarNode* nodes, int count, uint32_t result, const int32_t* in_dt,
-                               const int* modes, int nin, int32_t out_dt, bool vec) {
-    return generate(nodes, count, result, in_dt, modes, nin, out_dt, vec);
+                               const int* modes, int nin, int32_t out_dt, bool vec, int chunks_per_thread) {
+    return generate(nodes, count, result, in_dt, modes, nin, out_dt, vec, chunks_per_thread);
 }
 
 } // namespace sandy_hip
@@ -375,7 +378,8 @@ extern "C" int sandy_hip_elementwise(const SandyScalarNode* nodes, int32_t node_
         args.ostrides[0] = 1;
     }
 
-    const std::string src = generate(nodes, node_count, result, dts, modes, input_count, out->dtype, vec);
+    const int U = vec_chunks(n);
+    const std::string src = generate(nodes, node_count, result, dts, modes, input_count, out->dtype, vec, U);
     int dev = 0;
     SANDY_HIP_TRY(hipGetDevice(&dev), e, "hipGetDevice");
     Compiled c;
@@ -391,9 +395,8 @@ extern "C" int sandy_hip_elementwise(const SandyScalarNode* nodes, int32_t node_
             c = it->second;
         }
     }
-    // vectorised: 512 chunks of 8 per workgroup per grid stride, at most 4096
-    // workgroups (16 per CU); scalar: one element per thread
-    const int U = vec_chunks();
+    // vectorised: 256 U chunks of 8 per workgroup per grid stride, at most
+    // 4096 workgroups (16 per CU); scalar: one element per thread
     const int64_t threads = vec ? (n / 8 + U - 1) / U : n;
     int64_t blocks64 = (threads + 255) / 256;
     if (vec) blocks64 = std::min<int64_t>(blocks64, env_int("SANDY_EW_MAX_BLOCKS", 4096));
