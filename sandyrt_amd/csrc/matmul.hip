@@ -482,7 +482,7 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
         int cps = env_int("SANDY_GEMM_CPS", 0);
         // K: at most 32 chunks (2048 k) per workgroup, split evenly; the
         // per-wave run is rounded up to a built run length
-        const int64_t ksplits = (chunks + 31) / 32;
+        int64_t ksplits = (chunks + 31) / 32;
         // chunks in flight per wave (4 only for RT * CT <= 2, register bound)
         int qdepth = 2;
         if (variant < 0 || variant > 8) {
@@ -495,7 +495,10 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
             //     the widest column tile giving >= 120 workgroups;
             //   4 chunks in flight per wave for weights under 8M elements
             //   (o projection at 32 rows 8.3 -> 6.1 us, q/k/v at one row
-            //   7.4 -> 5.5 us), 2 for the larger ones.
+            //   7.4 -> 5.5 us), 2 for the larger ones;
+            //   17..32 rows with K past 2048: up to 48 chunks per workgroup
+            //   and 4 in flight (down projection, 32 x 5632 x 2048: two K
+            //   splits of runs of 12, 12.8 -> 11.6 us, against three of 8).
             const bool big = p.N * p.K * 2 > (int64_t(64) << 20);
             int64_t rt = 1, ct = 1;
             if (p.M <= 16 && !big) {
@@ -504,6 +507,10 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
             } else if (p.M <= 32 && !big) {
                 ct = p.N * p.K >= 5 * (int64_t(1) << 20) ? 2 : 1;
                 qdepth = p.N * p.K < 8 * (int64_t(1) << 20) ? 4 : 2;
+                if (p.M > 16 && chunks > 32) {
+                    ksplits = (chunks + 47) / 48;
+                    qdepth = 4;
+                }
             } else {
                 rt = p.M <= 16 ? 1 : 2;
                 const int64_t rows = (p.M + 16 * rt - 1) / (16 * rt) * p.batches;
