@@ -496,18 +496,20 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
             //   4 chunks in flight per wave for weights under 8M elements
             //   (o projection at 32 rows 8.3 -> 6.1 us, q/k/v at one row
             //   7.4 -> 5.5 us), 2 for the larger ones;
-            //   17..32 rows with K past 2048: up to 48 chunks per workgroup
-            //   and 4 in flight (down projection, 32 x 5632 x 2048: two K
-            //   splits of runs of 12, 12.8 -> 11.6 us, against three of 8).
+            //   up to 32 rows with K past 2048: up to 48 chunks per
+            //   workgroup and 4 in flight (down projection, 5632 x 2048: two
+            //   K splits of runs of 12 against three of 8; 32 rows
+            //   12.8 -> 11.6 us, one row 9.2 -> 8.7 us).
             const bool big = p.N * p.K * 2 > (int64_t(64) << 20);
             int64_t rt = 1, ct = 1;
             if (p.M <= 16 && !big) {
                 ct = p.N >= 16384 ? 2 : 1;
                 qdepth = 4;
+                if (chunks > 32) ksplits = (chunks + 47) / 48;
             } else if (p.M <= 32 && !big) {
                 ct = p.N * p.K >= 5 * (int64_t(1) << 20) ? 2 : 1;
                 qdepth = p.N * p.K < 8 * (int64_t(1) << 20) ? 4 : 2;
-                if (p.M > 16 && chunks > 32) {
+                if (chunks > 32) {
                     ksplits = (chunks + 47) / 48;
                     qdepth = 4;
                 }
