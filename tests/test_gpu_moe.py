@@ -287,12 +287,13 @@ def test_moe_matmul_bad_offsets_sets_device_error(ops):
 # ------------------------------------------------------------------ moe_scatter_sum
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("T,H,K", [(512, 2816, 8), (9, 24, 3), (4, 100, 2), (1100, 16, 8), (3, 16, 90), (2, 16, 150),
-                                   (1, 8, 300)])
+                                   (1, 8, 300), (5, 1024, 3), (6, 1040, 4)])
 def test_moe_scatter_sum_bit_exact(ops, oracle, dtype, T, H, K):
     """Token row lists built by LDS appends and put back in row order (up to
     128 rows per token, 8800 rows in all at 1100 x 8), and tokens with more
     rows than a list holds (about 150 and 300 rows), which are collected in
-    row order by ballots instead."""
+    row order by ballots instead; rows of exactly two 512-column groups and
+    of two groups plus a ragged 16-column one."""
     r = rng(T + H)
     tok = np.sort(r.integers(0, T, T * K)).astype(np.int64)
     r.shuffle(tok)
