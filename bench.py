@@ -467,7 +467,8 @@ def gpt2_config1():
         match = tokens == _json.load(open(golden))["tokens"]
     if not os.path.exists(O.LIB_PATH):
         O.build()
-    cpu = GPT2Oracle(O.Oracle(), cfg, w)
+    kind = "reference" if os.path.exists(O.REF_PATH) else "port"
+    cpu = GPT2Oracle(O.Oracle(reference=(kind == "reference")), cfg, w)
     cpu.forward(prompt[:8])
     t0 = time.perf_counter()
     for t in (11, 12):
@@ -475,7 +476,24 @@ def gpt2_config1():
     cpu_tok_s = 2 / (time.perf_counter() - t0)
     return {"prompt_ms": round(t_prompt * 1e3, 2), "decode_tok_s": round(31 / t_decode, 1),
             "tokens_match_cpu": match, "cpu_decode_tok_s": round(cpu_tok_s, 2), "cpu_cores": 1,
-            "cpu_kind": "port", "cpu_sample": "oracle op chain, 2 single-token steps after an 8-token prompt"}
+            "cpu_kind": kind, **host_cpu_info(),
+            "cpu_sample": ("the GPT-2 op chain on the reference's src/core build" if kind == "reference" else
+                           "the GPT-2 op chain on the oracle restatement") +
+                          ", 2 single-token steps after an 8-token prompt, one thread"}
+
+
+def host_cpu_info():
+    """The host the CPU figures were timed on: CPU model (/proc/cpuinfo, as
+    lscpu reports it), logical CPUs of the machine and of this process."""
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"host_cpu": model, "nproc": os.cpu_count(), "nproc_usable": len(os.sched_getaffinity(0))}
 
 
 def time_kernels(kernels, iters, stream, torch):
@@ -561,6 +579,7 @@ def cpu_baseline(host, bytes_per, n_tokens, n_seqs):
         "unit": "GB/s",
         "cores": 1,
         "kind": kind,
+        **host_cpu_info(),
         "sample": (f"config-2 groups on {n_tokens} of {T} tokens and decode attention for {n_seqs} of {DEC_B} "
                    f"sequences (paged->dense K/V materialisation of CpuDevice.cpp:611-676 included, as the reference "
                    f"CPU device runs it before each attention), "

@@ -110,6 +110,29 @@ typedef struct SandyPagedView {
     int64_t page_count;       /* pages in the table (>= ceil(T / page_size)) */
 } SandyPagedView;
 
+/*
+ * The reference's paged tensor in its general form, as an input of any
+ * kernel family (CudaDeviceBufferView with paged = true, src/device/cuda/
+ * CudaKernels.h:19-28, built by CudaDevice::run, CudaDevice.cpp:468-493):
+ * `pages` is the device array of page_count page start addresses, `dims` the
+ * logical shape, and page p holds rows [p * page_size, (p + 1) * page_size)
+ * of dimension grow_dim for every leading element: [prefix, page_size, inner]
+ * with prefix the product of the dims before grow_dim and inner the product
+ * of those after it (addressing: CudaKernelUtils.cuh:82-108).  Elements on a
+ * page the table lacks (ordinal >= page_count, or a null address) read as 0.
+ */
+typedef struct SandyPagedTensor {
+    const void* pages;        /* device array of uint64 page addresses */
+    int32_t dtype;            /* F32, BF16, I32 or I64 */
+    int32_t rank;             /* 1..8 */
+    int64_t dims[SANDY_HIP_MAX_RANK];
+    int64_t grow_dim;         /* 0..rank-1 */
+    int64_t page_size;        /* power of two */
+    int64_t page_count;
+} SandyPagedTensor;
+
+#define SANDY_HIP_PAGED_STAGE_SLOTS 8
+
 /* One node of a fused element-wise scalar DAG (ScalarNode, src/ir/KernelIR.h:346-355). */
 typedef struct SandyScalarNode {
     uint32_t id;
@@ -133,6 +156,29 @@ const char* sandy_hip_version(void);
  * CudaRoPEKernels.cu:310-333, CudaGatherKernels.cu:291-294 and
  * CudaMoeScatterSumKernels.cu:218-239. */
 int sandy_hip_take_device_errors(void* stream, uint32_t* flags, char* err, size_t err_cap);
+
+/* ---------------------------------------------------------------- paged operands */
+
+/*
+ * Paged inputs of the families that read them (element-wise, norm, RoPE,
+ * softmax, reduction, embedding gather, attention q and positions): the
+ * reference reads such an input in place through load_float / load_int
+ * (CudaKernelUtils.cuh:82-157); this backend gathers it into a dense
+ * row-major copy, then the family's dense entry point reads the copy.  The
+ * copy is exact, so the results are the same.
+ *
+ * sandy_hip_paged_to_dense: into dst, a contiguous tensor of src's shape and
+ * dtype.  sandy_hip_paged_stage: into the library's per-device staging
+ * buffer `slot` (0..SANDY_HIP_PAGED_STAGE_SLOTS-1, grow-only, allocated on
+ * first use), described in *dense; it stays valid until the next stage call
+ * of the same slot on that device, so one launch stages each of its paged
+ * inputs in its own slot.  Calls that share a slot on one device and overlap
+ * on different streams race.
+ */
+int sandy_hip_paged_to_dense(const SandyPagedTensor* src, const SandyTensor* dst, void* stream, char* err,
+                             size_t err_cap);
+int sandy_hip_paged_stage(const SandyPagedTensor* src, int32_t slot, SandyTensor* dense, void* stream, char* err,
+                          size_t err_cap);
 
 /* ---------------------------------------------------------------- fused groups */
 
@@ -263,6 +309,9 @@ int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedCache* k_cac
  * in sandy_hip_attention; k and v are reference-layout paged views.  Decode
  * (Tq = 1, bf16, D 64/128/256) runs the MFMA paged decode kernel reading the
  * page table directly; other shapes run the general attention kernel.
+ * The decode kernel reads pages with 16-byte loads: a page address that is
+ * null or not 16-byte aligned is recorded as SANDY_DEVERR_BLOCK and the page
+ * contributes no keys.
  */
 int sandy_hip_attention_paged_view(const SandyTensor* q, const SandyPagedView* k, const SandyPagedView* v,
                                    const SandyTensor* position_offsets, int64_t window, double scale,

@@ -62,6 +62,18 @@ class SandyPagedCache(C.Structure):
     ]
 
 
+class SandyPagedTensor(C.Structure):
+    _fields_ = [
+        ("pages", C.c_void_p),
+        ("dtype", C.c_int32),
+        ("rank", C.c_int32),
+        ("dims", C.c_int64 * MAX_RANK),
+        ("grow_dim", C.c_int64),
+        ("page_size", C.c_int64),
+        ("page_count", C.c_int64),
+    ]
+
+
 class SandyPagedView(C.Structure):
     _fields_ = [
         ("pages", C.c_void_p),
@@ -151,6 +163,8 @@ SIGNATURES = {
     "sandy_hip_rope": [T, T, C.c_double, C.c_int64, C.c_int32, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_rope_pair": [T, T, T, C.c_double, C.c_int64, C.c_int32, T, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_softmax": [T, C.c_int64, T, C.c_void_p, ERR, C.c_size_t],
+    "sandy_hip_paged_to_dense": [C.POINTER(SandyPagedTensor), T, C.c_void_p, ERR, C.c_size_t],
+    "sandy_hip_paged_stage": [C.POINTER(SandyPagedTensor), C.c_int32, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_reduce_sum": [T, C.c_int64, C.c_int32, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_gather": [T, T, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_attention": [T, T, T, T, C.c_int64, C.c_double, T, C.c_void_p, ERR, C.c_size_t],

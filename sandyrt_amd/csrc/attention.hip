@@ -259,7 +259,9 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
             if (a.k_pages) {
                 kpv = a.k_pages[in ? page : 0];  // max_blocks >= 1
                 vpv = a.v_pages[in ? page : 0];
-                ok = kpv != 0 && vpv != 0;
+                // 16-byte buffer loads: a page that is null or not 16-byte aligned
+                // is reported like a block id outside the pool
+                ok = kpv != 0 && vpv != 0 && ((kpv | vpv) & 15u) == 0;
             } else {
                 int32_t id;
                 if constexpr (PRE) id = pre->id;

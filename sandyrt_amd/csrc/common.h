@@ -104,6 +104,11 @@ inline bool valid_rank(const SandyTensor* t) { return t && t->rank >= 0 && t->ra
 // creation).  Kernels atomicOr SandyDeviceError bits into it.
 uint32_t* device_error_word(Err e, int* status);
 
+// Workspace slots kPagedStageSlot0 .. + SANDY_HIP_PAGED_STAGE_SLOTS - 1 hold
+// staged paged operands (paged_operand.hip); slots below it belong to the
+// kernels' own scratch.
+constexpr int kPagedStageSlot0 = 8;
+
 // Per-device, per-purpose grow-only scratch.  The returned memory stays valid
 // until the next call with the same slot and a larger size; callers that
 // need zeroed memory keep it zero themselves.

@@ -54,6 +54,11 @@ struct QkvRope {
     int32_t k_max_blocks, v_max_blocks, page_shift, hq, hkv, d, split_half, pos_dt;
     const void* pos;
     uint32_t* errw;
+    // [row tiles] arrivals (zero between launches): the workgroup that counts
+    // itself in last advances the row tile's lengths, after every workgroup
+    // has read them (a tile that read an advanced length would take a valid
+    // append for a stale position)
+    uint32_t* arrivals;
     float denom[kQkvMaxPairs];  // theta^(2i / d), host float powf
     int32_t k_slots[kQkvMaxRows];
     int32_t v_slots[kQkvMaxRows];
@@ -378,6 +383,41 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
             if (u == 0) rope_ids();
     }
 
+    // q/k/v: this workgroup has read its rows' lengths (the values are used
+    // here, so the loads have returned) -- count it in; the workgroup that
+    // arrives last writes the advanced lengths at its end
+    uint32_t arrive = 0;
+    if constexpr (ROPE) {
+        if (tid == 0) {
+            int32_t dep = 0;
+#pragma unroll
+            for (int t = 0; t < RT; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) dep += qkl[t][i] + qvl[t][i];
+            asm volatile("" ::"v"(dep));
+            arrive = __hip_atomic_fetch_add(g.qr.arrivals + blockIdx.y, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    // the lengths of this row tile's rows advance to pos + 1 where the row was
+    // appended (position at the length, pages present), by the last arrival
+    auto rope_lengths = [&]() {
+        if (__builtin_amdgcn_readfirstlane(arrive) != gridDim.x - 1) return;
+        if (tid == 0) __hip_atomic_store(g.qr.arrivals + blockIdx.y, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((lane & 15) != 0) return;
+        const int32_t kmax = g.qr.k_max_blocks, vmax = g.qr.v_max_blocks;
+#pragma unroll
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int rr = static_cast<int>(r0) + 16 * t + 4 * (lane >> 4) + i;
+                const int32_t pos = qpos[t][i];
+                if (rr >= M || pos < 0 || qkl[t][i] != pos || qvl[t][i] != pos) continue;
+                const int32_t bi = pos >> g.qr.page_shift;
+                if (bi >= kmax || bi >= vmax || qkb[t][i] < 0 || qvb[t][i] < 0) continue;
+                g.qr.k_len[qks[t][i]] = pos + 1;
+                g.qr.v_len[qvs[t][i]] = pos + 1;
+            }
+    };
     // sum the four waves' partials in wave order (LDS reused after a barrier)
     __syncthreads();
     if (wave > 0) {
@@ -430,8 +470,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
             uint16_t* const q_out = g.qr.q_out;
             char* const k_pages = g.qr.k_pages;
             char* const v_pages = g.qr.v_pages;
-            int32_t* const k_len = g.qr.k_len;
-            int32_t* const v_len = g.qr.v_len;
             uint32_t* const errw = g.qr.errw;
             const int ncl = static_cast<int>(min<int64_t>(nc, N - 1));
             const int qk_cols = (hq + hkv) * d;
@@ -459,6 +497,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
                 const int32_t bi = pos >> shift;
                 const int32_t kb = bi < kmax ? qkb[t][i] : -1;
                 const int32_t vb = bi < vmax ? qvb[t][i] : -1;
+                // k and v are stored only where the row appends: at the sequence's
+                // device length (a stale position would overwrite committed history)
+                const bool at_len = qkl[t][i] == pos && qvl[t][i] == pos;
                 const int row_in_page = pos & (psz - 1);
                 if (ncl < qk_cols) {
                     const float x0 = second ? xp : x, x1 = second ? x : xp;
@@ -467,26 +508,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
                                          : f32_to_bf16(__fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn)));
                     if (head < hq)
                         rp[t][c][i] = q_out + (rr * hq + head) * d + dst;
-                    else if (kb >= 0)
+                    else if (kb >= 0 && at_len)
                         rp[t][c][i] = reinterpret_cast<uint16_t*>(k_pages + kb * page_bytes) +
                                       ((head - hq) * psz + row_in_page) * d + dst;
                 } else {
                     rv[t][c][i] = f32_to_bf16(x);
-                    if (vb >= 0)
+                    if (vb >= 0 && at_len)
                         rp[t][c][i] = reinterpret_cast<uint16_t*>(v_pages + vb * page_bytes) +
                                       ((head - hq - hkv) * psz + row_in_page) * d + cp;
                 }
-                // column tile 0, first column: the row's lengths advance to pos + 1
-                // (they must equal pos: the row is appended there)
+                // column tile 0, first column: the row's errors (the lengths
+                // advance in rope_lengths)
                 if (ct == 0 && c == 0 && (lane & 15) == 0) {
-                    const bool fits = kb >= 0 && vb >= 0;
-                    if (!fits) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
-                    if (qkl[t][i] != pos || qvl[t][i] != pos)
-                        atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_POSITION));
-                    else if (fits) {
-                        k_len[qks[t][i]] = pos + 1;
-                        v_len[qvs[t][i]] = pos + 1;
-                    }
+                    if (kb < 0 || vb < 0) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
+                    if (!at_len) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_POSITION));
                 }
             }
             return;
@@ -539,7 +574,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
                 for (int c = 0; c < CT; c++) emit(t, c, acc[t][c]);
         if constexpr (ROPE)
-            if (wave == 0) rope_stores();
+            if (wave == 0) {
+                rope_stores();
+                rope_lengths();
+            }
         return;
     }
     // split-K across workgroups: partials written through to the agent's coherence
@@ -571,6 +609,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         if (is_last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
+    if constexpr (ROPE)
+        if (wave == 0 && !is_last) rope_lengths();
     if (!is_last || wave != 0) return;
 #pragma unroll
     for (int t = 0; t < RT; t++)
@@ -598,7 +638,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
             }
             emit(t, c, sum);
         }
-    if constexpr (ROPE) rope_stores();
+    if constexpr (ROPE) {
+        rope_stores();
+        rope_lengths();
+    }
 }
 
 
@@ -614,8 +657,10 @@ void launch_waves_qkv(int variant, int cps, int qdepth, bool norm, dim3 grid, hi
 // The q/k/v decode GEMM with the RoPE + paged-append epilogue (QkvRope
 // filled in by the caller except its pointers' validation): lhs [m, k] bf16,
 // rhs [n, k] bf16 with n = (hq + 2 hkv) d; with lhs_stats and norm_weight the
-// RMSNorm prologue of sandy_hip_matmul_rms.  Defined in matmul.hip.
+// RMSNorm prologue of sandy_hip_matmul_rms.  dry: run every check and take
+// the workspace, launch nothing (so a caller can validate before it moves
+// bookkeeping).  Defined in matmul.hip.
 int matmul_qkv(const SandyTensor* lhs, const SandyRowStats* lhs_stats, const SandyTensor* norm_weight, double eps,
-               const SandyTensor* rhs, const QkvRope& qr, hipStream_t stream, Err e);
+               const SandyTensor* rhs, const QkvRope& qr, hipStream_t stream, Err e, bool dry = false);
 
 } // namespace sandy_hip

@@ -731,15 +731,21 @@ int qkv_step(SandyHipDevice* d, uint32_t k_pool, const uint32_t* k_tensors, uint
             for (int j = 0; j < i; j++)
                 if (ids[j] == ids[i]) return fail(e, SANDY_ERR_INVALID, "decode qkv tensors must be distinct");
         }
-    for (int i = 0; i < count; i++) {
+    // pages first, for every tensor, so a failed reservation leaves no length
+    // advanced; then the host bookkeeping advances in step with the device, as
+    // for the step append
+    for (int i = 0; i < count; i++)
         for (int which = 0; which < 2; which++) {
             PagedTensor& t = d->impl.tensors.find(which ? v_tensors[i] : k_tensors[i])->second;
             PagedPool& p = which ? vp : kp;
-            // host bookkeeping advances in step with the device, as for the step append
             if (t.grow_length + 1 > static_cast<int64_t>(t.pages.size()) * p.desc.page_size && !d->impl.capturing) {
                 const int st = reserve(d->impl, t, (t.grow_length + p.desc.page_size) / p.desc.page_size, e);
                 if (st) return st;
             }
+        }
+    for (int i = 0; i < count; i++) {
+        for (int which = 0; which < 2; which++) {
+            PagedTensor& t = d->impl.tensors.find(which ? v_tensors[i] : k_tensors[i])->second;
             t.grow_length += 1;
             (which ? q.v_slots : q.k_slots)[i] = t.slot;
         }
@@ -839,6 +845,14 @@ int sandy_hip_device_matmul_qkv(SandyHipDevice* d, const SandyTensor* lhs, const
         if (lhs->dtype != SANDY_BF16 || rhs->dtype != SANDY_BF16 || lhs->dims[1] % 32 != 0 || !contiguous(*lhs) ||
             !contiguous(*rhs) || ((reinterpret_cast<uintptr_t>(base_ptr(*lhs)) | reinterpret_cast<uintptr_t>(base_ptr(*rhs))) & 15u))
             return fail(e, SANDY_ERR_UNSUPPORTED, "qkv matmul needs contiguous 16-byte aligned bf16 operands, k a multiple of 32");
+        // the GEMM's own checks (norm weight, row statistics, plan, workspace)
+        // run dry before qkv_step moves any length
+        QkvRope probe{};
+        probe.hq = q_heads;
+        probe.hkv = static_cast<int32_t>(kit->second->prefix);
+        probe.d = static_cast<int32_t>(kit->second->inner);
+        st = matmul_qkv(lhs, lhs_stats, norm_weight, eps, rhs, probe, d->impl.stream, e, true);
+        if (st) return st;
     }
     for (uint32_t id : {k_pool, v_pool}) {
         auto it = d->impl.pools.find(id);

@@ -419,6 +419,7 @@ struct Fusion {
     const uint16_t* norm_w = nullptr;
     float eps = 0.0f;
     const QkvRope* qr = nullptr;  // q/k/v RoPE + paged-append epilogue
+    bool dry = false;             // every check and workspace, no launch
 };
 
 int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const SandyTensor* bias, const SandyTensor& o,
@@ -473,10 +474,13 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
             g.eps = fz->eps;
             if (fz->qr) g.qr = *fz->qr;
         }
-        // tile: 16 * RT rows x 16 * CT columns (variants: RT 1 / 2 / 4 with
-        // CT 1, then (RT, CT) = (2, 2), (1, 2), (2, 4), (1, 4), (4, 2), (4, 4))
-        static const int kRT[] = {1, 2, 4, 2, 1, 2, 1, 4, 4};
-        static const int kCT[] = {1, 1, 1, 2, 2, 4, 4, 2, 4};
+        // tile: 16 * RT rows x 16 * CT columns, variants (RT, CT) = 0 (1, 1),
+        // 1 (2, 1), 3 (2, 2), 4 (1, 2), 5 (2, 4), 6 (1, 4) -- the ones the
+        // heuristic below picks (2 is unused); SANDY_GEMM_TILE / SANDY_GEMM_CPS
+        // select one of them and a run length for the tests that cover every
+        // instantiated form
+        static const int kRT[] = {1, 2, 2, 2, 1, 2, 1};
+        static const int kCT[] = {1, 1, 1, 2, 2, 4, 4};
         const int64_t chunks = (p.K / 32 + 1) / 2;
         int variant = env_int("SANDY_GEMM_TILE", -1);
         int cps = env_int("SANDY_GEMM_CPS", 0);
@@ -485,7 +489,7 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
         int64_t ksplits = (chunks + 31) / 32;
         // chunks in flight per wave (4 only for RT * CT <= 2, register bound)
         int qdepth = 2;
-        if (variant < 0 || variant > 8) {
+        if (variant < 0 || variant > 6 || variant == 2) {
             // Measured on decode shapes with the weights streamed from HBM
             // (rotated over >= 1 GiB of copies):
             //   <= 16 rows: 16 x 16 tiles, 16 x 32 from N >= 16384 (lm-head);
@@ -527,8 +531,6 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
             variant = kPick[rt == 1 ? 0 : 1][ct == 1 ? 0 : ct == 2 ? 1 : 2];
         }
         qdepth = env_int("SANDY_GEMM_Q", qdepth);
-        // the RMSNorm-prologue kernels are built for 16- and 32-row tiles only
-        if (norm && kRT[variant] == 4) variant = kCT[variant] == 1 ? 1 : kCT[variant] == 2 ? 3 : 5;
         // the q/k/v epilogue kernels: 16-row tiles of 16 or 32 columns
         const bool qkv = fz && fz->qr;
         if (qkv) variant = kCT[variant] == 1 ? 0 : 4;
@@ -539,8 +541,9 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
             return fail(e, SANDY_ERR_UNSUPPORTED, "%s shape exceeds the launch grid", what);
         const int64_t tiles = row_tiles * col_tiles * p.batches;
         if (cps <= 0) cps = static_cast<int>(((chunks + ksplits - 1) / ksplits + 3) / 4);
-        static const int kRuns[] = {2, 3, 4, 5, 6, 8, 10, 12, 16};
-        int run = 16;
+        // built run lengths: per-split chunks are at most 48 (cps <= 12)
+        static const int kRuns[] = {2, 3, 4, 5, 6, 8, 10, 12};
+        int run = 12;
         for (int r : kRuns) {
             if (r >= cps) {
                 run = r;
@@ -575,9 +578,14 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
     switch (cps) {                                                                                         \
         WAVES_RUN(RT_, CT_, OCC_, 2) WAVES_RUN(RT_, CT_, OCC_, 3) WAVES_RUN(RT_, CT_, OCC_, 4)            \
         WAVES_RUN(RT_, CT_, OCC_, 5) WAVES_RUN(RT_, CT_, OCC_, 6) WAVES_RUN(RT_, CT_, OCC_, 8)            \
-        WAVES_RUN(RT_, CT_, OCC_, 10) WAVES_RUN(RT_, CT_, OCC_, 12) WAVES_RUN(RT_, CT_, OCC_, 16)         \
+        WAVES_RUN(RT_, CT_, OCC_, 10) WAVES_RUN(RT_, CT_, OCC_, 12)                                       \
     }
         if (qkv) {
+            int status = 0;
+            g.qr.arrivals = static_cast<uint32_t*>(
+                device_counters(3, static_cast<size_t>(row_tiles) * sizeof(uint32_t), stream, e, &status));
+            if (status) return status;
+            if (fz->dry) return ok(e);
             launch_waves_qkv(variant, cps, qdepth, norm, grid, stream, g);
             SANDY_HIP_TRY(hipGetLastError(), e, what);
             return ok(e);
@@ -590,13 +598,10 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
         switch (variant) {
             case 0: WAVES_CPS(1, 1, 4); break;
             case 1: WAVES_CPS(2, 1, 4); break;
-            case 2: WAVES_CPS(4, 1, 2); break;
             case 3: WAVES_CPS(2, 2, 2); break;
             case 4: WAVES_CPS(1, 2, 4); break;
             case 5: WAVES_CPS(2, 4, 2); break;
-            case 6: WAVES_CPS(1, 4, 2); break;
-            case 7: WAVES_CPS(4, 2, 2); break;
-            default: WAVES_CPS(4, 4, 2); break;
+            default: WAVES_CPS(1, 4, 2); break;
         }
 #undef WAVES_RUN
 #undef WAVES_CPS
@@ -757,7 +762,7 @@ extern "C" int sandy_hip_matmul_rms(const SandyTensor* lhs, const SandyRowStats*
 
 namespace sandy_hip {
 int matmul_qkv(const SandyTensor* lhs, const SandyRowStats* lhs_stats, const SandyTensor* norm_weight, double eps,
-               const SandyTensor* rhs, const QkvRope& qr, hipStream_t stream, Err e) {
+               const SandyTensor* rhs, const QkvRope& qr, hipStream_t stream, Err e, bool dry) {
     const char* what = "qkv matmul";
     if (!valid_rank(lhs) || !valid_rank(rhs)) return fail(e, SANDY_ERR_INVALID, "%s requires lhs and rhs", what);
     if (lhs->dtype != SANDY_BF16 || rhs->dtype != SANDY_BF16) return fail(e, SANDY_ERR_UNSUPPORTED, "%s takes bf16 operands", what);
@@ -793,6 +798,7 @@ int matmul_qkv(const SandyTensor* lhs, const SandyRowStats* lhs_stats, const San
         fz.eps = static_cast<float>(eps);
     }
     fz.qr = &qr;
+    fz.dry = dry;
     return launch(p, *lhs, *rhs, nullptr, full, false, true, stream, e, what, 0, &fz);
 }
 } // namespace sandy_hip

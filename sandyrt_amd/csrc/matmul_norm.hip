@@ -18,7 +18,7 @@ void launch_waves_norm(int variant, int cps, int qdepth, dim3 grid, hipStream_t 
     switch (cps) {                                                                                        \
         NORM_RUN(RT_, CT_, OCC_, 2) NORM_RUN(RT_, CT_, OCC_, 3) NORM_RUN(RT_, CT_, OCC_, 4)              \
         NORM_RUN(RT_, CT_, OCC_, 5) NORM_RUN(RT_, CT_, OCC_, 6) NORM_RUN(RT_, CT_, OCC_, 8)              \
-        NORM_RUN(RT_, CT_, OCC_, 10) NORM_RUN(RT_, CT_, OCC_, 12) NORM_RUN(RT_, CT_, OCC_, 16)           \
+        NORM_RUN(RT_, CT_, OCC_, 10) NORM_RUN(RT_, CT_, OCC_, 12)                                        \
     }
     // variants as in matmul.hip: (RT, CT) = 0 (1, 1), 1 (2, 1), 3 (2, 2), 4 (1, 2), 5 (2, 4), 6 (1, 4)
     switch (variant) {

@@ -21,7 +21,7 @@ void launch_waves_qkv(int variant, int cps, int qdepth, bool norm, dim3 grid, hi
 #define QKV_CPS(CT_, N_)                                                                                          \
     switch (cps) {                                                                                                \
         QKV_RUN(CT_, 2, N_) QKV_RUN(CT_, 3, N_) QKV_RUN(CT_, 4, N_) QKV_RUN(CT_, 5, N_) QKV_RUN(CT_, 6, N_)      \
-        QKV_RUN(CT_, 8, N_) QKV_RUN(CT_, 10, N_) QKV_RUN(CT_, 12, N_) default: QKV_RUN(CT_, 16, N_)              \
+        QKV_RUN(CT_, 8, N_) QKV_RUN(CT_, 10, N_) default: QKV_RUN(CT_, 12, N_)                                  \
     }
     if (norm) {
         if (variant == 0) QKV_CPS(1, true)

@@ -13,7 +13,7 @@ namespace sandy_hip {
 namespace {
 
 constexpr int kMaxDevices = 64;
-constexpr int kSlots = 8;
+constexpr int kSlots = kPagedStageSlot0 + SANDY_HIP_PAGED_STAGE_SLOTS;
 
 struct DeviceState {
     uint32_t* error_word = nullptr;

@@ -30,6 +30,65 @@ def _require_gpu(*ts):
             raise SandyError(1, "sandyrt_amd tensors must live on the GPU")
 
 
+class PagedTensor:
+    """The reference's paged tensor as a kernel input (CudaDeviceBufferView
+    with paged = true, src/device/cuda/CudaDevice.cpp:468-493): `pages` is a
+    device uint64 tensor of page start addresses, `dims` the logical shape,
+    and a page holds `page_size` rows of dimension `grow_dim` for every
+    leading element ([prefix, page_size, inner],
+    src/device/cuda/CudaKernelUtils.cuh:82-108).  The families that read
+    paged inputs in the reference (element-wise, norm, RoPE, softmax, sum,
+    embedding, attention q and positions) accept one wherever they take an
+    input tensor."""
+
+    def __init__(self, pages: torch.Tensor, dims, grow_dim: int, page_size: int, dtype: torch.dtype):
+        assert pages.is_cuda and pages.dtype in (torch.int64, torch.uint64) and pages.dim() == 1
+        self.pages, self.dims, self.grow_dim = pages, list(dims), grow_dim
+        self.page_size, self.dtype = page_size, dtype
+        self.is_cuda = True
+        self.device = pages.device
+        self.shape = torch.Size(self.dims)
+
+    def struct(self):
+        s = _lib.SandyPagedTensor()
+        s.pages = self.pages.data_ptr() if self.pages.numel() else None
+        s.dtype = _lib._TORCH_TO_CODE[self.dtype]
+        s.rank = len(self.dims)
+        for i, d in enumerate(self.dims):
+            s.dims[i] = d
+        s.grow_dim = self.grow_dim
+        s.page_size = self.page_size
+        s.page_count = self.pages.numel()
+        return C.pointer(s)
+
+
+def paged_to_dense(x: PagedTensor, out=None):
+    """The logical elements of a paged tensor as a contiguous tensor (the
+    gather every family runs on a paged input before its dense kernel)."""
+    out = torch.empty(x.dims, dtype=x.dtype, device=x.device) if out is None else out
+    call("sandy_hip_paged_to_dense", x.struct(), desc(out))
+    return out
+
+
+def _reads_paged(fn):
+    """Inputs given as PagedTensor (also inside a list of inputs) are gathered
+    to dense copies before the family's dense entry point runs."""
+    import functools
+
+    def dense(v):
+        if isinstance(v, PagedTensor):
+            return paged_to_dense(v)
+        if isinstance(v, (list, tuple)) and any(isinstance(u, PagedTensor) for u in v):
+            return type(v)(dense(u) for u in v)
+        return v
+
+    @functools.wraps(fn)
+    def run(*args, **kw):
+        return fn(*[dense(a) for a in args], **{k: (v if k == "out" else dense(v)) for k, v in kw.items()})
+
+    return run
+
+
 def check_device_errors() -> None:
     """Synchronise and raise the first recorded device-side value error
     (bad expert/token/position ids), worded like the reference."""
@@ -37,6 +96,7 @@ def check_device_errors() -> None:
 
 
 # ------------------------------------------------------------------ norms
+@_reads_paged
 def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, epsilon: float, out=None):
     """NormKernelOp RMSNorm (src/core/TensorCalc.cpp:1953-2000)."""
     _require_gpu(x, weight)
@@ -45,6 +105,7 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, epsilon: float, out=N
     return out
 
 
+@_reads_paged
 def layer_norm(x, weight, bias, epsilon: float, out=None):
     """NormKernelOp LayerNorm (src/core/TensorCalc.cpp:2010-2077)."""
     _require_gpu(x, weight, bias)
@@ -63,6 +124,7 @@ def add_rms_norm(x, residual, weight, epsilon: float, sum_out=None, out=None):
 
 
 # ------------------------------------------------------------------ rope / softmax / reductions
+@_reads_paged
 def rope(x, theta: float, rotary_dim: int = -1, split_half: bool = False, position_ids=None, out=None):
     """RoPEKernelOp (src/core/TensorCalc.cpp:1823-1951)."""
     _require_gpu(x, position_ids)
@@ -105,6 +167,7 @@ def rope_pair_cached(q, k, cache, q_out=None, k_out=None):
     return q_out, k_out
 
 
+@_reads_paged
 def softmax(x, axis: int = -1, out=None):
     """SoftmaxKernelOp (src/core/TensorCalc.cpp:1337-1399)."""
     _require_gpu(x)
@@ -113,6 +176,7 @@ def softmax(x, axis: int = -1, out=None):
     return out
 
 
+@_reads_paged
 def sum(x, axis: int = -1, keep_dims: bool = True, out=None):  # noqa: A001 - reference op name
     """ReductionKernelOp Sum over one axis (src/core/TensorCalc.cpp:1401-1445)."""
     _require_gpu(x)
@@ -127,6 +191,7 @@ def sum(x, axis: int = -1, keep_dims: bool = True, out=None):  # noqa: A001 - re
     return out
 
 
+@_reads_paged
 def embedding(ids, weight, out=None):
     """GatherKernelOp / embedding (src/core/TensorCalc.cpp:1520-1563)."""
     _require_gpu(ids, weight)
@@ -162,6 +227,7 @@ def _nodes(nodes):
     return arr
 
 
+@_reads_paged
 def elementwise(nodes, result: int, inputs, broadcast=None, out_shape=None, out_dtype=None, out=None):
     """Run one fused ElementwiseKernelOp.  `nodes` in dependency order;
     broadcast[i] True marks a right-aligned broadcast input."""
@@ -223,6 +289,7 @@ def residual_add_nodes():
 
 
 # ------------------------------------------------------------------ attention
+@_reads_paged
 def attention(q, k, v, position_offsets=None, window: int = 0, scale: float = -1.0, out=None):
     """AttentionKernelOp over dense K/V (src/core/TensorCalc.cpp:1167-1314)."""
     _require_gpu(q, k, v, position_offsets)

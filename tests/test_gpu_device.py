@@ -371,6 +371,60 @@ def test_matmul_qkv_position_must_equal_length():
         dev.close()
 
 
+def test_matmul_qkv_stale_position_keeps_history():
+    """A position behind the sequence's length (a stale one) is reported as a
+    device position error and stores nothing: the committed K/V rows stay as
+    they were.  A call that fails a check of the GEMM itself (bad row
+    statistics) fails before any length moves."""
+    from sandyrt_amd import ops
+    from sandyrt_amd._lib import BF16, SandyError
+    from sandyrt_amd.device import HipDevice
+    dev = HipDevice(0)
+    try:
+        kp = dev.create_paged_pool([1, 2, -1, 64], BF16, 2, 16, max_tensors=1, max_blocks=4)
+        vp = dev.create_paged_pool([1, 2, -1, 64], BF16, 2, 16, max_tensors=1, max_blocks=4)
+        k, v = dev.alloc_paged(kp), dev.alloc_paged(vp)
+        g = torch.Generator().manual_seed(7)
+        w = torch.randn(12 * 64, 64, generator=g).to(torch.bfloat16).cuda()
+        q = torch.empty(1, 8, 1, 64, dtype=torch.bfloat16, device="cuda")
+        for p in range(2):
+            x = torch.randn(1, 64, generator=g).to(torch.bfloat16).cuda()
+            dev.matmul_qkv(x, w, kp, [k], vp, [v], 8, torch.tensor([p], device="cuda"), 1e4, q)
+        ops.check_device_errors()
+        dev.paged_sync(kp)
+        dev.paged_sync(vp)
+        k0, v0 = dev.read_paged(k, np.uint16).copy(), dev.read_paged(v, np.uint16).copy()
+        assert k0.shape[2] == 2 and np.any(k0 != 0) and np.any(v0 != 0)
+        x = torch.randn(1, 64, generator=g).to(torch.bfloat16).cuda()
+        for stale in (0, 1):  # two behind the length, and one (pos = len - 1)
+            dev.matmul_qkv(x, w, kp, [k], vp, [v], 8, torch.tensor([stale], device="cuda"), 1e4, q)
+            with pytest.raises(SandyError, match="position"):
+                ops.check_device_errors()
+            dev.paged_sync(kp)
+            dev.paged_sync(vp)
+            np.testing.assert_array_equal(dev.read_paged(k, np.uint16), k0)
+            np.testing.assert_array_equal(dev.read_paged(v, np.uint16), v0)
+        nxt = torch.empty(1, dtype=torch.int64, device="cuda")
+        dev.lengths(kp, [k], nxt)
+        dev.synchronize()
+        assert nxt.tolist() == [2]
+        # bad row statistics (3 parts for a 64-wide row, which has 4)
+        bad_stats = torch.zeros(1, 3, dtype=torch.float64, device="cuda")
+        nw = torch.ones(64, dtype=torch.bfloat16, device="cuda")
+        with pytest.raises(SandyError, match="row statistics"):
+            dev.matmul_qkv(x, w, kp, [k], vp, [v], 8, torch.tensor([2], device="cuda"), 1e4, q, stats=bad_stats,
+                           norm_weight=nw, eps=1e-5)
+        with pytest.raises(SandyError, match="norm weight"):
+            dev.matmul_qkv(x, w, kp, [k], vp, [v], 8, torch.tensor([2], device="cuda"), 1e4, q,
+                           stats=torch.zeros(1, 4, dtype=torch.float64, device="cuda"), norm_weight=nw[:32], eps=1e-5)
+        assert dev.paged_meta(k).grow_length == 2 and dev.paged_meta(v).grow_length == 2
+        dev.lengths(kp, [k], nxt)
+        dev.synchronize()
+        assert nxt.tolist() == [2]
+    finally:
+        dev.close()
+
+
 def test_decode_qkv_rejects_bad_shapes():
     from sandyrt_amd._lib import BF16, SandyError
     from sandyrt_amd.device import HipDevice

@@ -36,3 +36,43 @@ def test_version_string():
 def test_code_object_targets_gfx950():
     data = open(_lib.LIB_PATH, "rb").read()
     assert b"gfx950" in data
+
+
+def test_paged_operand_checks_on_the_host():
+    """sandy_hip_paged_to_dense / _stage reject descriptors the reference's
+    pack_tensor_arg rejects (CudaKernelUtils.cuh:290-374) before any device
+    work, so these run without a GPU."""
+    import pytest
+
+    def pt(**kw):
+        s = _lib.SandyPagedTensor()
+        s.pages, s.dtype, s.rank = 0x1000, _lib.F32, 3
+        for i, d in enumerate([2, 3, 4]):
+            s.dims[i] = d
+        s.grow_dim, s.page_size, s.page_count = 1, 2, 2
+        for k, v in kw.items():
+            setattr(s, k, v)
+        return ctypes.pointer(s)
+
+    dst = _lib.SandyTensor()
+    dst.rank, dst.dtype = 3, _lib.F32
+    for i, (d, st) in enumerate([(2, 12), (3, 4), (4, 1)]):
+        dst.dims[i], dst.strides[i] = d, st
+    dst.data = 0x2000
+    cases = [
+        (pt(page_size=3), "page_size must be a power of two"),
+        (pt(page_size=0), "page_size must be > 0"),
+        (pt(grow_dim=3), "grow_dim out of range"),
+        (pt(page_count=-1), "page_count must be >= 0"),
+        (pt(pages=None), "page table is null"),
+        (pt(dtype=_lib.U8), "unsupported dtype"),
+    ]
+    for p, msg in cases:
+        with pytest.raises(_lib.SandyError, match=msg):
+            _lib.call("sandy_hip_paged_to_dense", p, ctypes.byref(dst), stream=0)
+    bad = _lib.SandyTensor.from_buffer_copy(dst)
+    bad.dims[2] = 5
+    with pytest.raises(_lib.SandyError, match="destination must be a contiguous tensor"):
+        _lib.call("sandy_hip_paged_to_dense", pt(), ctypes.byref(bad), stream=0)
+    with pytest.raises(_lib.SandyError, match="slot out of range"):
+        _lib.call("sandy_hip_paged_stage", pt(), ctypes.c_int32(-1), ctypes.byref(dst), stream=0)
