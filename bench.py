@@ -53,6 +53,9 @@ def parse():
     p.add_argument("--cpu-tokens", type=int, default=4096, help="C2 rows timed on the CPU")
     p.add_argument("--cpu-seqs", type=int, default=8, help="decode sequences timed on the CPU")
     p.add_argument("--only", default="", help="comma list of kernels to run (profiling)")
+    p.add_argument("--kv-layout", choices=["split", "interleaved"], default="split",
+                   help="config-3 KV pool: separate K and V pools, or one pool with each block's K and V pages "
+                        "side by side")
     p.add_argument("--no-extras", action="store_true", help="skip the per-kernel table of the other configs")
     p.add_argument("--no-decode-step", action="store_true", help="skip the whole-model decode tok/s measurement")
     p.add_argument("--gpt2-only", action="store_true",
@@ -90,7 +93,7 @@ class Prepared:
             raise RuntimeError(self.buf.value.decode())
 
 
-def build_workload(replicas):
+def build_workload(replicas, kv_layout="split"):
     import numpy as np
     import torch
     from sandyrt_amd import _lib, ops
@@ -148,8 +151,15 @@ def build_workload(replicas):
                                                  C.c_uint32(result), arr, bc, C.c_int32(2), d["act"]))
         if rep < reps["paged_decode"]:
             g.manual_seed(2 + 1000 * rep)
-            kpool = torch.randn(DEC_POOL, HKV, DEC_PAGE, HD, generator=g, device=dev).to(bf)
-            vpool = torch.randn(DEC_POOL, HKV, DEC_PAGE, HD, generator=g, device=dev).to(bf)
+            if kv_layout == "interleaved":
+                kvpool = torch.randn(DEC_POOL, 2, HKV, DEC_PAGE, HD, generator=g, device=dev).to(bf)
+                kpool, vpool = kvpool[:, 0], kvpool[:, 1]
+                kcache, vcache = ops.PagedCache.interleaved(kvpool)
+                keep.append(kvpool)
+            else:
+                kpool = torch.randn(DEC_POOL, HKV, DEC_PAGE, HD, generator=g, device=dev).to(bf)
+                vpool = torch.randn(DEC_POOL, HKV, DEC_PAGE, HD, generator=g, device=dev).to(bf)
+                kcache, vcache = ops.PagedCache(kpool), ops.PagedCache(vpool)
             qd = torch.randn(DEC_B, HQ, 1, HD, generator=g, device=dev).to(bf)
             od = torch.empty_like(qd)
             perm = np.random.default_rng(2 + rep).permutation(DEC_POOL).astype(np.int32)
@@ -160,7 +170,7 @@ def build_workload(replicas):
                 off += nblk[b]
             table_t = torch.from_numpy(table).to(dev)
             pos_t = torch.from_numpy(ctx - 1).to(dev)
-            kc, vc = ops.PagedCache(kpool).struct(), ops.PagedCache(vpool).struct()
+            kc, vc = kcache.struct(), vcache.struct()
             keep += [kpool, vpool, qd, od, table_t, pos_t, kc, vc]
             d.update({n: desc(t) for n, t in dict(qd=qd, od=od, table=table_t, pos=pos_t).items()})
             kernels["paged_decode"].append(Prepared("sandy_hip_paged_attention", d["qd"], kc, vc, d["table"],
@@ -626,7 +636,7 @@ def main():
         print(json.dumps({"metric": "TinyLlama decode step, batch 32, config-3 contexts", "us_per_step": round(us, 1),
                           "tok_s": round(tps, 1), "gbs": round(by / (us * 1e-6) / 1e9, 1)}), flush=True)
         return
-    kernels, bytes_per, keep, host = build_workload(args.replicas)
+    kernels, bytes_per, keep, host = build_workload(args.replicas, args.kv_layout)
     if args.only:
         kernels = {k: v for k, v in kernels.items() if k in args.only.split(",")}
         bytes_per = {k: v for k, v in bytes_per.items() if k in kernels}

@@ -76,17 +76,21 @@ typedef struct SandyTensor {
  * inner] (the reference's page layout, src/device/cuda/CudaPagedTensor.cpp:
  * 187-226, addressing src/device/cuda/CudaKernelUtils.cuh:82-108).  Pages live
  * in one pool allocation and are named by int32 block ids (pool + id *
- * prefix * page_size * inner elements) instead of the reference's per-page
- * void* table.
+ * page_stride elements) instead of the reference's per-page void* table.
+ * page_stride 0 means dense pages (prefix * page_size * inner); a larger
+ * stride lets K and V share one allocation with block b's K page and V page
+ * side by side ([pages, 2, prefix, page_size, inner]: K at pool, V at pool +
+ * prefix * page_size * inner, both with stride 2 * prefix * page_size * inner).
  */
 typedef struct SandyPagedCache {
-    void* pool;               /* device base address of the page pool */
+    void* pool;               /* device base address of the page pool (of page 0) */
     int32_t dtype;
     int32_t reserved;
     int64_t page_size;        /* rows of the grow dimension per page (power of two) */
     int64_t prefix;           /* elements before the grow dim, e.g. kv heads */
     int64_t inner;            /* elements after the grow dim, e.g. head dim */
     int64_t num_pages;        /* pool capacity in pages */
+    int64_t page_stride;      /* elements from one page to the next; 0: prefix * page_size * inner */
 } SandyPagedCache;
 
 /*
@@ -458,6 +462,26 @@ int sandy_hip_matmul_rms(const SandyTensor* lhs, const SandyRowStats* lhs_stats,
                          char* err, size_t err_cap);
 int sandy_hip_linear(const SandyTensor* x, const SandyTensor* weight, const SandyTensor* bias,
                      const SandyTensor* out, void* stream, char* err, size_t err_cap);
+
+/*
+ * Decode rows (1 to 4 of them) through the reference's fp32 chain
+ *     out = [residual +] act(LinearKernelOp([NormKernelOp LayerNorm](x), weight, bias))
+ * in one launch: the per-block op sequence of the GPT-2 program
+ * (src/models/gpt2_small.sandy.go: ln_1 -> q/k/v, c_proj + residual,
+ * ln_2 -> c_fc -> GELU, c_proj + residual; CPU arithmetic src/core/
+ * TensorCalc.cpp layer_norm 2010-2077, linear 722-773, add 562-663, the GELU
+ * of src/ir/BuiltinLowering.cpp:116-140).  x [..., k] f32 (rows = numel / k),
+ * weight [n, k] f32, out [..., n]; ln_weight / ln_bias [k] (both or
+ * neither: no LayerNorm), bias [n] or NULL, activation 0 (none) or 2
+ * (GELU), residual like out or NULL.  The whole machine reads the weight in
+ * one pass; the dot products sum in another order than the reference's k
+ * loop (fp32 rounding, not bit for bit).  k a multiple of 4, rows * k <=
+ * 16384; x and weight 16-byte aligned.
+ */
+int sandy_hip_decode_linear(const SandyTensor* x, const SandyTensor* ln_weight, const SandyTensor* ln_bias,
+                            double eps, const SandyTensor* weight, const SandyTensor* bias, int32_t activation,
+                            const SandyTensor* residual, const SandyTensor* out, void* stream, char* err,
+                            size_t err_cap);
 
 /* ---------------------------------------------------------------- safetensors weights
  *

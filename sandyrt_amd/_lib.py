@@ -59,6 +59,7 @@ class SandyPagedCache(C.Structure):
         ("prefix", C.c_int64),
         ("inner", C.c_int64),
         ("num_pages", C.c_int64),
+        ("page_stride", C.c_int64),
     ]
 
 
@@ -163,6 +164,7 @@ SIGNATURES = {
     "sandy_hip_rope": [T, T, C.c_double, C.c_int64, C.c_int32, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_rope_pair": [T, T, T, C.c_double, C.c_int64, C.c_int32, T, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_softmax": [T, C.c_int64, T, C.c_void_p, ERR, C.c_size_t],
+    "sandy_hip_decode_linear": [T, T, T, C.c_double, T, T, C.c_int32, T, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_paged_to_dense": [C.POINTER(SandyPagedTensor), T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_paged_stage": [C.POINTER(SandyPagedTensor), C.c_int32, T, C.c_void_p, ERR, C.c_size_t],
     "sandy_hip_reduce_sum": [T, C.c_int64, C.c_int32, T, C.c_void_p, ERR, C.c_size_t],

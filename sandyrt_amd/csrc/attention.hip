@@ -62,7 +62,7 @@ struct PagedArgs {
     int64_t o_sb, o_sh;
     const uint16_t* k_pool;
     const uint16_t* v_pool;
-    int64_t page_elems;  // Hkv * P * D
+    int64_t page_elems;  // elements from one page to the next
     int64_t num_pages;
     const int32_t* table;
     int64_t table_stride;
@@ -1034,6 +1034,111 @@ __global__ __launch_bounds__(256) void attention_staged_kernel(GenArgs a) {
     }
 }
 
+// fp32 single-query steps (decode, Tq = 1) with up to kGenStage keys, head
+// dim 32 / 64 / 128 / 256: the GPT-2 decode attention.  The scores are the
+// reference's -- one thread per key sums q.k over d in order (float, no
+// contraction: bit for bit the reference's score) from 16-byte loads of its
+// K row, all in flight -- and so are the max and the double sum of exp(s -
+// max).  P.V spreads over every thread: 256 / D groups of D threads take
+// consecutive key ranges, each summing its range in key order with all of
+// its V rows requested at once, and the groups' partials are added in group
+// order.  That last split is the only change of order against the
+// reference's single in-order sum (fp32 rounding, not bit for bit).
+template <int D>
+__global__ __launch_bounds__(256) void attention_decode_f32_kernel(GenArgs a) {
+    constexpr int kG = 256 / D;   // key groups in P.V
+    constexpr int kB = 16;        // V rows per group in flight
+    __shared__ float fred[4];
+    __shared__ double dred[4];
+    __shared__ __attribute__((aligned(16))) float qv[D];
+    __shared__ float sprob[kGenStage];
+    __shared__ int64_t svrow[kGenStage];
+    __shared__ float part[kG][D];
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int kh = h / (a.hq / a.hkv);
+    int64_t qpos = 0;
+    if (a.pos) {
+        qpos = load_index(a.pos, a.pos_dt, b);
+        if (qpos < 0) {
+            if (tid == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
+            return;
+        }
+    }
+    const int64_t min_key = a.window > 0 ? max<int64_t>(0, qpos + 1 - a.window) : 0;
+    const int64_t k_end = min<int64_t>(a.tk, qpos + 1);
+    const float* qg = static_cast<const float*>(a.q) + b * a.qs[0] + h * a.qs[1];
+    if (tid < D) qv[tid] = qg[tid];
+    __syncthreads();
+    const float* kp = static_cast<const float*>(a.k);  // pool mode: k and v are the pools
+    const float* vp = static_cast<const float*>(a.v);
+    float lmax = -INFINITY;
+    bool ok = true;
+    for (int64_t key = min_key + tid; key < k_end; key += 256) {
+        const int64_t krow = kv_row(a, a.ks, a.k_pages, b, kh, key, ok);
+        svrow[key - min_key] = kv_row(a, a.vs, a.v_pages, b, kh, key, ok);
+        const float4* kr = reinterpret_cast<const float4*>(kp + krow);
+        float4 kv[D / 4];
+#pragma unroll
+        for (int j = 0; j < D / 4; j++) kv[j] = kr[j];
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < D / 4; j++) {
+            acc = __fadd_rn(acc, __fmul_rn(qv[4 * j], kv[j].x));
+            acc = __fadd_rn(acc, __fmul_rn(qv[4 * j + 1], kv[j].y));
+            acc = __fadd_rn(acc, __fmul_rn(qv[4 * j + 2], kv[j].z));
+            acc = __fadd_rn(acc, __fmul_rn(qv[4 * j + 3], kv[j].w));
+        }
+        const float sc = __fmul_rn(acc, a.scale);
+        sprob[key - min_key] = sc;
+        lmax = fmaxf(lmax, sc);
+    }
+    if (!ok) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
+    lmax = wave_max(lmax);
+    if ((tid & 63) == 0) fred[tid >> 6] = lmax;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(fred[0], fred[1]), fmaxf(fred[2], fred[3]));
+    float* og = static_cast<float*>(a.out) + b * a.os[0] + h * a.os[1];
+    const int64_t n = max<int64_t>(0, k_end - min_key);
+    if (mx == -INFINITY) {
+        if (tid < D) og[tid] = 0.0f;
+        return;
+    }
+    double sum = 0.0;
+    for (int64_t i = tid; i < n; i += 256) sum += exp(static_cast<double>(__fsub_rn(sprob[i], mx)));
+    sum = wave_sum(sum);
+    if ((tid & 63) == 0) dred[tid >> 6] = sum;
+    __syncthreads();
+    const double total = dred[0] + dred[1] + dred[2] + dred[3];
+    const float inv = 1.0f / static_cast<float>(total);
+    for (int64_t i = tid; i < n; i += 256) sprob[i] = __fmul_rn(expf(__fsub_rn(sprob[i], mx)), inv);
+    __syncthreads();
+    // P.V: group g sums keys [g * per, (g + 1) * per) in order
+    const int g = tid / D, d = tid % D;
+    const int64_t per = (n + kG - 1) / kG;
+    const int64_t i0 = g * per, i1 = min<int64_t>(n, i0 + per);
+    float acc = 0.0f;
+    for (int64_t c = i0; c < i1; c += kB) {
+        float vv[kB];
+#pragma unroll
+        for (int j = 0; j < kB; j++) {
+            const int64_t i = c + j < i1 ? c + j : i1 - 1;
+            vv[j] = vp[svrow[i] + d];
+        }
+#pragma unroll
+        for (int j = 0; j < kB; j++)
+            if (c + j < i1) acc = __fadd_rn(acc, __fmul_rn(sprob[c + j], vv[j]));
+    }
+    part[g][d] = acc;
+    __syncthreads();
+    if (tid < D) {
+        float o = part[0][tid];
+#pragma unroll
+        for (int q = 1; q < kG; q++) o = __fadd_rn(o, part[q][tid]);
+        og[tid] = o;
+    }
+}
+
 } // namespace
 } // namespace sandy_hip
 
@@ -1127,6 +1232,7 @@ struct PagedCall {
     // v_pool) or the reference's page tables (k_pages / v_pages)
     const void* k_pool;
     const void* v_pool;
+    int64_t page_elems;  // elements from one page to the next (K and V alike)
     int64_t num_pages;
     const int32_t* table;
     int64_t table_stride;
@@ -1149,6 +1255,10 @@ int check_paged(const SandyTensor* q, const SandyPagedCache* kc, const SandyPage
     if (vc->prefix != hkv || vc->page_size != P || vc->inner != kc->inner || vc->num_pages != kc->num_pages)
         return fail(e, SANDY_ERR_INVALID, "attention k and v head count mismatch");
     if (kc->inner != D) return fail(e, SANDY_ERR_INVALID, "attention head dimension mismatch");
+    const int64_t dense_page = hkv * kc->page_size * D;
+    const int64_t stride = kc->page_stride ? kc->page_stride : dense_page;
+    if ((vc->page_stride ? vc->page_stride : dense_page) != stride || stride < dense_page)
+        return fail(e, SANDY_ERR_INVALID, "paged attention k and v page strides must match and hold a page");
     if (P <= 0 || (P & (P - 1)) != 0) return fail(e, SANDY_ERR_INVALID, "paged tensor pool page_size must be a power of two");
     if (hq <= 0 || hkv <= 0 || hq % hkv != 0) return fail(e, SANDY_ERR_INVALID, "attention heads must be divisible by kv_heads");
     if (window < 0) return fail(e, SANDY_ERR_INVALID, "attention window must be >= 0");
@@ -1180,6 +1290,7 @@ int check_paged(const SandyTensor* q, const SandyPagedCache* kc, const SandyPage
     c->o_sh = out->strides[1];
     c->k_pool = kc->pool;
     c->v_pool = vc->pool;
+    c->page_elems = stride;
     c->num_pages = kc->num_pages;
     c->table = static_cast<const int32_t*>(base_ptr(*table));
     c->table_stride = table->strides[0];
@@ -1208,7 +1319,7 @@ int launch_paged_mfma(const PagedCall& c, const SandyTensor* q, const SandyTenso
     a.o_sh = c.o_sh;
     a.k_pool = static_cast<const uint16_t*>(c.k_pool);
     a.v_pool = static_cast<const uint16_t*>(c.v_pool);
-    a.page_elems = hkv * P * D;
+    a.page_elems = c.page_elems;
     a.num_pages = c.num_pages;
     a.table = c.table;
     a.table_stride = c.table_stride;
@@ -1318,7 +1429,7 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
     a.v = vc->pool;
     a.dt = q->dtype;
     a.paged = 1;
-    a.page_elems = hkv * P * D;
+    a.page_elems = c.page_elems;
     a.page_size = P;
     a.num_pages = kc->num_pages;
     a.table = static_cast<const int32_t*>(base_ptr(*table));
@@ -1338,7 +1449,19 @@ extern "C" int sandy_hip_paged_attention(const SandyTensor* q, const SandyPagedC
     if (status) return status;
     a.errw = errw;
     dim3 grid(1, static_cast<unsigned>(hq), static_cast<unsigned>(B));
-    if (a.tk <= kGenStage && env_int("SANDY_ATTN_UNSTAGED", 0) == 0) {
+    // fp32 steps of the common head dims: the decode kernel (16-byte rows)
+    const bool dec = q->dtype == SANDY_F32 && a.tk <= kGenStage && (D == 32 || D == 64 || D == 128 || D == 256) &&
+                     (c.page_elems % 4) == 0 && ((reinterpret_cast<uintptr_t>(kc->pool) |
+                                                  reinterpret_cast<uintptr_t>(vc->pool)) & 15u) == 0 &&
+                     env_int("SANDY_ATTN_UNSTAGED", 0) == 0;
+    if (dec) {
+        switch (D) {
+            case 32: hipLaunchKernelGGL(attention_decode_f32_kernel<32>, grid, dim3(256), 0, stream, a); break;
+            case 64: hipLaunchKernelGGL(attention_decode_f32_kernel<64>, grid, dim3(256), 0, stream, a); break;
+            case 128: hipLaunchKernelGGL(attention_decode_f32_kernel<128>, grid, dim3(256), 0, stream, a); break;
+            default: hipLaunchKernelGGL(attention_decode_f32_kernel<256>, grid, dim3(256), 0, stream, a); break;
+        }
+    } else if (a.tk <= kGenStage && env_int("SANDY_ATTN_UNSTAGED", 0) == 0) {
         if (q->dtype == SANDY_BF16) hipLaunchKernelGGL(attention_staged_kernel<BF16>, grid, dim3(256), 0, stream, a);
         else hipLaunchKernelGGL(attention_staged_kernel<F32>, grid, dim3(256), 0, stream, a);
     } else if (q->dtype == SANDY_BF16) {

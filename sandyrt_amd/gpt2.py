@@ -97,6 +97,11 @@ class GPT2Runner:
         self.dev = dev if dev is not None else HipDevice(0)
         self._own_dev = dev is None
         self.w = {k: torch.from_numpy(np.ascontiguousarray(v)).cuda() for k, v in host_weights.items()}
+        # the decode step's q/k/v projection as one [3 hidden, hidden] linear
+        for i in range(cfg.layers):
+            p = f"h.{i}.attn."
+            for part in ("weight", "bias"):
+                self.w[p + "qkv." + part] = torch.cat([self.w[p + n + "_proj." + part] for n in ("q", "k", "v")]).contiguous()
         pages = (max_seq + page_size - 1) // page_size
         self.k_pools, self.v_pools, self.k_seq, self.v_seq = [], [], [], []
         for _ in range(cfg.layers):
@@ -116,8 +121,8 @@ class GPT2Runner:
         dv, H, f32 = "cuda", cfg.hidden, torch.float32
         self.token = torch.zeros(1, 1, dtype=torch.int64, device=dv)
         self.pos = torch.zeros(1, dtype=torch.int64, device=dv)
-        self.bufs = {n: torch.empty(1, H, dtype=f32, device=dv) for n in ("te", "pe", "x", "x2", "h", "q", "k", "v",
-                                                                           "ctx", "o", "m")}
+        self.bufs = {n: torch.empty(1, H, dtype=f32, device=dv) for n in ("te", "pe", "x", "x2", "h", "ctx", "o", "m")}
+        self.bufs["qkv"] = torch.empty(1, 3 * H, dtype=f32, device=dv)
         self.bufs["f"] = torch.empty(1, cfg.ffn, dtype=f32, device=dv)
         self.bufs["g"] = torch.empty(1, cfg.ffn, dtype=f32, device=dv)
         self.logits = torch.empty(1, cfg.vocab, dtype=f32, device=dv)
@@ -195,12 +200,13 @@ class GPT2Runner:
             return _Call("sandy_hip_elementwise", cn, C.c_int32(len(nodes)), C.c_uint32(res), arr, bc,
                          C.c_int32(len(ins)), d(out), stream=s)
 
-        def linear(x, name, out):
-            return _Call("sandy_hip_linear", d(x), d(w[name + ".weight"]), d(w[name + ".bias"]), d(out), stream=s)
-
-        def norm(x, name, out):
-            return _Call("sandy_hip_norm", C.c_int32(1), d(x), d(w[name + ".weight"]), d(w[name + ".bias"]),
-                         C.c_double(c.eps), d(out), stream=s)
+        def linear(x, name, out, ln=None, gelu=False, residual=None):
+            """[residual +] gelu?(linear(layer_norm?(x))) in one launch"""
+            lw, lb = (d(w[ln + ".weight"]), d(w[ln + ".bias"])) if ln else (None, None)
+            bias = d(w[name + ".bias"]) if name + ".bias" in w else None
+            return _Call("sandy_hip_decode_linear", d(x), lw, lb, C.c_double(c.eps), d(w[name + ".weight"]), bias,
+                         C.c_int32(2 if gelu else 0), d(residual) if residual is not None else None, d(out),
+                         stream=s)
 
         head4 = lambda t: t.view(1, c.heads, 1, c.head_dim)  # noqa: E731
         ids0 = (C.c_uint32 * 1)(self.k_seq[0])
@@ -212,34 +218,28 @@ class GPT2Runner:
                           stream=s))
         prog.append(ew(self.add, self.add_res, [b["te"], b["pe"]], b["x"]))
         x, x2 = b["x"], b["x2"]
+        H = c.hidden
+        q, k, v = b["qkv"][:, :H], b["qkv"][:, H:2 * H], b["qkv"][:, 2 * H:]
         for i in range(c.layers):
             p = f"h.{i}."
-            prog.append(norm(x, p + "ln_1", b["h"]))
-            prog.append(linear(b["h"], p + "attn.q_proj", b["q"]))
-            prog.append(linear(b["h"], p + "attn.k_proj", b["k"]))
-            prog.append(linear(b["h"], p + "attn.v_proj", b["v"]))
+            prog.append(linear(x, p + "attn.qkv", b["qkv"], ln=p + "ln_1"))
             kid, vid = (C.c_uint32 * 1)(self.k_seq[i]), (C.c_uint32 * 1)(self.v_seq[i])
             self._keep += [kid, vid]
             prog.append(_DevCall("sandy_hip_device_paged_append_step", dev.handle, C.c_uint32(self.k_pools[i]), kid,
-                                 C.c_int32(1), d(head4(b["k"]))))
+                                 C.c_int32(1), d(head4(k))))
             prog.append(_DevCall("sandy_hip_device_paged_append_step", dev.handle, C.c_uint32(self.v_pools[i]), vid,
-                                 C.c_int32(1), d(head4(b["v"]))))
+                                 C.c_int32(1), d(head4(v))))
             kc, table, _ = dev.paged_views(self.k_pools[i])
             vc, _, _ = dev.paged_views(self.v_pools[i])
             table.contents.dims[0] = 1
             self._keep += [kc, vc, table]
-            prog.append(_Call("sandy_hip_paged_attention", d(head4(b["q"])), kc, vc, table, d(self.pos),
+            prog.append(_Call("sandy_hip_paged_attention", d(head4(q)), kc, vc, table, d(self.pos),
                               C.c_int64(0), C.c_double(-1.0), d(head4(b["ctx"])), stream=s))
-            prog.append(linear(b["ctx"], p + "attn.c_proj", b["o"]))
-            prog.append(ew(self.add, self.add_res, [x, b["o"]], x2))
-            prog.append(norm(x2, p + "ln_2", b["h"]))
-            prog.append(linear(b["h"], p + "mlp.c_fc", b["f"]))
-            prog.append(ew(self.gelu, self.gelu_res, [b["f"]], b["g"]))
-            prog.append(linear(b["g"], p + "mlp.c_proj", b["m"]))
-            prog.append(ew(self.add, self.add_res, [x2, b["m"]], x))
-        prog.append(norm(x, "ln_f", b["h"]))
-        prog.append(_Call("sandy_hip_matmul", d(b["h"]), d(w["wte.weight"]), C.c_int32(0), C.c_int32(1),
-                          d(self.logits), stream=s))
+            prog.append(linear(b["ctx"], p + "attn.c_proj", x2, residual=x))
+            prog.append(linear(x2, p + "mlp.c_fc", b["g"], ln=p + "ln_2", gelu=True))
+            prog.append(linear(b["g"], p + "mlp.c_proj", x, residual=x2))
+        # logits = layer_norm(x) wte^T (no bias)
+        prog.append(linear(x, "wte", self.logits, ln="ln_f"))
         prog.append(_Call("sandy_hip_topk", d(self.logits), C.c_int64(1), C.c_int64(-1), d(self.top_v),
                           d(self.token), stream=s))
         return prog

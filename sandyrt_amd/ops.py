@@ -301,21 +301,37 @@ def attention(q, k, v, position_offsets=None, window: int = 0, scale: float = -1
 
 @dataclass
 class PagedCache:
-    """A KV page pool: pool tensor [num_pages, prefix, page_size, inner]."""
+    """A KV page pool: pool tensor [num_pages, prefix, page_size, inner], or
+    one half of a K/V pool [num_pages, 2, prefix, page_size, inner] (`half`
+    0 = K, 1 = V: block b's K and V pages side by side, see interleaved)."""
 
     pool: torch.Tensor
+    half: int = -1
+
+    @staticmethod
+    def interleaved(kv_pool: torch.Tensor):
+        """(K cache, V cache) over one [num_pages, 2, prefix, page_size, inner] pool."""
+        return PagedCache(kv_pool, 0), PagedCache(kv_pool, 1)
 
     def struct(self):
         p = self.pool
-        if p.dim() != 4 or not p.is_contiguous():
-            raise SandyError(1, "paged pool must be a contiguous [pages, prefix, page_size, inner] tensor")
         s = _lib.SandyPagedCache()
-        s.pool = p.data_ptr()
         s.dtype = _lib._TORCH_TO_CODE[p.dtype]
-        s.page_size = p.shape[2]
-        s.prefix = p.shape[1]
-        s.inner = p.shape[3]
-        s.num_pages = p.shape[0]
+        if self.half < 0:
+            if p.dim() != 4 or not p.is_contiguous():
+                raise SandyError(1, "paged pool must be a contiguous [pages, prefix, page_size, inner] tensor")
+            s.pool = p.data_ptr()
+            dims = p.shape
+        else:
+            if p.dim() != 5 or p.shape[1] != 2 or not p.is_contiguous():
+                raise SandyError(1, "interleaved paged pool must be a contiguous [pages, 2, prefix, page_size, inner] tensor")
+            s.pool = p[:, self.half].data_ptr()
+            dims = [p.shape[0]] + list(p.shape[2:])
+            s.page_stride = 2 * p.shape[2] * p.shape[3] * p.shape[4]
+        s.page_size = dims[2]
+        s.prefix = dims[1]
+        s.inner = dims[3]
+        s.num_pages = dims[0]
         return C.pointer(s)
 
 
@@ -530,6 +546,19 @@ def matmul_rms(x, stats, norm_weight, epsilon: float, weight, activation: str | 
     out = torch.empty(list(x.shape[:-1]) + [n], dtype=x.dtype, device=x.device) if out is None else out
     call("sandy_hip_matmul_rms", desc(x), C.byref(row_stats(stats)), desc(norm_weight), float(epsilon), desc(weight),
          code, desc(out))
+    return out
+
+
+def decode_linear(x, weight, bias=None, ln_weight=None, ln_bias=None, epsilon: float = 1e-5, activation: str | None = None,
+                  residual=None, out=None):
+    """[residual +] act(linear([layer_norm](x), weight, bias)) for 1-4 fp32
+    rows in one launch (the GPT-2 decode chain); activation None or "gelu"."""
+    _require_gpu(x, weight, bias, ln_weight, ln_bias, residual)
+    shape = list(x.shape[:-1]) + [weight.shape[0]]
+    out = torch.empty(shape, dtype=x.dtype, device=x.device) if out is None else out
+    act = {None: 0, "gelu": 2}[activation]
+    call("sandy_hip_decode_linear", desc(x), desc(ln_weight), desc(ln_bias), C.c_double(epsilon), desc(weight),
+         desc(bias), C.c_int32(act), desc(residual), desc(out))
     return out
 
 

@@ -187,7 +187,10 @@ def test_general_attention_staged_equals_unstaged(ops, monkeypatch, dtype):
     monkeypatch.setenv("SANDY_ATTN_UNSTAGED", "1")
     want = ops.paged_attention(*args, window=5)
     monkeypatch.delenv("SANDY_ATTN_UNSTAGED")
-    assert torch.equal(got, want), "paged"
+    if dtype == torch.float32:  # fp32 decode steps take the decode kernel (its P.V sums in four key ranges)
+        assert_close(got, to_oracle(want), dtype, "paged fp32 decode kernel vs general kernel")
+    else:
+        assert torch.equal(got, want), "paged"
 
 
 def test_general_attention_long_keys_unstaged(ops, oracle):

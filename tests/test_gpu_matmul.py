@@ -333,3 +333,54 @@ def test_fused_gemms_reject_bad_stats(ops):
     with pytest.raises(SandyError, match="out must not alias lhs"):
         sq = torch.zeros(4, 64, dtype=torch.bfloat16, device="cuda")
         ops.matmul_residual(sq, torch.zeros(64, 64, dtype=torch.bfloat16, device="cuda"), sq, None, out=sq)
+
+
+@pytest.mark.parametrize("m,k,n,ln,act,res", [
+    (1, 768, 2304, True, None, False),     # GPT-2 ln_1 -> q/k/v
+    (1, 768, 768, False, None, True),      # c_proj + residual
+    (1, 768, 3072, True, "gelu", False),   # ln_2 -> c_fc -> GELU
+    (1, 3072, 768, False, None, True),     # mlp c_proj + residual
+    (1, 768, 50257, True, None, False),    # ln_f -> lm-head (no bias)
+    (3, 512, 333, True, "gelu", True),     # looped k, several rows, ragged n
+    (4, 100, 37, False, None, False),
+])
+def test_decode_linear_matches_oracle_chain(ops, oracle, m, k, n, ln, act, res):
+    """sandy_hip_decode_linear against the reference's unfused fp32 op chain
+    (layer_norm, linear, the GELU node chain, add) at the fp32 tolerance."""
+    from tests.test_gpu_groups import oracle_nodes
+    r = rng(m * 1000 + k + n)
+    x = from_f32(normal(r, (m, k)), torch.float32)
+    w = from_f32(normal(r, (n, k), 0.02), torch.float32)
+    bias = None if n == 50257 else from_f32(normal(r, (n,), 0.02), torch.float32)
+    lw = from_f32(1 + normal(r, (k,), 0.1), torch.float32) if ln else None
+    lb = from_f32(normal(r, (k,), 0.1), torch.float32) if ln else None
+    resid = from_f32(normal(r, (m, n)), torch.float32) if res else None
+    got = ops.decode_linear(x, w, bias, lw, lb, 1e-5, act, resid)
+    h = oracle.layer_norm(to_oracle(x), to_oracle(lw), to_oracle(lb), 1e-5) if ln else to_oracle(x)
+    if bias is None:
+        y = oracle.matmul(h, to_oracle(w), transpose_rhs=True)
+    else:
+        y = oracle.linear(h, to_oracle(w), to_oracle(bias))
+    if act == "gelu":
+        nodes, out_id = ops.gelu_nodes()
+        y = oracle.elementwise_dag(oracle_nodes(nodes), out_id, [y], [0], y.shape, np.float32)
+    if res:
+        y = oracle.binary("add", to_oracle(resid), y)
+    # the dot products sum in another k order than the reference's loop: an
+    # output near zero (cancellation) carries the rounding of its large terms,
+    # so the bound is 1e-5 of the larger of |want| and the outputs' rms
+    assert_close(got, y, torch.float32, f"decode linear {m}x{k}x{n}", floor=1.0)
+    again = ops.decode_linear(x, w, bias, lw, lb, 1e-5, act, resid)
+    assert torch.equal(got, again), "not deterministic"
+
+
+def test_decode_linear_rejects(ops):
+    from sandyrt_amd._lib import SandyError
+    x = torch.zeros(5, 64, device="cuda")
+    w = torch.zeros(8, 64, device="cuda")
+    with pytest.raises(SandyError, match="1 to 4 rows"):
+        ops.decode_linear(x, w)
+    with pytest.raises(SandyError, match="both LayerNorm weight and bias"):
+        ops.decode_linear(x[:1], w, ln_weight=torch.ones(64, device="cuda"))
+    with pytest.raises(SandyError, match="feature mismatch"):
+        ops.decode_linear(x[:1], w[:, :32].contiguous())
