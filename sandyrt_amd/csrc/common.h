@@ -300,6 +300,17 @@ __device__ __forceinline__ float sandy_tanh(float y) {
     return copysignf(fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f), y);
 }
 
+// h * (1 + tanh(h)) -- the tail of the SiLU node chain (x * sigmoid(x) with
+// h = x / 2) -- by the identity 1 + tanh(h) = 2 / (1 + e^(-2h)): 2h / (1 +
+// e^(-2h)) with the hardware exp2 and reciprocal, about 3e-7 relative
+// everywhere (no cancellation: the denominator is at least 1) in four VALU
+// operations instead of tanh's two branches; -inf side -> -0, +inf side ->
+// 2h.  The element-wise generator emits it for that node pattern and the
+// gated GEMM epilogue calls it, so fused and unfused SiLU agree bit for bit.
+__device__ __forceinline__ float sandy_silu_half(float h) {
+    return (h + h) * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * h));
+}
+
 // Sum over aligned groups of G lanes (G = 2, 4, 8 or 16) with DPP lane moves
 // (quad swaps, then the half-row and row mirrors): every lane of a group ends
 // with the group's total.  ALU-latency moves, unlike __shfl_xor's LDS

@@ -97,6 +97,11 @@ __device__ __forceinline__ float sandy_tanh(float y) {
   const float e = __builtin_amdgcn_exp2f(2.8853900817779268f * a);
   return copysignf(fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f), y);
 }
+// h * (1 + tanh(h)) as 2h / (1 + e^(-2h)): the same code as the library's
+// sandy_silu_half (common.h), emitted for the SiLU node pattern
+__device__ __forceinline__ float sandy_silu_half(float h) {
+  return (h + h) * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * h));
+}
 __device__ __forceinline__ void ld8_bf16(const void* p, i64 i, float* v) {
   uint4 r = *(const uint4*)((const u16*)p + i);
   unsigned w[4] = {r.x, r.y, r.z, r.w};
@@ -175,6 +180,32 @@ std::string node_expr(const SandyScalarNode& n) {
     return "0.0f";
 }
 
+// The SiLU tail h * (1 + tanh(h)) of the reference's lowering (x * sigmoid(x)
+// as (x / 2)(1 + tanh(x / 2)), src/ir/BuiltinLowering.cpp:142-158): for a MUL
+// node whose operands are h and ADD(CONST 1, TANH(h)) (either order), the
+// id of h, else -1.  Such a node is emitted as sandy_silu_half(h).
+int64_t silu_tail_of(const SandyScalarNode* nodes, int count, const SandyScalarNode& n) {
+    if (n.op != 4 || n.operand_count != 2) return -1;
+    auto find = [&](uint32_t id) -> const SandyScalarNode* {
+        for (int i = 0; i < count; i++)
+            if (nodes[i].id == id) return &nodes[i];
+        return nullptr;
+    };
+    for (int side = 0; side < 2; side++) {
+        const uint32_t h = n.operands[side];
+        const SandyScalarNode* a = find(n.operands[1 - side]);
+        if (!a || a->op != 2 || a->operand_count != 2) continue;
+        for (int as = 0; as < 2; as++) {
+            const SandyScalarNode* c = find(a->operands[as]);
+            const SandyScalarNode* t = find(a->operands[1 - as]);
+            if (c && t && c->op == 1 && static_cast<float>(c->constant) == 1.0f && t->op == 13 &&
+                t->operand_count == 1 && t->operands[0] == h)
+                return h;
+        }
+    }
+    return -1;
+}
+
 // chunks of 8 elements per thread per grid stride of the vectorised kernel:
 // one below 2^20 elements, where twice the workgroups beat two chunks in
 // flight per thread (GeGLU [64, 10240]: 3.55 -> 3.04 us), two above
@@ -225,6 +256,7 @@ std::string generate(const SandyScalarNode* nodes, int count, uint32_t result, c
                 const auto& n = nodes[j];
                 s << "      const float s" << n.id << " = ";
                 if (n.op == 0) s << "in" << n.input_index << suf << "[k];\n";
+                else if (silu_tail_of(nodes, count, n) >= 0) s << "sandy_silu_half(s" << silu_tail_of(nodes, count, n) << ");\n";
                 else s << node_expr(n) << ";\n";
             }
             s << "      r[k] = s" << result << ";\n    }\n";
@@ -249,6 +281,7 @@ std::string generate(const SandyScalarNode* nodes, int count, uint32_t result, c
             const auto& n = nodes[j];
             s << "  const float s" << n.id << " = ";
             if (n.op == 0) s << "in" << n.input_index << ";\n";
+            else if (silu_tail_of(nodes, count, n) >= 0) s << "sandy_silu_half(s" << silu_tail_of(nodes, count, n) << ");\n";
             else s << node_expr(n) << ";\n";
         }
         s << "  const i64 o = strided_index(a.odims, a.ostrides, a.orank, lin);\n";

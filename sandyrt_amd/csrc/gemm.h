@@ -98,7 +98,7 @@ struct GemmArgs {
 __device__ __forceinline__ float glu_pair(int kind, float gv, float uv) {
     if (kind == 1) {
         const float h = __fmul_rn(0.5f, gv);
-        return __fmul_rn(__fmul_rn(h, __fadd_rn(1.0f, sandy_tanh(h))), uv);
+        return __fmul_rn(sandy_silu_half(h), uv);
     }
     const float h = __fmul_rn(0.5f, gv);
     const float x3 = __fmul_rn(__fmul_rn(gv, gv), gv);
