@@ -201,15 +201,6 @@ __device__ __forceinline__ int64_t lane_read64(int64_t v, int l) {
 // wave at D = 64), with S^T = K Q^T and O^T += V^T P^T on MFMA and the online
 // softmax in the exp2 domain.  The waves merge through LDS and the piece ends
 // as the final output rows (final_out) or as partial slots slot0 + g*stride.
-// Q^T and this wave's block ids, issued by the caller before it knows the
-// sequence's position (static schedule); `id` is lane i's raw table entry for
-// tile tile_a + wave + 4i (-1 when past the table), validated here.
-template <int D>
-struct PieceInputs {
-    uint4 qv[D / 32];
-    int32_t id;
-};
-
 template <int D>
 __device__ __forceinline__ void load_q_columns(const PagedArgs& a, int b, int kh, int lane, uint4 (&qv)[D / 32]) {
     // Q^T as B operands: column g, d = 32 kk + 8 j .. + 7.  Pad columns
@@ -221,23 +212,17 @@ __device__ __forceinline__ void load_q_columns(const PagedArgs& a, int b, int kh
     for (int kk = 0; kk < D / 32; kk++) qv[kk] = qp[kk * 4];
 }
 
-template <int D, int NB, int NT, int S, bool PRE = false>
+template <int D, int NB, int NT, int S>
 __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* smem, int lane, int wave, int b,
                                              int kh, const SplitRange& sr, int64_t tile_a, int64_t tile_b,
-                                             bool final_out, int64_t slot0, int64_t slot_stride, bool coherent,
-                                             const PieceInputs<D>* pre = nullptr) {
+                                             bool final_out, int64_t slot0, int64_t slot_stride, bool coherent) {
     constexpr int kRow = 2 * D + 8;  // bytes per V row in LDS (8-byte pad: conflict-free transposed reads)
     const int G = a.group;
     const int g = lane & 15;
     const int j = lane >> 4;
 
     uint4 qv[D / 32];
-    if constexpr (PRE) {
-#pragma unroll
-        for (int kk = 0; kk < D / 32; kk++) qv[kk] = pre->qv[kk];
-    } else {
-        load_q_columns<D>(a, b, kh, lane, qv);
-    }
+    load_q_columns<D>(a, b, kh, lane, qv);
 
     float m = -INFINITY, l = 0.0f;
     f32x4_t acc[D / 16];
@@ -263,9 +248,7 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
                 // is reported like a block id outside the pool
                 ok = kpv != 0 && vpv != 0 && ((kpv | vpv) & 15u) == 0;
             } else {
-                int32_t id;
-                if constexpr (PRE) id = pre->id;
-                else id = a.table[b * a.table_stride + (in ? page : 0)];
+                const int32_t id = a.table[b * a.table_stride + (in ? page : 0)];
                 ok = id >= 0 && id < a.num_pages;
                 kpv = reinterpret_cast<uint64_t>(a.k_pool + static_cast<int64_t>(ok ? id : 0) * a.page_elems);
                 vpv = reinterpret_cast<uint64_t>(a.v_pool + static_cast<int64_t>(ok ? id : 0) * a.page_elems);
@@ -622,66 +605,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     fused_merge<D>(a, u.b, u.kh, n_splits, slot0);
 }
 
-// ------------------------------------------------ static schedule (fused merge)
-// Workgroup lin takes unit (split = lin / (B Hkv), b = lin / Hkv mod B,
-// kh = lin mod Hkv); splits are absolute ranges of 16 * kSplitTiles keys from
-// key 0.  The unit's block ids and Q columns therefore do not depend on the
-// sequence's position, and all three are requested at once: one memory round
-// trip before the K/V stream instead of two (position scan, then table).
-// Units past the sequence's last split exit when the position arrives.
-// Split-major numbering, rotated by the split, makes consecutive workgroups
-// (dealt round-robin to the XCDs) belong to different sequences and kv heads
-// and spreads each sequence's splits over the XCDs.
-template <int D, int NB, int NT, int S, int OCC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void paged_decode_static_kernel(PagedArgs a) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    constexpr int kSplitTiles = 4 * NT;  // the host passes split_keys == 16 * kSplitTiles
-    const int per_split = a.batch * a.hkv;
-    const int split = static_cast<int>(blockIdx.x) / per_split;
-    // rotated by the split so one sequence's splits land on successive XCDs
-    // (XCD = workgroup id mod 8): every XCD gets a share of every long
-    // sequence instead of a fixed subset of the sequences
-    int r = static_cast<int>(blockIdx.x) - split * per_split - split % per_split;
-    if (r < 0) r += per_split;
-    const int b = r / a.hkv;
-    const int kh = r - b * a.hkv;
-    const PosWords pw = vector_position(a, b);
-    PieceInputs<D> in;
-    load_q_columns<D>(a, b, kh, lane, in.qv);
-    {
-        const int64_t tile = static_cast<int64_t>(split) * kSplitTiles + wave + 4 * lane;
-        const int64_t page = (16 * tile) >> a.log2_page;
-        const bool ok = lane < NT && page < a.max_blocks;
-        const int32_t id = a.table[b * a.table_stride + (ok ? page : 0)];
-        in.id = ok ? id : -1;
-    }
-    const int64_t pos = join_position(a, pw);
-    if (pos < 0) {  // no keys: zero rows for this kv head's q heads, and the flag
-        if (split == 0) {
-            const int G = a.group;
-            for (int idx = threadIdx.x; idx < G * D; idx += 256)
-                a.out[b * a.o_sb + (kh * G + idx / D) * a.o_sh + idx % D] = 0;
-            if (kh == 0 && threadIdx.x == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
-        }
-        return;
-    }
-    SplitRange sr = seq_range(a, pos);
-    sr.key_begin = 0;  // absolute tiling; a sliding window only masks (and skips whole tiles)
-    sr.n_tiles = static_cast<int>((sr.n_keys + 15) >> 4);
-    const int n_splits = (sr.n_tiles + kSplitTiles - 1) / kSplitTiles;
-    if (split >= n_splits) return;
-    const int64_t ta = static_cast<int64_t>(split) * kSplitTiles;
-    const int64_t tb = min<int64_t>(sr.n_tiles, ta + kSplitTiles);
-    const bool whole = n_splits == 1;
-    const int64_t slot0 = (static_cast<int64_t>(b) * a.hq + kh * a.group) * a.max_splits;
-    attend_piece<D, NB, NT, S, true>(a, smem, lane, wave, b, kh, sr, ta, tb, whole, slot0 + split, a.max_splits, true,
-                                     &in);
-    if (whole) return;
-    fused_merge<D>(a, b, kh, n_splits, slot0);
-}
-
 // Combines the split partials of one (sequence, q head) under the split-unit
 // schedule.  The position is loaded with the first slots' partials (one
 // memory round trip for up to 16 splits); slots at or past the sequence's
@@ -758,19 +681,6 @@ const void* units_for(int nt) {
 
 const void* units_kernel(int D, int nt) {
     return D == 64 ? units_for<64, 2>(nt) : D == 128 ? units_for<128, 1>(nt) : units_for<256, 1>(nt);
-}
-
-template <int D, int NB>
-const void* static_for(int nt) {
-    constexpr int kOcc4 = D == 64 ? 5 : 1;
-    return nt == 2   ? reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 2, 2, kOcc4>)
-           : nt == 4 ? reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 4, 2, kOcc4>)
-           : nt == 8 ? reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 8, 2, 1>)
-                     : reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 16, 2, 1>);
-}
-
-const void* static_kernel(int D, int nt) {
-    return D == 64 ? static_for<64, 2>(nt) : D == 128 ? static_for<128, 1>(nt) : static_for<256, 1>(nt);
 }
 
 // ---------------------------------------------------------------- general kernel
@@ -1382,13 +1292,8 @@ int launch_paged_mfma(const PagedCall& c, const SandyTensor* q, const SandyTenso
     }
     a.ws_o = reinterpret_cast<float*>(ws);
     a.ws_ml = reinterpret_cast<float*>(ws + slots * D * sizeof(float));
-    // schedule: work units numbered over the active splits (default; best
-    // when context lengths vary) or the static
-    // split-major schedule (SANDY_PAGED_STATIC=1; one fewer memory round
-    // trip, best when the batch's contexts are about equal: 22.2 vs
-    // 25.1 us at 32 x 2304 keys, 26.4 vs 24.9 us at U[512, 4096])
-    const bool stat = a.fused && !c.k_pages && env_int("SANDY_PAGED_STATIC", 0) != 0;
-    SANDY_HIP_TRY(hipLaunchKernel(stat ? static_kernel(static_cast<int>(D), nt) : units_kernel(static_cast<int>(D), nt),
+    // work units numbered over the active splits
+    SANDY_HIP_TRY(hipLaunchKernel(units_kernel(static_cast<int>(D), nt),
                                   dim3(static_cast<unsigned>(units)), dim3(256), args, lds, stream),
                   e, "paged attention launch");
     const void* mfn = D == 64 ? reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<64>)

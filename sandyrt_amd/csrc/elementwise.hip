@@ -132,14 +132,6 @@ __device__ __forceinline__ void st8_bf16(void* p, i64 i, const float* v) {
   typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
   __builtin_nontemporal_store(u32x4{r.x, r.y, r.z, r.w}, (u32x4*)((u16*)p + i));
 }
-__device__ __forceinline__ void stc8_bf16(void* p, i64 i, const float* v) {
-  uint4 r;
-  r.x = (unsigned)f2bf(v[0]) | ((unsigned)f2bf(v[1]) << 16);
-  r.y = (unsigned)f2bf(v[2]) | ((unsigned)f2bf(v[3]) << 16);
-  r.z = (unsigned)f2bf(v[4]) | ((unsigned)f2bf(v[5]) << 16);
-  r.w = (unsigned)f2bf(v[6]) | ((unsigned)f2bf(v[7]) << 16);
-  *(uint4*)((u16*)p + i) = r;
-}
 __device__ __forceinline__ void st8_f32(void* p, i64 i, const float* v) {
   typedef float f32x4 __attribute__((ext_vector_type(4)));
   f32x4* q = (f32x4*)((float*)p + i);
@@ -210,11 +202,7 @@ int64_t silu_tail_of(const SandyScalarNode* nodes, int count, const SandyScalarN
 // one below 2^20 elements, where twice the workgroups beat two chunks in
 // flight per thread (GeGLU [64, 10240]: 3.55 -> 3.04 us), two above
 // (SwiGLU [4096, 704]: 4.8 vs 5.4 us with one; four is slower everywhere)
-int vec_chunks(int64_t n) {
-    const int u = static_cast<int>(env_int("SANDY_EW_CHUNKS", 0));
-    if (u == 1 || u == 2 || u == 4 || u == 8) return u;
-    return n < (int64_t{1} << 20) ? 1 : 2;
-}
+int vec_chunks(int64_t n) { return n < (int64_t{1} << 20) ? 1 : 2; }
 
 std::string generate(const SandyScalarNode* nodes, int count, uint32_t result, const int32_t* in_dt,
                      const int* modes, int nin, int32_t out_dt, bool vec, int U) {
@@ -225,7 +213,6 @@ std::string generate(const SandyScalarNode* nodes, int count, uint32_t result, c
     if (vec) {
         // chunk j of 8 elements; a thread takes chunks c, c + 256, ... of each
         // (256 U)-chunk stride of the grid, all U chunks' loads issued first
-        const bool plain_st = env_int("SANDY_EW_PLAIN_STORE", 0) != 0;
         s << "  const i64 chunks = a.n >> 3;\n";
         s << "  for (i64 c0 = (i64)blockIdx.x * " << 256 * U << " + threadIdx.x; c0 < chunks; c0 += (i64)gridDim.x * "
           << 256 * U << ") {\n";
@@ -260,7 +247,7 @@ std::string generate(const SandyScalarNode* nodes, int count, uint32_t result, c
                 else s << node_expr(n) << ";\n";
             }
             s << "      r[k] = s" << result << ";\n    }\n";
-            s << "    " << (out_dt == SANDY_BF16 ? (plain_st ? "stc8_bf16" : "st8_bf16") : "st8_f32") << "(a.out, " << cidx
+            s << "    " << (out_dt == SANDY_BF16 ? "st8_bf16" : "st8_f32") << "(a.out, " << cidx
               << " * 8, r);\n    }\n";
         }
         s << "  }\n}\n";
@@ -432,7 +419,7 @@ extern "C" int sandy_hip_elementwise(const SandyScalarNode* nodes, int32_t node_
     // 4096 workgroups (16 per CU); scalar: one element per thread
     const int64_t threads = vec ? (n / 8 + U - 1) / U : n;
     int64_t blocks64 = (threads + 255) / 256;
-    if (vec) blocks64 = std::min<int64_t>(blocks64, env_int("SANDY_EW_MAX_BLOCKS", 4096));
+    if (vec) blocks64 = std::min<int64_t>(blocks64, 4096);
     const unsigned blocks = static_cast<unsigned>(blocks64);
     EwVecArgs vargs{};
     if (vec) {

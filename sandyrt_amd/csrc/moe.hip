@@ -1408,8 +1408,7 @@ extern "C" int sandy_hip_moe_gather(const SandyTensor* x, const SandyTensor* top
     const int aligned = (row_bytes % 16 == 0) &&
                         ((reinterpret_cast<uintptr_t>(base_ptr(*x)) | reinterpret_cast<uintptr_t>(base_ptr(*packed_x))) & 15) == 0;
     if (routes <= kDispatchRoutes && batch <= 65535 && aligned && top_k <= 64 && 2 * num_experts + 64 <= 16384 &&
-        env_int("SANDY_MOE_ROUTE_GENERAL", 0) == 0 &&
-        env_int("SANDY_MOE_DISPATCH_EXPERTS", 0) == 0) {
+        env_int("SANDY_MOE_ROUTE_GENERAL", 0) == 0) {
         // token-major: about 256 workgroups of ceil(seq / 256) tokens (at most 64 routes each)
         const int64_t tpw = std::max<int64_t>(1, std::min<int64_t>(64 / top_k, (seq + 255) / 256));
         const int64_t wgs = (seq + tpw - 1) / tpw;

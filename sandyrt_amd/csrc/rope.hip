@@ -493,7 +493,7 @@ int rope_run(const SandyTensor* const* xs, const SandyTensor* const* outs, int n
         const int chunks = static_cast<int>(split_half ? dim / 16 : dim / 8);
         // split-half rows whose two halves fit one shuffle group take the
         // whole-line kernel (twice the lanes, each with one piece)
-        lines = split_half && chunks <= 32 && (chunks & (chunks - 1)) == 0 && !std::getenv("SANDY_ROPE_HALVES");
+        lines = split_half && chunks <= 32 && (chunks & (chunks - 1)) == 0;
         const int64_t base_threads = seq * chunks * (lines ? 2 : 1);
         if (mode[0] == 3) {
             groups = static_cast<int>(outer);

@@ -276,51 +276,3 @@ def test_paged_decode_many_sequences(ops, oracle, B):
     run_case(ops, oracle, 600 + B, B, 8, 2, 64, 16, ctx, torch.bfloat16)
 
 
-# ------------------------------------------------------------------ static schedule
-@pytest.mark.parametrize("split", ["128", "256", "512", "2048"])
-def test_paged_decode_static_schedule_splits(ops, oracle, monkeypatch, split):
-    """The opt-in static split-major schedule (block ids and Q requested
-    before the position is known) matches the oracle at every split size,
-    ragged contexts included, and repeats bit for bit."""
-    monkeypatch.setenv("SANDY_PAGED_STATIC", "1")
-    monkeypatch.setenv("SANDY_PAGED_SPLIT", split)
-    out1 = run_case(ops, oracle, 40, 5, 32, 4, 64, 16, [1, 300, 1500, 2049, 700], torch.bfloat16)
-    out2 = run_case(ops, oracle, 40, 5, 32, 4, 64, 16, [1, 300, 1500, 2049, 700], torch.bfloat16)
-    assert torch.equal(out1, out2)
-
-
-@pytest.mark.parametrize("window", [1, 7, 64, 500])
-def test_paged_decode_static_schedule_window(ops, oracle, monkeypatch, window):
-    """Absolute splits under a sliding window: splits wholly below the window
-    carry no keys and drop out of the merge."""
-    monkeypatch.setenv("SANDY_PAGED_STATIC", "1")
-    monkeypatch.setenv("SANDY_PAGED_SPLIT", "256")
-    run_case(ops, oracle, 10 + window, 4, 16, 2, 64, 16, [5, 100, 700, 1200], torch.bfloat16, window=window)
-
-
-@pytest.mark.parametrize("group,D", [(1, 128), (8, 64), (3, 256)])
-def test_paged_decode_static_schedule_shapes(ops, oracle, monkeypatch, group, D):
-    monkeypatch.setenv("SANDY_PAGED_STATIC", "1")
-    run_case(ops, oracle, 4 + group, 3, 2 * group, 2, D, 32, [70, 900, 33], torch.bfloat16)
-    r = rng(77)
-    ctx = [int(c) for c in r.integers(1, 90, 150)]
-    run_case(ops, oracle, 77, 150, 2 * group, 2, D, 16, ctx, torch.bfloat16)
-
-
-def test_paged_decode_static_schedule_negative_position(ops, oracle, monkeypatch):
-    from sandyrt_amd._lib import SandyError
-    monkeypatch.setenv("SANDY_PAGED_STATIC", "1")
-    monkeypatch.setenv("SANDY_PAGED_SPLIT", "128")
-    r = rng(91)
-    ctx = [100, 50, 700, 1]
-    q, kpool, vpool, table, pos = make_paged(r, 4, 8, 2, 64, 16, ctx, 80, torch.bfloat16)
-    bad = pos.copy()
-    bad[1] = -3
-    out = ops.paged_attention(q, ops.PagedCache(kpool), ops.PagedCache(vpool), torch.from_numpy(table).cuda(),
-                              torch.from_numpy(bad).cuda(), window=0, scale=-1.0)
-    with pytest.raises(SandyError, match="attention position_offsets must be non-negative"):
-        ops.check_device_errors()
-    sel = np.array([0, 2, 3])
-    want = oracle_paged(oracle, q[sel], kpool, vpool, table[sel], pos[sel], 0, -1.0)
-    assert_close(out[sel], want, torch.bfloat16, "rows with valid positions")
-    assert torch.count_nonzero(out[1]).item() == 0

@@ -122,23 +122,6 @@ def test_rope(ops, oracle, dtype, case):
     assert_close(got, want, dtype, f"rope {case}")
 
 
-@pytest.mark.parametrize("dtype", DTYPES)
-def test_rope_whole_line_kernel_equals_half_row_kernel(ops, monkeypatch, dtype):
-    """Split-half rows with a power-of-two piece count run the whole-line
-    kernel (partner lanes swap halves); SANDY_ROPE_HALVES forces the half-row
-    kernel: both must agree bit for bit, partial rotary and ids included."""
-    r = rng(23)
-    for shape, rot in [((1, 32, 300, 64), -1), ((2, 4, 33, 128), -1), ((1, 2, 9, 512), 128), ((3, 5, 16), -1),
-                       ((1, 36, 4096, 64), -1)]:  # 36 heads: groups of 6
-        x = from_f32(normal(r, shape), dtype)
-        ids = torch.tensor([17], device="cuda")
-        got = ops.rope(x, 1e4, rotary_dim=rot, split_half=True, position_ids=ids)
-        monkeypatch.setenv("SANDY_ROPE_HALVES", "1")
-        want = ops.rope(x, 1e4, rotary_dim=rot, split_half=True, position_ids=ids)
-        monkeypatch.delenv("SANDY_ROPE_HALVES")
-        assert torch.equal(got, want), shape
-
-
 @pytest.mark.parametrize("kind", ["offset", "seq", "vectors"])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_rope_position_ids(ops, oracle, kind, dtype):
@@ -302,3 +285,21 @@ def test_rope_cache_rejects(ops):
     q = torch.zeros(1, 2, 8, 48, dtype=torch.bfloat16, device="cuda")  # half 24: not a power-of-two multiple of 8
     with pytest.raises(SandyError, match="rope from a cache takes"):
         ops.rope_pair_cached(q, None, cache)
+
+
+def test_rope_sin_cos_accuracy(ops):
+    """The kernels' sin / cos of the RoPE angle against float64 sin / cos: with
+    theta = 1 every pair's angle is the position itself, and rotating the
+    pair (1, 0) returns (cos, sin) exactly (x cos - 0 sin, x sin + 0 cos), so
+    the output is the sin / cos the kernel computed.  Positions up to 2^20;
+    within 1 ulp (2^-23 absolute for values in [-1, 1])."""
+    r = rng(12)
+    pos = np.concatenate([np.arange(0, 4096), r.integers(0, 1 << 20, 4096)]).astype(np.int64)
+    T, D = pos.size, 64
+    x = torch.zeros(1, 1, T, D, dtype=torch.float32, device="cuda")
+    x[..., : D // 2] = 1.0
+    out = ops.rope(x, 1.0, split_half=True, position_ids=torch.from_numpy(pos).cuda()).cpu().numpy()[0, 0]
+    ang = pos.astype(np.float32).astype(np.float64)
+    c, s = np.cos(ang)[:, None], np.sin(ang)[:, None]
+    err = max(np.abs(out[:, : D // 2] - c).max(), np.abs(out[:, D // 2:] - s).max())
+    assert err <= 2.0 ** -23, err
