@@ -53,11 +53,22 @@ def oracle_step(oracle, cfg, w, kc, vc, token, pos):
     return oracle.matmul(h, w["lm_head"], transpose_rhs=True)
 
 
-def test_decode_step_eager_and_graph_match_oracle(oracle):
+@pytest.mark.parametrize("width", ["reduced", "tinyllama"])
+def test_decode_step_eager_and_graph_match_oracle(oracle, width):
+    """The decode step's fused kernels (q/k/v GEMM with the RMSNorm prologue
+    and the RoPE + append epilogue, o and down GEMMs with the residual
+    epilogue, gate/up GEMM with the gated epilogue, lm-head with the final
+    norm) against the oracle's unfused op chain: a reduced model (2 blocks,
+    hidden 256), and one block at TinyLlama-1.1B's full width (hidden 2048,
+    32 q / 4 kv heads, FFN 5632; the vocabulary cut to 1000)."""
     from sandyrt_amd.decode import DecodeConfig, TinyLlamaDecoder, random_weights
     from sandyrt_amd.device import HipDevice
-    cfg = DecodeConfig(layers=2, hidden=256, heads=8, kv_heads=2, head_dim=64, ffn=512, vocab=1000, page_size=32,
-                       max_context=128)
+    if width == "reduced":
+        cfg = DecodeConfig(layers=2, hidden=256, heads=8, kv_heads=2, head_dim=64, ffn=512, vocab=1000, page_size=32,
+                           max_context=128)
+    else:
+        cfg = DecodeConfig(layers=1, hidden=2048, heads=32, kv_heads=4, head_dim=64, ffn=5632, vocab=1000,
+                           page_size=16, max_context=128)
     w = random_weights(cfg, seed=1)
     wn = {k: to_oracle(v) for k, v in w.items()}
     dev = HipDevice(0)
