@@ -59,6 +59,7 @@ struct QkvRope {
     // has read them (a tile that read an advanced length would take a valid
     // append for a stale position)
     uint32_t* arrivals;
+    int32_t kv_arrivals;  // workgroups per row tile whose columns include k or v
     float denom[kQkvMaxPairs];  // theta^(2i / d), host float powf
     int32_t k_slots[kQkvMaxRows];
     int32_t v_slots[kQkvMaxRows];
@@ -325,14 +326,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
             }
         }
     };
+    // q/k/v: column tiles that hold a k or v column (the first of them, kv_first,
+    // reports the rows' position and block errors); q-only tiles store no cache
+    // rows and read no block ids or lengths
+    const int64_t q_cols = ROPE ? static_cast<int64_t>(g.qr.hq) * g.qr.d : 0;
+    const bool kv_tile = ROPE && n0 + 16 * CT > q_cols;
+    const int kv_first = static_cast<int>(q_cols / (16 * CT));
     auto rope_ids = [&]() {
         // slot -> block id of the row's page and the slot's lengths, requested
         // unconditionally (clamped indices; a block index past the table is
         // flagged in the epilogue, the loaded id ignored)
+        if (!kv_tile) {
+#pragma unroll
+            for (int t = 0; t < RT; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    qkb[t][i] = qvb[t][i] = 0;
+                    qkl[t][i] = qvl[t][i] = qpos[t][i];
+                }
+        }
 #pragma unroll
         for (int t = 0; t < RT; t++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
+            for (int i = 0; i < 4 && kv_tile; i++) {
                 const int32_t bi = max(qpos[t][i], 0) >> g.qr.page_shift;
                 const int32_t ks = qks[t][i], vs = qvs[t][i];
                 qkb[t][i] = g.qr.k_table[ks * g.qr.k_max_blocks + min(bi, g.qr.k_max_blocks - 1)];
@@ -370,6 +386,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 #pragma unroll
         for (int i = 0; i < 2 * RT; i++) invx[i] = inv_s[(lane >> 3) + 8 * i];
     }
+    // q/k/v: a workgroup whose columns include k or v (only those store into
+    // the caches, so only those read the lengths) counts itself in once it has
+    // its rows' lengths (the values are used before the atomic, so the loads
+    // have returned); the one that arrives last writes the advanced lengths at
+    // its end.  The count goes out inside the K loop, after the chunk that was
+    // requested behind the lengths, so its round trip overlaps the remaining
+    // chunks.
+    uint32_t arrive = 0;
+    auto count_in = [&]() {
+        if (tid == 0 && kv_tile) {
+            int32_t dep = 0;
+#pragma unroll
+            for (int t = 0; t < RT; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) dep += qkl[t][i] + qvl[t][i];
+            asm volatile("" ::"v"(dep));
+            arrive = __hip_atomic_fetch_add(g.qr.arrivals + blockIdx.y, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    };
+    constexpr int kCountAt = Q + 1 < CPS ? Q + 1 : CPS - 1;
     store(0, 0);
 #pragma unroll
     for (int u = 0; u < CPS; u++) {
@@ -379,29 +415,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         load(c + Q, u % Q);
         // q/k/v epilogue ids after the first chunk: the positions they index by
         // arrived with it, so nothing waits and every first chunk went out first
-        if constexpr (ROPE)
+        if constexpr (ROPE) {
             if (u == 0) rope_ids();
-    }
-
-    // q/k/v: this workgroup has read its rows' lengths (the values are used
-    // here, so the loads have returned) -- count it in; the workgroup that
-    // arrives last writes the advanced lengths at its end
-    uint32_t arrive = 0;
-    if constexpr (ROPE) {
-        if (tid == 0) {
-            int32_t dep = 0;
-#pragma unroll
-            for (int t = 0; t < RT; t++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) dep += qkl[t][i] + qvl[t][i];
-            asm volatile("" ::"v"(dep));
-            arrive = __hip_atomic_fetch_add(g.qr.arrivals + blockIdx.y, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (u == kCountAt) count_in();
         }
     }
     // the lengths of this row tile's rows advance to pos + 1 where the row was
     // appended (position at the length, pages present), by the last arrival
     auto rope_lengths = [&]() {
-        if (__builtin_amdgcn_readfirstlane(arrive) != gridDim.x - 1) return;
+        if (!kv_tile || __builtin_amdgcn_readfirstlane(arrive) != static_cast<uint32_t>(g.qr.kv_arrivals - 1)) return;
         if (tid == 0) __hip_atomic_store(g.qr.arrivals + blockIdx.y, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if ((lane & 15) != 0) return;
         const int32_t kmax = g.qr.k_max_blocks, vmax = g.qr.v_max_blocks;
@@ -517,9 +539,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
                         rp[t][c][i] = reinterpret_cast<uint16_t*>(v_pages + vb * page_bytes) +
                                       ((head - hq - hkv) * psz + row_in_page) * d + cp;
                 }
-                // column tile 0, first column: the row's errors (the lengths
-                // advance in rope_lengths)
-                if (ct == 0 && c == 0 && (lane & 15) == 0) {
+                // the first k/v column tile, first column: the row's errors (the
+                // lengths advance in rope_lengths)
+                if (ct == kv_first && c == 0 && (lane & 15) == 0) {
                     if (kb < 0 || vb < 0) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
                     if (!at_len) atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_POSITION));
                 }

@@ -585,6 +585,9 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
             g.qr.arrivals = static_cast<uint32_t*>(
                 device_counters(3, static_cast<size_t>(row_tiles) * sizeof(uint32_t), stream, e, &status));
             if (status) return status;
+            // column tiles holding a k or v column, times the K splits
+            const int64_t q_cols = static_cast<int64_t>(g.qr.hq) * g.qr.d;
+            g.qr.kv_arrivals = static_cast<int32_t>((col_tiles - std::min<int64_t>(col_tiles, q_cols / (16 * CT))) * splits);
             if (fz->dry) return ok(e);
             launch_waves_qkv(variant, cps, qdepth, norm, grid, stream, g);
             SANDY_HIP_TRY(hipGetLastError(), e, what);
