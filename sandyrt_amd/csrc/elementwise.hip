@@ -73,6 +73,13 @@ struct EwArgs {
 struct EwVecArgs { const void* in[8]; i64 numel[8]; void* out; i64 n; };
 __device__ __forceinline__ float bf2f(u16 b) { return __uint_as_float(((unsigned)b) << 16); }
 __device__ __forceinline__ u16 f2bf(float f) { unsigned u = __float_as_uint(f); return (u16)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16); }
+// two values in one v_cvt_pk_bf16_f32: round to nearest even like f2bf for every
+// value but a NaN (kept a NaN, where f2bf can carry some NaN payloads into -0 or inf)
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ unsigned pk2bf(float lo, float hi) {
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2v{lo, hi}, bf16x2v));
+}
 __device__ __forceinline__ i64 strided_index(const i64* dims, const i64* strides, int rank, i64 lin) {
   i64 off = 0;
   for (int d = rank - 1; d >= 0; d--) { i64 c = lin % dims[d]; lin /= dims[d]; off += c * strides[d]; }
@@ -125,10 +132,10 @@ __device__ __forceinline__ void ld8_f32(const void* p, i64 i, float* v) {
 }
 __device__ __forceinline__ void st8_bf16(void* p, i64 i, const float* v) {
   uint4 r;
-  r.x = (unsigned)f2bf(v[0]) | ((unsigned)f2bf(v[1]) << 16);
-  r.y = (unsigned)f2bf(v[2]) | ((unsigned)f2bf(v[3]) << 16);
-  r.z = (unsigned)f2bf(v[4]) | ((unsigned)f2bf(v[5]) << 16);
-  r.w = (unsigned)f2bf(v[6]) | ((unsigned)f2bf(v[7]) << 16);
+  r.x = pk2bf(v[0], v[1]);
+  r.y = pk2bf(v[2], v[3]);
+  r.z = pk2bf(v[4], v[5]);
+  r.w = pk2bf(v[6], v[7]);
   typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
   __builtin_nontemporal_store(u32x4{r.x, r.y, r.z, r.w}, (u32x4*)((u16*)p + i));
 }
