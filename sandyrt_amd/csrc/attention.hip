@@ -725,22 +725,23 @@ struct GenArgs {
 __device__ __forceinline__ int64_t kv_row(const GenArgs& a, const int64_t* st, const uint64_t* pages, int b, int kh,
                                           int64_t key, bool& ok) {
     if (!a.paged) return b * st[0] + kh * st[1] + key * st[2];
+    // page_size is a power of two (checked on the host): shifts, not 64-bit divisions
+    const int sh = __builtin_ctzll(static_cast<uint64_t>(a.page_size));
+    const int64_t page = key >> sh, in_page = key & (a.page_size - 1);
     if (pages) {
-        const uint64_t at = pages[key / a.page_size];
+        const uint64_t at = pages[page];
         if (at == 0) {
             ok = false;
             return 0;
         }
-        const int64_t esz = a.dt == SANDY_F32 ? 4 : 2;
-        return static_cast<int64_t>(at) / esz + ((b * a.kv_rows_b + kh) * a.page_size + key % a.page_size) * a.d;
+        return static_cast<int64_t>(at >> (a.dt == SANDY_F32 ? 2 : 1)) + ((b * a.kv_rows_b + kh) * a.page_size + in_page) * a.d;
     }
-    const int64_t page = key / a.page_size;
     const int32_t blk = a.table[b * a.table_stride + page];
     if (blk < 0 || blk >= a.num_pages) {
         ok = false;
         return 0;
     }
-    return static_cast<int64_t>(blk) * a.page_elems + (kh * a.page_size + key % a.page_size) * a.d;
+    return static_cast<int64_t>(blk) * a.page_elems + (kh * a.page_size + in_page) * a.d;
 }
 
 // The reference's algorithm per (query, head, batch), in its operation order:
