@@ -331,6 +331,65 @@ def _check_matmul_qkv(shape, split_half, norm, P, pos_dtype):
         dev.close()
 
 
+@pytest.mark.parametrize("split_half", [True, False])
+def test_matmul_qkv_matches_oracle_chain(oracle, split_half):
+    """sandy_hip_device_matmul_qkv at TinyLlama's width against the oracle's
+    op chain (RMSNorm, q/k/v matmul, RoPE of q and k at each sequence's
+    position): the q rows and the K/V rows appended at that position, bf16
+    tolerance per op, the earlier history untouched."""
+    from sandyrt_amd import ops
+    from sandyrt_amd._lib import BF16
+    from sandyrt_amd.device import HipDevice
+    B, hq, hkv, D, K, P = 3, 32, 4, 64, 2048, 16
+    dev = HipDevice(0)
+    try:
+        kp = dev.create_paged_pool([1, hkv, -1, D], BF16, 2, P, max_tensors=B, max_blocks=8)
+        vp = dev.create_paged_pool([1, hkv, -1, D], BF16, 2, P, max_tensors=B, max_blocks=8)
+        ks, vs = [dev.alloc_paged(kp) for _ in range(B)], [dev.alloc_paged(vp) for _ in range(B)]
+        r = rng(91 + split_half)
+        ctx = [16, 5, 47]
+        hist = []
+        for s, n in enumerate(ctx):
+            k0 = from_f32(normal(r, (1, hkv, n, D)), torch.bfloat16)
+            v0 = from_f32(normal(r, (1, hkv, n, D)), torch.bfloat16)
+            for t, h in ((ks[s], k0), (vs[s], v0)):
+                dev.reserve_paged(t, 8)
+                dev.append_paged(t, h)
+            hist.append((to_oracle(k0), to_oracle(v0)))
+        x = from_f32(normal(r, (B, K)), torch.bfloat16)
+        w = from_f32(normal(r, ((hq + 2 * hkv) * D, K), K ** -0.5), torch.bfloat16)
+        nw = from_f32(1.0 + normal(r, (K,), 0.1), torch.bfloat16)
+        v = x.double().cpu().numpy()
+        stats = torch.from_numpy((v * v).reshape(B, K // 16, 16).sum(axis=2)).cuda()
+        pos = torch.tensor(ctx, dtype=torch.int64, device="cuda")
+        q_got = torch.empty(B, hq, 1, D, dtype=torch.bfloat16, device="cuda")
+        dev.matmul_qkv(x, ops.pair_rope_weight(w, hq, hkv, D, split_half), kp, ks, vp, vs, hq, pos, 1e4, q_got,
+                       split_half=split_half, stats=stats, norm_weight=nw, eps=1e-5)
+        dev.synchronize()
+        ops.check_device_errors()
+        qkv = oracle.matmul(oracle.rms_norm(to_oracle(x), to_oracle(nw), 1e-5), to_oracle(w), transpose_rhs=True)
+        positions = np.array(ctx, np.int64)
+
+        def roped(lo, heads):  # [1, heads, B, D] with sequence b at position ctx[b]
+            t = np.ascontiguousarray(qkv[:, lo:lo + heads * D].reshape(B, heads, D).transpose(1, 0, 2)[None])
+            return oracle.rope(t, 1e4, split_half=split_half, position_ids=positions)[0].transpose(1, 0, 2)
+
+        assert_close(q_got.view(B, hq, D), roped(0, hq), torch.bfloat16, "q")
+        k_new = roped(hq * D, hkv)
+        v_new = qkv[:, (hq + hkv) * D:].reshape(B, hkv, D)
+        dev.paged_sync(kp)
+        dev.paged_sync(vp)
+        for s in range(B):
+            gk = dev.read_paged(ks[s], np.uint16)
+            gv = dev.read_paged(vs[s], np.uint16)
+            assert gk.shape[2] == gv.shape[2] == ctx[s] + 1
+            assert np.array_equal(gk[:, :, :ctx[s]], hist[s][0]) and np.array_equal(gv[:, :, :ctx[s]], hist[s][1])
+            assert_close(gk[0, :, ctx[s]], k_new[s], torch.bfloat16, f"k row of sequence {s}")
+            assert_close(gv[0, :, ctx[s]], v_new[s], torch.bfloat16, f"v row of sequence {s}")
+    finally:
+        dev.close()
+
+
 def test_matmul_qkv_position_must_equal_length():
     """A position that is not the sequence's length is reported as a device
     position error (SANDY_DEVERR_POSITION) and leaves the length as it was."""

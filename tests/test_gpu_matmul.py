@@ -321,6 +321,49 @@ def test_fused_chain_matches_unfused_block(ops):
     assert torch.equal(act, ops.matmul_glu(h, wgu, "silu"))
 
 
+@pytest.mark.parametrize("m", [1, 32])
+def test_fused_decode_gemms_match_oracle_chain(ops, oracle, m):
+    """The fused decode GEMMs at TinyLlama's widths against the oracle's op
+    chain (not against the unfused HIP ops): o projection + residual, then
+    RMSNorm -> gate/up -> SiLU-gate, then down projection (K split over
+    workgroups) + residual, then RMSNorm -> q/k/v, each stage fed the GPU's
+    previous output so the comparison is per op; bf16 tolerance."""
+    from tests.test_gpu_groups import oracle_nodes
+    r = rng(4100 + m)
+    d, f, nq = 2048, 5632, 2560
+    ctx = from_f32(normal(r, (m, d)), torch.bfloat16)
+    x = from_f32(normal(r, (m, d)), torch.bfloat16)
+    wo = from_f32(normal(r, (d, d), 0.02), torch.bfloat16)
+    wg = from_f32(normal(r, (f, d), 0.02), torch.bfloat16)
+    wu = from_f32(normal(r, (f, d), 0.02), torch.bfloat16)
+    wd = from_f32(normal(r, (d, f), 0.02), torch.bfloat16)
+    wqkv = from_f32(normal(r, (nq, d), 0.02), torch.bfloat16)
+    nw1 = from_f32(1.0 + normal(r, (d,), 0.1), torch.bfloat16)
+    nw2 = from_f32(1.0 + normal(r, (d,), 0.1), torch.bfloat16)
+    st_b, st_a = ops.row_stats_buffer(m, d), ops.row_stats_buffer(m, d)
+    silu, sres = ops.silu_mul_nodes()
+
+    s = ops.matmul_residual(ctx, wo, x, st_b)
+    want_s = oracle.binary("add", to_oracle(x), oracle.matmul(to_oracle(ctx), to_oracle(wo), transpose_rhs=True))
+    assert_close(s, want_s, torch.bfloat16, "o projection + residual")
+    np.testing.assert_array_equal(st_b.cpu().numpy(), _row_sumsq_groups(s))
+
+    act = ops.matmul_rms(s, st_b, nw1, 1e-5, ops.interleave_glu_weight(wg, wu), "silu")
+    h = oracle.rms_norm(to_oracle(s), to_oracle(nw1), 1e-5)
+    g_, u_ = (oracle.matmul(h, to_oracle(w_), transpose_rhs=True) for w_ in (wg, wu))
+    want_act = oracle.elementwise_dag(oracle_nodes(silu), sres, [g_, u_], [0, 0], (m, f), g_.dtype)
+    assert_close(act, want_act, torch.bfloat16, "RMSNorm -> gate/up -> SiLU-gate")
+
+    x2 = ops.matmul_residual(act, wd, s, st_a)
+    want_x2 = oracle.binary("add", to_oracle(s), oracle.matmul(to_oracle(act), to_oracle(wd), transpose_rhs=True))
+    assert_close(x2, want_x2, torch.bfloat16, "down projection + residual")
+    np.testing.assert_array_equal(st_a.cpu().numpy(), _row_sumsq_groups(x2))
+
+    qkv = ops.matmul_rms(x2, st_a, nw2, 1e-5, wqkv)
+    want_qkv = oracle.matmul(oracle.rms_norm(to_oracle(x2), to_oracle(nw2), 1e-5), to_oracle(wqkv), transpose_rhs=True)
+    assert_close(qkv, want_qkv, torch.bfloat16, "RMSNorm -> q/k/v")
+
+
 def test_fused_gemms_reject_bad_stats(ops):
     from sandyrt_amd._lib import SandyError
     x = torch.zeros(4, 64, dtype=torch.bfloat16, device="cuda")
