@@ -228,6 +228,12 @@ extern "C" int sandy_hip_decode_linear(const SandyTensor* x, const SandyTensor* 
     if (activation != 0 && activation != 2) return fail(e, SANDY_ERR_INVALID, "decode linear activation must be 0 or 2 (gelu)");
     const uintptr_t al = reinterpret_cast<uintptr_t>(base_ptr(*x)) | reinterpret_cast<uintptr_t>(base_ptr(*weight));
     if (al & 15u) return fail(e, SANDY_ERR_UNSUPPORTED, "decode linear needs 16-byte aligned x and weight");
+    {
+        // every workgroup stages all of x while others already write out
+        const uintptr_t xb = reinterpret_cast<uintptr_t>(base_ptr(*x)), ob = reinterpret_cast<uintptr_t>(base_ptr(*out));
+        const uintptr_t xe = xb + static_cast<uintptr_t>(M * K) * sizeof(float), oe = ob + static_cast<uintptr_t>(M * N) * sizeof(float);
+        if (M * N > 0 && xb < oe && ob < xe) return fail(e, SANDY_ERR_INVALID, "decode linear out must not alias x");
+    }
     if (N == 0) return ok(e);
     const int pieces = K == 768 ? 3 : K == 3072 ? 12 : 0;
     const int rw = pieces == 3 ? 2 : 1;

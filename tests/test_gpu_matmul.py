@@ -427,3 +427,6 @@ def test_decode_linear_rejects(ops):
         ops.decode_linear(x[:1], w, ln_weight=torch.ones(64, device="cuda"))
     with pytest.raises(SandyError, match="feature mismatch"):
         ops.decode_linear(x[:1], w[:, :32].contiguous())
+    sq = torch.zeros(1, 64, device="cuda")
+    with pytest.raises(SandyError, match="out must not alias x"):
+        ops.decode_linear(sq, torch.zeros(64, 64, device="cuda"), out=sq)
