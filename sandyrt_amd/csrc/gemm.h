@@ -122,7 +122,10 @@ __device__ __forceinline__ float glu_pair(int kind, float gv, float uv) {
 // four partial accumulators are summed in wave order through LDS; when the
 // grid also splits K across workgroups, the last-arriving workgroup of each
 // tile sums the splits' fp32 partials in split order (deterministic).
-template <int RT, int CT, int Q, int CPS, int OCC, bool NORM = false, bool ROPE = false>
+// NT: the weight stream is read with the non-temporal policy (each line is
+// used once per launch); off where another workgroup's re-read of the same
+// weights should still find them in L2 (row tiles that do not run together)
+template <int RT, int CT, int Q, int CPS, int OCC, bool NORM = false, bool ROPE = false, bool NT = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void gemm_waves_kernel(GemmArgs g) {
     constexpr int kWTile = 16 * CT * 128;
     // activation rows staged through LDS as whole lines (XL) for tiles of up to
@@ -258,7 +261,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
         const int kb = max(0, min(ch, c_end - 1)) * 128;
 #pragma unroll
         for (int i = 0; i < 2 * CT; i++)
-            wv[slot][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wlane + i * wstep + kb, 0, 0));
+            wv[slot][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wlane + i * wstep + kb, 0, NT ? 2 : 0));
         // XL: the activation rows as whole lines too (8 rows x 128 bytes per
         // instruction), staged through LDS like the weights; otherwise the
         // A operands themselves (half of 16 lines per instruction)
@@ -667,14 +670,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
 }
 
 
-// Launches gemm_waves_kernel with the RMSNorm prologue (matmul_norm.hip):
-// tile variant as in the host heuristic (RT 1 or 2), run length cps, chunks
-// in flight qdepth.
+// Launchers of gemm_waves_kernel, one translation unit per (form, NT) so they
+// compile in parallel: tile variant as in the host heuristic of matmul.hip
+// ((RT, CT) = 0 (1, 1), 1 (2, 1), 3 (2, 2), 4 (1, 2), 5 (2, 4), 6 (1, 4)), run
+// length cps, chunks in flight qdepth.
+// plain (matmul_waves.hip, matmul_waves_nt.hip)
+template <bool NT>
+void launch_waves_plain(int variant, int cps, int qdepth, dim3 grid, hipStream_t stream, const GemmArgs& g);
+// with the RMSNorm prologue (matmul_norm.hip, matmul_norm_nt.hip)
+template <bool NT>
 void launch_waves_norm(int variant, int cps, int qdepth, dim3 grid, hipStream_t stream, const GemmArgs& g);
-
-// Launches gemm_waves_kernel with the q/k/v epilogue (matmul_qkv.hip): RT 1,
-// CT 1 or 2 (variant 0 or 4), run length cps, four chunks in flight.
+// with the q/k/v epilogue (matmul_qkv.hip, matmul_qkv_nt.hip): RT 1, CT 1 or 2
+// (variant 0 or 4), four chunks in flight from run length 4
+template <bool NT>
 void launch_waves_qkv(int variant, int cps, int qdepth, bool norm, dim3 grid, hipStream_t stream, const GemmArgs& g);
+extern template void launch_waves_plain<false>(int, int, int, dim3, hipStream_t, const GemmArgs&);
+extern template void launch_waves_plain<true>(int, int, int, dim3, hipStream_t, const GemmArgs&);
+extern template void launch_waves_norm<false>(int, int, int, dim3, hipStream_t, const GemmArgs&);
+extern template void launch_waves_norm<true>(int, int, int, dim3, hipStream_t, const GemmArgs&);
+extern template void launch_waves_qkv<false>(int, int, int, bool, dim3, hipStream_t, const GemmArgs&);
+extern template void launch_waves_qkv<true>(int, int, int, bool, dim3, hipStream_t, const GemmArgs&);
 
 // The q/k/v decode GEMM with the RoPE + paged-append epilogue (QkvRope
 // filled in by the caller except its pointers' validation): lhs [m, k] bf16,

@@ -37,6 +37,9 @@
 namespace sandy_hip {
 namespace {
 
+// decode GEMM workgroups resident at once (two per CU on the 256 CUs)
+constexpr int64_t kWavesResident = 512;
+
 // Prefill-sized products: workgroup = 16 * RT rows x 64 * CT columns of one
 // batch; wave w owns columns n0 = (tile * 4 + w) * 16 * CT .. + 16 * CT.  Per
 // chunk of 64 k the workgroup stages its activation rows once in LDS and
@@ -567,19 +570,13 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
         }
         const dim3 grid(static_cast<unsigned>(col_tiles * splits), static_cast<unsigned>(row_tiles),
                         static_cast<unsigned>(p.batches));
-#define WAVES_RUN(RT_, CT_, OCC_, R_)                                                                          \
-    case R_:                                                                                                   \
-        if (qdepth >= 4 && R_ >= 4 && RT_ * CT_ <= 2)                                                          \
-            hipLaunchKernelGGL((gemm_waves_kernel<RT_, CT_, 4, R_, 1>), grid, dim3(256), 0, stream, g);       \
-        else                                                                                                   \
-            hipLaunchKernelGGL((gemm_waves_kernel<RT_, CT_, 2, R_, OCC_>), grid, dim3(256), 0, stream, g);    \
-        break;
-#define WAVES_CPS(RT_, CT_, OCC_)                                                                          \
-    switch (cps) {                                                                                         \
-        WAVES_RUN(RT_, CT_, OCC_, 2) WAVES_RUN(RT_, CT_, OCC_, 3) WAVES_RUN(RT_, CT_, OCC_, 4)            \
-        WAVES_RUN(RT_, CT_, OCC_, 5) WAVES_RUN(RT_, CT_, OCC_, 6) WAVES_RUN(RT_, CT_, OCC_, 8)            \
-        WAVES_RUN(RT_, CT_, OCC_, 10) WAVES_RUN(RT_, CT_, OCC_, 12)                                       \
-    }
+        // the weight stream non-temporal where nothing re-reads it from L2 later:
+        // one row tile, or every workgroup resident at once (the row tiles of a
+        // column tile run together); measured at 1 row: q/k/v 5.2 -> 4.6 us,
+        // o 5.1 -> 4.5, gate/up 10.4 -> 9.3, down 8.5 -> 7.8; at 32 rows the
+        // 704-workgroup gate/up re-reads its weights after 352 other workgroups
+        // (15.3 -> 16.5 us non-temporal) and keeps the default policy
+        const bool nt = row_tiles == 1 || col_tiles * splits * row_tiles * p.batches <= kWavesResident;
         if (qkv) {
             int status = 0;
             g.qr.arrivals = static_cast<uint32_t*>(
@@ -589,25 +586,17 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
             const int64_t q_cols = static_cast<int64_t>(g.qr.hq) * g.qr.d;
             g.qr.kv_arrivals = static_cast<int32_t>((col_tiles - std::min<int64_t>(col_tiles, q_cols / (16 * CT))) * splits);
             if (fz->dry) return ok(e);
-            launch_waves_qkv(variant, cps, qdepth, norm, grid, stream, g);
-            SANDY_HIP_TRY(hipGetLastError(), e, what);
-            return ok(e);
+            if (nt) launch_waves_qkv<true>(variant, cps, qdepth, norm, grid, stream, g);
+            else launch_waves_qkv<false>(variant, cps, qdepth, norm, grid, stream, g);
+        } else if (norm) {
+            if (nt) launch_waves_norm<true>(variant, cps, qdepth, grid, stream, g);
+            else launch_waves_norm<false>(variant, cps, qdepth, grid, stream, g);
+        } else {
+            if (nt) launch_waves_plain<true>(variant, cps, qdepth, grid, stream, g);
+            else launch_waves_plain<false>(variant, cps, qdepth, grid, stream, g);
         }
-        if (norm) {
-            launch_waves_norm(variant, cps, qdepth, grid, stream, g);
-            SANDY_HIP_TRY(hipGetLastError(), e, what);
-            return ok(e);
-        }
-        switch (variant) {
-            case 0: WAVES_CPS(1, 1, 4); break;
-            case 1: WAVES_CPS(2, 1, 4); break;
-            case 3: WAVES_CPS(2, 2, 2); break;
-            case 4: WAVES_CPS(1, 2, 4); break;
-            case 5: WAVES_CPS(2, 4, 2); break;
-            default: WAVES_CPS(1, 4, 2); break;
-        }
-#undef WAVES_RUN
-#undef WAVES_CPS
+        SANDY_HIP_TRY(hipGetLastError(), e, what);
+        return ok(e);
     } else if (lines) {
         // 64 x 256 tiles for prefill-sized products (the K loop is rolled and
         // the grid never splits K)
