@@ -1147,8 +1147,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void m
             const bool win = 2 * ch + (w_hi ? 1 : 0) < ksteps;
 #pragma unroll
             for (int i = 0; i < 2 * CT; i++) {
+                // non-temporal: each expert weight line is read by exactly one
+                // workgroup (gate 97.5 -> 92.7 us, down 106.6 -> 98.4 at config 5)
                 const uint4 v = __builtin_bit_cast(
-                    uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wlane, static_cast<int>(i * wstep + ch * 128), 0));
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(wres, wlane, static_cast<int>(i * wstep + ch * 128), 2));
                 wv[i] = win ? v : make_uint4(0, 0, 0, 0);
             }
 #pragma unroll
