@@ -338,7 +338,8 @@ __global__ __launch_bounds__(256) void argmax_wide_kernel(const void* __restrict
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int64_t i0 = c0 + 2048 * u + 8 * tid;
-            raw[u] = Vec8<T>::load_raw(x, rbase + (i0 < n ? i0 : 0));  // n % 8 == 0: a vector is all in or all out
+            // non-temporal (each element is read once): Gemma [64, 262144] 11.8 -> 11.5 us
+            raw[u] = Vec8<T>::load_raw_nt(x, rbase + (i0 < n ? i0 : 0));  // n % 8 == 0: a vector is all in or all out
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
