@@ -163,9 +163,9 @@ __global__ __launch_bounds__(256) void rope_split_kernel(
 // row (a power of two dividing 64) each load and store one 16- or 32-byte
 // piece, the first chunks lanes from the first half and the rest from the
 // second, so every load and store instruction covers whole rows instead of
-// one half of each.  Each lane also reads its partner's (lane ^ chunks) piece
-// from the same lines, and computes the sin/cos of four of its eight pairs,
-// taking the other four from its partner.  Same arithmetic as
+// one half of each.  Each lane takes its partner's (lane ^ chunks) piece by a
+// lane exchange, and computes the sin/cos of four of its eight pairs, taking
+// the other four from its partner.  Same arithmetic as
 // rope_split_kernel.
 // TAB: the cos/sin of every (sequence index, pair) come from a table built
 // by rope_cache_kernel (one [seq, rot_pairs] float2 table shared by q, k and
@@ -216,17 +216,13 @@ __global__ __launch_bounds__(256) void rope_split_lines_kernel(
                 tv[i] = tab[s * rot_pairs + (FULL || p < rot_pairs ? p : 0)];
             }
         }
-        typename Vec8<T>::raw mine[U], oth[U];
+        typename Vec8<T>::raw mine[U];
 #pragma unroll
         for (int j = 0; j < U; j++) {
             if (FULL || o0 + j < o_end) {
                 const bool sec = o0 + j >= outer_first;
                 const int64_t base = ((o0 + j - (sec ? outer_first : 0)) * seq + s) * dim;
-                mine[j] = Vec8<T>::load_raw(sec ? x2 : x, base + (hi ? half : 0) + c * 8);
-                // the partner lane's piece, read again from the line this wave
-                // requests (a cache hit) instead of exchanged through the LDS
-                // crossbar: 9.1 -> 8.9 us at config 2
-                oth[j] = Vec8<T>::load_raw(sec ? x2 : x, base + (hi ? 0 : half) + c * 8);
+                mine[j] = Vec8<T>::load_raw_nt(sec ? x2 : x, base + (hi ? half : 0) + c * 8);
             }
         }
         if (fresh) {
@@ -265,7 +261,17 @@ __global__ __launch_bounds__(256) void rope_split_lines_kernel(
         for (int j = 0; j < U; j++) {
             // every lane of a row takes the same branch here (o_end is per row group)
             if (!FULL && o0 + j >= o_end) break;
-            const typename Vec8<T>::raw other = oth[j];
+            // the partner lane's piece (lane ^ chunks) through the LDS crossbar: the
+            // rows are read once, non-temporal (8.8 -> 8.5 us at config 2; reading
+            // the partner's piece again from the cached line ran 8.8-8.9 with plain
+            // loads and 9.3-9.7 with non-temporal ones; ds_swizzle 9.1-9.3)
+            typename Vec8<T>::raw other;
+            {
+                const uint32_t* src = reinterpret_cast<const uint32_t*>(&mine[j]);
+                uint32_t* dst = reinterpret_cast<uint32_t*>(&other);
+#pragma unroll
+                for (int w = 0; w < static_cast<int>(sizeof(mine[j]) / 4); w++) dst[w] = __shfl_xor(src[w], m, 64);
+            }
             const bool sec = o0 + j >= outer_first;
             const int64_t base = ((o0 + j - (sec ? outer_first : 0)) * seq + s) * dim;
             float a[8], b[8], res[8];
