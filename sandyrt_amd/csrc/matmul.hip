@@ -497,7 +497,9 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
             // (rotated over >= 1 GiB of copies):
             //   <= 16 rows: 16 x 16 tiles, 16 x 32 from N >= 16384 (lm-head);
             //   <= 32 rows: 16-row tiles (the second row tile re-reads the
-            //     weights from cache), 32 columns from N K >= 5M;
+            //     weights from cache), 32 columns from N K >= 5M; 17..32 rows
+            //     of N K >= 16M without the norm prologue: one 32-row tile
+            //     (weights streamed once);
             //   weights past 64 MB at 32 rows, and 33..64 rows: 32-row tiles,
             //     the widest column tile giving >= 120 workgroups;
             //   4 chunks in flight per wave for weights under 8M elements
@@ -513,6 +515,15 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
                 ct = p.N >= 16384 ? 2 : 1;
                 qdepth = 4;
                 if (chunks > 32) ksplits = (chunks + 47) / 48;
+            } else if (p.M <= 32 && !big && !norm && p.M > 16 && p.N * p.K >= 16 * (int64_t(1) << 20) && chunks <= 32) {
+                // 17..32 rows of a wide projection (gate/up, 2048 x 11264): one
+                // 32-row tile, so the weights stream once, non-temporal, with four
+                // chunks in flight (15.2 -> 14.2 us; two 16-row tiles re-read
+                // them from L2 and must keep them cached).  Not with the RMSNorm
+                // prologue, whose work grows with the rows of a tile (gated
+                // gate/up 17.0 -> 18.2 us)
+                rt = 2;
+                qdepth = 4;
             } else if (p.M <= 32 && !big) {
                 ct = p.N * p.K >= 5 * (int64_t(1) << 20) ? 2 : 1;
                 qdepth = p.N * p.K < 8 * (int64_t(1) << 20) ? 4 : 2;
