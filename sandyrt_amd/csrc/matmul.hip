@@ -587,7 +587,9 @@ int launch(const Plan& p, const SandyTensor& l, const SandyTensor& r, const Sand
         // o 5.1 -> 4.5, gate/up 10.4 -> 9.3, down 8.5 -> 7.8; at 32 rows the
         // 704-workgroup gate/up re-reads its weights after 352 other workgroups
         // (15.3 -> 16.5 us non-temporal) and keeps the default policy
-        const bool nt = row_tiles == 1 || col_tiles * splits * row_tiles * p.batches <= kWavesResident;
+        // (batched products may share one rhs across the batch: only a single
+        // matrix counts as read once when the grid is not resident at once)
+        const bool nt = (row_tiles == 1 && p.batches == 1) || col_tiles * splits * row_tiles * p.batches <= kWavesResident;
         if (qkv) {
             int status = 0;
             g.qr.arrivals = static_cast<uint32_t*>(
