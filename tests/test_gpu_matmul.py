@@ -130,8 +130,12 @@ def test_matmul_empty(ops):
 
 # ---------------------------------------------------------------- MFMA path
 # (M, N, K): decode rows against projection-like weights, ragged N, odd k-steps
+# (24, 8192, 2048): 17-32 rows of a wide projection, one 32-row tile with the non-temporal weight stream;
+# (1, 4096, 2048): one row tile, non-temporal (the default policy at 32 rows: (32, 2048, 512) and the
+# RMSNorm-prologue tests, which compare bit for bit with the plain GEMM)
 MFMA_SHAPES = [(1, 256, 64), (7, 200, 96), (16, 512, 2048), (32, 2048, 512), (33, 300, 160), (64, 1000, 256),
-               (3, 700, 2560), (40, 96, 5632), (100, 520, 224), (256, 640, 1024), (130, 300, 96)]
+               (3, 700, 2560), (40, 96, 5632), (100, 520, 224), (256, 640, 1024), (130, 300, 96), (24, 8192, 2048),
+               (1, 4096, 2048)]
 
 
 @pytest.mark.parametrize("m,n,k", MFMA_SHAPES)
