@@ -593,6 +593,16 @@ int sandy_hip_device_paged_append(SandyHipDevice* dev, uint32_t tensor, const Sa
  * new rows must already be reserved (sandy_hip_device_paged_reserve). */
 int sandy_hip_device_paged_append_step(SandyHipDevice* dev, uint32_t pool, const uint32_t* tensors, int32_t count,
                                        const SandyTensor* rows, char* err, size_t err_cap);
+/* The K and V step appends of one decode step in one launch: as two
+ * sandy_hip_device_paged_append_step calls, (k_pool, k_tensors, k_rows) and
+ * (v_pool, v_tensors, v_rows), for count <= 64 tensors each.  Every check runs
+ * before any bookkeeping moves.  The two Engine::paged_append_op calls of a
+ * decode step (src/engine/Engine.cpp:548-596, one per cache); the reference
+ * has no single counterpart. */
+int sandy_hip_device_paged_append_step_kv(SandyHipDevice* dev, uint32_t k_pool, const uint32_t* k_tensors,
+                                          uint32_t v_pool, const uint32_t* v_tensors, int32_t count,
+                                          const SandyTensor* k_rows, const SandyTensor* v_rows, char* err,
+                                          size_t err_cap);
 /* One decode step's q/k/v post-processing in one launch, for `count` <= 256
  * sequences: qkv is the [count, (q_heads + 2 kv_heads) head_dim] bf16 output
  * of the fused q/k/v projection.  q heads are rotated into q_out [count,

@@ -208,6 +208,7 @@ DEVICE_SIGNATURES = {
     "sandy_hip_device_paged_reserve": ([DEV, C.c_uint32, C.c_int64], C.c_int),
     "sandy_hip_device_paged_append": ([DEV, C.c_uint32, T], C.c_int),
     "sandy_hip_device_paged_append_step": ([DEV, C.c_uint32, U32P, C.c_int32, T], C.c_int),
+    "sandy_hip_device_paged_append_step_kv": ([DEV, C.c_uint32, U32P, C.c_uint32, U32P, C.c_int32, T, T], C.c_int),
     "sandy_hip_device_paged_positions": ([DEV, C.c_uint32, U32P, C.c_int32, T], C.c_int),
     "sandy_hip_device_paged_lengths": ([DEV, C.c_uint32, U32P, C.c_int32, T], C.c_int),
     "sandy_hip_device_decode_qkv": ([DEV, C.c_uint32, U32P, C.c_uint32, U32P, C.c_int32, T, C.c_int32, T, C.c_double,

@@ -80,19 +80,17 @@ __global__ __launch_bounds__(256) void paged_append_kernel(const char* __restric
     }
 }
 
-// one new grow row per tensor; position = device length; block per tensor
-__global__ __launch_bounds__(256) void paged_append_step_kernel(const char* __restrict__ rows, char* __restrict__ pages,
-                                                                const int32_t* __restrict__ table,
-                                                                int32_t* __restrict__ lengths, int64_t max_blocks,
-                                                                int64_t prefix, int64_t page_size, int64_t row_bytes,
-                                                                int64_t page_bytes, uint32_t* errw, StepArgs args,
-                                                                int32_t aligned16) {
-    const int i = blockIdx.x;
+// One grow row of tensor i of a step append (workgroup per row): rows of up
+// to 1 KiB, 16-byte multiples at 16-byte aligned addresses (`aligned16`
+// covers the rows view and the page pool), are requested before the slot ->
+// length -> block-table chain they do not depend on.
+__device__ __forceinline__ void append_step_row(const char* __restrict__ rows, char* __restrict__ pages,
+                                                const int32_t* __restrict__ table, int32_t* __restrict__ lengths,
+                                                int64_t max_blocks, int64_t prefix, int64_t page_size,
+                                                int64_t row_bytes, int64_t page_bytes, uint32_t* errw, int i,
+                                                int32_t slot, int32_t aligned16) {
     const int lane = threadIdx.x & 63;
-    // rows of up to 1 KiB (16-byte multiples at 16-byte aligned addresses:
-    // `aligned16` covers the rows view and the page pool), up to 16 of them:
-    // this thread's pieces (rows wave + 4j, piece lane) are requested before
-    // the slot -> length -> block-table chain they do not depend on
+    // up to 16 rows of a tensor: this thread's pieces (rows wave + 4j, piece lane)
     const bool vec = aligned16 && (row_bytes & 15) == 0;
     const bool pre = vec && row_bytes <= 1024 && prefix <= 16;
     // (four named registers: an array here was placed in LDS, whose writes
@@ -109,7 +107,6 @@ __global__ __launch_bounds__(256) void paged_append_step_kernel(const char* __re
         p2 = *at(w4 + 8);
         p3 = *at(w4 + 12);
     }
-    const int32_t slot = args.slots[i];
     const int32_t len = lengths[slot];
     __syncthreads();  // every wave has read the length before it advances
     const int32_t page = len / page_size;
@@ -140,6 +137,36 @@ __global__ __launch_bounds__(256) void paged_append_step_kernel(const char* __re
         if (blk >= 0) lengths[slot] = len + 1;
         else atomicOr(errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));  // no page reserved for the row
     }
+}
+
+// one new grow row per tensor; position = device length; block per tensor
+__global__ __launch_bounds__(256) void paged_append_step_kernel(const char* __restrict__ rows, char* __restrict__ pages,
+                                                                const int32_t* __restrict__ table,
+                                                                int32_t* __restrict__ lengths, int64_t max_blocks,
+                                                                int64_t prefix, int64_t page_size, int64_t row_bytes,
+                                                                int64_t page_bytes, uint32_t* errw, StepArgs args,
+                                                                int32_t aligned16) {
+    append_step_row(rows, pages, table, lengths, max_blocks, prefix, page_size, row_bytes, page_bytes, errw,
+                    blockIdx.x, args.slots[blockIdx.x], aligned16);
+}
+
+// The K and V step appends of one decode step in one launch: blockIdx.y
+// selects the set (0: K, 1: V), blockIdx.x the tensor.
+constexpr int kMaxKvStep = 64;
+struct KvStepSet {
+    const char* rows;
+    char* pages;
+    const int32_t* table;
+    int32_t* lengths;
+    int64_t max_blocks, prefix, page_size, row_bytes, page_bytes;
+    int32_t aligned16;
+    int32_t slots[kMaxKvStep];
+};
+
+__global__ __launch_bounds__(256) void paged_append_step_kv_kernel(KvStepSet k, KvStepSet v, uint32_t* errw) {
+    const KvStepSet& a = blockIdx.y ? v : k;
+    append_step_row(a.rows, a.pages, a.table, a.lengths, a.max_blocks, a.prefix, a.page_size, a.row_bytes,
+                    a.page_bytes, errw, blockIdx.x, a.slots[blockIdx.x], a.aligned16);
 }
 
 // One decode step's q/k/v post-processing for `count` sequences in one
@@ -683,6 +710,81 @@ int sandy_hip_device_paged_append_step(SandyHipDevice* d, uint32_t pool, const u
                        static_cast<int64_t>(p.page_elems * p.elem), errw, args,
                        static_cast<int32_t>(((reinterpret_cast<uintptr_t>(base_ptr(*rows)) |
                                               reinterpret_cast<uintptr_t>(p.pages)) & 15u) == 0));
+    SANDY_HIP_TRY(hipGetLastError(), e, "paged append step launch");
+    return ok(e);
+}
+
+int sandy_hip_device_paged_append_step_kv(SandyHipDevice* d, uint32_t k_pool, const uint32_t* k_tensors,
+                                          uint32_t v_pool, const uint32_t* v_tensors, int32_t count,
+                                          const SandyTensor* k_rows, const SandyTensor* v_rows, char* err,
+                                          size_t err_cap) {
+    Err e{err, err_cap};
+    int st = set_device(d, e);
+    if (st) return st;
+    std::lock_guard<std::mutex> lock(d->impl.mu);
+    if (count <= 0 || count > kMaxKvStep)
+        return fail(e, SANDY_ERR_INVALID, "paged append step count out of range (K and V together: at most %d)", kMaxKvStep);
+    if (!k_tensors || !v_tensors) return fail(e, SANDY_ERR_INVALID, "hip device paged tensor not found");
+    const uint32_t pools[2] = {k_pool, v_pool};
+    const uint32_t* ids[2] = {k_tensors, v_tensors};
+    const SandyTensor* rows[2] = {k_rows, v_rows};
+    PagedPool* pp[2] = {nullptr, nullptr};
+    // every check before any bookkeeping moves
+    for (int s = 0; s < 2; s++) {
+        auto pit = d->impl.pools.find(pools[s]);
+        if (pit == d->impl.pools.end()) return fail(e, SANDY_ERR_INVALID, "hip device paged pool not found");
+        pp[s] = pit->second.get();
+        const PagedPool& p = *pp[s];
+        if (!rows[s] || !contiguous(*rows[s]) || rows[s]->dtype != p.desc.dtype ||
+            numel(*rows[s]) != count * p.prefix * p.inner)
+            return fail(e, SANDY_ERR_INVALID, "hip device paged append step rows shape mismatch");
+        for (int i = 0; i < count; i++) {
+            auto it = d->impl.tensors.find(ids[s][i]);
+            if (it == d->impl.tensors.end() || it->second.pool != pools[s])
+                return fail(e, SANDY_ERR_INVALID, "hip device paged tensor not found");
+            for (int j = 0; j < i; j++)
+                if (ids[s][j] == ids[s][i]) return fail(e, SANDY_ERR_INVALID, "paged append step tensors must be distinct");
+        }
+    }
+    if (k_pool == v_pool)
+        for (int i = 0; i < count; i++)
+            for (int j = 0; j < count; j++)
+                if (k_tensors[i] == v_tensors[j])
+                    return fail(e, SANDY_ERR_INVALID, "paged append step tensors must be distinct");
+    uint32_t* errw = device_error_word(e, &st);
+    if (st) return st;
+    // pages for every new row first (outside capture), then the lengths
+    for (int s = 0; s < 2; s++)
+        for (int i = 0; i < count; i++) {
+            PagedTensor& t = d->impl.tensors.at(ids[s][i]);
+            const PagedPool& p = *pp[s];
+            if (t.grow_length + 1 > static_cast<int64_t>(t.pages.size()) * p.desc.page_size && !d->impl.capturing) {
+                st = reserve(d->impl, t, (t.grow_length + p.desc.page_size) / p.desc.page_size, e);
+                if (st) return st;
+            }
+        }
+    KvStepSet set[2];
+    for (int s = 0; s < 2; s++) {
+        const PagedPool& p = *pp[s];
+        KvStepSet& a = set[s];
+        a.rows = static_cast<const char*>(base_ptr(*rows[s]));
+        a.pages = p.pages;
+        a.table = p.table;
+        a.lengths = p.lengths;
+        a.max_blocks = p.desc.max_blocks;
+        a.prefix = p.prefix;
+        a.page_size = p.desc.page_size;
+        a.row_bytes = static_cast<int64_t>(p.inner * p.elem);
+        a.page_bytes = static_cast<int64_t>(p.page_elems * p.elem);
+        a.aligned16 = static_cast<int32_t>(((reinterpret_cast<uintptr_t>(a.rows) | reinterpret_cast<uintptr_t>(p.pages)) & 15u) == 0);
+        for (int i = 0; i < count; i++) {
+            PagedTensor& t = d->impl.tensors.at(ids[s][i]);
+            t.grow_length += 1;  // host bookkeeping in step with the device
+            a.slots[i] = t.slot;
+        }
+    }
+    hipLaunchKernelGGL(paged_append_step_kv_kernel, dim3(static_cast<unsigned>(count), 2), dim3(256), 0, d->impl.stream,
+                       set[0], set[1], errw);
     SANDY_HIP_TRY(hipGetLastError(), e, "paged append step launch");
     return ok(e);
 }

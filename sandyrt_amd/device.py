@@ -108,6 +108,16 @@ class HipDevice:
         dcall("sandy_hip_device_paged_append_step", self.handle, C.c_uint32(pool), ids, C.c_int32(len(tensors)),
               desc(rows))
 
+    def append_step_kv(self, k_pool: int, k_tensors, v_pool: int, v_tensors, k_rows: torch.Tensor,
+                       v_rows: torch.Tensor):
+        """append_step of the K rows and of the V rows, one launch."""
+        kids = (C.c_uint32 * len(k_tensors))(*k_tensors)
+        vids = (C.c_uint32 * len(v_tensors))(*v_tensors)
+        if len(k_tensors) != len(v_tensors):
+            raise ValueError("append_step_kv takes as many K as V tensors")
+        dcall("sandy_hip_device_paged_append_step_kv", self.handle, C.c_uint32(k_pool), kids, C.c_uint32(v_pool), vids,
+              C.c_int32(len(k_tensors)), desc(k_rows), desc(v_rows))
+
     def decode_qkv(self, k_pool: int, k_tensors, v_pool: int, v_tensors, qkv: torch.Tensor, q_heads: int,
                    positions: torch.Tensor, theta: float, q_out: torch.Tensor, split_half: bool = True):
         """RoPE q into q_out, RoPE k and append it, append v -- one launch for

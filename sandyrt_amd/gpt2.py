@@ -225,10 +225,9 @@ class GPT2Runner:
             prog.append(linear(x, p + "attn.qkv", b["qkv"], ln=p + "ln_1"))
             kid, vid = (C.c_uint32 * 1)(self.k_seq[i]), (C.c_uint32 * 1)(self.v_seq[i])
             self._keep += [kid, vid]
-            prog.append(_DevCall("sandy_hip_device_paged_append_step", dev.handle, C.c_uint32(self.k_pools[i]), kid,
-                                 C.c_int32(1), d(head4(k))))
-            prog.append(_DevCall("sandy_hip_device_paged_append_step", dev.handle, C.c_uint32(self.v_pools[i]), vid,
-                                 C.c_int32(1), d(head4(v))))
+            # this token's K and V rows appended together (one launch)
+            prog.append(_DevCall("sandy_hip_device_paged_append_step_kv", dev.handle, C.c_uint32(self.k_pools[i]), kid,
+                                 C.c_uint32(self.v_pools[i]), vid, C.c_int32(1), d(head4(k)), d(head4(v))))
             kc, table, _ = dev.paged_views(self.k_pools[i])
             vc, _, _ = dev.paged_views(self.v_pools[i])
             table.contents.dims[0] = 1

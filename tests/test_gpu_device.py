@@ -559,3 +559,53 @@ def test_append_step_rejects_repeated_tensor(dev):
     rows = torch.zeros(2, 2, 1, 64, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(SandyError, match="tensors must be distinct"):
         dev.append_step(pool, [t, t], rows)
+
+
+def test_append_step_kv_equals_two_step_appends(dev):
+    """K and V step appends in one launch: the pages read back as the rows
+    appended, for both caches (a K and a V pool, three sequences, a page
+    boundary crossed), lengths advanced on the host and the device."""
+    from sandyrt_amd._lib import BF16
+    count, hkv, D = 3, 2, 64
+    torch.cuda.synchronize()
+    kp = dev.create_paged_pool([1, hkv, -1, D], BF16, 2, 16, max_tensors=count, max_blocks=4)
+    vp = dev.create_paged_pool([1, hkv, -1, D], BF16, 2, 16, max_tensors=count, max_blocks=4)
+    ks, vs = [dev.alloc_paged(kp) for _ in range(count)], [dev.alloc_paged(vp) for _ in range(count)]
+    r = rng(77)
+    want_k, want_v = [[] for _ in ks], [[] for _ in vs]
+    for step in range(20):
+        kr = from_f32(normal(r, (count, hkv, 1, D)), torch.bfloat16)
+        vr = from_f32(normal(r, (count, hkv, 1, D)), torch.bfloat16)
+        torch.cuda.synchronize()
+        dev.append_step_kv(kp, ks, vp, vs, kr, vr)
+        for i in range(count):
+            want_k[i].append(bf16_np(kr[i:i + 1]))
+            want_v[i].append(bf16_np(vr[i:i + 1]))
+    dev.synchronize()
+    for i in range(count):
+        assert dev.paged_meta(ks[i]).grow_length == 20 and dev.paged_meta(vs[i]).grow_length == 20
+        assert np.array_equal(dev.read_paged(ks[i], np.uint16), np.concatenate(want_k[i], axis=2))
+        assert np.array_equal(dev.read_paged(vs[i], np.uint16), np.concatenate(want_v[i], axis=2))
+    lengths = torch.empty(count, dtype=torch.int64, device="cuda")
+    dev.lengths(vp, vs, lengths)
+    dev.synchronize()
+    assert lengths.tolist() == [20] * count
+
+
+def test_append_step_kv_rejects_before_moving_bookkeeping(dev):
+    from sandyrt_amd._lib import BF16, SandyError
+    kp = dev.create_paged_pool([1, 2, -1, 64], BF16, 2, 16, max_tensors=2, max_blocks=2)
+    vp = dev.create_paged_pool([1, 2, -1, 64], BF16, 2, 16, max_tensors=2, max_blocks=2)
+    ks, vs = [dev.alloc_paged(kp) for _ in range(2)], [dev.alloc_paged(vp) for _ in range(2)]
+    good = torch.zeros(2, 2, 1, 64, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(SandyError, match="rows shape mismatch"):
+        dev.append_step_kv(kp, ks, vp, vs, good, torch.zeros(2, 2, 1, 32, dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(SandyError, match="tensors must be distinct"):
+        dev.append_step_kv(kp, [ks[0], ks[0]], vp, vs, good, good)
+    with pytest.raises(SandyError, match="paged tensor not found"):
+        dev.append_step_kv(kp, ks, vp, [vs[0], ks[1]], good, good)  # a K tensor given as V
+    for t in ks + vs:
+        assert dev.paged_meta(t).grow_length == 0  # nothing moved
+    with pytest.raises(SandyError, match="count out of range"):
+        many = torch.zeros(65, 2, 1, 64, dtype=torch.bfloat16, device="cuda")
+        dev.append_step_kv(kp, list(range(65)), vp, list(range(65)), many, many)
