@@ -731,8 +731,11 @@ __device__ __forceinline__ int64_t kv_row(const GenArgs& a, const int64_t* st, c
     if (pages) {
         const uint64_t at = pages[page];
         if (at == 0) {
+            // no page: flagged, and the row offset points at q (readable memory:
+            // offsets are absolute element addresses here, and loads through
+            // this row stay inside q's first row)
             ok = false;
-            return 0;
+            return static_cast<int64_t>(reinterpret_cast<uintptr_t>(a.q) >> (a.dt == SANDY_F32 ? 2 : 1));
         }
         return static_cast<int64_t>(at >> (a.dt == SANDY_F32 ? 2 : 1)) + ((b * a.kv_rows_b + kh) * a.page_size + in_page) * a.d;
     }
@@ -839,6 +842,8 @@ __global__ __launch_bounds__(256) void attention_general_kernel(GenArgs a) {
         }
         Vec8<T>::store1(a.out, ooff + d * a.os[3], acc);
     }
+    // V rows are looked up only here: a missing V page is flagged after the loop
+    if (!ok) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_BLOCK));
 }
 
 // The same algorithm and operation order for up to kGenStage keys, with the

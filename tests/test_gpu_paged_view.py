@@ -89,3 +89,28 @@ def test_paged_view_errors(ops):
     odd = ops.PagedView(kv.pages, [2, 2, 40, 64], 12, torch.bfloat16)
     with pytest.raises(SandyError, match="power of two"):
         ops.attention_paged_view(q, odd, odd, pos)
+
+
+@pytest.mark.parametrize("dtype,tq,D,unstaged", [(torch.float32, 1, 64, False), (torch.bfloat16, 5, 64, False),
+                                                 (torch.bfloat16, 1, 64, False), (torch.bfloat16, 1, 96, False),
+                                                 (torch.float32, 1, 64, True), (torch.bfloat16, 5, 64, True)])
+def test_null_page_is_a_device_error(ops, monkeypatch, dtype, tq, D, unstaged):
+    """A page-table entry of 0 inside the attended range is reported as a
+    device error by every kernel that reads the view (f32 decode and prefill
+    through the general kernels, bf16 decode through the MFMA kernel, a head
+    dim the MFMA kernel does not take), and nothing is read from address 0."""
+    from sandyrt_amd._lib import SandyError
+    r = rng(11)
+    kv, _, keep_k = make_view(ops, r, [2, 2], 40, D, 16, dtype)
+    vv, _, keep_v = make_view(ops, r, [2, 2], 40, D, 16, dtype)
+    holed = kv.pages.clone()
+    holed[1] = 0  # keys 16..31 have no page
+    kz = ops.PagedView(holed, [2, 2, 40, D], 16, dtype)
+    vz = ops.PagedView(holed.clone(), [2, 2, 40, D], 16, dtype)
+    q = from_f32(normal(r, (2, 4, tq, D)), dtype)
+    pos = torch.tensor([39 - (tq - 1), 39 - (tq - 1)], dtype=torch.int64, device="cuda")
+    for k_view, v_view in ((kz, vv), (kv, vz)):
+        ops.attention_paged_view(q, k_view, v_view, pos)
+        with pytest.raises(SandyError, match="block id outside the pool"):
+            ops.check_device_errors()
+    torch.cuda.synchronize()
