@@ -201,11 +201,34 @@ __global__ __launch_bounds__(256) void rope_split_lines_kernel(
         RopeWords pw{0, 0};
         float den4[4];
         if (!TAB && fresh) {
-            pw = rope_position_words(mode, ids, ids_dt, o0 * seq + s, s, errw);
+            // mode 0 needs no position word: the sin/cos then depend on no
+            // vector load and are computed while the rows are in flight
+            if (mode != 0) pw = rope_position_words(mode, ids, ids_dt, o0 * seq + s, s, errw);
+            if (chunks <= 4) {
+                // rows of up to 64 pairs: every candidate denominator is a
+                // uniform (scalar) load, selected by the lane's quarter-chunk
+                // (constant offsets into the argument block: the first 32
+                // denominators in scalar registers; entries past rot_pairs
+                // feed only pairs that pass through unrotated)
+                // (readfirstlane keeps each value a scalar: a select between
+                // loads would otherwise become one per-lane vector load)
+                const int sel = 2 * c + (hi ? 1 : 0);
+                int all[32];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int p = c * 8 + (hi ? 4 : 0) + i;
-                den4[i] = args.denom[FULL || p < rot_pairs ? p : 0];
+                for (int q = 0; q < 32; q++) all[q] = __builtin_amdgcn_readfirstlane(__float_as_int(args.denom[q]));
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    int d = all[i];
+#pragma unroll
+                    for (int q = 1; q < 8; q++) d = q == sel ? all[4 * q + i] : d;
+                    den4[i] = __int_as_float(d);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int p = c * 8 + (hi ? 4 : 0) + i;
+                    den4[i] = args.denom[FULL || p < rot_pairs ? p : 0];
+                }
             }
         }
         float2 tv[4];

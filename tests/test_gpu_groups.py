@@ -138,7 +138,7 @@ def test_rope_angles_bit_exact_at_long_positions(ops, oracle):
     """Angles pos / theta^(2i/d) are identical to the CPU (host powf, correctly
     rounded division); remaining error is cos/sin ulp only."""
     x = torch.zeros(1, 1, 8192, 64, device="cuda")
-    x[..., 0] = 1.0  # output[0] = cos(angle_0), output[32] = sin(angle_0)
+    x[..., :32] = 1.0  # output[p] = cos(angle_p), output[32 + p] = sin(angle_p), every pair
     got = ops.rope(x, 10000.0, split_half=True)
     want = oracle.rope(to_oracle(x), 10000.0, split_half=True)
     np.testing.assert_allclose(got.cpu().numpy(), want, atol=2e-7)
