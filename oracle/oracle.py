@@ -68,6 +68,8 @@ def build(reference: bool = False) -> None:
     subprocess.run(["make", "-s", "-C", HERE, "all"], check=True)
     if reference and os.path.isdir("/root/reference/src/core"):
         subprocess.run(["make", "-s", "-C", HERE, "ref"], check=True)
+        if os.path.exists(os.path.join(os.path.dirname(HERE), "sandyrt_amd", "libsandyrt_hip.so")):
+            subprocess.run(["make", "-s", "-C", HERE, "binding"], check=True)
 
 
 def dtype_code(a: np.ndarray, bf16: bool = False) -> int:
