@@ -349,6 +349,102 @@ int main() {
         run("moe_scatter_sum_bf16", ss, {dense_view(mo), dense_view(pw), dense_view(tok), dense_view(ref)},
             {&mo, &pw, &tok}, {&so});
     }
+    // reduction: sum over the last dim, keep dims, f32 [4, 300]
+    {
+        kir::ReductionKernelOp op(id++, kir::ReduceOp::Sum, 0, 1, {1}, true);
+        HostTensor x = random_tensor("x", DType::F32, {4, 300}, 16);
+        HostTensor o = empty_tensor("out", DType::F32, {4, 1});
+        upload(x);
+        run("reduce_sum_f32", op, {dense_view(x)}, {&x}, {&o});
+    }
+    // linear with bias, f32 [3, 96] x [40, 96]^T + [40]
+    {
+        kir::LinearKernelOp op(id++, 0, 1, 2, 3);
+        HostTensor x = random_tensor("x", DType::F32, {3, 96}, 17), w = random_tensor("w", DType::F32, {40, 96}, 18);
+        HostTensor b = random_tensor("b", DType::F32, {40}, 19);
+        HostTensor o = empty_tensor("out", DType::F32, {3, 40});
+        upload(x);
+        upload(w);
+        upload(b);
+        run("linear_f32", op, {dense_view(x), dense_view(w), dense_view(b)}, {&x, &w, &b}, {&o});
+    }
+    // matmul, rhs transposed, bf16 [2, 5, 128] x [2, 48, 128]^T
+    {
+        kir::MatMulKernelOp op(id++, 0, 1, 2, false, true);
+        HostTensor l = random_tensor("lhs", DType::BF16, {2, 5, 128}, 20);
+        HostTensor r = random_tensor("rhs", DType::BF16, {2, 48, 128}, 21);
+        HostTensor o = empty_tensor("out", DType::BF16, {2, 5, 48});
+        upload(l);
+        upload(r);
+        run("matmul_bf16", op, {dense_view(l), dense_view(r)}, {&l, &r}, {&o});
+    }
+    // gather (embedding rows), int64 ids into a bf16 [50, 64] table
+    {
+        kir::GatherKernelOp op(id++, 0, 1, 2);
+        HostTensor ids = index_tensor("ids", DType::I64, {6}, std::vector<int64_t>{3, 0, 49, 3, 17, 8});
+        HostTensor t = random_tensor("table", DType::BF16, {50, 64}, 22);
+        HostTensor o = empty_tensor("out", DType::BF16, {6, 64});
+        upload(ids);
+        upload(t);
+        run("gather_bf16", op, {dense_view(ids), dense_view(t)}, {&ids, &t}, {&o});
+    }
+    // LayerNorm with weight and bias, f32 [3, 768]
+    {
+        kir::NormKernelOp ln(id++, kir::NormKind::LayerNorm, std::vector<kir::ValueId>{0, 1, 2}, 3, 1e-5);
+        HostTensor x = random_tensor("x", DType::F32, {3, 768}, 23), w = random_tensor("w", DType::F32, {768}, 24);
+        HostTensor b = random_tensor("b", DType::F32, {768}, 25);
+        HostTensor o = empty_tensor("out", DType::F32, {3, 768});
+        upload(x);
+        upload(w);
+        upload(b);
+        run("layer_norm_f32", ln, {dense_view(x), dense_view(w), dense_view(b)}, {&x, &w, &b}, {&o});
+    }
+    // interleaved partial RoPE with position ids, theta 5e5, f32 [1, 2, 16, 64]
+    {
+        kir::RoPEKernelOp rope(id++, std::vector<kir::ValueId>{0, 1}, 2, 500000.0, 32, false);
+        HostTensor x = random_tensor("x", DType::F32, {1, 2, 16, 64}, 26);
+        std::vector<int64_t> p(16);
+        for (int i = 0; i < 16; ++i) p[static_cast<size_t>(i)] = 1000 + 37 * i;
+        HostTensor ids = index_tensor("ids", DType::I64, {16}, p);
+        HostTensor o = empty_tensor("out", DType::F32, {1, 2, 16, 64});
+        upload(x);
+        upload(ids);
+        run("rope_ids_f32", rope, {dense_view(x), dense_view(ids)}, {&x, &ids}, {&o});
+    }
+    // layout: a transposed view of a [4, 6] f32 buffer made contiguous
+    {
+        kir::LayoutTransformOp op(id++, kir::LayoutTransformKind::Transpose, 0, 1, {1, 0});
+        HostTensor x = random_tensor("x", DType::F32, {4, 6}, 27);
+        HostTensor o = empty_tensor("out", DType::F32, {6, 4});
+        upload(x);
+        HipDeviceBufferView v = dense_view(x);
+        v.view.desc = TensorDesc(Shape(std::vector<int64_t>{6, 4}), DType::F32);
+        v.view.strides = {1, 6};
+        run("layout_transpose_f32", op, {v}, {&x}, {&o});
+    }
+    // softmax over a paged bf16 input [2, 5, 8] (grow dim 1, pages of 4 rows)
+    {
+        kir::SoftmaxKernelOp sm(id++, 0, 1, -1);
+        HostTensor x = random_tensor("x", DType::BF16, {2, 5, 8}, 28, 3.0f);
+        HostTensor o = empty_tensor("out", DType::BF16, {2, 5, 8});
+        PagedOperand px = make_paged(x, 1, 4);
+        run("softmax_paged_bf16", sm, {px.view}, {&x}, {&o});
+    }
+    // dense attention (prefill, causal from positions), bf16 q [1, 8, 4, 64], K/V [1, 2, 12, 64]
+    {
+        kir::AttentionKernelOp at(id++, 0, 1, 2, 3, 4, 0, -1.0);
+        HostTensor q = random_tensor("q", DType::BF16, {1, 8, 4, 64}, 29);
+        HostTensor k = random_tensor("k", DType::BF16, {1, 2, 12, 64}, 30);
+        HostTensor v = random_tensor("v", DType::BF16, {1, 2, 12, 64}, 31);
+        HostTensor pos = index_tensor("pos", DType::I64, {1}, std::vector<int64_t>{8});
+        HostTensor o = empty_tensor("out", DType::BF16, {1, 8, 4, 64});
+        upload(q);
+        upload(k);
+        upload(v);
+        upload(pos);
+        run("attention_dense_bf16", at, {dense_view(q), dense_view(k), dense_view(v), dense_view(pos)},
+            {&q, &k, &v, &pos}, {&o});
+    }
     sandy_hip_device_destroy(g_dev);
     return 0;
 }

@@ -101,3 +101,50 @@ def test_moe_chain(cases, oracle):
     s, _ = _case(cases, "moe_scatter_sum_bf16")
     want = oracle.moe_scatter_sum(s["packed_out"], s["packed_w"], s["token_ids"], 8)
     assert_close(s["out"], want, torch.bfloat16, "moe_scatter_sum")
+
+
+def test_reduce_sum(cases, oracle):
+    t, _ = _case(cases, "reduce_sum_f32")
+    assert_close(t["out"], oracle.sum(t["x"]), torch.float32, "reduce sum")
+
+
+def test_linear(cases, oracle):
+    t, _ = _case(cases, "linear_f32")
+    assert_close(t["out"], oracle.linear(t["x"], t["w"], t["b"]), torch.float32, "linear")
+
+
+def test_matmul(cases, oracle):
+    t, _ = _case(cases, "matmul_bf16")
+    assert_close(t["out"], oracle.matmul(t["lhs"], t["rhs"], transpose_rhs=True), torch.bfloat16, "matmul")
+
+
+def test_gather(cases, oracle):
+    t, _ = _case(cases, "gather_bf16")
+    assert_equal(t["out"], oracle.embedding(t["ids"], t["table"]), "gather")
+
+
+def test_layer_norm(cases, oracle):
+    t, _ = _case(cases, "layer_norm_f32")
+    assert_close(t["out"], oracle.layer_norm(t["x"], t["w"], t["b"], 1e-5), torch.float32, "layer_norm")
+
+
+def test_rope_position_ids(cases, oracle):
+    t, _ = _case(cases, "rope_ids_f32")
+    want = oracle.rope(t["x"], 500000.0, rotary_dim=32, split_half=False, position_ids=t["ids"])
+    assert_close(t["out"], want, torch.float32, "rope with ids")
+
+
+def test_layout_transpose(cases):
+    t, _ = _case(cases, "layout_transpose_f32")
+    assert_equal(t["out"], np.ascontiguousarray(t["x"].T), "transpose")
+
+
+def test_softmax_paged(cases, oracle):
+    t, _ = _case(cases, "softmax_paged_bf16")
+    assert_close(t["out"], oracle.softmax(t["x"]), torch.bfloat16, "paged softmax")
+
+
+def test_dense_attention(cases, oracle):
+    t, _ = _case(cases, "attention_dense_bf16")
+    want = oracle.attention(t["q"], t["k"], t["v"], position_offsets=t["pos"])
+    assert_close(t["out"], want, torch.bfloat16, "dense attention")
