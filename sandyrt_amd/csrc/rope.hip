@@ -163,14 +163,19 @@ __global__ __launch_bounds__(256) void rope_split_kernel(
 // row (a power of two dividing 64) each load and store one 16- or 32-byte
 // piece, the first chunks lanes from the first half and the rest from the
 // second, so every load and store instruction covers whole rows instead of
-// one half of each.  Each lane takes its partner's (lane ^ chunks) piece by a
-// lane exchange, and computes the sin/cos of four of its eight pairs, taking
+// one half of each.  Each lane takes its partner's piece (the same piece
+// index in the other half) by a lane exchange, and computes the sin/cos of four of its eight pairs, taking
 // the other four from its partner.  Same arithmetic as
 // rope_split_kernel.
 // TAB: the cos/sin of every (sequence index, pair) come from a table built
 // by rope_cache_kernel (one [seq, rot_pairs] float2 table shared by q, k and
 // every layer of a forward pass) instead of being evaluated here.
-template <typename T, int U, bool FULL, bool TAB = false>
+// XCH: how a lane reaches its partner.  0: ds_bpermute to lane ^ chunks;
+// otherwise a DPP mirror (0x141 row_half_mirror for 8 lanes a row, 0x140
+// row_mirror for 16) with the second half's pieces laid out in reverse lane
+// order, so the mirrored lane holds the partner piece (one VALU move per word
+// instead of an LDS-crossbar round trip: 8.52-8.60 -> 8.45-8.47 us at config 2).
+template <typename T, int U, bool FULL, bool TAB = false, int XCH = 0>
 __global__ __launch_bounds__(256) void rope_split_lines_kernel(
         const void* __restrict__ x, void* __restrict__ out, const void* __restrict__ x2, void* __restrict__ out2,
         int64_t outer_first, const void* __restrict__ ids, int32_t ids_dt, int mode, int64_t seq, int64_t outer,
@@ -184,13 +189,17 @@ __global__ __launch_bounds__(256) void rope_split_lines_kernel(
     if (t >= static_cast<uint32_t>(seq) * lanes * static_cast<uint32_t>(groups)) return;
     const uint32_t r = t & (lanes - 1);
     const bool hi = r >= chunks;
-    const int c = static_cast<int>(r & (chunks - 1));
+    const int c = static_cast<int>(XCH != 0 && hi ? lanes - 1 - r : r & (chunks - 1));
     const uint32_t rest = t / lanes;
     const int64_t s = rest % static_cast<uint32_t>(seq);
     const int g = static_cast<int>(rest / static_cast<uint32_t>(seq));
     const int64_t o_begin = static_cast<int64_t>(g) * per_group;
     const int64_t o_end = min(outer, o_begin + per_group);
     const int m = static_cast<int>(chunks);
+    auto partner = [&](uint32_t v) -> uint32_t {
+        if constexpr (XCH != 0) return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), XCH, 0xf, 0xf, false));
+        else return static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), m, 64));
+    };
     float cs[8], sn[8];
     bool have = false;
     for (int64_t o0 = o_begin; o0 < o_end; o0 += U) {
@@ -273,7 +282,8 @@ __global__ __launch_bounds__(256) void rope_split_lines_kernel(
             }
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float so = __shfl_xor(s4[i], m, 64), co = __shfl_xor(c4[i], m, 64);
+                const float so = __uint_as_float(partner(__float_as_uint(s4[i])));
+                const float co = __uint_as_float(partner(__float_as_uint(c4[i])));
                 sn[i] = hi ? so : s4[i];
                 cs[i] = hi ? co : c4[i];
                 sn[4 + i] = hi ? s4[i] : so;
@@ -284,16 +294,16 @@ __global__ __launch_bounds__(256) void rope_split_lines_kernel(
         for (int j = 0; j < U; j++) {
             // every lane of a row takes the same branch here (o_end is per row group)
             if (!FULL && o0 + j >= o_end) break;
-            // the partner lane's piece (lane ^ chunks) through the LDS crossbar: the
-            // rows are read once, non-temporal (8.8 -> 8.5 us at config 2; reading
-            // the partner's piece again from the cached line ran 8.8-8.9 with plain
-            // loads and 9.3-9.7 with non-temporal ones; ds_swizzle 9.1-9.3)
+            // the partner lane's piece by a lane exchange: the rows are read
+            // once, non-temporal (8.8 -> 8.5 us at config 2 against re-reading the
+            // partner's piece from the cached line: 8.8-8.9 with plain loads,
+            // 9.3-9.7 with non-temporal ones; ds_swizzle 9.1-9.3)
             typename Vec8<T>::raw other;
             {
                 const uint32_t* src = reinterpret_cast<const uint32_t*>(&mine[j]);
                 uint32_t* dst = reinterpret_cast<uint32_t*>(&other);
 #pragma unroll
-                for (int w = 0; w < static_cast<int>(sizeof(mine[j]) / 4); w++) dst[w] = __shfl_xor(src[w], m, 64);
+                for (int w = 0; w < static_cast<int>(sizeof(mine[j]) / 4); w++) dst[w] = partner(src[w]);
             }
             const bool sec = o0 + j >= outer_first;
             const int64_t base = ((o0 + j - (sec ? outer_first : 0)) * seq + s) * dim;
@@ -564,8 +574,8 @@ int rope_run(const SandyTensor* const* xs, const SandyTensor* const* outs, int n
         int u = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
         if (lines && per == 6) u = 6;  // the whole-line kernel takes 6 heads' loads at once
         const bool full = outer % per == 0 && per % u == 0 && rot_pairs == dim / 2;
-#define SANDY_ROPE_LAUNCH(KERNEL, T, U, F)                                                                        \
-    hipLaunchKernelGGL((KERNEL<T, U, F>), grid, dim3(256), 0, stream, px, po, px2, po2, outer_first, ids, ids_dt, \
+#define SANDY_ROPE_LAUNCH(KERNEL, T, U, F, ...)                                                                   \
+    hipLaunchKernelGGL((KERNEL<T, U, F, ##__VA_ARGS__>), grid, dim3(256), 0, stream, px, po, px2, po2, outer_first, ids, ids_dt, \
                        md, seq, outer, static_cast<int>(dim), rot_pairs, groups, per, args, errw)
 #define SANDY_ROPE_F(KERNEL, T, U)                                 \
     do {                                                           \
@@ -579,11 +589,31 @@ int rope_run(const SandyTensor* const* xs, const SandyTensor* const* outs, int n
         else SANDY_ROPE_F(KERNEL, T, 1);                \
     } while (0)
         if (lines) {
-            if (u == 6) {
-                if (bf) SANDY_ROPE_F(rope_split_lines_kernel, BF16, 6);
-                else SANDY_ROPE_F(rope_split_lines_kernel, F32, 6);
-            } else if (bf) SANDY_ROPE_U(rope_split_lines_kernel, BF16);
-            else SANDY_ROPE_U(rope_split_lines_kernel, F32);
+            // the partner exchange by DPP mirror for 8 or 16 lanes a row (half = 32 or 64 elements)
+            const int lane_count = static_cast<int>(dim / 8);
+#define SANDY_ROPE_LINES(T, U, F)                                                                           \
+    do {                                                                                                     \
+        if (lane_count == 8) SANDY_ROPE_LAUNCH(rope_split_lines_kernel, T, U, F, false, 0x141);              \
+        else if (lane_count == 16) SANDY_ROPE_LAUNCH(rope_split_lines_kernel, T, U, F, false, 0x140);        \
+        else SANDY_ROPE_LAUNCH(rope_split_lines_kernel, T, U, F, false, 0);                                  \
+    } while (0)
+#define SANDY_ROPE_LINES_F(T, U)                 \
+    do {                                         \
+        if (full) SANDY_ROPE_LINES(T, U, true);  \
+        else SANDY_ROPE_LINES(T, U, false);      \
+    } while (0)
+#define SANDY_ROPE_LINES_T(T)                          \
+    do {                                               \
+        if (u == 6) SANDY_ROPE_LINES_F(T, 6);          \
+        else if (u == 4) SANDY_ROPE_LINES_F(T, 4);     \
+        else if (u == 2) SANDY_ROPE_LINES_F(T, 2);     \
+        else SANDY_ROPE_LINES_F(T, 1);                 \
+    } while (0)
+            if (bf) SANDY_ROPE_LINES_T(BF16);
+            else SANDY_ROPE_LINES_T(F32);
+#undef SANDY_ROPE_LINES_T
+#undef SANDY_ROPE_LINES_F
+#undef SANDY_ROPE_LINES
         } else if (split_half) {
             if (bf) SANDY_ROPE_U(rope_split_kernel, BF16);
             else SANDY_ROPE_U(rope_split_kernel, F32);
@@ -743,10 +773,16 @@ extern "C" int sandy_hip_rope_pair_cached(const SandyTensor* q, const SandyTenso
     const float2* tab = static_cast<const float2*>(base_ptr(*cache));
     dim3 grid(static_cast<unsigned>((threads + 255) / 256));
     hipStream_t stream = static_cast<hipStream_t>(stream_);
-#define SANDY_ROPE_TAB(T, U, F)                                                                                     \
-    hipLaunchKernelGGL((rope_split_lines_kernel<T, U, F, true>), grid, dim3(256), 0, stream, px, po, px2, po2,     \
+#define SANDY_ROPE_TAB_X(T, U, F, X)                                                                                \
+    hipLaunchKernelGGL((rope_split_lines_kernel<T, U, F, true, X>), grid, dim3(256), 0, stream, px, po, px2, po2,  \
                        sh[0].outer, nullptr, SANDY_I64, 0, seq, outer, static_cast<int>(dim), rot_pairs, groups, per, \
                        args, errw, tab)
+#define SANDY_ROPE_TAB(T, U, F)                                    \
+    do {                                                           \
+        if (chunks == 4) SANDY_ROPE_TAB_X(T, U, F, 0x141);         \
+        else if (chunks == 8) SANDY_ROPE_TAB_X(T, U, F, 0x140);    \
+        else SANDY_ROPE_TAB_X(T, U, F, 0);                         \
+    } while (0)
 #define SANDY_ROPE_TAB_F(T, U)                 \
     do {                                       \
         if (full) SANDY_ROPE_TAB(T, U, true);  \
@@ -764,6 +800,7 @@ extern "C" int sandy_hip_rope_pair_cached(const SandyTensor* q, const SandyTenso
 #undef SANDY_ROPE_TAB_T
 #undef SANDY_ROPE_TAB_F
 #undef SANDY_ROPE_TAB
+#undef SANDY_ROPE_TAB_X
     SANDY_HIP_TRY(hipGetLastError(), e, "rope launch");
     return ok(e);
 }

@@ -113,6 +113,10 @@ def test_elementwise_rejects_bad_dag(ops):
     dict(shape=(2, 4, 7, 96), split=True, rot=-1),         # 3 pieces per half: half-row kernel
     dict(shape=(2, 2, 9, 80), split=True, rot=48),         # 5 pieces, partial rotary
     dict(shape=(1, 3, 5, 16), split=True, rot=-1),         # one piece per half: 2-lane rows
+    dict(shape=(2, 4, 9, 128), split=True, rot=-1),        # 16-lane rows (DPP row mirror exchange)
+    dict(shape=(2, 3, 5, 128), split=True, rot=64),        # the same, partial rotary
+    dict(shape=(3, 6, 7, 64), split=True, rot=48),         # 8-lane rows (DPP half-row mirror), partial
+    dict(shape=(2, 5, 3, 32), split=True, rot=-1),         # 4-lane rows (lane exchange by ds_bpermute)
 ])
 def test_rope(ops, oracle, dtype, case):
     r = rng(hash(tuple(case["shape"])) % 2**32)
@@ -245,15 +249,16 @@ def test_rope_pair_rejects_mismatched_tensors(ops):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("ids_kind", [None, "offset", "seq"])
 @pytest.mark.parametrize("rotary", [-1, 32])
-def test_rope_from_cache_equals_direct(ops, dtype, ids_kind, rotary):
+@pytest.mark.parametrize("hd", [64, 128])
+def test_rope_from_cache_equals_direct(ops, dtype, ids_kind, rotary, hd):
     """A cos/sin cache built once, applied to q and k: bit-identical to the
     direct rope_pair (same angle, same sin/cos), full and partial rotary."""
     r = rng(19)
-    q = from_f32(normal(r, (1, 12, 40, 64)), dtype)
-    k = from_f32(normal(r, (1, 2, 40, 64)), dtype)
+    q = from_f32(normal(r, (1, 12, 40, hd)), dtype)
+    k = from_f32(normal(r, (1, 2, 40, hd)), dtype)
     ids = {None: None, "offset": torch.tensor([4000], device="cuda"),
            "seq": torch.from_numpy(r.integers(0, 100000, 40)).cuda()}[ids_kind]
-    cache = ops.rope_cache(40, 64, 1e4, rotary_dim=rotary, split_half=True, position_ids=ids)
+    cache = ops.rope_cache(40, hd, 1e4, rotary_dim=rotary, split_half=True, position_ids=ids)
     qc, kc = ops.rope_pair_cached(q, k, cache)
     qd, kd = ops.rope_pair(q, k, 1e4, rotary_dim=rotary, split_half=True, position_ids=ids)
     assert torch.equal(qc, qd) and torch.equal(kc, kd)
