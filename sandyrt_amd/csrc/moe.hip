@@ -1469,6 +1469,41 @@ extern "C" int sandy_hip_moe_gather(const SandyTensor* x, const SandyTensor* top
     return ok(e);
 }
 
+namespace sandy_hip {
+namespace {
+// Column tile (16 * CT columns a wave, 64 * CT a workgroup) of the 64-row
+// grouped-GEMM kernel: the one whose workgroups fill whole rounds of the
+// resident slots best (two workgroups a CU), counting the padded columns of
+// the last tile; ties go to the wider tile (fewer activation re-reads).
+// Config 5: gate and up (704 columns, 128 experts) take 192-column tiles,
+// 512 workgroups, one full round (gate 91.4 -> 86.1 us, up 85.2 -> 81.0);
+// down (2816 columns) keeps 256 (98.0 us against 100.6-101.0 at 192).
+int moe_column_tile(int64_t M, int64_t groups) {
+    static const int slots = [] {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        return 2 * cus;
+    }();
+    int best = 4;
+    double best_eff = -1.0;
+    for (int ct = 4; ct >= 2; ct--) {
+        const int64_t tiles = (M + 64 * ct - 1) / (64 * ct);
+        const int64_t wgs = tiles * groups;
+        const int64_t rounds = (wgs + slots - 1) / slots;
+        const double eff = static_cast<double>(M) / static_cast<double>(tiles * 64 * ct) *
+                           static_cast<double>(wgs) / static_cast<double>(rounds * slots);
+        if (eff > best_eff + 1e-9) {
+            best_eff = eff;
+            best = ct;
+        }
+    }
+    return best;
+}
+} // namespace
+} // namespace sandy_hip
+
 extern "C" int sandy_hip_moe_matmul(const SandyTensor* x, const SandyTensor* expert_offsets, const SandyTensor* weight,
                                     int32_t transpose_rhs, const SandyTensor* out, void* stream_, char* err,
                                     size_t err_cap) {
@@ -1507,8 +1542,10 @@ extern "C" int sandy_hip_moe_matmul(const SandyTensor* x, const SandyTensor* exp
         const auto* pw = static_cast<const uint16_t*>(base_ptr(*weight));
         auto* po = static_cast<uint16_t*>(base_ptr(*out));
         const void* po_ = base_ptr(*expert_offsets);
-        // tile: 16 rows x 32 columns per wave for decode-sized batches, 64 x 64 otherwise
-        const int variant = env_int("SANDY_MOE_GEMM", avg <= 16 ? 0 : 1);
+        // tile: 16 rows x 32 columns per wave for decode-sized batches, otherwise
+        // 64 rows x the column tile of moe_column_tile
+        const int col_tile = avg <= 16 ? 2 : moe_column_tile(M, batch * experts);
+        const int variant = env_int("SANDY_MOE_GEMM", avg <= 16 ? 0 : col_tile == 3 ? 5 : col_tile == 2 ? 2 : 1);
         auto grid_for = [&](int ct) {
             return dim3(static_cast<unsigned>(batch * experts), static_cast<unsigned>((M + 64 * ct - 1) / (64 * ct)));
         };
@@ -1520,6 +1557,7 @@ extern "C" int sandy_hip_moe_matmul(const SandyTensor* x, const SandyTensor* exp
             case 2: LINES_LAUNCH(4, 2); break;
             case 3: LINES_LAUNCH(2, 4); break;
             case 4: LINES_LAUNCH(2, 2); break;
+            case 5: LINES_LAUNCH(4, 3); break;
             default: LINES_LAUNCH(4, 4); break;
         }
 #undef LINES_LAUNCH

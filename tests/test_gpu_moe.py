@@ -239,7 +239,7 @@ def test_moe_matmul_small(ops, oracle, dtype, transpose_rhs):
     _moe_matmul_ragged(ops, oracle, dtype, transpose_rhs)
 
 
-@pytest.mark.parametrize("tile", ["0", "1", "2", "3", "4"])
+@pytest.mark.parametrize("tile", ["0", "1", "2", "3", "4", "5"])
 def test_moe_matmul_tile_shapes(ops, oracle, monkeypatch, tile):
     """Every tile shape of the bf16 grouped-GEMM kernel on the ragged case."""
     monkeypatch.setenv("SANDY_MOE_GEMM", tile)
