@@ -45,6 +45,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <mutex>
+#include <vector>
 
 namespace sandy_hip {
 namespace {
@@ -467,32 +468,42 @@ struct Unit {
     int total;  // active units (set when !active)
 };
 
+// LPT: every sequence's whole splits first, then the shorter last splits, so
+// the workgroups dispatched last carry the least work (for grids of more than
+// one round of resident workgroups); otherwise each sequence's splits in order.
+template <bool LPT>
 __device__ __forceinline__ Unit find_unit(const PagedArgs& a, int lin, int split_tiles, int lane) {
     int base = 0;
-    for (int c0 = 0; c0 < a.batch; c0 += 64) {
-        const int bi = c0 + lane;
-        const int64_t p = lane_position(a, bi < a.batch ? bi : 0);
-        const bool live = bi < a.batch && p >= 0;
-        const int units = live ? a.hkv * ((seq_range(a, p).n_tiles + split_tiles - 1) / split_tiles) : 0;
-        int incl = units;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int t = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += t;
+    for (int phase = 0; phase < (LPT ? 2 : 1); phase++) {
+        for (int c0 = 0; c0 < a.batch; c0 += 64) {
+            const int bi = c0 + lane;
+            const int64_t p = lane_position(a, bi < a.batch ? bi : 0);
+            const bool live = bi < a.batch && p >= 0;
+            const int n_tiles = live ? seq_range(a, p).n_tiles : 0;
+            const int full = n_tiles / split_tiles;
+            const int part = n_tiles % split_tiles != 0 ? 1 : 0;
+            const int units = a.hkv * (!LPT ? full + part : phase == 0 ? full : part);
+            int incl = units;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int t = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += t;
+            }
+            const int total = __builtin_amdgcn_readlane(incl, 63);
+            if (lin < base + total) {
+                const int bl = __builtin_ctzll(__ballot(lin < base + incl));
+                const int r = lin - base - __builtin_amdgcn_readlane(incl - units, bl);
+                Unit u;
+                u.b = c0 + bl;
+                u.split = phase == 0 ? r / a.hkv : __builtin_amdgcn_readlane(full, bl);
+                u.kh = phase == 0 ? r - u.split * a.hkv : r;
+                u.pos = lane_read64(p, bl);
+                u.active = true;
+                return u;
+            }
+            base += total;
         }
-        const int total = __builtin_amdgcn_readlane(incl, 63);
-        if (lin < base + total) {
-            const int bl = __builtin_ctzll(__ballot(lin < base + incl));
-            const int r = lin - base - __builtin_amdgcn_readlane(incl - units, bl);
-            Unit u;
-            u.b = c0 + bl;
-            u.split = r / a.hkv;
-            u.kh = r - u.split * a.hkv;
-            u.pos = lane_read64(p, bl);
-            u.active = true;
-            return u;
-        }
-        base += total;
     }
     Unit u{};
     u.active = false;
@@ -576,13 +587,13 @@ __device__ __forceinline__ void fused_merge(const PagedArgs& a, int b, int kh, i
 // OCC: waves per SIMD the register allocation must allow (1 = no limit).  The
 // D = 64 four-tile kernel (256-key splits) is held to 5, where it needs no
 // scratch and 1280 of its workgroups are resident at once.
-template <int D, int NB, int NT, int S, int OCC>
+template <int D, int NB, int NT, int S, int OCC, bool LPT = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void paged_decode_units_kernel(PagedArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     constexpr int kSplitTiles = 4 * NT;  // the host passes split_keys == 16 * kSplitTiles
-    const Unit u = find_unit(a, blockIdx.x, kSplitTiles, lane);
+    const Unit u = find_unit<LPT>(a, blockIdx.x, kSplitTiles, lane);
     if (!u.active) {
         if (a.fused) {
             const int nb = negative_sequence(a, static_cast<int>(blockIdx.x) - u.total, lane);
@@ -661,26 +672,45 @@ __global__ __launch_bounds__(64) void paged_decode_units_merge_kernel(PagedArgs 
 }
 
 // ------------------------------------------------ kernel selection (host)
-template <int D, int NB>
+template <int D, int NB, bool LPT>
 const void* units_for(int nt) {
     constexpr int kOcc4 = D == 64 ? 5 : 1;  // spill-free only for D = 64, four tiles per wave
     if constexpr (D == 256) {
         // held to 2 waves per SIMD: 248 VGPRs and no spills, where the unbounded
         // allocation (246 VGPRs + 64 AGPRs) leaves one wave per SIMD -- twice the
         // resident units (config 4: 132.0 -> 122.9 us with 512-key splits)
-        return nt == 2   ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 2, 2, 2>)
-               : nt == 4 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 4, 2, 2>)
-               : nt == 8 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 8, 2, 2>)
-                         : reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 16, 2, 2>);
+        return nt == 2   ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 2, 2, 2, LPT>)
+               : nt == 4 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 4, 2, 2, LPT>)
+               : nt == 8 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 8, 2, 2, LPT>)
+                         : reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 16, 2, 2, LPT>);
     }
-    return nt == 2   ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 2, 2, kOcc4>)
-           : nt == 4 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 4, 2, kOcc4>)
-           : nt == 8 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 8, 2, 1>)
-                     : reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 16, 2, 1>);
+    return nt == 2   ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 2, 2, kOcc4, LPT>)
+           : nt == 4 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 4, 2, kOcc4, LPT>)
+           : nt == 8 ? reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 8, 2, 1, LPT>)
+                     : reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 16, 2, 1, LPT>);
 }
 
-const void* units_kernel(int D, int nt) {
-    return D == 64 ? units_for<64, 2>(nt) : D == 128 ? units_for<128, 1>(nt) : units_for<256, 1>(nt);
+const void* units_kernel(int D, int nt, bool lpt = false) {
+    if (lpt) return D == 64 ? units_for<64, 2, true>(nt) : D == 128 ? units_for<128, 1, true>(nt) : units_for<256, 1, true>(nt);
+    return D == 64 ? units_for<64, 2, false>(nt) : D == 128 ? units_for<128, 1, false>(nt) : units_for<256, 1, false>(nt);
+}
+
+// Workgroups of 256 threads of kernel fn with `lds` bytes of dynamic LDS
+// resident on the whole device at once (occupancy times CUs), cached.
+int64_t resident_workgroups(const void* fn, size_t lds) {
+    static std::mutex mu;
+    static std::vector<std::pair<std::pair<const void*, size_t>, int64_t>> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto& c : cache)
+        if (c.first.first == fn && c.first.second == lds) return c.second;
+    int dev = 0, cus = 0, blocks = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 256, lds) != hipSuccess || blocks <= 0) blocks = 1;
+    const int64_t n = static_cast<int64_t>(blocks) * cus;
+    cache.push_back({{fn, lds}, n});
+    return n;
 }
 
 // ---------------------------------------------------------------- general kernel
@@ -1298,9 +1328,14 @@ int launch_paged_mfma(const PagedCall& c, const SandyTensor* q, const SandyTenso
     }
     a.ws_o = reinterpret_cast<float*>(ws);
     a.ws_ml = reinterpret_cast<float*>(ws + slots * D * sizeof(float));
-    // work units numbered over the active splits
-    SANDY_HIP_TRY(hipLaunchKernel(units_kernel(static_cast<int>(D), nt),
-                                  dim3(static_cast<unsigned>(units)), dim3(256), args, lds, stream),
+    // work units numbered over the active splits; whole splits first when the
+    // grid (active and idle units) exceeds two rounds of resident workgroups,
+    // where the active ones alone take more than one (config 4: 121.2-122.8 ->
+    // 119.0-120.2 us); config 3's 640 active of 1024 units fit one round and
+    // keep sequence order (23.5-23.9 against 23.6-23.9 with whole splits first)
+    const bool lpt = units > 2 * resident_workgroups(units_kernel(static_cast<int>(D), nt), lds);
+    SANDY_HIP_TRY(hipLaunchKernel(units_kernel(static_cast<int>(D), nt, lpt), dim3(static_cast<unsigned>(units)),
+                                  dim3(256), args, lds, stream),
                   e, "paged attention launch");
     const void* mfn = D == 64 ? reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<64>)
                     : D == 128 ? reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<128>)
