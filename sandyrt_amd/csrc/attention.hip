@@ -469,8 +469,9 @@ struct Unit {
 };
 
 // LPT: every sequence's whole splits first, then the shorter last splits, so
-// the workgroups dispatched last carry the least work (for grids of more than
-// one round of resident workgroups); otherwise each sequence's splits in order.
+// the workgroups dispatched last carry the least work (the host picks it when
+// the active units take more than one round of resident workgroups);
+// otherwise each sequence's splits in order.
 template <bool LPT>
 __device__ __forceinline__ Unit find_unit(const PagedArgs& a, int lin, int split_tiles, int lane) {
     int base = 0;
