@@ -1004,9 +1004,25 @@ __global__ __launch_bounds__(256) void attention_decode_f32_kernel(GenArgs a) {
     const int h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x;
     const int kh = h / (a.hq / a.hkv);
+    // requested together before any is waited for: the position's words
+    // (relaxed atomic loads stay on the vector memory path), this thread's q
+    // value and the block id of key tid's page -- with no window the first
+    // keys are 0..255 whatever the position (clamped to the table's width)
+    uint32_t plo = 0, phi = 0;
+    if (a.pos) {
+        const bool i32 = a.pos_dt == SANDY_I32;
+        uint32_t* pp = reinterpret_cast<uint32_t*>(const_cast<void*>(a.pos)) + (i32 ? b : 2 * b);
+        plo = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        phi = __hip_atomic_load(pp + (i32 ? 0 : 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const float* qg = static_cast<const float*>(a.q) + b * a.qs[0] + h * a.qs[1];
+    const float qt = qg[tid < D ? tid : 0];
+    const int sh = __builtin_ctzll(static_cast<uint64_t>(a.page_size));  // a power of two (host-checked)
+    const int32_t blk0 = a.max_blocks > 0 ? a.table[b * a.table_stride + min<int64_t>(tid >> sh, a.max_blocks - 1)] : -1;
     int64_t qpos = 0;
     if (a.pos) {
-        qpos = load_index(a.pos, a.pos_dt, b);
+        qpos = a.pos_dt == SANDY_I32 ? static_cast<int64_t>(static_cast<int32_t>(plo))
+                                     : static_cast<int64_t>((static_cast<uint64_t>(phi) << 32) | plo);
         if (qpos < 0) {
             if (tid == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
             return;
@@ -1014,16 +1030,24 @@ __global__ __launch_bounds__(256) void attention_decode_f32_kernel(GenArgs a) {
     }
     const int64_t min_key = a.window > 0 ? max<int64_t>(0, qpos + 1 - a.window) : 0;
     const int64_t k_end = min<int64_t>(a.tk, qpos + 1);
-    const float* qg = static_cast<const float*>(a.q) + b * a.qs[0] + h * a.qs[1];
-    if (tid < D) qv[tid] = qg[tid];
+    if (tid < D) qv[tid] = qt;
     __syncthreads();
     const float* kp = static_cast<const float*>(a.k);  // pool mode: k and v are the pools
     const float* vp = static_cast<const float*>(a.v);
     float lmax = -INFINITY;
     bool ok = true;
     for (int64_t key = min_key + tid; key < k_end; key += 256) {
-        const int64_t krow = kv_row(a, a.ks, a.k_pages, b, kh, key, ok);
-        svrow[key - min_key] = kv_row(a, a.vs, a.v_pages, b, kh, key, ok);
+        // pool mode: a key's K and V rows sit at the same offset of their pools
+        int64_t krow;
+        if (min_key == 0 && key == tid) {  // the block id requested up front
+            const int64_t in_page = key & (a.page_size - 1);
+            const bool bok = blk0 >= 0 && blk0 < a.num_pages;
+            ok = ok && bok;
+            krow = bok ? static_cast<int64_t>(blk0) * a.page_elems + (kh * a.page_size + in_page) * a.d : 0;
+        } else {
+            krow = kv_row(a, a.ks, a.k_pages, b, kh, key, ok);
+        }
+        svrow[key - min_key] = krow;
         const float4* kr = reinterpret_cast<const float4*>(kp + krow);
         float4 kv[D / 4];
 #pragma unroll
