@@ -276,3 +276,20 @@ def test_paged_decode_many_sequences(ops, oracle, B):
     run_case(ops, oracle, 600 + B, B, 8, 2, 64, 16, ctx, torch.bfloat16)
 
 
+
+
+@pytest.mark.parametrize("D,P", [(64, 16), (128, 64)])
+def test_paged_decode_longest_first_unit_order(ops, oracle, D, P):
+    """A grid past two rounds of resident workgroups (256 sequences of
+    300..3000 keys: three 1024-key splits each at most, whole splits numbered
+    before the shorter last splits), pages of 16 and 64 keys; against the
+    oracle on a subset that holds the shortest, the longest and split-boundary
+    lengths, and the whole batch against itself run twice (the merge adds
+    the splits in split order whichever workgroup arrives last)."""
+    r = rng(700 + D)
+    ctx = [int(c) for c in r.integers(300, 3001, 256)]
+    ctx[0], ctx[1], ctx[2], ctx[3] = 300, 3000, 1024, 2049
+    sub = [0, 1, 2, 3, int(np.argmin(ctx)), int(np.argmax(ctx)), 100, 255]
+    out1 = run_case(ops, oracle, 800 + D, 256, 16, 4, D, P, ctx, torch.bfloat16, subset=sub)
+    out2 = run_case(ops, oracle, 800 + D, 256, 16, 4, D, P, ctx, torch.bfloat16, subset=sub)
+    assert torch.equal(out1, out2)
