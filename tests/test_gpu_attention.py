@@ -90,9 +90,10 @@ def test_paged_decode_group_shapes(ops, oracle, group, D):
     run_case(ops, oracle, 4 + group, 3, 2 * group, 2, D, 32, [70, 200, 33], torch.bfloat16)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("window", [1, 7, 64, 500])
-def test_paged_decode_sliding_window(ops, oracle, window):
-    run_case(ops, oracle, 10 + window, 4, 16, 2, 64, 16, [5, 100, 700, 1200], torch.bfloat16, window=window)
+def test_paged_decode_sliding_window(ops, oracle, window, dtype):
+    run_case(ops, oracle, 10 + window, 4, 16, 2, 64, 16, [5, 100, 700, 1200], dtype, window=window)
 
 
 def test_paged_decode_small_pages_use_general_kernel(ops, oracle):
