@@ -213,10 +213,33 @@ __device__ __forceinline__ void load_q_columns(const PagedArgs& a, int b, int kh
     for (int kk = 0; kk < D / 32; kk++) qv[kk] = qp[kk * 4];
 }
 
-template <int D, int NB, int NT, int S>
+// Raw page-table word(s) of a tile's page: the K and V page addresses (the
+// reference's paged tensor) or the block id (pool mode, low 32 bits of k).
+struct PageRaw {
+    uint64_t k, v;
+};
+
+__device__ __forceinline__ PageRaw load_page_raw(const PagedArgs& a, int b, int64_t page) {
+    PageRaw r;
+    if (a.k_pages) {
+        r.k = a.k_pages[page];
+        r.v = a.v_pages[page];
+    } else {
+        r.k = static_cast<uint32_t>(a.table[b * a.table_stride + page]);
+        r.v = 0;
+    }
+    return r;
+}
+
+// PRE: the caller requested this lane's raw page words (pre) for tile
+// tile_a + wave + 4 * lane, page (16 * tile) >> log2_page clamped below
+// max_blocks, before the sequence's position was known (no sliding window:
+// key_begin is 0); otherwise they are loaded here.
+template <int D, int NB, int NT, int S, bool PRE = false>
 __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* smem, int lane, int wave, int b,
                                              int kh, const SplitRange& sr, int64_t tile_a, int64_t tile_b,
-                                             bool final_out, int64_t slot0, int64_t slot_stride, bool coherent) {
+                                             bool final_out, int64_t slot0, int64_t slot_stride, bool coherent,
+                                             PageRaw pre = PageRaw{0, 0}) {
     constexpr int kRow = 2 * D + 8;  // bytes per V row in LDS (8-byte pad: conflict-free transposed reads)
     const int G = a.group;
     const int g = lane & 15;
@@ -242,14 +265,15 @@ __device__ __forceinline__ void attend_piece(const PagedArgs& a, unsigned char* 
             const bool in = lane < NT && tile < tile_b && page < a.max_blocks &&
                             sr.key_begin + 16 * tile + 15 >= sr.min_key;
             bool ok;
+            const PageRaw raw = PRE ? pre : load_page_raw(a, b, in ? page : 0);  // max_blocks >= 1
             if (a.k_pages) {
-                kpv = a.k_pages[in ? page : 0];  // max_blocks >= 1
-                vpv = a.v_pages[in ? page : 0];
+                kpv = raw.k;
+                vpv = raw.v;
                 // 16-byte buffer loads: a page that is null or not 16-byte aligned
                 // is reported like a block id outside the pool
                 ok = kpv != 0 && vpv != 0 && ((kpv | vpv) & 15u) == 0;
             } else {
-                const int32_t id = a.table[b * a.table_stride + (in ? page : 0)];
+                const int32_t id = static_cast<int32_t>(static_cast<uint32_t>(raw.k));
                 ok = id >= 0 && id < a.num_pages;
                 kpv = reinterpret_cast<uint64_t>(a.k_pool + static_cast<int64_t>(ok ? id : 0) * a.page_elems);
                 vpv = reinterpret_cast<uint64_t>(a.v_pool + static_cast<int64_t>(ok ? id : 0) * a.page_elems);
@@ -617,6 +641,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void
     fused_merge<D>(a, u.b, u.kh, n_splits, slot0);
 }
 
+// Static schedule for grids no larger than the CU count, with no sliding
+// window: workgroup (sequence b, split, kv head) in sequence order over every
+// split the block table can hold.  With no window a tile's page does not
+// depend on the position, so each lane requests its tile's page-table word
+// together with the position: the block ids arrive with it instead of one
+// round trip later, and no scan of the positions precedes them.  A split past
+// the sequence's length exits; under the fused merge, split 0 of a negative
+// position writes its zero rows and raises the flag.  (On larger grids the
+// idle splits interleaved with the active ones cost more than this saves.)
+template <int D, int NB, int NT, int S, int OCC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(OCC))) void paged_decode_static_kernel(PagedArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr int kSplitTiles = 4 * NT;  // the host passes split_keys == 16 * kSplitTiles
+    const int lin = static_cast<int>(blockIdx.x);
+    const int kh = lin % a.hkv;
+    const int split = (lin / a.hkv) % a.max_splits;
+    const int b = lin / (a.hkv * a.max_splits);
+    const PosWords pw = vector_position(a, b);
+    const int64_t ta = static_cast<int64_t>(split) * kSplitTiles;
+    const int64_t page = min<int64_t>((16 * (ta + wave + 4 * lane)) >> a.log2_page, a.max_blocks - 1);
+    const PageRaw raw = load_page_raw(a, b, page);
+    const int64_t pos = join_position(a, pw);
+    if (pos < 0) {
+        if (a.fused && split == 0) {
+            for (int idx = threadIdx.x; idx < a.group * D; idx += 256)
+                a.out[b * a.o_sb + (kh * a.group + idx / D) * a.o_sh + idx % D] = 0;
+            if (kh == 0 && threadIdx.x == 0) atomicOr(a.errw, static_cast<uint32_t>(SANDY_DEVERR_ATTN_POS));
+        }
+        return;
+    }
+    const SplitRange sr = seq_range(a, pos);
+    const int n_splits = (sr.n_tiles + kSplitTiles - 1) / kSplitTiles;
+    if (split >= n_splits) return;
+    const int64_t tb = min<int64_t>(sr.n_tiles, ta + kSplitTiles);
+    const bool whole = n_splits == 1;
+    const int64_t slot0 = (static_cast<int64_t>(b) * a.hq + kh * a.group) * a.max_splits;
+    attend_piece<D, NB, NT, S, true>(a, smem, lane, wave, b, kh, sr, ta, tb, whole, slot0 + split, a.max_splits,
+                                     a.fused != 0, raw);
+    if (!a.fused || whole) return;
+    fused_merge<D>(a, b, kh, n_splits, slot0);
+}
+
 // Combines the split partials of one (sequence, q head) under the split-unit
 // schedule.  The position is loaded with the first slots' partials (one
 // memory round trip for up to 16 splits); slots at or past the sequence's
@@ -691,9 +759,41 @@ const void* units_for(int nt) {
                      : reinterpret_cast<const void*>(&paged_decode_units_kernel<D, NB, 16, 2, 1, LPT>);
 }
 
+// the static-schedule kernels (same register bounds as units_for)
+template <int D, int NB>
+const void* static_for(int nt) {
+    constexpr int kOcc4 = D == 64 ? 5 : 1;
+    if constexpr (D == 256) {
+        return nt == 2   ? reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 2, 2, 2>)
+               : nt == 4 ? reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 4, 2, 2>)
+               : nt == 8 ? reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 8, 2, 2>)
+                         : reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 16, 2, 2>);
+    }
+    return nt == 2   ? reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 2, 2, kOcc4>)
+           : nt == 4 ? reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 4, 2, kOcc4>)
+           : nt == 8 ? reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 8, 2, 1>)
+                     : reinterpret_cast<const void*>(&paged_decode_static_kernel<D, NB, 16, 2, 1>);
+}
+
+const void* static_kernel(int D, int nt) {
+    return D == 64 ? static_for<64, 2>(nt) : D == 128 ? static_for<128, 1>(nt) : static_for<256, 1>(nt);
+}
+
 const void* units_kernel(int D, int nt, bool lpt = false) {
     if (lpt) return D == 64 ? units_for<64, 2, true>(nt) : D == 128 ? units_for<128, 1, true>(nt) : units_for<256, 1, true>(nt);
     return D == 64 ? units_for<64, 2, false>(nt) : D == 128 ? units_for<128, 1, false>(nt) : units_for<256, 1, false>(nt);
+}
+
+// CUs of the current device (256 on MI355X), read once.
+int64_t device_cu_count() {
+    static const int64_t cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        return static_cast<int64_t>(n);
+    }();
+    return cus;
 }
 
 // Workgroups of 256 threads of kernel fn with `lds` bytes of dynamic LDS
@@ -704,12 +804,9 @@ int64_t resident_workgroups(const void* fn, size_t lds) {
     std::lock_guard<std::mutex> lock(mu);
     for (const auto& c : cache)
         if (c.first.first == fn && c.first.second == lds) return c.second;
-    int dev = 0, cus = 0, blocks = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        cus = 256;
+    int blocks = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 256, lds) != hipSuccess || blocks <= 0) blocks = 1;
-    const int64_t n = static_cast<int64_t>(blocks) * cus;
+    const int64_t n = static_cast<int64_t>(blocks) * device_cu_count();
     cache.push_back({{fn, lds}, n});
     return n;
 }
@@ -1359,8 +1456,12 @@ int launch_paged_mfma(const PagedCall& c, const SandyTensor* q, const SandyTenso
     // 119.0-120.2 us); config 3's 640 active of 1024 units fit one round and
     // keep sequence order (23.5-23.9 against 23.6-23.9 with whole splits first)
     const bool lpt = units > 2 * resident_workgroups(units_kernel(static_cast<int>(D), nt), lds);
-    SANDY_HIP_TRY(hipLaunchKernel(units_kernel(static_cast<int>(D), nt, lpt), dim3(static_cast<unsigned>(units)),
-                                  dim3(256), args, lds, stream),
+    // grids of at most one workgroup a CU with no window (batch-1 decode
+    // steps): the static schedule, block ids requested with the position
+    // (TinyLlama batch-1 step 1044.1-1045.4 -> 1038.3-1040.4 us)
+    const bool stat = window == 0 && units <= device_cu_count();
+    SANDY_HIP_TRY(hipLaunchKernel(stat ? static_kernel(static_cast<int>(D), nt) : units_kernel(static_cast<int>(D), nt, lpt),
+                                  dim3(static_cast<unsigned>(units)), dim3(256), args, lds, stream),
                   e, "paged attention launch");
     const void* mfn = D == 64 ? reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<64>)
                     : D == 128 ? reinterpret_cast<const void*>(&paged_decode_units_merge_kernel<128>)
